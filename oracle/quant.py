@@ -1,0 +1,121 @@
+"""Oracle for the symmetric int4 group quantizer, packer and unpack.
+
+Restates ``quantize.py:64-213`` and ``models/quantized.py:61-163`` of the
+reference. The format:
+
+* a weight is ``[out, in]``; the reduction axis is cut into groups of
+  ``group_size`` columns sharing one scale;
+* ``scale = max|w| / 7`` in f32, an all-zero group takes ``1 / 7``;
+* ``code = clip(rint(w / scale), -8, 7)``, f32 division, round half to even;
+* eight codes per ``int32`` word, code ``8j + k`` at bits ``4k`` of word ``j``;
+* the stored scale is ``scale`` rounded to the weight dtype (bf16, RNE), while
+  the codes come from the f32 scale (``models/quantized.py:149-163``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import from_bf16_bits, round_bf16, to_bf16_bits
+
+INT4_MIN = -8
+INT4_MAX = 7
+INT4_MAGNITUDE = 7
+NIBBLES_PER_WORD = 8
+
+
+def check_group_size(group_size: int, inner: int, packed_width: int = NIBBLES_PER_WORD) -> int:
+    """Validate a group size (``quantize.py:64-92``)."""
+
+    if group_size <= 0:
+        raise ValueError(f"quantization group size must be positive, got {group_size}")
+    if group_size % packed_width != 0:
+        raise ValueError(
+            f"quantization group size must be a multiple of {packed_width}, got {group_size}"
+        )
+    if inner % group_size != 0:
+        raise ValueError(
+            f"quantization group size {group_size} does not divide the reduction length {inner}"
+        )
+    return group_size
+
+
+def quantize_int4(weight, group_size: int = 64) -> tuple[np.ndarray, np.ndarray]:
+    """``(packed int32 [out, in/8], scales f32 [out, in/group])`` (``quantize.py:95-152``)."""
+
+    matrix = np.asarray(weight, dtype=np.float32)
+    if matrix.ndim != 2:
+        raise ValueError(f"quantization expects a 2-D weight, got {matrix.shape}")
+    rows, inner = matrix.shape
+    check_group_size(group_size, inner)
+    groups = inner // group_size
+    blocks = matrix.reshape(rows, groups, group_size)
+    widest = np.abs(blocks).max(axis=-1)
+    scale = (np.where(widest > np.float32(0.0), widest, np.float32(1.0)) / np.float32(INT4_MAGNITUDE)).astype(np.float32)
+    codes = np.clip(np.rint(blocks / scale[:, :, None]), INT4_MIN, INT4_MAGNITUDE)
+    codes = codes.astype(np.int32).reshape(rows, inner)
+    packed = np.zeros((rows, inner // NIBBLES_PER_WORD), dtype=np.int32)
+    for position in range(NIBBLES_PER_WORD):
+        field = (codes[:, position::NIBBLES_PER_WORD] & 0xF).astype(np.int32)
+        packed |= field << (4 * position)
+    return packed, scale
+
+
+def unpack_codes(packed) -> np.ndarray:
+    """Signed codes ``int8 [out, in]`` from packed words (``quantize.py:175-187``)."""
+
+    words = np.asarray(packed).astype(np.int64)
+    rows, count = words.shape
+    codes = np.empty((rows, count * NIBBLES_PER_WORD), dtype=np.int8)
+    for nibble in range(NIBBLES_PER_WORD):
+        field = ((words >> (4 * nibble)) & 0xF).astype(np.int8)
+        codes[:, nibble::NIBBLES_PER_WORD] = np.where(field >= 8, field - 16, field)
+    return codes
+
+
+def dequantize_int4(packed, scales, group_size: int) -> np.ndarray:
+    """f32 weights ``code * scale`` (``quantize.py:201-213``)."""
+
+    codes = unpack_codes(packed)
+    return codes.astype(np.float32) * np.repeat(np.asarray(scales, dtype=np.float32), group_size, axis=-1)
+
+
+def pack_weight_bf16(weight, group_size: int = 64) -> tuple[np.ndarray, np.ndarray]:
+    """Pack a weight held in bf16 and store bf16 scales (``models/quantized.py:133-163``).
+
+    ``weight`` is f32 values that are already bf16-representable (the model's
+    parameters widened), or ``uint16`` bf16 bits. Returns ``(packed int32,
+    scales uint16 bf16 bits)``.
+    """
+
+    w = np.asarray(weight)
+    if w.dtype == np.uint16:
+        w = from_bf16_bits(w)
+    packed, scales = quantize_int4(w.astype(np.float32), group_size)
+    return packed, to_bf16_bits(scales)
+
+
+def dequantize_i4_bf16(packed, scales_bf16_bits, group_size: int) -> np.ndarray:
+    """The torch op in the scales' dtype: ``bf16(code * scale_bf16)`` as f32.
+
+    ``models/quantized.py:61-76``: codes are cast to the scale dtype (exact for
+    -8..7) and multiplied in bf16, so each weight is the product rounded once.
+    """
+
+    codes = unpack_codes(packed).astype(np.float32)
+    scales = from_bf16_bits(scales_bf16_bits)
+    return round_bf16(codes * np.repeat(scales, group_size, axis=-1))
+
+
+def dequantize_i4_exact(packed, scales_bf16_bits, group_size: int) -> np.ndarray:
+    """``code * scale_bf16`` without a rounding step (exact in f32: 4 x 8 bits).
+
+    This is the weight the decode GEMV multiplies by: it never materializes a
+    rounded weight and accumulates ``code * (x * scale)`` in f32
+    (``codegen/matmul.py:696-704``); ``x * scale`` of two bf16 values is exact in
+    f32, so every product is exact and only the summation rounds.
+    """
+
+    codes = unpack_codes(packed).astype(np.float32)
+    scales = from_bf16_bits(scales_bf16_bits)
+    return codes * np.repeat(scales, group_size, axis=-1)

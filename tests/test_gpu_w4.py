@@ -1,0 +1,154 @@
+"""GPU parity of the W4 pack/unpack and decode GEMV kernels against the oracle.
+
+Pack and unpack must be bit-exact. The GEMV (f32 accumulation in a different
+order than the oracle's exact sum) must land within one bf16 ulp of the oracle,
+which also meets the north-star bars (max abs <= 2e-2, cosine >= 0.999).
+Shapes: the Qwen2.5-0.5B projections (config 2) and edge cases - a row count
+that is not a multiple of a block, a single row, the smallest K, other groups.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.ops import w4_gemv as oracle_gemv
+from oracle.quant import dequantize_i4_bf16, pack_weight_bf16
+from tests.helpers import assert_bf16_parity, bf16_bits_of, bf16_normal, from_gpu_bf16, to_gpu_bf16, to_gpu_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from aotolith_amd import ops
+
+    return ops
+
+
+def _packed_case(rng, n, k, group=64, std=0.02):
+    weight = bf16_normal(rng, (n, k), std)
+    packed, scales = pack_weight_bf16(weight, group)
+    return weight, packed, scales
+
+
+@pytest.mark.parametrize("n,k,group", [(1152, 896, 64), (896, 4864, 64), (37, 256, 32), (3, 512, 128)])
+@pytest.mark.parametrize("source", ["bf16", "f32"])
+def test_quantize_is_bit_exact(n, k, group, source):
+    rng = np.random.default_rng(n * 7 + k)
+    weight = bf16_normal(rng, (n, k), 0.02)
+    if source == "f32":
+        weight = rng.standard_normal((n, k)).astype(np.float32) * np.float32(0.02)
+        weight[0, :group] = 0.0  # an all-zero group
+        tensor = torch.from_numpy(weight).cuda()
+    else:
+        weight[0, :group] = 0.0
+        tensor = to_gpu_bf16(weight)
+    packed, scales = _ops().w4_quantize(tensor, group)
+    ref_packed, ref_scales = pack_weight_bf16(weight, group)
+    np.testing.assert_array_equal(packed.cpu().numpy(), ref_packed)
+    np.testing.assert_array_equal(bf16_bits_of(scales), ref_scales)
+
+
+def test_dequantize_is_bit_exact():
+    rng = np.random.default_rng(5)
+    _, packed, scales = _packed_case(rng, 300, 896)
+    out = _ops().w4_dequantize(torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64)
+    np.testing.assert_array_equal(from_gpu_bf16(out), dequantize_i4_bf16(packed, scales, 64))
+
+
+GEMV_SHAPES = [
+    (4864, 896),  # gate / up
+    (896, 4864),  # down
+    (896, 896),  # o
+    (1152, 896),  # packed q/k/v
+    (1000, 64),  # ragged rows, tiny K
+    (1, 32),  # single row, smallest K
+]
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+@pytest.mark.parametrize("lanes", [0, 4, 16, 64])
+def test_gemv_plain(n, k, lanes):
+    rng = np.random.default_rng(n + k + lanes)
+    group = 32 if k < 64 else 64
+    _, packed, scales = _packed_case(rng, n, k, group)
+    x = bf16_normal(rng, (k,))
+    y = _ops().w4_gemv(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), group,
+                       lanes_per_row=lanes)
+    assert_bf16_parity(from_gpu_bf16(y), oracle_gemv(x, packed, scales, group))
+
+
+@pytest.mark.parametrize("lanes", [0, 8, 32])
+def test_gemv_qkv_norm_and_bias(lanes):
+    rng = np.random.default_rng(21 + lanes)
+    _, packed, scales = _packed_case(rng, 1152, 896)
+    x = bf16_normal(rng, (896,), 3.0)
+    norm = bf16_normal(rng, (896,), 0.3) + np.float32(1.0)
+    norm = norm.astype(np.float32)
+    bias = bf16_normal(rng, (1152,), 0.02)
+    from oracle.bf16 import round_bf16
+
+    norm = round_bf16(norm)
+    y = _ops().w4_gemv(
+        to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64,
+        norm_weight=to_gpu_bf16(norm), eps=1e-6, bias=to_gpu_bf16(bias), lanes_per_row=lanes,
+    )
+    expected = oracle_gemv(x, packed, scales, 64, norm_weight=norm, eps=1e-6, bias=bias)
+    assert_bf16_parity(from_gpu_bf16(y), expected)
+
+
+@pytest.mark.parametrize("n,k", [(896, 896), (896, 4864)])
+def test_gemv_residual(n, k):
+    rng = np.random.default_rng(n + 3 * k)
+    _, packed, scales = _packed_case(rng, n, k)
+    x = bf16_normal(rng, (k,))
+    residual = bf16_normal(rng, (n,), 2.0)
+    y = _ops().w4_gemv(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64,
+                       bias=to_gpu_bf16(residual))
+    assert_bf16_parity(from_gpu_bf16(y), oracle_gemv(x, packed, scales, 64, bias=residual))
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_gemv_paired_gate_up(norm):
+    rng = np.random.default_rng(99 + norm)
+    _, gate, gate_s = _packed_case(rng, 4864, 896)
+    _, up, up_s = _packed_case(rng, 4864, 896)
+    x = bf16_normal(rng, (896,))
+    norm_w = bf16_normal(rng, (896,), 0.1) if norm else None
+    from oracle.bf16 import round_bf16
+
+    if norm_w is not None:
+        norm_w = round_bf16(norm_w + np.float32(1.0))
+    y = _ops().w4_gemv(
+        to_gpu_bf16(x), torch.from_numpy(gate).cuda(), to_gpu_bits(gate_s), 64,
+        norm_weight=None if norm_w is None else to_gpu_bf16(norm_w),
+        up=(torch.from_numpy(up).cuda(), to_gpu_bits(up_s)),
+    )
+    expected = oracle_gemv(x, gate, gate_s, 64, norm_weight=norm_w, up_packed=up, up_scales_bits=up_s)
+    assert_bf16_parity(from_gpu_bf16(y), expected)
+
+
+def test_gemv_extreme_codes():
+    """Every group holds both +7 and -7 (and a -8 word): a wrong sign extension shows."""
+
+    rng = np.random.default_rng(78)
+    n, k = 64, 128
+    weight = np.zeros((n, k), dtype=np.float32)
+    weight[:, 0::2] = 3.0
+    weight[:, 1::2] = -3.0
+    packed, scales = pack_weight_bf16(weight, 32)
+    packed[:, 0] = np.int32(-2023406815)  # codes 1..7, -8 in the first word of every row
+    x = bf16_normal(rng, (k,))
+    y = _ops().w4_gemv(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 32)
+    assert_bf16_parity(from_gpu_bf16(y), oracle_gemv(x, packed, scales, 32))
+
+
+def test_gemv_rejects_unsupported_group():
+    from aotolith_amd._lib import UnsupportedShape
+
+    rng = np.random.default_rng(1)
+    _, packed, scales = _packed_case(rng, 8, 64, 16)
+    with pytest.raises(UnsupportedShape):
+        _ops().w4_gemv(to_gpu_bf16(bf16_normal(rng, (64,))), torch.from_numpy(packed).cuda(),
+                       to_gpu_bits(scales), 16)
