@@ -126,7 +126,9 @@ def test_gemv_paired_gate_up(norm):
         up=(torch.from_numpy(up).cuda(), to_gpu_bits(up_s)),
     )
     expected = oracle_gemv(x, gate, gate_s, 64, norm_weight=norm_w, up_packed=up, up_scales_bits=up_s)
-    assert_bf16_parity(from_gpu_bf16(y), expected)
+    # Two roundings in series (the gate to bf16, then the product): a gate that
+    # lands one ulp away moves the output by up to one more ulp.
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0)
 
 
 def test_gemv_extreme_codes():
