@@ -27,6 +27,7 @@ AOTO_ERR_UNSUPPORTED = 4
 _c_int = ctypes.c_int
 _c_float = ctypes.c_float
 _c_size = ctypes.c_size_t
+_i64 = ctypes.c_int64
 _p = ctypes.c_void_p
 
 #: Every exported entry point with its argument types, in header order.
@@ -42,7 +43,31 @@ SIGNATURES: dict[str, tuple] = {
         _p, _p, _p, _p, _p, _p, _c_float, _p, _c_float, _c_float, _p,
         _c_int, _c_int, _c_int, _c_int, _p,
     ),
+    "aoto_hip_w4_gemm": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p),
+    "aoto_hip_rms_norm": (_p, _p, _c_float, _p, _c_int, _c_int, _p),
+    "aoto_hip_rope": (_p, _p, _p, _p, _c_int, _c_int, _p, _i64, _c_int, _p),
+    "aoto_hip_rope_qkv_prefill": (
+        _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p,
+    ),
+    "aoto_hip_rope_kv_cache_append": (
+        _p, _c_int, _p, _p, _c_int, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _p,
+    ),
+    "aoto_hip_decode_attention_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int, _c_int),
+    "aoto_hip_decode_attention": (
+        _p, _p, _p, _i64, _i64, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+        _c_float, _c_int, _p, _p, _p,
+    ),
+    "aoto_hip_prefill_attention": (
+        _p, _p, _p, _i64, _i64, _p, _i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+        _c_float, _p, _p,
+    ),
+    "aoto_hip_embedding": (_p, _p, _c_int, _c_int, _i64, _p, _p, _p),
+    "aoto_hip_argmax": (_p, _c_int, _c_int, _i64, _p, _p, _p, _p),
 }
+
+#: Entry points returning a size rather than a status.
+SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_decode_attention_workspace"}
 
 
 class HipBackendUnavailable(RuntimeError):
@@ -82,7 +107,7 @@ def library() -> ctypes.CDLL:
             for name, argtypes in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = list(argtypes)
-                fn.restype = _c_size if name == "aoto_hip_last_error" else _c_int
+                fn.restype = _c_size if name in SIZE_RETURNING else _c_int
             _lib = lib
     return _lib
 

@@ -80,6 +80,30 @@ int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* strea
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+unsigned blocks_for(long long items, int threads) { return (unsigned)((items + threads - 1) / threads); }
+
+// Decode attention split choice: enough blocks to spread a long window over
+// the chip, at most 512 keys per block (the kernel's LDS score buffer).
+void decode_split(int batch, int kv_heads, int capacity, int requested, int* splits, int* chunk) {
+  int s = requested;
+  if (s <= 0) {
+    const int heads = batch * kv_heads;
+    s = (128 + heads - 1) / heads;
+    const int most = (capacity + 63) / 64;
+    if (s > most) s = most;
+    if (s < 1) s = 1;
+  }
+  int c = (capacity + s - 1) / s;
+  c = (c + 15) / 16 * 16;
+  if (c > 512) {
+    c = 512;
+  }
+  s = (capacity + c - 1) / c;
+  *splits = s;
+  *chunk = c;
+}
 
 }  // namespace
 
@@ -198,6 +222,194 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   snprintf(name, sizeof(name), "aoto_w4_gemv_l%d_n%d_p%d_b%d", lpr, norm, paired ? 1 : 0, has_bias);
   return launch(name, dim3(blocks), dim3(256), shared, stream, x, words, scales, up_words, up_scales,
                 norm_weight, eps, bias, alpha, beta, y, K, N, group);
+}
+
+int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
+                     const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                     int tile, void* stream) {
+  if (!x || !words || !scales || !y) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: null pointer");
+  if (M <= 0 || N <= 0 || K <= 0) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: empty shape M=%d N=%d K=%d", M, N, K);
+  if (K % 64 != 0 || N % 16 != 0 || group <= 0 || group % 32 != 0 || K % group != 0)
+    return fail(AOTO_ERR_UNSUPPORTED, "w4_gemm: needs K %% 64 == 0, N %% 16 == 0, group %% 32 == 0 dividing K "
+                "(M=%d N=%d K=%d group=%d)", M, N, K, group);
+  const int epilogues = (bias != nullptr) + (residual != nullptr) + (gate != nullptr);
+  if (epilogues > 1) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: at most one of bias, residual, gate");
+  if (!aligned16(x) || !aligned8(y) || (bias && !aligned8(bias)) || (residual && !aligned8(residual)) ||
+      (gate && !aligned8(gate)))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemm: x must be 16-byte aligned, y/bias/residual/gate 8-byte aligned");
+  // tile: 0 = choose; else TN*10 + TM/4 code: 14, 18, 24, 28 (n tiles per wave, m tiles per wave).
+  int tn = 0, tm = 0;
+  if (tile == 0) {
+    tm = M <= 64 ? 4 : 8;
+    const long long mb = (M + 16 * tm - 1) / (16 * tm);
+    tn = (mb * ((N + 127) / 128) >= 256) ? 2 : 1;
+  } else {
+    tn = tile / 10;
+    tm = (tile % 10) == 4 ? 4 : 8;
+    if ((tn != 1 && tn != 2) || (tile % 10 != 4 && tile % 10 != 8))
+      return fail(AOTO_ERR_ARGUMENT, "w4_gemm: tile code %d is not one of 14, 18, 24, 28", tile);
+  }
+  const int bn = 64 * tn, bm = 16 * tm;
+  const int b = bias != nullptr, r = residual != nullptr, g = gate != nullptr;
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_w4_gemm_n%d_m%d_b%d_r%d_g%d", tn, tm, b, r, g);
+  return launch(name, dim3((N + bn - 1) / bn, (M + bm - 1) / bm), dim3(256), 0, stream, x, words, scales, bias,
+                residual, gate, y, M, N, K, group);
+}
+
+int aoto_hip_rms_norm(const void* x, const void* weight, float eps, void* out, int rows, int hidden,
+                      void* stream) {
+  if (!x || !weight || !out) return fail(AOTO_ERR_ARGUMENT, "rms_norm: null pointer");
+  if (rows <= 0 || hidden <= 0) return fail(AOTO_ERR_ARGUMENT, "rms_norm: empty shape %dx%d", rows, hidden);
+  if (hidden % 8 != 0) return fail(AOTO_ERR_UNSUPPORTED, "rms_norm: hidden %d is not a multiple of 8", hidden);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out))
+    return fail(AOTO_ERR_ARGUMENT, "rms_norm: x, weight and out must be 16-byte aligned");
+  return launch("aoto_rms_norm", dim3((rows + 3) / 4), dim3(256), 0, stream, x, weight, eps, out, rows, hidden);
+}
+
+int aoto_hip_rope(const void* x, const void* cos_table, const void* sin_table, const int64_t* positions,
+                  int rows_per_position, int position_count, void* out, int64_t rows, int head_dim,
+                  void* stream) {
+  if (!x || !cos_table || !sin_table || !positions || !out) return fail(AOTO_ERR_ARGUMENT, "rope: null pointer");
+  if (rows <= 0 || head_dim <= 0 || head_dim % 2 != 0 || rows_per_position <= 0 || position_count <= 0)
+    return fail(AOTO_ERR_ARGUMENT, "rope: bad shape rows=%lld head_dim=%d", (long long)rows, head_dim);
+  long long items = (long long)rows * head_dim;
+  return launch("aoto_rope", dim3(blocks_for(items, 256)), dim3(256), 0, stream, x, cos_table, sin_table,
+                positions, rows_per_position, position_count, out, (long long)rows, head_dim);
+}
+
+int aoto_hip_rope_qkv_prefill(const void* qkv, const int64_t* positions, const void* cos_table,
+                              const void* sin_table, void* q_out, void* pair, int batch, int tokens,
+                              int query_heads, int kv_heads, int head_dim, int capacity, int slot0,
+                              int zero_prefix, void* stream) {
+  if (!qkv || !positions || !cos_table || !sin_table || !q_out || !pair)
+    return fail(AOTO_ERR_ARGUMENT, "rope_qkv_prefill: null pointer");
+  if (batch <= 0 || tokens <= 0 || query_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2)
+    return fail(AOTO_ERR_ARGUMENT, "rope_qkv_prefill: bad shape");
+  if (slot0 < 0 || slot0 + tokens > capacity)
+    return fail(AOTO_ERR_ARGUMENT, "rope_qkv_prefill: slots [%d, %d) exceed capacity %d", slot0, slot0 + tokens,
+                capacity);
+  long long items = (long long)batch * (query_heads + 2 * kv_heads) * tokens * head_dim;
+  if (zero_prefix) items += 2LL * batch * kv_heads * slot0 * head_dim;
+  return launch("aoto_rope_qkv_prefill", dim3(blocks_for(items, 256)), dim3(256), 0, stream, qkv, positions,
+                cos_table, sin_table, q_out, pair, batch, tokens, query_heads, kv_heads, head_dim, capacity, slot0,
+                zero_prefix);
+}
+
+int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* cos_table, const void* sin_table,
+                                  int position, const void* pair_in, void* pair_out, void* q_out, int batch,
+                                  int query_heads, int kv_heads, int capacity, int head_dim, int query_start,
+                                  int key_start, int value_start, int mode, int slot, void* stream) {
+  if (!row || !cos_table || !sin_table || !pair_out || !q_out)
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: null pointer");
+  if (mode != 0 && mode != 1) return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: mode must be 0 or 1");
+  if (mode == 0 && (pair_in == nullptr || pair_in == pair_out))
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: the roll needs a separate input window");
+  if (batch <= 0 || query_heads <= 0 || kv_heads <= 0 || capacity <= 0 || head_dim <= 0 || head_dim % 8)
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: bad shape");
+  if (position < 0 || position >= capacity)
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: position %d outside the %d-row table", position,
+                capacity);
+  if (mode == 1 && (slot < 0 || slot >= capacity))
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: slot %d outside capacity %d", slot, capacity);
+  if (query_start < 0 || key_start < 0 || value_start < 0 || query_start + query_heads * head_dim > row_width ||
+      key_start + kv_heads * head_dim > row_width || value_start + kv_heads * head_dim > row_width)
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: q/k/v columns exceed the row width %d", row_width);
+  if (mode == 0 && (!aligned16(pair_in) || !aligned16(pair_out)))
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: windows must be 16-byte aligned");
+  long long items = (long long)batch * (query_heads + kv_heads) * head_dim;
+  if (mode == 0) items += 2LL * batch * kv_heads * (capacity - 1) * (head_dim / 8);
+  return launch("aoto_rope_kv_append", dim3(blocks_for(items, 256)), dim3(256), 0, stream, row, row_width,
+                cos_table, sin_table, position, pair_in, pair_out, q_out, batch, query_heads, kv_heads, capacity,
+                head_dim, query_start, key_start, value_start, mode, slot);
+}
+
+size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_heads, int capacity, int head_dim,
+                                           int splits) {
+  int s = 0, c = 0;
+  decode_split(batch, kv_heads, capacity, splits, &s, &c);
+  const size_t partials = (size_t)batch * query_heads * s * (head_dim + 2) * sizeof(float);
+  const size_t counters = (size_t)batch * kv_heads * sizeof(int);
+  return (partials + 255) / 256 * 256 + counters;
+}
+
+int aoto_hip_decode_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
+                              int64_t kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid,
+                              int ring_offset, int batch, int query_heads, int kv_heads, int capacity,
+                              int head_dim, float scale, int splits, void* workspace, void* out, void* stream) {
+  if (!q || !keys || !values || !out) return fail(AOTO_ERR_ARGUMENT, "decode_attention: null pointer");
+  if (batch <= 0 || query_heads <= 0 || kv_heads <= 0 || capacity <= 0 || query_heads % kv_heads)
+    return fail(AOTO_ERR_ARGUMENT, "decode_attention: bad shape (Hq=%d Hkv=%d cap=%d)", query_heads, kv_heads,
+                capacity);
+  const int G = query_heads / kv_heads;
+  if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 7 && G != 8))
+    return fail(AOTO_ERR_UNSUPPORTED, "decode_attention: head_dim %d with %d query heads per kv head", head_dim, G);
+  if (mask == nullptr && (valid < 0 || valid > capacity || ring_offset < 0 || ring_offset >= capacity))
+    return fail(AOTO_ERR_ARGUMENT, "decode_attention: valid %d / ring offset %d outside capacity %d", valid,
+                ring_offset, capacity);
+  if (!aligned16(q) || !aligned16(keys) || !aligned16(values) || (kv_head_stride % 8) || (kv_batch_stride % 8))
+    return fail(AOTO_ERR_ARGUMENT, "decode_attention: q/keys/values must be 16-byte aligned");
+  int s = 0, chunk = 0;
+  if (workspace == nullptr) {
+    if (capacity > 512 || splits > 1)
+      return fail(AOTO_ERR_ARGUMENT, "decode_attention: %d keys need a split workspace", capacity);
+    s = 1;
+    chunk = capacity;
+  } else {
+    decode_split(batch, kv_heads, capacity, splits, &s, &chunk);
+  }
+  float* partials = static_cast<float*>(workspace);
+  int* counters = nullptr;
+  if (workspace != nullptr) {
+    const size_t pbytes = (size_t)batch * query_heads * s * (head_dim + 2) * sizeof(float);
+    counters = reinterpret_cast<int*>(static_cast<char*>(workspace) + (pbytes + 255) / 256 * 256);
+  }
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_decode_attention_d%d_g%d", head_dim, G);
+  return launch(name, dim3(s, batch * kv_heads), dim3(256), 0, stream, q, keys, values, (long long)kv_batch_stride,
+                (long long)kv_head_stride, mask, mask_batch_stride, valid, ring_offset, capacity, kv_heads, scale,
+                chunk, partials, counters, out);
+}
+
+int aoto_hip_prefill_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
+                               int64_t kv_head_stride, const uint8_t* mask, int64_t mask_batch_stride, int causal,
+                               int key_start, int batch, int tokens, int key_tokens, int query_heads,
+                               int kv_heads, int head_dim, float scale, void* out, void* stream) {
+  if (!q || !keys || !values || !out) return fail(AOTO_ERR_ARGUMENT, "prefill_attention: null pointer");
+  if (batch <= 0 || tokens <= 0 || key_tokens <= 0 || query_heads <= 0 || kv_heads <= 0 ||
+      query_heads % kv_heads)
+    return fail(AOTO_ERR_ARGUMENT, "prefill_attention: bad shape");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(AOTO_ERR_UNSUPPORTED, "prefill_attention: head_dim %d (64 or 128)", head_dim);
+  if (!aligned16(q) || !aligned16(keys) || !aligned16(values) || !aligned8(out) || (kv_head_stride % 8) ||
+      (kv_batch_stride % 8))
+    return fail(AOTO_ERR_ARGUMENT, "prefill_attention: q/keys/values 16-byte, out 8-byte aligned");
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_flash_attention_d%d", head_dim);
+  return launch(name, dim3((tokens + 63) / 64, batch * query_heads), dim3(256), 0, stream, q, keys, values,
+                (long long)kv_batch_stride, (long long)kv_head_stride, mask, (long long)mask_batch_stride, causal,
+                key_start, tokens, key_tokens, query_heads, kv_heads, scale, out);
+}
+
+int aoto_hip_embedding(const void* weight, const int64_t* ids, int count, int hidden, int64_t vocab, void* out,
+                       int* error, void* stream) {
+  if (!weight || !ids || !out) return fail(AOTO_ERR_ARGUMENT, "embedding: null pointer");
+  if (count <= 0 || hidden <= 0 || vocab <= 0) return fail(AOTO_ERR_ARGUMENT, "embedding: empty shape");
+  if (hidden % 8 != 0) return fail(AOTO_ERR_UNSUPPORTED, "embedding: hidden %d is not a multiple of 8", hidden);
+  if (!aligned16(weight) || !aligned16(out)) return fail(AOTO_ERR_ARGUMENT, "embedding: 16-byte alignment");
+  long long items = (long long)count * (hidden / 8);
+  return launch("aoto_embedding", dim3(blocks_for(items, 256)), dim3(256), 0, stream, weight, ids, count, hidden,
+                (long long)vocab, out, error);
+}
+
+int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,
+                    int* history_len, void* stream) {
+  if (!logits || !out) return fail(AOTO_ERR_ARGUMENT, "argmax: null pointer");
+  if (rows <= 0 || n <= 0 || row_stride < n) return fail(AOTO_ERR_ARGUMENT, "argmax: bad shape");
+  if ((history == nullptr) != (history_len == nullptr) || (history != nullptr && rows != 1))
+    return fail(AOTO_ERR_ARGUMENT, "argmax: a token history needs one row and both pointers");
+  return launch("aoto_argmax", dim3(rows), dim3(1024), 0, stream, logits, n, (long long)row_stride, out, history,
+                history_len);
 }
 
 }  // extern "C"

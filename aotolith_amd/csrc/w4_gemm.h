@@ -1,0 +1,196 @@
+// Prefill W4 GEMM on bf16 MFMA with the dequant fused in registers.
+//
+//   Y[m][n] = epilogue( sum_k X[m][k] * bf16(code[n][k] * s[n][k/group]) )
+//
+// The reference prefill unpacks the weight to bf16 (codegen/quantize.py:27-63,
+// models/quantized.py:61-76) and runs a tiled GEMM over it with a bias /
+// residual / silu_mul epilogue (codegen/matmul.py:1443-1471, 1721-1742). Here
+// the unpacked weight never exists in memory: each packed int32 word is exactly
+// one lane's 8-element operand of v_mfma_f32_16x16x32_bf16 (8 consecutive k of
+// one row), so lanes load words straight from HBM and expand them in registers
+// to the same bf16(code * scale) values.
+//
+// MFMA formulation: C^T = W . X^T per 16x16 tile, so
+//   A (16 n x 32 k): lane l holds W[n0 + l%16][k0 + (l/16)*8 + j]  -> one packed word
+//   B (32 k x 16 m): lane l holds X[m0 + l%16][k0 + (l/16)*8 + j]  -> 16 B of an X row
+//   C (16 n x 16 m): lane l holds Y[m0 + l%16][n0 + (l/16)*4 + i]  -> 8-byte stores
+//
+// Block: 4 waves side by side along n; wave tile TN x TM 16x16 tiles
+// (block tile BN = 64*TN columns by BM = 16*TM rows). The X tile [BM][64] is
+// staged in LDS (rows padded by 16 B) and shared by the four waves; each wave
+// dequantizes only its own words, once, and reuses them for all TM row tiles
+// (TM = 8 keeps the dequant VALU work under the MFMA time).
+#pragma once
+
+#include "common.h"
+
+namespace aoto {
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+
+// Eight bf16(code * s) values of one packed word, in k order.
+AOTO_DEVICE bf16x8_v dequant_word(uint32_t w, float s) {
+  bf16x8_v out;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int code = (int)(w << (28 - 4 * j)) >> 28;
+    out[j] = (__bf16)((float)code * s);
+  }
+  return out;
+}
+
+constexpr int kGemmBK = 64;
+constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
+
+template <int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE>
+__device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __restrict__ words,
+                             const uint16_t* __restrict__ scales, const uint16_t* __restrict__ bias,
+                             const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate,
+                             uint16_t* __restrict__ Y, int M, int N, int K, int group) {
+  constexpr int BM = 16 * TM;
+  constexpr int BN = 64 * TN;
+  constexpr int XVEC = BM * (kGemmBK / 8);        // 16-byte vectors per X tile
+  constexpr int XPT = (XVEC + 255) / 256;         // per thread
+  __shared__ __attribute__((aligned(16))) uint16_t xs[BM * kGemmLdsStride];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_block = blockIdx.x * BN;
+  const int m_block = blockIdx.y * BM;
+  const int n_wave = n_block + wave * (16 * TN);
+  const int kw = K >> 3;           // words per weight row
+  const int groups = K / group;
+  const int col = lane & 15;       // n (A) / m (B, C) within a tile
+  const int quad = lane >> 4;      // k block of 8 (A, B) / n block of 4 (C)
+
+  f32x4_v acc[TN][TM];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int u = 0; u < TM; ++u) acc[t][u] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+
+  // Rows of W this lane reads (clamped: rows past N compute garbage that is never stored).
+  int wrow[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) wrow[t] = min(n_wave + t * 16 + col, N - 1);
+
+  uint4 xr[XPT];
+  uint32_t wr[TN][2];
+  auto load_x = [&](int k0) {
+#pragma unroll
+    for (int v = 0; v < XPT; ++v) {
+      const int idx = threadIdx.x + v * 256;
+      xr[v] = make_uint4(0, 0, 0, 0);
+      if (idx < XVEC) {
+        const int r = idx / (kGemmBK / 8), c = idx % (kGemmBK / 8);
+        const int m = m_block + r;
+        if (m < M) xr[v] = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0)[c];
+      }
+    }
+  };
+  auto store_x = [&]() {
+#pragma unroll
+    for (int v = 0; v < XPT; ++v) {
+      const int idx = threadIdx.x + v * 256;
+      if (idx < XVEC) {
+        const int r = idx / (kGemmBK / 8), c = idx % (kGemmBK / 8);
+        *reinterpret_cast<uint4*>(xs + r * kGemmLdsStride + c * 8) = xr[v];
+      }
+    }
+  };
+  auto load_w = [&](int k0) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) wr[t][ks] = words[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
+  };
+
+  load_x(0);
+  load_w(0);
+  for (int k0 = 0; k0 < K; k0 += kGemmBK) {
+    __syncthreads();
+    store_x();
+    uint32_t wcur[TN][2];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      wcur[t][0] = wr[t][0];
+      wcur[t][1] = wr[t][1];
+    }
+    float scur[TN][2];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        scur[t][ks] = bf16_to_f32(scales[(size_t)wrow[t] * groups + (k0 + ks * 32) / group]);
+    __syncthreads();
+    if (k0 + kGemmBK < K) {
+      load_x(k0 + kGemmBK);
+      load_w(k0 + kGemmBK);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8_v a[TN];
+#pragma unroll
+      for (int t = 0; t < TN; ++t) a[t] = dequant_word(wcur[t][ks], scur[t][ks]);
+#pragma unroll
+      for (int u = 0; u < TM; ++u) {
+        const bf16x8_v b =
+            *reinterpret_cast<const bf16x8_v*>(xs + (u * 16 + col) * kGemmLdsStride + ks * 32 + quad * 8);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b, acc[t][u], 0, 0, 0);
+      }
+    }
+  }
+
+  // Epilogue: lane holds Y[m0 + col][n0 + quad*4 + i].
+#pragma unroll
+  for (int u = 0; u < TM; ++u) {
+    const int m = m_block + u * 16 + col;
+    if (m >= M) continue;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int n = n_wave + t * 16 + quad * 4;
+      if (n >= N) continue;
+      float v[4] = {acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]};
+      if (BIAS) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(bias + n);
+        v[0] += bf16_lo(bb.x);
+        v[1] += bf16_hi(bb.x);
+        v[2] += bf16_lo(bb.y);
+        v[3] += bf16_hi(bb.y);
+      }
+      if (RESIDUAL) {
+        const uint2 rr = *reinterpret_cast<const uint2*>(residual + (size_t)m * N + n);
+        v[0] += bf16_lo(rr.x);
+        v[1] += bf16_hi(rr.x);
+        v[2] += bf16_lo(rr.y);
+        v[3] += bf16_hi(rr.y);
+      }
+      if (GATE) {
+        const uint2 gg = *reinterpret_cast<const uint2*>(gate + (size_t)m * N + n);
+        const float g[4] = {bf16_lo(gg.x), bf16_hi(gg.x), bf16_lo(gg.y), bf16_hi(gg.y)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = v[i] * (g[i] / (1.0f + expf(-g[i])));
+      }
+      uint2 o;
+      o.x = pack_bf16x2(v[0], v[1]);
+      o.y = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
+    }
+  }
+}
+
+}  // namespace aoto
+
+#define AOTO_GEMM_INSTANCE(TN, TM, BIAS, RES, GATE)                                                        \
+  extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_n##TN##_m##TM##_b##BIAS##_r##RES##_g##GATE( \
+      const uint16_t* X, const uint32_t* words, const uint16_t* scales, const uint16_t* bias,              \
+      const uint16_t* residual, const uint16_t* gate, uint16_t* Y, int M, int N, int K, int group) {       \
+    aoto::w4_gemm_body<TN, TM, BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K, group); \
+  }
+
+#define AOTO_GEMM_EPILOGUES(TN, TM)      \
+  AOTO_GEMM_INSTANCE(TN, TM, 0, 0, 0)    \
+  AOTO_GEMM_INSTANCE(TN, TM, 1, 0, 0)    \
+  AOTO_GEMM_INSTANCE(TN, TM, 0, 1, 0)    \
+  AOTO_GEMM_INSTANCE(TN, TM, 0, 0, 1)

@@ -149,3 +149,326 @@ def w4_gemv(
         )
     )
     return out
+
+
+def _i64(tensor: torch.Tensor, name: str) -> None:
+    _expect(tensor, name, torch.int64)
+
+
+def w4_matmul(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    *,
+    bias: torch.Tensor | None = None,
+    residual: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    tile: int = 0,
+) -> torch.Tensor:
+    """Prefill W4 matmul ``[M, K] -> [M, N]`` on MFMA with one fused epilogue.
+
+    ``bias`` ``[N]`` (q/k/v bias), ``residual`` ``[M, N]`` or ``gate`` ``[M, N]``
+    (``silu_mul``: ``bf16(acc * silu(gate))``), as the reference's prefill GEMM.
+    """
+
+    _expect(packed, "packed", torch.int32)
+    if packed.dim() != 2:
+        raise ValueError("packed must be 2-D [N, K/8]")
+    n, words = packed.shape
+    k = words * 8
+    _expect(x, "x", BF16)
+    if x.shape[-1] != k:
+        raise ValueError(f"x has last dimension {x.shape[-1]}, the weight reduces over {k}")
+    m = x.numel() // k
+    _expect(scales, "scales", BF16, (n, k // group_size))
+    for name, tensor, numel in (("bias", bias, n), ("residual", residual, m * n), ("gate", gate, m * n)):
+        if tensor is not None:
+            _expect(tensor, name, BF16)
+            if tensor.numel() != numel:
+                raise ValueError(f"{name} has {tensor.numel()} elements, expected {numel}")
+    shape = tuple(x.shape[:-1]) + (n,)
+    if out is None:
+        out = torch.empty(shape, dtype=BF16, device=x.device)
+    else:
+        _expect(out, "out", BF16)
+        if out.numel() != m * n:
+            raise ValueError(f"out has {out.numel()} elements, expected {m * n}")
+    _ready(x)
+    _lib.check(
+        _lib.library().aoto_hip_w4_gemm(
+            _ptr(x), _ptr(packed), _ptr(scales), _ptr(bias), _ptr(residual), _ptr(gate), _ptr(out),
+            m, n, k, group_size, int(tile), _stream(),
+        )
+    )
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Row RMSNorm over the last dimension, ``bf16((x * rsqrt(mean(x^2) + eps)) * w)``."""
+
+    _expect(x, "x", BF16)
+    hidden = x.shape[-1]
+    _expect(weight, "weight", BF16, (hidden,))
+    rows = x.numel() // hidden
+    if out is None:
+        out = torch.empty_like(x)
+    else:
+        _expect(out, "out", BF16, tuple(x.shape))
+    _ready(x)
+    _lib.check(_lib.library().aoto_hip_rms_norm(_ptr(x), _ptr(weight), float(eps), _ptr(out), rows, hidden, _stream()))
+    return out
+
+
+def rope(
+    x: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor, positions: torch.Tensor
+) -> torch.Tensor:
+    """RoPE of ``x [B, H, S, D]`` with table rows ``positions [B, S]`` (int64)."""
+
+    _expect(x, "x", BF16)
+    if x.dim() != 4:
+        raise ValueError("x must be [B, H, S, D]")
+    batch, heads, seq, dim = x.shape
+    _expect(cos_table, "cos_table", BF16)
+    _expect(sin_table, "sin_table", BF16, tuple(cos_table.shape))
+    if cos_table.shape[-1] != dim:
+        raise ValueError("table width must equal the head dimension")
+    _i64(positions, "positions")
+    if positions.numel() != batch * seq:
+        raise ValueError(f"positions must hold B*S = {batch * seq} entries")
+    if batch != 1:
+        raise ValueError("rope takes one batch row (positions are per token)")
+    out = torch.empty_like(x)
+    _ready(x)
+    _lib.check(
+        _lib.library().aoto_hip_rope(
+            _ptr(x), _ptr(cos_table), _ptr(sin_table), _ptr(positions), 1, seq, _ptr(out),
+            batch * heads * seq, dim, _stream(),
+        )
+    )
+    return out
+
+
+def rope_qkv_prefill(
+    qkv: torch.Tensor,
+    positions: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    pair: torch.Tensor,
+    *,
+    query_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    slot0: int,
+    zero_prefix: bool = True,
+    q_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Rotate q/k of ``qkv [B, M, W]`` into ``q [B, Hq, M, D]`` and fill ``pair [2, B, Hkv, cap, D]``."""
+
+    _expect(qkv, "qkv", BF16)
+    batch, tokens, width = qkv.shape
+    if width != (query_heads + 2 * kv_heads) * head_dim:
+        raise ValueError("qkv width does not match the head counts")
+    _i64(positions, "positions")
+    if positions.numel() != batch * tokens:
+        raise ValueError("positions must be [B, M]")
+    _expect(pair, "pair", BF16)
+    if pair.dim() != 5 or tuple(pair.shape[:3]) != (2, batch, kv_heads) or pair.shape[4] != head_dim:
+        raise ValueError(f"pair must be [2, {batch}, {kv_heads}, cap, {head_dim}], got {tuple(pair.shape)}")
+    capacity = pair.shape[3]
+    if q_out is None:
+        q_out = torch.empty((batch, query_heads, tokens, head_dim), dtype=BF16, device=qkv.device)
+    else:
+        _expect(q_out, "q_out", BF16, (batch, query_heads, tokens, head_dim))
+    _ready(qkv)
+    _lib.check(
+        _lib.library().aoto_hip_rope_qkv_prefill(
+            _ptr(qkv), _ptr(positions), _ptr(cos_table), _ptr(sin_table), _ptr(q_out), _ptr(pair), batch,
+            tokens, query_heads, kv_heads, head_dim, capacity, int(slot0), int(bool(zero_prefix)), _stream(),
+        )
+    )
+    return q_out
+
+
+def rope_kv_cache_append(
+    row: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    position: int,
+    pair_out: torch.Tensor,
+    *,
+    pair_in: torch.Tensor | None,
+    query_heads: int,
+    query_start: int,
+    key_start: int,
+    value_start: int,
+    ring_slot: int | None = None,
+    q_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The decode ``rope_kv_cache_append``: returns ``q [B, Hq, D]``.
+
+    ``pair_in`` given: the reference's roll into ``pair_out``. ``ring_slot``
+    given instead: the new key/value is written in place at that slot.
+    """
+
+    _expect(row, "row", BF16)
+    batch, width = row.shape[0], row.shape[-1]
+    _expect(pair_out, "pair_out", BF16)
+    _, b2, kv_heads, capacity, head_dim = pair_out.shape
+    if b2 != batch:
+        raise ValueError("row and pair batch differ")
+    mode = 1 if ring_slot is not None else 0
+    if mode == 0:
+        if pair_in is None:
+            raise ValueError("the roll needs pair_in")
+        _expect(pair_in, "pair_in", BF16, tuple(pair_out.shape))
+    if q_out is None:
+        q_out = torch.empty((batch, query_heads, head_dim), dtype=BF16, device=row.device)
+    _ready(row)
+    _lib.check(
+        _lib.library().aoto_hip_rope_kv_cache_append(
+            _ptr(row), width, _ptr(cos_table), _ptr(sin_table), int(position), _ptr(pair_in), _ptr(pair_out),
+            _ptr(q_out), batch, query_heads, kv_heads, capacity, head_dim, query_start, key_start, value_start,
+            mode, int(ring_slot or 0), _stream(),
+        )
+    )
+    return q_out
+
+
+def decode_attention_workspace(batch: int, query_heads: int, kv_heads: int, capacity: int, head_dim: int,
+                               splits: int = 0, device=None) -> torch.Tensor:
+    """A zero-filled workspace for :func:`decode_attention` with these shapes."""
+
+    size = _lib.library().aoto_hip_decode_attention_workspace(batch, query_heads, kv_heads, capacity, head_dim, splits)
+    return torch.zeros((size,), dtype=torch.uint8, device=device)
+
+
+def decode_attention(
+    q: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    *,
+    valid: int | None = None,
+    ring_offset: int = 0,
+    mask: torch.Tensor | None = None,
+    scale: float | None = None,
+    workspace: torch.Tensor | None = None,
+    splits: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Single-query GQA attention: ``q [B, Hq, D]`` over ``keys/values [B, Hkv, cap, D]``."""
+
+    _expect(q, "q", BF16)
+    batch, query_heads, head_dim = q.shape
+    if keys.dtype != BF16 or values.dtype != BF16 or keys.shape != values.shape or keys.dim() != 4:
+        raise ValueError("keys/values must be bf16 [B, Hkv, cap, D] of one shape")
+    if keys.stride(-1) != 1 or keys.stride(-2) != head_dim or values.stride() != keys.stride():
+        raise ValueError("keys/values rows must be contiguous with matching strides")
+    _, kv_heads, capacity, _ = keys.shape
+    if scale is None:
+        scale = float(torch.tensor(head_dim ** -0.5, dtype=torch.float32))
+    mask_ptr = None
+    mask_stride = 0
+    if mask is not None:
+        if mask.dtype != torch.bool:
+            raise TypeError("mask must be bool")
+        mask = mask.reshape(-1, capacity).to(torch.uint8).contiguous()
+        mask_stride = capacity if mask.shape[0] == batch else 0
+        mask_ptr = mask
+    elif valid is None:
+        raise ValueError("pass valid= or mask=")
+    if out is None:
+        out = torch.empty_like(q)
+    _ready(q)
+    _lib.check(
+        _lib.library().aoto_hip_decode_attention(
+            _ptr(q), _ptr(keys), _ptr(values), keys.stride(0), keys.stride(1), _ptr(mask_ptr), mask_stride,
+            int(valid or 0), int(ring_offset), batch, query_heads, kv_heads, capacity, head_dim, float(scale),
+            int(splits), _ptr(workspace), _ptr(out), _stream(),
+        )
+    )
+    return out
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    *,
+    causal: bool = True,
+    key_start: int = 0,
+    mask: torch.Tensor | None = None,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Prefill GQA attention: ``q [B, Hq, M, D]``, ``keys/values [B, Hkv, Mk, D]`` (rows contiguous)
+    -> ``[B, M, Hq*D]``."""
+
+    _expect(q, "q", BF16)
+    batch, query_heads, tokens, head_dim = q.shape
+    if keys.dtype != BF16 or values.dtype != BF16 or keys.shape != values.shape or keys.dim() != 4:
+        raise ValueError("keys/values must be bf16 [B, Hkv, Mk, D] of one shape")
+    if keys.stride(-1) != 1 or keys.stride(-2) != head_dim or values.stride() != keys.stride():
+        raise ValueError("keys/values rows must be contiguous with matching strides")
+    _, kv_heads, key_tokens, _ = keys.shape
+    if scale is None:
+        scale = float(torch.tensor(head_dim ** -0.5, dtype=torch.float32))
+    mask_ptr = None
+    mask_stride = 0
+    if mask is not None:
+        if mask.dtype != torch.bool:
+            raise TypeError("mask must be bool")
+        mask = mask.reshape(-1, tokens, key_tokens).to(torch.uint8).contiguous()
+        mask_stride = tokens * key_tokens if mask.shape[0] == batch and batch > 1 else 0
+        mask_ptr = mask
+    if out is None:
+        out = torch.empty((batch, tokens, query_heads * head_dim), dtype=BF16, device=q.device)
+    _ready(q)
+    _lib.check(
+        _lib.library().aoto_hip_prefill_attention(
+            _ptr(q), _ptr(keys), _ptr(values), keys.stride(0), keys.stride(1), _ptr(mask_ptr), mask_stride,
+            int(bool(causal)), int(key_start), batch, tokens, key_tokens, query_heads, kv_heads, head_dim,
+            float(scale), _ptr(out), _stream(),
+        )
+    )
+    return out
+
+
+def embedding(weight: torch.Tensor, ids: torch.Tensor, *, out: torch.Tensor | None = None,
+              error: torch.Tensor | None = None) -> torch.Tensor:
+    """``weight[ids]`` for int64 device ``ids``; out-of-range ids give zero rows and set ``error``."""
+
+    _expect(weight, "weight", BF16)
+    _i64(ids, "ids")
+    vocab, hidden = weight.shape
+    count = ids.numel()
+    if out is None:
+        out = torch.empty(tuple(ids.shape) + (hidden,), dtype=BF16, device=weight.device)
+    if error is not None:
+        _expect(error, "error", torch.int32)
+    _ready(weight)
+    _lib.check(
+        _lib.library().aoto_hip_embedding(
+            _ptr(weight), _ptr(ids), count, hidden, vocab, _ptr(out), _ptr(error), _stream()
+        )
+    )
+    return out
+
+
+def argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None, history: torch.Tensor | None = None,
+           history_len: torch.Tensor | None = None) -> torch.Tensor:
+    """First-index argmax over the last dimension of bf16 ``logits`` -> int64 ``[rows]``."""
+
+    _expect(logits, "logits", BF16)
+    n = logits.shape[-1]
+    rows = logits.numel() // n
+    if out is None:
+        out = torch.empty((rows,), dtype=torch.int64, device=logits.device)
+    _ready(logits)
+    _lib.check(
+        _lib.library().aoto_hip_argmax(
+            _ptr(logits), rows, n, n, _ptr(out), _ptr(history), _ptr(history_len), _stream()
+        )
+    )
+    return out

@@ -33,7 +33,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 1
+#define AOTO_HIP_ABI_VERSION 2
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -85,6 +85,107 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales,
                      const int32_t* up_words, const void* up_scales, const void* norm_weight,
                      float eps, const void* bias, float alpha, float beta, void* y, int K, int N,
                      int group, int lanes_per_row, void* stream);
+
+/* Prefill W4 GEMM, Y[M, N] = X[M, K] . bf16(code * scale)[N, K]^T with at most
+ * one fused epilogue. Replaces the prefill pair the reference runs for M > 1:
+ * the dequant kernel (codegen/quantize.py:27-153) feeding the tiled GEMM
+ * _emit_mpp_matmul_source (codegen/matmul.py:1228-1473) with its bias /
+ * residual / silu_mul epilogue (:1443-1471, 1721-1742; passes/fusion.py:406-498):
+ *   bias     bf16 [N]     -> bf16(bias[n] + acc)        (packed q/k/v bias)
+ *   residual bf16 [M, N]  -> bf16(residual[m][n] + acc)
+ *   gate     bf16 [M, N]  -> bf16(acc * silu(gate[m][n]))
+ * Limits: K % 64 == 0, N % 16 == 0, group % 32 == 0 dividing K. x 16-byte and
+ * y/bias/residual/gate 8-byte aligned. tile: 0 chooses, else 14/18/24/28 (n
+ * tiles x m tiles of 16 per wave). */
+int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
+                     const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                     int tile, void* stream);
+
+/* Row RMSNorm, out = bf16((x * rsqrt(mean(x^2) + eps)) * weight) over [rows, hidden]
+ * (codegen/norm.py:75-323, _compile_normalization(kind="rms_norm");
+ * runtime/mlx_ops/normalization.py:73-119). hidden % 8 == 0. */
+int aoto_hip_rms_norm(const void* x, const void* weight, float eps, void* out, int rows, int hidden,
+                      void* stream);
+
+/* RoPE over [rows, head_dim] rows (codegen/index.py:22-126, _compile_rope;
+ * runtime/mlx_ops/__init__.py:276-280): row r uses the table row
+ * positions[(r / rows_per_position) % position_count]; out = bf16(x * cos +
+ * rotate_half(x) * sin). Tables are the [capacity, head_dim] bf16 cos/sin of
+ * models/decoder.py:323-334. */
+int aoto_hip_rope(const void* x, const void* cos_table, const void* sin_table, const int64_t* positions,
+                  int rows_per_position, int position_count, void* out, int64_t rows, int head_dim,
+                  void* stream);
+
+/* Prefill RoPE fused with the cache fill for one layer: from the packed q/k/v
+ * projection qkv [batch, tokens, (Hq + 2 Hkv) * head_dim], writes rotated
+ * queries q_out [batch, Hq, tokens, head_dim] and the layer's key/value window
+ * pair [2, batch, Hkv, capacity, head_dim] at slots slot0 .. slot0 + tokens
+ * (slots below slot0 zeroed when zero_prefix). Replaces the prefill module's two
+ * RoPE launches and the compact-cache stack + pad_cache of
+ * models/decoder.py:524-561, 870-887. positions: int64 [batch, tokens]. */
+int aoto_hip_rope_qkv_prefill(const void* qkv, const int64_t* positions, const void* cos_table,
+                              const void* sin_table, void* q_out, void* pair, int batch, int tokens,
+                              int query_heads, int kv_heads, int head_dim, int capacity, int slot0,
+                              int zero_prefix, void* stream);
+
+/* Decode RoPE + KV-cache append (rope_kv_cache_append, codegen/kv_cache.py:96-215,
+ * 295-383; semantics runtime/mlx_ops/__init__.py:207-236). Rotates the step's q
+ * and k out of the projection row [batch, row_width] with the table row at
+ * `position`; q_out [batch, Hq, head_dim].
+ *   mode 0 (the reference op): pair_out = pair_in shifted down one slot with
+ *          (k_rot, v) at capacity - 1; pair_in/pair_out are one layer's
+ *          [2, batch, Hkv, capacity, head_dim] windows and must not overlap.
+ *   mode 1 (ring): (k_rot, v) written in place at `slot` of pair_out. */
+int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* cos_table, const void* sin_table,
+                                  int position, const void* pair_in, void* pair_out, void* q_out, int batch,
+                                  int query_heads, int kv_heads, int capacity, int head_dim, int query_start,
+                                  int key_start, int value_start, int mode, int slot, void* stream);
+
+/* Bytes of the split-K workspace aoto_hip_decode_attention needs for these
+ * shapes and `splits` (0 = the launcher's own choice). */
+size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_heads, int capacity, int head_dim,
+                                           int splits);
+
+/* Single-query GQA attention over a key/value window (the decode kernel
+ * _emit_decode_attention_source, codegen/attention.py:447-656, 761-815; fallback
+ * runtime/mlx_ops/attention.py:89-122). q [batch, Hq, head_dim]; keys/values at
+ * base + b * kv_batch_stride + h * kv_head_stride + slot * head_dim (elements);
+ * out [batch, Hq, head_dim]. Kept slots: mask[b * mask_batch_stride + slot] != 0
+ * when mask is non-null, else the last `valid` logical slots, logical slot =
+ * (slot - ring_offset) mod capacity. head_dim 64 or 128; Hq / Hkv in {1,2,4,7,8}.
+ * workspace: NULL (one block per kv head, capacity <= 512) or a buffer of
+ * aoto_hip_decode_attention_workspace() bytes, zero-filled before its first use
+ * (the kernel returns its counters to zero); calls sharing one workspace must
+ * be ordered on one stream. */
+int aoto_hip_decode_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
+                              int64_t kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid,
+                              int ring_offset, int batch, int query_heads, int kv_heads, int capacity,
+                              int head_dim, float scale, int splits, void* workspace, void* out, void* stream);
+
+/* Prefill GQA attention on MFMA (the flash kernels of codegen/attention.py:68-422,
+ * 671-759 and 817-1400, with the SDPA legalization's scale and safe_softmax,
+ * legalize/attention.py:105-170). q [batch, Hq, tokens, head_dim]; keys/values as
+ * for decode with key_tokens rows; out [batch, tokens, Hq * head_dim]. Kept pairs:
+ * mask[b * mask_batch_stride + i * key_tokens + j] != 0 when mask is non-null,
+ * else j >= key_start and (when causal) j <= i + key_tokens - tokens - the
+ * reference's prefill_mask (models/decoder.py:226-247) at key_start =
+ * tokens - length. Fully masked query rows give 0. head_dim 64 or 128. */
+int aoto_hip_prefill_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
+                               int64_t kv_head_stride, const uint8_t* mask, int64_t mask_batch_stride, int causal,
+                               int key_start, int batch, int tokens, int key_tokens, int query_heads,
+                               int kv_heads, int head_dim, float scale, void* out, void* stream);
+
+/* Embedding gather out[i] = weight[ids[i]] (the embedding op, runtime/bounds.py:
+ * 104-107). ids are int64 in device memory. An id outside [0, vocab) yields a
+ * zero row and sets *error = 1 when error is non-null (checked, not faulted). */
+int aoto_hip_embedding(const void* weight, const int64_t* ids, int count, int hidden, int64_t vocab, void* out,
+                       int* error, void* stream);
+
+/* Greedy argmax per row of bf16 logits, first index on ties (mx.argmax in the
+ * greedy loop, models/decoder.py:1069, 1080). out int64 [rows]. With history
+ * non-null (rows == 1): history[*history_len] = token, ++*history_len. */
+int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,
+                    int* history_len, void* stream);
 
 #ifdef __cplusplus
 }

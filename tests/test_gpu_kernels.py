@@ -1,0 +1,308 @@
+"""GPU parity of the prefill GEMM, norms, RoPE, cache append, attention, embedding and argmax.
+
+Every kernel runs through the C ABI (``aotolith_amd.ops`` -> ``libaoto_hip.so``) on
+seeded inputs at the configs' shapes and is compared with the CPU oracle. Index
+and copy work (cache roll/ring writes, embedding rows, argmax, the value half of
+the cache) must be bit-exact; arithmetic lands within the north-star bars
+(max abs <= 2e-2, cosine >= 0.999) and within a small number of bf16 ulps.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops as oracle
+from oracle.bf16 import round_bf16
+from oracle.quant import pack_weight_bf16
+from tests.helpers import assert_bf16_parity, bf16_bits_of, bf16_normal, from_gpu_bf16, to_gpu_bf16, to_gpu_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from aotolith_amd import ops
+
+    return ops
+
+
+def _packed(rng, n, k, group=64, std=0.02):
+    weight = bf16_normal(rng, (n, k), std)
+    packed, scales = pack_weight_bf16(weight, group)
+    return packed, scales
+
+
+def _gpu_packed(packed, scales):
+    return torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
+
+
+# ---------------------------------------------------------------- prefill GEMM
+GEMM_CASES = [
+    (128, 4864, 896, 64),   # gate / up at the Qwen prefill length
+    (128, 896, 4864, 64),   # down
+    (16, 4864, 896, 64),    # config 2, M = 16
+    (1, 896, 896, 64),      # a single row through the GEMM
+    (200, 1152, 896, 32),   # ragged M, group 32
+    (300, 2048, 512, 128),  # group 128, several m blocks
+]
+
+
+@pytest.mark.parametrize("m,n,k,group", GEMM_CASES)
+@pytest.mark.parametrize("tile", [0, 14, 28])
+def test_w4_matmul_plain(m, n, k, group, tile):
+    rng = np.random.default_rng(m + n + k + tile)
+    packed, scales = _packed(rng, n, k, group)
+    x = bf16_normal(rng, (m, k))
+    y = _ops().w4_matmul(to_gpu_bf16(x), *_gpu_packed(packed, scales), group, tile=tile)
+    assert_bf16_parity(from_gpu_bf16(y), oracle.w4_matmul(x, packed, scales, group), max_ulp=1.0)
+
+
+@pytest.mark.parametrize("epilogue", ["bias", "residual", "gate"])
+def test_w4_matmul_epilogues(epilogue):
+    rng = np.random.default_rng({"bias": 1, "residual": 2, "gate": 3}[epilogue])
+    m, n, k = 128, 1152 if epilogue == "bias" else 896, 896
+    packed, scales = _packed(rng, n, k)
+    x = bf16_normal(rng, (m, k))
+    kwargs = {}
+    if epilogue == "bias":
+        kwargs["bias"] = bf16_normal(rng, (n,), 0.02)
+    elif epilogue == "residual":
+        kwargs["residual"] = bf16_normal(rng, (m, n), 2.0)
+    else:
+        kwargs["gate"] = bf16_normal(rng, (m, n))
+    gpu_kwargs = {key: to_gpu_bf16(value) for key, value in kwargs.items()}
+    y = _ops().w4_matmul(to_gpu_bf16(x), *_gpu_packed(packed, scales), 64, **gpu_kwargs)
+    expected = oracle.w4_matmul(x, packed, scales, 64, **kwargs)
+    # silu_mul rounds once after a product of two inexact terms; allow one more ulp there.
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0 if epilogue == "gate" else 1.0)
+
+
+def test_w4_matmul_rejects_unsupported_k():
+    from aotolith_amd._lib import UnsupportedShape
+
+    rng = np.random.default_rng(4)
+    packed, scales = _packed(rng, 64, 96, 32)
+    with pytest.raises(UnsupportedShape):
+        _ops().w4_matmul(to_gpu_bf16(bf16_normal(rng, (4, 96))), *_gpu_packed(packed, scales), 32)
+
+
+# ---------------------------------------------------------------- RMSNorm / RoPE
+@pytest.mark.parametrize("rows,hidden,eps", [(128, 896, 1e-6), (7, 4096, 1e-5), (1, 64, 1e-6)])
+def test_rms_norm(rows, hidden, eps):
+    rng = np.random.default_rng(rows * hidden)
+    x = bf16_normal(rng, (rows, hidden), 3.0)
+    w = round_bf16(np.float32(1.0) + bf16_normal(rng, (hidden,), 0.2))
+    y = _ops().rms_norm(to_gpu_bf16(x), to_gpu_bf16(w), eps)
+    assert_bf16_parity(from_gpu_bf16(y), oracle.rms_norm(x, w, eps), max_ulp=1.0)
+
+
+def _tables(capacity, head_dim, theta):
+    cos, sin = oracle.rope_tables(capacity, head_dim, theta)
+    return cos, sin, to_gpu_bf16(cos), to_gpu_bf16(sin)
+
+
+@pytest.mark.parametrize("heads,seq,dim,theta", [(14, 128, 64, 1e6), (8, 40, 128, 5e5)])
+def test_rope(heads, seq, dim, theta):
+    rng = np.random.default_rng(seq)
+    cos, sin, gcos, gsin = _tables(192, dim, theta)
+    x = bf16_normal(rng, (1, heads, seq, dim))
+    positions = np.arange(seq) + 5
+    y = _ops().rope(to_gpu_bf16(x), gcos, gsin, torch.from_numpy(positions).cuda())
+    expected = oracle.rope(x, cos[positions][None, None], sin[positions][None, None])
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0)
+
+
+def test_rope_qkv_prefill_fills_queries_and_cache():
+    rng = np.random.default_rng(8)
+    hq, hkv, dim, m, cap = 14, 2, 64, 128, 192
+    cos, sin, gcos, gsin = _tables(cap, dim, 1e6)
+    qkv = bf16_normal(rng, (1, m, (hq + 2 * hkv) * dim))
+    positions = np.arange(m)
+    pair = torch.full((2, 1, hkv, cap, dim), 7.0, dtype=torch.bfloat16, device="cuda")
+    q = _ops().rope_qkv_prefill(to_gpu_bf16(qkv), torch.from_numpy(positions).cuda(), gcos, gsin, pair,
+                                query_heads=hq, kv_heads=hkv, head_dim=dim, slot0=cap - m)
+    qd, kd = hq * dim, hkv * dim
+    rows = qkv[0]
+    ref_q = oracle.rope(rows[:, :qd].reshape(m, hq, dim).transpose(1, 0, 2)[None], cos[:m][None, None], sin[:m][None, None])
+    ref_k = oracle.rope(rows[:, qd:qd + kd].reshape(m, hkv, dim).transpose(1, 0, 2)[None], cos[:m][None, None], sin[:m][None, None])
+    ref_v = rows[:, qd + kd:].reshape(m, hkv, dim).transpose(1, 0, 2)[None]
+    assert_bf16_parity(from_gpu_bf16(q), ref_q, max_ulp=1.0)
+    got = from_gpu_bf16(pair)
+    assert np.all(got[:, :, :, : cap - m] == 0.0), "left pad must be zero"
+    assert_bf16_parity(got[0, :, :, cap - m:], ref_k[0][None][0], max_ulp=1.0)
+    np.testing.assert_array_equal(got[1, :, :, cap - m:], ref_v)
+
+
+# ---------------------------------------------------------------- decode cache append
+@pytest.mark.parametrize("mode", ["roll", "ring"])
+def test_rope_kv_cache_append(mode):
+    rng = np.random.default_rng(11)
+    layers, hq, hkv, dim, cap = 3, 14, 2, 64, 192
+    cos, sin, gcos, gsin = _tables(cap, dim, 1e6)
+    cache = bf16_normal(rng, (layers, 2, 1, hkv, cap, dim))
+    row = bf16_normal(rng, (1, (hq + 2 * hkv) * dim))
+    position, layer = 150, 1
+    ref_q, ref_pair = oracle.rope_kv_cache_append(
+        cache, row, cos[position], sin[position], layer=layer, query_heads=hq,
+        query_start=0, key_start=hq * dim, value_start=(hq + hkv) * dim,
+    )
+    gcache = to_gpu_bf16(cache)
+    if mode == "roll":
+        out_pair = torch.empty_like(gcache[layer])
+        q = _ops().rope_kv_cache_append(to_gpu_bf16(row), gcos, gsin, position, out_pair, pair_in=gcache[layer],
+                                        query_heads=hq, query_start=0, key_start=hq * dim,
+                                        value_start=(hq + hkv) * dim)
+        got = from_gpu_bf16(out_pair)
+        np.testing.assert_array_equal(got[:, :, :, : cap - 1], ref_pair[:, :, :, : cap - 1])
+        np.testing.assert_array_equal(got[1, :, :, cap - 1], ref_pair[1, :, :, cap - 1])
+        assert_bf16_parity(got[0, :, :, cap - 1], ref_pair[0, :, :, cap - 1], max_ulp=1.0)
+    else:
+        slot = 37
+        pair = gcache[layer]
+        q = _ops().rope_kv_cache_append(to_gpu_bf16(row), gcos, gsin, position, pair, pair_in=None,
+                                        query_heads=hq, query_start=0, key_start=hq * dim,
+                                        value_start=(hq + hkv) * dim, ring_slot=slot)
+        got = from_gpu_bf16(pair)
+        untouched = np.ones(cap, dtype=bool)
+        untouched[slot] = False
+        np.testing.assert_array_equal(got[:, :, :, untouched], cache[layer][:, :, :, untouched])
+        np.testing.assert_array_equal(got[1, :, :, slot], ref_pair[1, :, :, cap - 1])
+        assert_bf16_parity(got[0, :, :, slot], ref_pair[0, :, :, cap - 1], max_ulp=1.0)
+        # the other layers of the cache are not touched
+        np.testing.assert_array_equal(from_gpu_bf16(gcache[0]), cache[0])
+    assert_bf16_parity(from_gpu_bf16(q).reshape(ref_q.shape), ref_q, max_ulp=1.0)
+
+
+# ---------------------------------------------------------------- attention
+DECODE_CASES = [
+    # (hq, hkv, dim, cap, valid, splits)
+    (14, 2, 64, 192, 129, 0),
+    (14, 2, 64, 192, 191, 1),
+    (14, 2, 64, 192, 150, 3),
+    (32, 8, 128, 768, 600, 0),
+    (32, 8, 128, 2304, 2300, 0),
+    (4, 4, 64, 64, 1, 1),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,dim,cap,valid,splits", DECODE_CASES)
+def test_decode_attention_last_valid_slots(hq, hkv, dim, cap, valid, splits):
+    rng = np.random.default_rng(cap + valid)
+    q = bf16_normal(rng, (1, hq, 1, dim))
+    k = bf16_normal(rng, (1, hkv, cap, dim))
+    v = bf16_normal(rng, (1, hkv, cap, dim))
+    keep = oracle.decode_mask(valid, cap)
+    expected = oracle.attention(q, k, v, keep)
+    ops = _ops()
+    workspace = None
+    if splits != 1:
+        workspace = ops.decode_attention_workspace(1, hq, hkv, cap, dim, splits, device="cuda")
+    for _ in range(2):  # the split counters must return to zero between calls
+        out = ops.decode_attention(to_gpu_bf16(q[:, :, 0]), to_gpu_bf16(k), to_gpu_bf16(v), valid=valid,
+                                   workspace=workspace, splits=splits)
+        assert_bf16_parity(from_gpu_bf16(out), expected.reshape(1, hq, dim), max_ulp=2.0)
+
+
+def test_decode_attention_ring_and_mask_agree_with_the_roll():
+    rng = np.random.default_rng(5)
+    hq, hkv, dim, cap, valid, offset = 14, 2, 64, 192, 140, 61
+    q = bf16_normal(rng, (1, hq, dim))
+    k = bf16_normal(rng, (1, hkv, cap, dim))
+    v = bf16_normal(rng, (1, hkv, cap, dim))
+    # physical slot p holds logical slot (p - offset) mod cap
+    logical = (np.arange(cap) - offset) % cap
+    keep_phys = logical >= cap - valid
+    expected = oracle.attention(q[:, :, None], k, v, keep_phys[None, None, None, :])
+    ops = _ops()
+    ring = ops.decode_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(v), valid=valid, ring_offset=offset)
+    masked = ops.decode_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(v),
+                                  mask=torch.from_numpy(keep_phys).cuda())
+    assert_bf16_parity(from_gpu_bf16(ring), expected.reshape(1, hq, dim), max_ulp=2.0)
+    np.testing.assert_array_equal(bf16_bits_of(ring), bf16_bits_of(masked))
+
+
+def test_decode_attention_fully_masked_gives_zero():
+    rng = np.random.default_rng(6)
+    q = bf16_normal(rng, (1, 14, 64))
+    k = bf16_normal(rng, (1, 2, 192, 64))
+    out = _ops().decode_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(k), valid=0)
+    assert np.all(from_gpu_bf16(out) == 0.0)
+
+
+PREFILL_CASES = [
+    # (hq, hkv, dim, m, length)
+    (14, 2, 64, 128, 128),   # config 3 prefill, causal
+    (14, 2, 64, 128, 77),    # left-padded bucket
+    (32, 8, 128, 200, 200),  # Llama heads, ragged length
+    (4, 4, 64, 64, 64),      # MHA
+]
+
+
+@pytest.mark.parametrize("hq,hkv,dim,m,length", PREFILL_CASES)
+def test_prefill_attention_causal_left_pad(hq, hkv, dim, m, length):
+    rng = np.random.default_rng(m + length + dim)
+    q = bf16_normal(rng, (1, hq, m, dim))
+    k = bf16_normal(rng, (1, hkv, m, dim))
+    v = bf16_normal(rng, (1, hkv, m, dim))
+    mask = oracle.prefill_mask(length, m)
+    expected = oracle.attention(q, k, v, mask)
+    out = _ops().prefill_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(v), causal=True, key_start=m - length)
+    got = from_gpu_bf16(out).reshape(1, m, hq, dim).transpose(0, 2, 1, 3)
+    # P is rounded to bf16 before the P.V product, as the reference's flash kernel
+    # does (codegen/attention.py:367-371): the error scales with |v|, not with the
+    # output, so the bound is absolute - 2^-6 for N(0,1) values - and not in ulps.
+    assert_bf16_parity(got, expected, max_ulp=None, atol=2.0 ** -6)
+    if length < m:
+        assert np.all(got[:, :, : m - length] == 0.0), "fully masked pad rows must be zero"
+
+
+def test_prefill_attention_explicit_mask_matches_the_implicit_one():
+    rng = np.random.default_rng(9)
+    hq, hkv, dim, m, length = 14, 2, 64, 128, 90
+    q = bf16_normal(rng, (1, hq, m, dim))
+    k = bf16_normal(rng, (1, hkv, m, dim))
+    mask = oracle.prefill_mask(length, m)
+    ops = _ops()
+    implicit = ops.prefill_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(k), causal=True, key_start=m - length)
+    explicit = ops.prefill_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(k),
+                                     mask=torch.from_numpy(mask.copy()).cuda())
+    np.testing.assert_array_equal(bf16_bits_of(implicit), bf16_bits_of(explicit))
+
+
+# ---------------------------------------------------------------- embedding / argmax
+def test_embedding_is_exact_and_flags_bad_ids():
+    rng = np.random.default_rng(10)
+    table = bf16_normal(rng, (1000, 896))
+    ids = np.array([0, 999, 17, 17, 500], dtype=np.int64)
+    ops = _ops()
+    error = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    out = ops.embedding(to_gpu_bf16(table), torch.from_numpy(ids).cuda(), error=error)
+    np.testing.assert_array_equal(from_gpu_bf16(out), table[ids])
+    assert int(error.item()) == 0
+    bad = ops.embedding(to_gpu_bf16(table), torch.tensor([3, 1000], device="cuda"), error=error)
+    assert int(error.item()) == 1
+    assert np.all(from_gpu_bf16(bad)[1] == 0.0)
+
+
+def test_argmax_first_index_on_ties():
+    rng = np.random.default_rng(12)
+    logits = bf16_normal(rng, (3, 151936))
+    logits[1, 5] = logits[1, 100] = logits[1, 150000] = 50.0   # tie: the first wins
+    logits[2, :] = -1.0
+    logits[2, 151935] = -0.5
+    got = _ops().argmax(to_gpu_bf16(logits)).cpu().numpy()
+    np.testing.assert_array_equal(got, oracle.argmax_first(logits))
+    assert got[1] == 5
+
+
+def test_argmax_records_history():
+    ops = _ops()
+    history = torch.zeros((4,), dtype=torch.int64, device="cuda")
+    length = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    for token in (3, 9, 1):
+        logits = torch.zeros((1, 64), dtype=torch.bfloat16, device="cuda")
+        logits[0, token] = 1.0
+        ops.argmax(logits, history=history, history_len=length)
+    assert history.cpu().tolist()[:3] == [3, 9, 1]
+    assert int(length.item()) == 3
