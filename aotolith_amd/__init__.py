@@ -2,13 +2,46 @@
 
 Target name: ``"hip-gfx950"``. Kernels are hand-written HIP for CDNA4, built into
 one gfx950 code object and reached through the C ABI of ``include/aoto_hip.h``
-from torch-ROCm tensors.
+from torch-ROCm tensors. The public names mirror the reference's static-cache
+API (``compile_qwen2_static_cache``, ``compile_llama_static_cache`` and their
+bucketed forms) with ``target="hip-gfx950"``.
 """
 
 from __future__ import annotations
 
 from ._version import __version__
+from .plan import TARGET
 
-TARGET = "hip-gfx950"
+__all__ = [
+    "TARGET",
+    "__version__",
+    "compile_decoder_static_cache",
+    "compile_decoder_bucketed",
+    "compile_llama_bucketed",
+    "compile_llama_static_cache",
+    "compile_qwen2_bucketed",
+    "compile_qwen2_static_cache",
+    "load_runtime",
+]
 
-__all__ = ["TARGET", "__version__"]
+
+def __getattr__(name: str):
+    # The compile entry points import torch-side modules; keep `import aotolith_amd`
+    # light for the C-ABI checks that run without a GPU.
+    if name in ("compile_qwen2_static_cache", "compile_qwen2_bucketed"):
+        from . import qwen2
+
+        return getattr(qwen2, name)
+    if name in ("compile_llama_static_cache", "compile_llama_bucketed"):
+        from . import llama
+
+        return getattr(llama, name)
+    if name in ("compile_decoder_static_cache", "compile_decoder_bucketed"):
+        from . import decoder
+
+        return getattr(decoder, name)
+    if name == "load_runtime":
+        from .artifact import load_runtime
+
+        return load_runtime
+    raise AttributeError(name)

@@ -299,7 +299,8 @@ int aoto_hip_rope_qkv_prefill(const void* qkv, const int64_t* positions, const v
 int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* cos_table, const void* sin_table,
                                   int position, const void* pair_in, void* pair_out, void* q_out, int batch,
                                   int query_heads, int kv_heads, int capacity, int head_dim, int query_start,
-                                  int key_start, int value_start, int mode, int slot, void* stream) {
+                                  int key_start, int value_start, int mode, int slot,
+                                  const int32_t* step_state, void* stream) {
   if (!row || !cos_table || !sin_table || !pair_out || !q_out)
     return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: null pointer");
   if (mode != 0 && mode != 1) return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: mode must be 0 or 1");
@@ -307,10 +308,12 @@ int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* co
     return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: the roll needs a separate input window");
   if (batch <= 0 || query_heads <= 0 || kv_heads <= 0 || capacity <= 0 || head_dim <= 0 || head_dim % 8)
     return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: bad shape");
-  if (position < 0 || position >= capacity)
+  if (step_state != nullptr && mode != 1)
+    return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: device step state drives the ring mode only");
+  if (step_state == nullptr && (position < 0 || position >= capacity))
     return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: position %d outside the %d-row table", position,
                 capacity);
-  if (mode == 1 && (slot < 0 || slot >= capacity))
+  if (step_state == nullptr && mode == 1 && (slot < 0 || slot >= capacity))
     return fail(AOTO_ERR_ARGUMENT, "rope_kv_cache_append: slot %d outside capacity %d", slot, capacity);
   if (query_start < 0 || key_start < 0 || value_start < 0 || query_start + query_heads * head_dim > row_width ||
       key_start + kv_heads * head_dim > row_width || value_start + kv_heads * head_dim > row_width)
@@ -321,7 +324,7 @@ int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* co
   if (mode == 0) items += 2LL * batch * kv_heads * (capacity - 1) * (head_dim / 8);
   return launch("aoto_rope_kv_append", dim3(blocks_for(items, 256)), dim3(256), 0, stream, row, row_width,
                 cos_table, sin_table, position, pair_in, pair_out, q_out, batch, query_heads, kv_heads, capacity,
-                head_dim, query_start, key_start, value_start, mode, slot);
+                head_dim, query_start, key_start, value_start, mode, slot, step_state);
 }
 
 size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_heads, int capacity, int head_dim,
@@ -336,7 +339,8 @@ size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_he
 int aoto_hip_decode_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
                               int64_t kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid,
                               int ring_offset, int batch, int query_heads, int kv_heads, int capacity,
-                              int head_dim, float scale, int splits, void* workspace, void* out, void* stream) {
+                              int head_dim, float scale, int splits, void* workspace, const int32_t* step_state,
+                              void* out, void* stream) {
   if (!q || !keys || !values || !out) return fail(AOTO_ERR_ARGUMENT, "decode_attention: null pointer");
   if (batch <= 0 || query_heads <= 0 || kv_heads <= 0 || capacity <= 0 || query_heads % kv_heads)
     return fail(AOTO_ERR_ARGUMENT, "decode_attention: bad shape (Hq=%d Hkv=%d cap=%d)", query_heads, kv_heads,
@@ -344,7 +348,8 @@ int aoto_hip_decode_attention(const void* q, const void* keys, const void* value
   const int G = query_heads / kv_heads;
   if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 7 && G != 8))
     return fail(AOTO_ERR_UNSUPPORTED, "decode_attention: head_dim %d with %d query heads per kv head", head_dim, G);
-  if (mask == nullptr && (valid < 0 || valid > capacity || ring_offset < 0 || ring_offset >= capacity))
+  if (mask == nullptr && step_state == nullptr &&
+      (valid < 0 || valid > capacity || ring_offset < 0 || ring_offset >= capacity))
     return fail(AOTO_ERR_ARGUMENT, "decode_attention: valid %d / ring offset %d outside capacity %d", valid,
                 ring_offset, capacity);
   if (!aligned16(q) || !aligned16(keys) || !aligned16(values) || (kv_head_stride % 8) || (kv_batch_stride % 8))
@@ -368,7 +373,12 @@ int aoto_hip_decode_attention(const void* q, const void* keys, const void* value
   snprintf(name, sizeof(name), "aoto_decode_attention_d%d_g%d", head_dim, G);
   return launch(name, dim3(s, batch * kv_heads), dim3(256), 0, stream, q, keys, values, (long long)kv_batch_stride,
                 (long long)kv_head_stride, mask, mask_batch_stride, valid, ring_offset, capacity, kv_heads, scale,
-                chunk, partials, counters, out);
+                chunk, partials, counters, step_state, out);
+}
+
+int aoto_hip_step_advance(int32_t* step_state, int capacity, void* stream) {
+  if (!step_state || capacity <= 0) return fail(AOTO_ERR_ARGUMENT, "step_advance: bad arguments");
+  return launch("aoto_step_advance", dim3(1), dim3(64), 0, stream, step_state, capacity);
 }
 
 int aoto_hip_prefill_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,

@@ -30,16 +30,23 @@ AOTO_DEVICE float rope_value(const uint16_t* __restrict__ head, const uint16_t* 
 //   must not overlap.
 // * `mode == 1` (ring): (k_rot, v) is written in place at slot `slot` of
 //   pair_out; nothing else moves (pair_in is unused).
-// q_out is [B][Hq][D]. Work items: B*Hq*D query elements, B*Hkv*D key and value
+// With `step` non-null the position and slot come from device memory
+// (step[0] = position, step[3] = slot), so a captured decode step replays
+// without host updates. q_out is [B][Hq][D]. Work items: B*Hq*D query elements, B*Hkv*D key and value
 // elements, then (roll only) the copy of the 2*B*Hkv*(cap-1)*D window, 8
 // elements per thread.
 extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
     const uint16_t* __restrict__ row, int row_width, const uint16_t* __restrict__ cos_table,
     const uint16_t* __restrict__ sin_table, int position, const uint16_t* __restrict__ pair_in,
     uint16_t* __restrict__ pair_out, uint16_t* __restrict__ q_out, int batch, int query_heads,
-    int kv_heads, int cap, int D, int query_start, int key_start, int value_start, int mode, int slot) {
+    int kv_heads, int cap, int D, int query_start, int key_start, int value_start, int mode, int slot,
+    const int* __restrict__ step) {
   const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const int half = D >> 1;
+  if (step != nullptr) {
+    position = step[0];
+    slot = step[3];
+  }
   const uint16_t* cos_row = cos_table + (size_t)position * D;
   const uint16_t* sin_row = sin_table + (size_t)position * D;
   const long long q_items = (long long)batch * query_heads * D;
@@ -90,6 +97,9 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
 // least cap - valid (the last `valid` slots of the reference's rolled window when
 // ring_offset == 0; a ring buffer rotated by ring_offset otherwise).
 //
+// With `step` non-null, valid = step[1] and ring_offset = step[2] (device-side
+// step state of a captured decode loop).
+//
 // Grid (splits, B*Hkv); 256 threads. Each block handles keys
 // [split*chunk, min(cap, (split+1)*chunk)) for the G query heads of one kv head:
 // LPK lanes per key (D/8 lanes, 16 B each), 64/LPK keys per wave per pass, the
@@ -103,7 +113,12 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
                                       long long kv_head_stride, const uint8_t* __restrict__ mask,
                                       int mask_batch_stride, int valid, int ring_offset, int cap, int kv_heads,
                                       float scale, int chunk, float* __restrict__ partials,
-                                      int* __restrict__ counters, uint16_t* __restrict__ out) {
+                                      int* __restrict__ counters, const int* __restrict__ step,
+                                      uint16_t* __restrict__ out) {
+  if (step != nullptr) {
+    valid = step[1];
+    ring_offset = step[2];
+  }
   constexpr int LPK = D / 8;            // lanes per key
   constexpr int KPW = 64 / LPK;         // keys per wave per pass
   constexpr int WAVES = 4;
@@ -408,14 +423,26 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
   }
 }
 
+// Advance the decode-loop step state by one token: position and valid length
+// grow by one, the ring offset and the next write slot move one slot on
+// (state = {position, valid, ring_offset, slot}). One thread.
+extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  state[0] += 1;
+  state[1] += 1;
+  state[2] = state[2] + 1 == cap ? 0 : state[2] + 1;
+  state[3] = state[3] + 1 == cap ? 0 : state[3] + 1;
+}
+
 }  // namespace aoto
 
 #define AOTO_DECODE_ATTENTION_INSTANCE(D, G)                                                              \
   extern "C" __global__ __launch_bounds__(256) void aoto_decode_attention_d##D##_g##G(                   \
       const uint16_t* q, const uint16_t* kbase, const uint16_t* vbase, long long kv_batch_stride,         \
       long long kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid, int ring_offset,   \
-      int cap, int kv_heads, float scale, int chunk, float* partials, int* counters, uint16_t* out) {     \
+      int cap, int kv_heads, float scale, int chunk, float* partials, int* counters, const int* step,     \
+      uint16_t* out) {                                                                                      \
     aoto::decode_attention_body<D, G>(q, kbase, vbase, kv_batch_stride, kv_head_stride, mask,             \
                                       mask_batch_stride, valid, ring_offset, cap, kv_heads, scale, chunk, \
-                                      partials, counters, out);                                           \
+                                      partials, counters, step, out);                                     \
   }

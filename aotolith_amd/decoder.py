@@ -1,0 +1,1067 @@
+"""Static-KV-cache W4 decoder runtime for the hip-gfx950 target.
+
+The host-side mirror of the reference's static-cache adapter
+(``models/decoder.py``): the same cache ABI, the same plan pair per prompt
+bucket and the same runtime methods (``prefill_ids``, ``prefill_padded``,
+``pad_cache``, ``decode_token``, ``decode_mask``, ``greedy_generate``,
+``memory_footprint``, ``check_memory_budget``, ``save``), with every node of
+both plans a gfx950 kernel:
+
+prefill (per layer)   rms_norm -> W4 GEMM (+q/k/v bias) -> fused RoPE + cache fill
+                      -> MFMA flash attention -> W4 GEMM (+residual) -> rms_norm
+                      -> W4 GEMM (gate) -> W4 GEMM (up, silu_mul) -> W4 GEMM (down, +residual);
+                      the final norm is the LM-head GEMV's prologue on the last row.
+decode  (per layer)   W4 GEMV (norm prologue, bias) -> RoPE + KV append
+                      -> split-K decode attention -> W4 GEMV (+residual)
+                      -> paired gate/up W4 GEMV (norm, silu) -> W4 GEMV (+residual);
+                      LM-head GEMV (norm), argmax.
+
+``decode_token`` keeps the reference's functional contract (the cache it
+returns is the input window rolled by one slot). ``greedy_generate`` runs the
+same kernels on a ring-buffer cache with device-resident step state, captured
+once as a HIP graph and replayed per token with no host work in between.
+"""
+
+from __future__ import annotations
+
+import os
+from collections.abc import Sequence
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import ops
+from .errors import (
+    BucketRangeError,
+    CompilationError,
+    DeviceError,
+    DynamicShapeError,
+    MemoryBudgetError,
+    PlanInputError,
+    UnsupportedDTypeError,
+    UnsupportedModelError,
+)
+from .plan import ARCHITECTURE, TARGET, CompiledPlan, PlanNode, require_native
+from .selection import KernelSelection
+
+BF16 = torch.bfloat16
+
+#: Family name -> accepted ``config.model_type`` values (models/decoder.py:65-89).
+FAMILIES: dict[str, tuple[str, ...]] = {"qwen2": ("qwen2",), "llama": ("llama",)}
+_LABELS = {"qwen2": "Qwen2/Qwen2.5", "llama": "Llama"}
+
+#: Targets this package compiles for; the reference's own two are named so the
+#: error for them can say where they live.
+TARGETS: tuple[str, ...] = (TARGET,)
+MEMORY_POLICIES: tuple[str, ...] = ("latency", "balanced", "minimal")
+
+
+# ----------------------------------------------------------------------------- spec
+@dataclass(frozen=True)
+class DecoderSpec:
+    """The shape of a decoder the adapter compiles (read from a model config)."""
+
+    family: str
+    vocab: int
+    hidden: int
+    intermediate: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    eps: float
+    theta: float
+    qkv_bias: bool
+    tied: bool = False
+    max_position: int = 1 << 20
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    @property
+    def attention_width(self) -> int:
+        return self.heads * self.head_dim
+
+
+def family_for(model: torch.nn.Module, *, require: str | None = None) -> str:
+    """The family of ``model``; refuse others (models/decoder.py:92-133)."""
+
+    model_type = str(getattr(model.config, "model_type", None))
+    family = next((name for name, types in FAMILIES.items() if model_type in types), None)
+    if family is None:
+        supported = ", ".join(f"{_LABELS[n]} ({'/'.join(t)})" for n, t in FAMILIES.items())
+        raise UnsupportedModelError(
+            f"the static-cache adapter does not cover model_type {model_type!r}; it covers {supported}",
+            hint="add the family once its module tree and causal mask have been checked",
+        )
+    if require is not None and family != require:
+        raise UnsupportedModelError(
+            f"this entry point compiles {require} and the model is {_LABELS[family]} ({model_type!r})",
+            hint=f"call compile_{family}_static_cache instead",
+        )
+    return family
+
+
+def _rope_theta(config) -> float:
+    """RoPE base from either config generation.
+
+    transformers < 5 stores ``rope_theta``; transformers 5 moves it into
+    ``rope_parameters`` (``{"rope_theta": ..., "rope_type": "default"}``) and
+    leaves ``rope_scaling`` as that same dict. Only the default (unscaled) type
+    is accepted, as the reference refuses RoPE scaling (models/decoder.py:299-306).
+    """
+
+    params = getattr(config, "rope_parameters", None)
+    scaling = getattr(config, "rope_scaling", None)
+    for block in (params, scaling):
+        if isinstance(block, dict):
+            kind = block.get("rope_type", block.get("type", "default"))
+            if kind not in (None, "default"):
+                raise UnsupportedModelError(
+                    f"RoPE scaling {kind!r} is not supported yet",
+                    hint="the adapter builds one rotary table from rope_theta",
+                )
+    theta = getattr(config, "rope_theta", None)
+    if theta is None and isinstance(params, dict):
+        theta = params.get("rope_theta")
+    if theta is None and isinstance(scaling, dict):
+        theta = scaling.get("rope_theta")
+    return float(theta if theta is not None else 10000.0)
+
+
+def spec_from_model(model: torch.nn.Module, *, require: str | None = None) -> DecoderSpec:
+    family = family_for(model, require=require)
+    config = model.config
+    layer_types = getattr(config, "layer_types", None)
+    if getattr(model.model, "has_sliding_layers", False) or (
+        isinstance(layer_types, (list, tuple)) and any(t == "sliding_attention" for t in layer_types)
+    ):
+        raise UnsupportedModelError(
+            "sliding-window attention is not supported: the static-cache adapter builds a plain causal mask"
+        )
+    hidden = int(config.hidden_size)
+    heads = int(config.num_attention_heads)
+    attention = model.model.layers[0].self_attn
+    biases = [getattr(attention, name).bias for name in ("q_proj", "k_proj", "v_proj")]
+    if any(b is None for b in biases) and not all(b is None for b in biases):
+        raise UnsupportedModelError("the attention has a bias on some of q/k/v and not others")
+    act = str(getattr(config, "hidden_act", "silu"))
+    if act != "silu":
+        raise UnsupportedModelError(
+            f"MLP activation {act!r}: the fused gate/up kernels implement silu_mul only",
+            hint="the W4 path fuses silu(gate) * up into the projection epilogue",
+        )
+    return DecoderSpec(
+        family=family,
+        vocab=int(config.vocab_size),
+        hidden=hidden,
+        intermediate=int(config.intermediate_size),
+        layers=int(config.num_hidden_layers),
+        heads=heads,
+        kv_heads=int(config.num_key_value_heads),
+        head_dim=int(getattr(config, "head_dim", None) or hidden // heads),
+        eps=float(config.rms_norm_eps),
+        theta=_rope_theta(config),
+        qkv_bias=biases[0] is not None,
+        tied=bool(getattr(config, "tie_word_embeddings", False)),
+        max_position=int(getattr(config, "max_position_embeddings", 1 << 20)),
+    )
+
+
+# ----------------------------------------------------------------------------- state
+@dataclass
+class PackedWeight:
+    """A W4 weight in the reference's format: int32 words [N, K/8], bf16 scales [N, K/g]."""
+
+    packed: torch.Tensor
+    scales: torch.Tensor
+    group: int
+
+    @property
+    def out_features(self) -> int:
+        return int(self.packed.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.packed.shape[1]) * 8
+
+    @property
+    def nbytes(self) -> int:
+        return self.packed.numel() * 4 + self.scales.numel() * 2
+
+
+@dataclass
+class LayerState:
+    qkv: PackedWeight
+    o: PackedWeight
+    gate: PackedWeight
+    up: PackedWeight
+    down: PackedWeight
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    qkv_bias: torch.Tensor | None = None
+
+
+@dataclass
+class DecoderState:
+    """Device-resident plan state: the packed weights and the bf16 tensors."""
+
+    embed: torch.Tensor
+    final_norm: torch.Tensor
+    lm_head: PackedWeight
+    layers: list[LayerState]
+
+    def tensors(self) -> list[torch.Tensor]:
+        out = [self.embed, self.final_norm, self.lm_head.packed, self.lm_head.scales]
+        for layer in self.layers:
+            for weight in (layer.qkv, layer.o, layer.gate, layer.up, layer.down):
+                out += [weight.packed, weight.scales]
+            out += [layer.input_norm, layer.post_norm]
+            if layer.qkv_bias is not None:
+                out.append(layer.qkv_bias)
+        return out
+
+    @property
+    def nbytes(self) -> int:
+        seen = {}
+        for tensor in self.tensors():
+            seen[tensor.data_ptr()] = tensor.numel() * tensor.element_size()
+        return sum(seen.values())
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise DeviceError(
+            f"the {TARGET} target needs a ROCm GPU (MI355X, gfx950); none is visible",
+            hint="run on the GPU host, or use the CPU oracle for reference numbers",
+        )
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _pack(weight: torch.Tensor, group: int, device) -> PackedWeight:
+    w = weight.detach().to(device=device)
+    if w.dtype not in (BF16, torch.float32):
+        w = w.to(BF16)
+    packed, scales = ops.w4_quantize(w.contiguous(), group)
+    return PackedWeight(packed, scales, group)
+
+
+def pack_model_state(model: torch.nn.Module, spec: DecoderSpec, group: int) -> DecoderState:
+    """Pack an HF model's projections on the GPU (models/decoder.py:640-698).
+
+    The packer is the bit-exact gfx950 quantizer (symmetric int4, bf16 scales);
+    the q/k/v projections are concatenated into one packed weight, the embedding
+    and norms stay bf16, and any bias besides q/k/v is refused.
+    """
+
+    device = _device()
+    dtype = next(model.parameters()).dtype
+    if dtype != BF16:
+        raise UnsupportedDTypeError(
+            f"the {TARGET} W4 path computes in bf16; the model is {dtype}",
+            hint="load the checkpoint with torch_dtype=torch.bfloat16",
+        )
+
+    def dev(t: torch.Tensor) -> torch.Tensor:
+        return t.detach().to(device=device, dtype=BF16).contiguous()
+
+    layers = []
+    for index, layer in enumerate(model.model.layers):
+        attention, mlp = layer.self_attn, layer.mlp
+        for owner, name in ((attention, "o_proj"), (mlp, "gate_proj"), (mlp, "up_proj"), (mlp, "down_proj")):
+            if getattr(owner, name).bias is not None:
+                raise UnsupportedModelError(
+                    f"packed compilation cannot pack the {name} bias of layer {index}",
+                    hint="the quantized plan holds only the packed q/k/v bias",
+                )
+        qkv = torch.cat((attention.q_proj.weight, attention.k_proj.weight, attention.v_proj.weight), dim=0)
+        bias = None
+        if spec.qkv_bias:
+            bias = dev(torch.cat((attention.q_proj.bias, attention.k_proj.bias, attention.v_proj.bias), dim=0))
+        layers.append(
+            LayerState(
+                qkv=_pack(qkv, group, device),
+                o=_pack(attention.o_proj.weight, group, device),
+                gate=_pack(mlp.gate_proj.weight, group, device),
+                up=_pack(mlp.up_proj.weight, group, device),
+                down=_pack(mlp.down_proj.weight, group, device),
+                input_norm=dev(layer.input_layernorm.weight),
+                post_norm=dev(layer.post_attention_layernorm.weight),
+                qkv_bias=bias,
+            )
+        )
+    head = getattr(model, "lm_head", None)
+    if head is not None and getattr(head, "bias", None) is not None:
+        raise UnsupportedModelError("packed compilation cannot pack an lm_head bias")
+    return DecoderState(
+        embed=dev(model.model.embed_tokens.weight),
+        final_norm=dev(model.model.norm.weight),
+        lm_head=_pack(model.lm_head.weight, group, device),
+        layers=layers,
+    )
+
+
+def random_state(spec: DecoderSpec, group: int = 64, *, seed: int = 0, std: float = 0.02,
+                 norm_std: float = 0.0) -> DecoderState:
+    """A seeded random-init state built directly on the GPU, one tensor at a time.
+
+    Weights and biases ~ N(0, std) in bf16 (q/k/v biases seeded, unlike HF's
+    zero init), norms 1 + N(0, norm_std). No fp32 model is ever materialized, so
+    an 8B-shape state needs only its packed size plus one bf16 projection.
+    """
+
+    device = _device()
+    generator = torch.Generator(device=device)
+    generator.manual_seed(seed)
+
+    def normal(*shape, scale=std):
+        return (torch.randn(*shape, generator=generator, device=device, dtype=torch.float32) * scale).to(BF16)
+
+    def norm(n):
+        if norm_std == 0.0:
+            return torch.ones(n, device=device, dtype=BF16)
+        return (1.0 + torch.randn(n, generator=generator, device=device) * norm_std).to(BF16)
+
+    def packed(n, k):
+        w = normal(n, k)
+        out = _pack(w, group, device)
+        del w
+        return out
+
+    h, i = spec.hidden, spec.intermediate
+    layers = []
+    for _ in range(spec.layers):
+        layers.append(
+            LayerState(
+                qkv=packed(spec.qkv_width, h),
+                o=packed(h, spec.attention_width),
+                gate=packed(i, h),
+                up=packed(i, h),
+                down=packed(h, i),
+                input_norm=norm(h),
+                post_norm=norm(h),
+                qkv_bias=normal(spec.qkv_width) if spec.qkv_bias else None,
+            )
+        )
+    embed = normal(spec.vocab, h)
+    lm_head = _pack(embed, group, device) if spec.tied else packed(spec.vocab, h)
+    return DecoderState(embed=embed, final_norm=norm(h), lm_head=lm_head, layers=layers)
+
+
+# ----------------------------------------------------------------------------- tables
+def rope_tables(capacity: int, head_dim: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 cos/sin tables [capacity, head_dim], built as the reference builds them.
+
+    models/decoder.py:323-334: the angle ``pos / theta^(2i/D)`` is formed in
+    f32 by torch on the host, duplicated over the two halves, cast to the model
+    dtype (bf16) *before* ``cos``/``sin``, and the bf16 results are the tables.
+    The same torch CPU ops are used here so the tables match bit for bit; they
+    are built once per plan and uploaded.
+    """
+
+    frequencies = torch.arange(capacity, dtype=torch.float32)[:, None] / torch.pow(
+        torch.tensor(theta, dtype=torch.float32),
+        torch.arange(0, head_dim, 2, dtype=torch.float32)[None, :] / head_dim,
+    )
+    frequencies = torch.cat((frequencies, frequencies), dim=-1).to(BF16)
+    return frequencies.cos().to(device).contiguous(), frequencies.sin().to(device).contiguous()
+
+
+def prefill_mask(length: int, bucket: int) -> np.ndarray:
+    """``[1, 1, bucket, bucket]`` keep-mask, causal and not a left pad (models/decoder.py:226-247)."""
+
+    if bucket <= 0 or length <= 0:
+        raise PlanInputError(f"need 0 < length <= bucket, got length={length}, bucket={bucket}")
+    if length > bucket:
+        raise BucketRangeError(f"a {length}-token prompt does not fit a {bucket}-token bucket")
+    query = np.arange(bucket)[:, None]
+    key = np.arange(bucket)[None, :]
+    return ((key <= query) & (key >= bucket - length))[None, None]
+
+
+# ----------------------------------------------------------------------------- selections
+def _sel(index: int, op: str, output: str, kind: str, reason: str, artifact: str) -> KernelSelection:
+    name = None
+    if torch.cuda.is_available():
+        try:
+            name = torch.cuda.get_device_name()
+        except Exception:  # noqa: BLE001 - the name is informational
+            name = None
+    return KernelSelection(
+        op_index=index,
+        op=op,
+        output_id=output,
+        implementation="hip_kernel",
+        kind=kind,
+        reason=reason,
+        artifact_name=artifact,
+        device_name=name,
+        device_architecture=ARCHITECTURE,
+    )
+
+
+def _gemv_symbol(norm: bool, paired: bool, bias: bool) -> str:
+    return f"aoto_w4_gemv_n{int(norm)}_p{int(paired)}_b{int(bias)}"
+
+
+def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
+    problems = []
+    if spec.head_dim not in (64, 128):
+        problems.append(f"head_dim {spec.head_dim} (attention kernels take 64 or 128)")
+    if spec.heads % spec.kv_heads or spec.heads // spec.kv_heads not in (1, 2, 4, 7, 8):
+        problems.append(f"{spec.heads}/{spec.kv_heads} query heads per kv head (1, 2, 4, 7 or 8)")
+    for name, k in (("hidden", spec.hidden), ("intermediate", spec.intermediate),
+                    ("attention width", spec.attention_width)):
+        if k % 64:
+            problems.append(f"{name} {k} is not a multiple of 64")
+    for name, n in (("hidden", spec.hidden), ("intermediate", spec.intermediate), ("qkv width", spec.qkv_width)):
+        if n % 16:
+            problems.append(f"{name} {n} is not a multiple of 16")
+    if group % 32 or spec.hidden % group or spec.intermediate % group:
+        problems.append(f"group size {group} must be a multiple of 32 dividing hidden and intermediate")
+    if problems:
+        raise CompilationError(
+            f"{TARGET} cannot compile this decoder: " + "; ".join(problems),
+            hint="every node must run as a gfx950 kernel; there is no fallback",
+        )
+
+
+def decode_selections(spec: DecoderSpec) -> tuple[KernelSelection, ...]:
+    """The decode plan's nodes after the reference's fusions (passes/fusion.py, passes/cache.py)."""
+
+    out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather by device token", "aoto_embedding")]
+    g = spec.heads // spec.kv_heads
+    for layer in range(spec.layers):
+        base = len(out)
+        out += [
+            _sel(base, "addmm", f"qkv_{layer}", "w4_gemv",
+                 "packed W4 GEMV (M=1) with RMSNorm prologue" + (" and q/k/v bias epilogue" if spec.qkv_bias else ""),
+                 _gemv_symbol(True, False, spec.qkv_bias)),
+            _sel(base + 1, "rope_kv_cache_append", f"query_{layer}", "rope_kv_append",
+                 "rotates q/k and appends (k, v) to the layer's cache window", "aoto_rope_kv_append"),
+            _sel(base + 2, "attention", f"attention_{layer}", "decode_attention",
+                 f"single-query GQA ({g} query heads per kv head), split-K with in-kernel merge",
+                 f"aoto_decode_attention_d{spec.head_dim}_g{g}"),
+            _sel(base + 3, "addmm", f"hidden_{layer}a", "w4_gemv", "packed W4 GEMV with residual epilogue",
+                 _gemv_symbol(False, False, True)),
+            _sel(base + 4, "matmul", f"mlp_{layer}", "w4_gemv",
+                 "paired gate/up W4 GEMV with RMSNorm prologue and silu_mul_paired epilogue",
+                 _gemv_symbol(True, True, False)),
+            _sel(base + 5, "addmm", f"hidden_{layer}b", "w4_gemv", "packed W4 GEMV with residual epilogue",
+                 _gemv_symbol(False, False, True)),
+        ]
+    n = len(out)
+    out.append(_sel(n, "matmul", "logits", "w4_gemv", "LM-head W4 GEMV with final RMSNorm prologue",
+                    _gemv_symbol(True, False, False)))
+    return tuple(out)
+
+
+def prefill_selections(spec: DecoderSpec) -> tuple[KernelSelection, ...]:
+    out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather", "aoto_embedding")]
+    for layer in range(spec.layers):
+        base = len(out)
+        out += [
+            _sel(base, "rms_norm", f"norm_{layer}a", "rms_norm", "row RMSNorm", "aoto_rms_norm"),
+            _sel(base + 1, "addmm" if spec.qkv_bias else "matmul", f"qkv_{layer}", "w4_gemm",
+                 "fused-dequant W4 GEMM on bf16 MFMA" + (" with q/k/v bias epilogue" if spec.qkv_bias else ""),
+                 "aoto_w4_gemm"),
+            _sel(base + 2, "rope", f"rope_{layer}", "rope_qkv_prefill",
+                 "RoPE of q and k fused with the layer's cache fill", "aoto_rope_qkv_prefill"),
+            _sel(base + 3, "attention", f"attention_{layer}", "flash_attention",
+                 "causal + left-pad masked GQA flash attention on MFMA",
+                 f"aoto_flash_attention_d{spec.head_dim}"),
+            _sel(base + 4, "addmm", f"hidden_{layer}a", "w4_gemm", "W4 GEMM with residual epilogue", "aoto_w4_gemm"),
+            _sel(base + 5, "rms_norm", f"norm_{layer}b", "rms_norm", "row RMSNorm", "aoto_rms_norm"),
+            _sel(base + 6, "matmul", f"gate_{layer}", "w4_gemm", "W4 GEMM", "aoto_w4_gemm"),
+            _sel(base + 7, "matmul", f"up_{layer}", "w4_gemm", "W4 GEMM with silu_mul epilogue", "aoto_w4_gemm"),
+            _sel(base + 8, "addmm", f"hidden_{layer}b", "w4_gemm", "W4 GEMM with residual epilogue", "aoto_w4_gemm"),
+        ]
+    n = len(out)
+    out.append(_sel(n, "matmul", "logits", "w4_gemv", "LM-head W4 GEMV on the last row with final RMSNorm prologue",
+                    _gemv_symbol(True, False, False)))
+    return tuple(out)
+
+
+# ----------------------------------------------------------------------------- engine
+@dataclass
+class _Engine:
+    """Kernel sequences of one bucket over one shared state."""
+
+    spec: DecoderSpec
+    state: DecoderState
+    prompt_length: int
+    capacity: int
+    device: torch.device
+    attention_splits: int = 0
+    cos: torch.Tensor = field(init=False)
+    sin: torch.Tensor = field(init=False)
+
+    def __post_init__(self) -> None:
+        s = self.spec
+        dev = self.device
+        self.cos, self.sin = rope_tables(self.capacity, s.head_dim, s.theta, dev)
+        self.scale = float(np.float32(s.head_dim ** -0.5))
+        # decode buffers
+        self.hidden = torch.empty(s.hidden, dtype=BF16, device=dev)
+        self.qkv = torch.empty(s.qkv_width, dtype=BF16, device=dev)
+        self.q = torch.empty((1, s.heads, s.head_dim), dtype=BF16, device=dev)
+        self.attn = torch.empty((1, s.heads, s.head_dim), dtype=BF16, device=dev)
+        self.act = torch.empty(s.intermediate, dtype=BF16, device=dev)
+        self.logits = torch.empty((1, 1, s.vocab), dtype=BF16, device=dev)
+        self.token = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.step_state = torch.zeros((4,), dtype=torch.int32, device=dev)
+        self.workspace = ops.decode_attention_workspace(
+            1, s.heads, s.kv_heads, self.capacity, s.head_dim, self.attention_splits, device=dev
+        )
+        self.ring = torch.zeros((s.layers, 2, 1, s.kv_heads, self.capacity, s.head_dim), dtype=BF16, device=dev)
+        self.history = torch.zeros((self.capacity + 1,), dtype=torch.int64, device=dev)
+        self.history_len = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self._graph = None
+        self.graph_error: str | None = None
+
+    # -- decode -----------------------------------------------------------------
+    def _gemv(self, x, w: PackedWeight, out, **kwargs):
+        return ops.w4_gemv(x, w.packed, w.scales, w.group, out=out, **kwargs)
+
+    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool):
+        """Run the per-layer decode kernels; ``hidden`` holds the embedded token."""
+
+        s = self.spec
+        qd, kd = s.heads * s.head_dim, s.kv_heads * s.head_dim
+        for index, layer in enumerate(self.state.layers):
+            self._gemv(self.hidden, layer.qkv, self.qkv, norm_weight=layer.input_norm, eps=s.eps,
+                       bias=layer.qkv_bias)
+            pair_out = cache_out[index]
+            if ring:
+                ops.rope_kv_cache_append(self.qkv.view(1, -1), self.cos, self.sin, 0, pair_out, pair_in=None,
+                                         query_heads=s.heads, query_start=0, key_start=qd, value_start=qd + kd,
+                                         step_state=self.step_state, q_out=self.q)
+                ops.decode_attention(self.q, pair_out[0], pair_out[1], scale=self.scale, workspace=self.workspace,
+                                     splits=self.attention_splits, step_state=self.step_state, out=self.attn)
+            else:
+                position = valid - 1
+                ops.rope_kv_cache_append(self.qkv.view(1, -1), self.cos, self.sin, position, pair_out,
+                                         pair_in=cache_in[index], query_heads=s.heads, query_start=0,
+                                         key_start=qd, value_start=qd + kd, q_out=self.q)
+                ops.decode_attention(self.q, pair_out[0], pair_out[1], valid=valid, scale=self.scale,
+                                     workspace=self.workspace, splits=self.attention_splits, out=self.attn)
+            self._gemv(self.attn.view(-1), layer.o, self.hidden, bias=self.hidden)
+            self._gemv(self.hidden, layer.gate, self.act, norm_weight=layer.post_norm, eps=s.eps,
+                       up=(layer.up.packed, layer.up.scales))
+            self._gemv(self.act, layer.down, self.hidden, bias=self.hidden)
+        self._gemv(self.hidden, self.state.lm_head, self.logits.view(-1), norm_weight=self.state.final_norm,
+                   eps=s.eps)
+
+    def decode_functional(self, token: torch.Tensor, cache: torch.Tensor, valid: int):
+        """The reference decode plan: fresh logits and the rolled next cache."""
+
+        ops.embedding(self.state.embed, token.reshape(-1)[:1], out=self.hidden.view(1, -1))
+        next_cache = torch.empty_like(cache)
+        self._decode_layers(cache, next_cache, valid=valid, ring=False)
+        return self.logits.clone(), next_cache
+
+    def _ring_step(self) -> None:
+        """One captured-loop step: token -> logits -> token, cache/step state advanced on device."""
+
+        ops.embedding(self.state.embed, self.token, out=self.hidden.view(1, -1))
+        self._decode_layers(None, self.ring, ring=True)
+        ops.argmax(self.logits.view(1, -1), out=self.token, history=self.history, history_len=self.history_len)
+        ops.step_advance(self.step_state, self.capacity)
+
+    def _ensure_graph(self) -> None:
+        if self._graph is not None or self.graph_error is not None:
+            return
+        if os.environ.get("AOTOLITH_HIP_GRAPH", "1") == "0":
+            self.graph_error = "disabled by AOTOLITH_HIP_GRAPH=0"
+            return
+        # Warm up once on dummy state (kernel lookup happens on first launch),
+        # then restore the buffers a real loop initializes anyway.
+        self.token.zero_()
+        self.step_state.copy_(torch.tensor([0, 1, 1 % self.capacity, 0], dtype=torch.int32))
+        self.history_len.zero_()
+        self._ring_step()
+        torch.cuda.synchronize()
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._ring_step()
+            self._graph = graph
+        except Exception as error:  # noqa: BLE001 - fall back to eager replay, recorded
+            self.graph_error = f"{type(error).__name__}: {error}"
+            self._graph = None
+        torch.cuda.synchronize()
+
+    def ring_loop(self, steps: int, start_valid: int, first_token: torch.Tensor, *, sync_each_step: bool,
+                  use_graph: bool = True) -> torch.Tensor:
+        """``steps`` device-driven decode steps after a prefill that filled ``self.ring``."""
+
+        if use_graph:
+            self._ensure_graph()
+        self.token.copy_(first_token.reshape(-1)[:1])
+        # state = {position, valid, ring_offset, slot} of the first decode step
+        self.step_state.copy_(
+            torch.tensor([start_valid, start_valid + 1, 1 % self.capacity, 0], dtype=torch.int32)
+        )
+        for _ in range(steps):
+            if use_graph and self._graph is not None:
+                self._graph.replay()
+            else:
+                self._ring_step()
+            if sync_each_step:
+                torch.cuda.synchronize()
+        return self.history
+
+    # -- prefill ----------------------------------------------------------------
+    def prefill_into(self, ids: torch.Tensor, positions: torch.Tensor, pair_of, slot0: int, window: int, *,
+                     key_start: int, mask: torch.Tensor | None = None) -> torch.Tensor:
+        """Run the prefill kernels; layer ``i``'s keys/values go to ``pair_of(i)`` at ``slot0``.
+
+        Returns logits ``[1, 1, V]`` of the last token.
+        """
+
+        s = self.spec
+        m = ids.numel()
+        dev = self.device
+        x = torch.empty((m, s.hidden), dtype=BF16, device=dev)
+        xn = torch.empty_like(x)
+        qkv = torch.empty((1, m, s.qkv_width), dtype=BF16, device=dev)
+        q = torch.empty((1, s.heads, m, s.head_dim), dtype=BF16, device=dev)
+        attn = torch.empty((1, m, s.attention_width), dtype=BF16, device=dev)
+        gate = torch.empty((m, s.intermediate), dtype=BF16, device=dev)
+        act = torch.empty_like(gate)
+        ops.embedding(self.state.embed, ids.reshape(-1), out=x)
+        for index, layer in enumerate(self.state.layers):
+            ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
+            ops.w4_matmul(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, bias=layer.qkv_bias,
+                          out=qkv.view(m, -1))
+            pair = pair_of(index)
+            ops.rope_qkv_prefill(qkv, positions.reshape(1, -1), self.cos, self.sin, pair, query_heads=s.heads,
+                                 kv_heads=s.kv_heads, head_dim=s.head_dim, slot0=slot0, zero_prefix=True, q_out=q)
+            keys = pair[0][:, :, slot0:slot0 + m]
+            values = pair[1][:, :, slot0:slot0 + m]
+            if mask is not None:
+                ops.prefill_attention(q, keys, values, mask=mask, scale=self.scale, out=attn)
+            else:
+                ops.prefill_attention(q, keys, values, causal=True, key_start=key_start, scale=self.scale, out=attn)
+            ops.w4_matmul(attn.view(m, -1), layer.o.packed, layer.o.scales, layer.o.group, residual=x, out=x)
+            ops.rms_norm(x, layer.post_norm, s.eps, out=xn)
+            ops.w4_matmul(xn, layer.gate.packed, layer.gate.scales, layer.gate.group, out=gate)
+            ops.w4_matmul(xn, layer.up.packed, layer.up.scales, layer.up.group, gate=gate, out=act)
+            ops.w4_matmul(act, layer.down.packed, layer.down.scales, layer.down.group, residual=x, out=x)
+        logits = torch.empty((1, 1, s.vocab), dtype=BF16, device=dev)
+        self._gemv(x[m - 1], self.state.lm_head, logits.view(-1), norm_weight=self.state.final_norm, eps=s.eps)
+        return logits
+
+
+# ----------------------------------------------------------------------------- runtime
+@dataclass(frozen=True)
+class DecoderMemoryFootprint:
+    """Resident and per-step bytes of one bucket (models/decoder.py:745-780)."""
+
+    weights_bytes: int
+    cache_bytes: int
+    scratch_bytes: int
+    masks_bytes: int
+    step_peak_bytes: int
+
+    def describe(self) -> str:
+        def mb(v):
+            return f"{v / (1 << 20):.1f} MiB"
+
+        return (f"weights {mb(self.weights_bytes)}, cache {mb(self.cache_bytes)}, masks {mb(self.masks_bytes)}, "
+                f"scratch {mb(self.scratch_bytes)}, step peak {mb(self.step_peak_bytes)}")
+
+
+def _as_ids(input_ids, device) -> torch.Tensor:
+    if isinstance(input_ids, torch.Tensor):
+        ids = input_ids.to(device=device, dtype=torch.int64)
+    else:
+        ids = torch.from_numpy(np.asarray(input_ids, dtype=np.int64)).to(device)
+    if ids.dim() == 1:
+        ids = ids[None, :]
+    return ids.contiguous()
+
+
+@dataclass(frozen=True)
+class DecoderStaticCacheRuntime:
+    """Executable prefill/decode plans of one bucket plus the host cache helpers."""
+
+    prefill: CompiledPlan
+    decode: CompiledPlan
+    prompt_length: int
+    max_new_tokens: int
+    cache_capacity: int
+    num_layers: int
+    num_key_value_heads: int
+    head_dim: int
+    family: str
+    memory: str
+    spec: DecoderSpec
+    engine: _Engine
+    group_size: int
+
+    # -- reference API -----------------------------------------------------------
+    def prefill_ids(self, input_ids):
+        ids = _as_ids(input_ids, self.engine.device)
+        if tuple(ids.shape) != (1, self.prompt_length):
+            raise PlanInputError(f"expected prompt shape (1, {self.prompt_length}), got {tuple(ids.shape)}")
+        positions = torch.arange(self.prompt_length, dtype=torch.int64, device=ids.device)[None, :]
+        return self.prefill(ids, positions, None)
+
+    def prefill_padded(self, input_ids):
+        ids = _as_ids(input_ids, self.engine.device)
+        if ids.shape[0] != 1:
+            raise PlanInputError(f"expected batch size 1, got {ids.shape[0]}")
+        length = int(ids.shape[1])
+        if length < 1:
+            raise PlanInputError(f"prompt length must be positive, got {length}")
+        if length > self.prompt_length:
+            raise BucketRangeError(f"a {length}-token prompt does not fit the {self.prompt_length}-token plan")
+        if length == self.prompt_length:
+            return self.prefill_ids(ids)
+        padding = self.prompt_length - length
+        zeros = torch.zeros((1, padding), dtype=torch.int64, device=ids.device)
+        padded_ids = torch.cat((zeros, ids), dim=1)
+        positions = torch.cat((zeros, torch.arange(length, dtype=torch.int64, device=ids.device)[None, :]), dim=1)
+        return self.prefill(padded_ids, positions, length)
+
+    def pad_cache(self, compact_cache: torch.Tensor) -> torch.Tensor:
+        expected = (self.num_layers, 2, 1, self.num_key_value_heads, self.prompt_length, self.head_dim)
+        if tuple(compact_cache.shape) != expected:
+            raise PlanInputError(f"expected compact cache shape {expected}, got {tuple(compact_cache.shape)}")
+        pad = torch.zeros(expected[:4] + (self.cache_capacity - self.prompt_length,) + expected[5:],
+                          dtype=compact_cache.dtype, device=compact_cache.device)
+        return torch.cat((pad, compact_cache), dim=4)
+
+    def decode_mask(self, valid_length: int) -> torch.Tensor:
+        if not 1 <= valid_length <= self.cache_capacity:
+            raise PlanInputError(f"valid_length must be in [1, {self.cache_capacity}], got {valid_length}")
+        window = torch.arange(self.cache_capacity) >= self.cache_capacity - valid_length
+        return window.reshape(1, 1, 1, self.cache_capacity)
+
+    def decode_token(self, token, cache: torch.Tensor, valid_length: int, *, verify_token: bool = True):
+        """One decode step ``(logits [1,1,V], rolled cache)`` (models/decoder.py:889-932)."""
+
+        if valid_length < 1 or valid_length >= self.cache_capacity:
+            raise PlanInputError(f"valid_length must be in [1, {self.cache_capacity}), got {valid_length}")
+        token = _as_ids(token, self.engine.device).reshape(-1)[:1]
+        if verify_token:
+            value = int(token.item())
+            if not 0 <= value < self.spec.vocab:
+                from .errors import IndexBoundsError
+
+                raise IndexBoundsError(f"token {value} is outside the vocabulary [0, {self.spec.vocab})")
+        return self.decode(token, cache, valid_length)
+
+    def greedy_generate(self, input_ids, *, max_new_tokens: int | None = None, sync_each_step: bool = False,
+                        use_graph: bool = True) -> torch.Tensor:
+        """Greedy tokens ``[1, steps]`` (models/decoder.py:934-951, 1054-1087).
+
+        Prefill fills the ring cache in place; the first token is the argmax of
+        its logits; the remaining ``steps - 1`` tokens come from device-driven
+        decode steps (HIP graph replays unless ``use_graph`` is False).
+        """
+
+        steps = self.max_new_tokens if max_new_tokens is None else max_new_tokens
+        if steps < 0 or steps > self.max_new_tokens:
+            raise PlanInputError(f"max_new_tokens must be in [0, {self.max_new_tokens}], got {steps}")
+        engine = self.engine
+        if steps == 0:
+            return torch.zeros((1, 0), dtype=torch.int64, device=engine.device)
+        if use_graph:
+            # Capture (and its warm-up step on dummy state) must precede the
+            # prefill: the warm-up writes the ring cache and the token history.
+            engine._ensure_graph()
+        ids = _as_ids(input_ids, engine.device)
+        if ids.shape[0] != 1:
+            raise PlanInputError(f"expected batch size 1, got {ids.shape[0]}")
+        length = int(ids.shape[1])
+        if length > self.prompt_length:
+            raise BucketRangeError(f"a {length}-token prompt does not fit the {self.prompt_length}-token plan")
+        logits = self._prefill_ring(ids)
+        engine.history_len.zero_()
+        ops.argmax(logits.view(1, -1), out=engine.token, history=engine.history, history_len=engine.history_len)
+        first = engine.token.clone()
+        if sync_each_step:
+            torch.cuda.synchronize()
+        engine.ring_loop(steps - 1, length, first, sync_each_step=sync_each_step, use_graph=use_graph)
+        return engine.history[:steps].clone().view(1, steps)
+
+    def save(self, prefix):
+        from .artifact import save_runtime
+
+        return save_runtime(self, prefix)
+
+    def memory_footprint(self) -> DecoderMemoryFootprint:
+        s = self.spec
+        cache = s.layers * 2 * s.kv_heads * self.cache_capacity * s.head_dim * 2
+        m = self.prompt_length
+        scratch = 2 * (m * s.hidden * 2 + m * s.qkv_width + s.heads * m * s.head_dim + m * s.attention_width
+                       + 2 * m * s.intermediate) + s.vocab * 2
+        masks = m * m + self.cache_capacity
+        weights = self.engine.state.nbytes
+        return DecoderMemoryFootprint(weights, cache, scratch, masks, weights + 2 * cache + masks + scratch)
+
+    def check_memory_budget(self, budget_bytes: int) -> DecoderMemoryFootprint:
+        footprint = self.memory_footprint()
+        if footprint.step_peak_bytes > budget_bytes:
+            raise MemoryBudgetError(
+                f"one step needs {footprint.step_peak_bytes} bytes but the budget is {budget_bytes} "
+                f"({footprint.describe()})",
+                hint="shorten prompt_length + max_new_tokens or raise the budget",
+            )
+        return footprint
+
+    # -- internals ---------------------------------------------------------------
+    def _prefill_ring(self, ids: torch.Tensor) -> torch.Tensor:
+        engine = self.engine
+        length = int(ids.shape[1])
+        padding = self.prompt_length - length
+        if padding:
+            zeros = torch.zeros((1, padding), dtype=torch.int64, device=ids.device)
+            ids = torch.cat((zeros, ids), dim=1)
+            positions = torch.cat((zeros, torch.arange(length, dtype=torch.int64, device=ids.device)[None, :]), 1)
+        else:
+            positions = torch.arange(length, dtype=torch.int64, device=ids.device)[None, :]
+        slot0 = self.cache_capacity - self.prompt_length
+        return engine.prefill_into(ids, positions, lambda i: engine.ring[i], slot0, self.cache_capacity,
+                                   key_start=padding)
+
+
+def _build_plans(spec: DecoderSpec, engine: _Engine, prompt_length: int):
+    capacity = engine.capacity
+
+    def run_prefill(ids, positions, mask_or_length=None):
+        """(ids [1,P], positions [1,P], mask [1,1,P,P] | real length | None) -> (logits, compact cache)."""
+
+        ids = _as_ids(ids, engine.device)
+        if tuple(ids.shape) != (1, prompt_length):
+            raise PlanInputError(f"expected ids of shape (1, {prompt_length}), got {tuple(ids.shape)}")
+        positions = _as_ids(positions, engine.device)
+        if int(positions.max()) >= capacity or int(positions.min()) < 0:
+            raise PlanInputError(f"positions must lie in [0, {capacity})")
+        compact = torch.empty((spec.layers, 2, 1, spec.kv_heads, prompt_length, spec.head_dim), dtype=BF16,
+                              device=engine.device)
+        mask = None
+        key_start = 0
+        if isinstance(mask_or_length, int):
+            key_start = prompt_length - mask_or_length
+        elif mask_or_length is not None:
+            mask = torch.as_tensor(np.asarray(mask_or_length) if not isinstance(mask_or_length, torch.Tensor)
+                                   else mask_or_length).to(device=engine.device, dtype=torch.bool)
+            mask = mask.reshape(1, prompt_length, prompt_length)
+        logits = engine.prefill_into(ids, positions, lambda i: compact[i], 0, prompt_length, key_start=key_start,
+                                     mask=mask)
+        return logits, compact
+
+    def run_decode(token, cache, valid_length):
+        expected = (spec.layers, 2, 1, spec.kv_heads, capacity, spec.head_dim)
+        if tuple(cache.shape) != expected or cache.dtype != BF16 or cache.device.type != "cuda":
+            raise PlanInputError(f"expected a bf16 device cache of shape {expected}, got {tuple(cache.shape)}")
+        return engine.decode_functional(token, cache.contiguous(), int(valid_length))
+
+    p_sel = prefill_selections(spec)
+    d_sel = decode_selections(spec)
+    require_native(p_sel, "prefill plan")
+    require_native(d_sel, "decode plan")
+    prefill = CompiledPlan("prefill", tuple(PlanNode(s) for s in p_sel), run_prefill,
+                           input_names=("input_ids", "positions", "attention_mask"),
+                           output_names=("logits", "cache"))
+    decode = CompiledPlan("decode", tuple(PlanNode(s) for s in d_sel), run_decode,
+                          input_names=("input_ids", "cache", "valid_length"), output_names=("logits", "cache"))
+    return prefill, decode
+
+
+def _check_target(target: str) -> None:
+    if target != TARGET:
+        raise CompilationError(
+            f"unknown target {target!r} for this package",
+            hint=f"this package implements {TARGET!r}; the reference's 'apple-metal' and 'mlx-reference' "
+                 "targets run on Apple silicon",
+        )
+
+
+def compile_decoder_state(
+    spec: DecoderSpec,
+    state: DecoderState,
+    *,
+    prompt_length: int,
+    max_new_tokens: int,
+    group_size: int = 64,
+    memory: str = "latency",
+    attention_splits: int = 0,
+) -> DecoderStaticCacheRuntime:
+    """Compile one bucket over an already-packed device state (shared across buckets)."""
+
+    if memory not in MEMORY_POLICIES:
+        raise CompilationError(f"unknown memory policy {memory!r}", hint="choose one of: " + ", ".join(MEMORY_POLICIES))
+    if prompt_length <= 0 or max_new_tokens < 0:
+        raise CompilationError("prompt_length must be positive and max_new_tokens non-negative")
+    capacity = prompt_length + max_new_tokens
+    if capacity > spec.max_position:
+        raise DynamicShapeError(
+            f"prompt_length + max_new_tokens exceeds the model's maximum position embeddings ({spec.max_position})"
+        )
+    _check_kernel_limits(spec, group_size)
+    engine = _Engine(spec, state, prompt_length, capacity, _device(), attention_splits)
+    prefill, decode = _build_plans(spec, engine, prompt_length)
+    return DecoderStaticCacheRuntime(
+        prefill=prefill, decode=decode, prompt_length=prompt_length, max_new_tokens=max_new_tokens,
+        cache_capacity=capacity, num_layers=spec.layers, num_key_value_heads=spec.kv_heads,
+        head_dim=spec.head_dim, family=spec.family, memory=memory, spec=spec, engine=engine,
+        group_size=group_size,
+    )
+
+
+def _check_quantize(quantize: int | None, quantize_bits: int) -> int:
+    if quantize_bits not in (4, 8):
+        raise CompilationError(f"quantize_bits must be 4 or 8, got {quantize_bits!r}")
+    if quantize is None:
+        raise CompilationError(
+            f"the {TARGET} target compiles the weight-only W4 path: pass quantize=<group size> (e.g. 64)",
+            hint="dense bf16 projections are not part of this backend",
+        )
+    if quantize_bits != 4:
+        raise CompilationError(f"the {TARGET} target packs 4-bit weights; quantize_bits={quantize_bits}")
+    return int(quantize)
+
+
+def compile_decoder_static_cache(
+    model: torch.nn.Module,
+    *,
+    prompt_length: int,
+    max_new_tokens: int,
+    codegen_matmul: bool = False,
+    codegen_attention: bool = False,
+    autotune: bool = False,
+    quantize: int | None = None,
+    quantize_bits: int = 4,
+    family: str | None = None,
+    target: str = TARGET,
+    memory: str = "latency",
+) -> DecoderStaticCacheRuntime:
+    """Compile a supported causal LM for greedy single-request generation (models/decoder.py:1090-1146)."""
+
+    _check_target(target)
+    group = _check_quantize(quantize, quantize_bits)
+    if getattr(model, "training", False):
+        raise CompilationError("compile_decoder_static_cache requires model.eval()")
+    spec = spec_from_model(model, require=family)
+    if prompt_length + max_new_tokens > spec.max_position:
+        raise DynamicShapeError(
+            "prompt_length + max_new_tokens exceeds the model's maximum position embeddings "
+            f"({spec.max_position})"
+        )
+    _check_kernel_limits(spec, group)
+    state = pack_model_state(model, spec, group)
+    return compile_decoder_state(spec, state, prompt_length=prompt_length, max_new_tokens=max_new_tokens,
+                                 group_size=group, memory=memory)
+
+
+@dataclass(frozen=True)
+class DecoderBucketedRuntime:
+    """One runtime per prompt-length bucket over one shared state (models/decoder.py:1292-1400)."""
+
+    buckets: tuple[DecoderStaticCacheRuntime, ...]
+    max_new_tokens: int
+
+    def __post_init__(self) -> None:
+        if not self.buckets:
+            raise CompilationError("at least one bucket is required")
+        widths = [b.prompt_length for b in self.buckets]
+        if widths != sorted(set(widths)):
+            raise CompilationError(f"buckets must be strictly increasing, got {widths}")
+
+    @property
+    def prompt_lengths(self) -> tuple[int, ...]:
+        return tuple(b.prompt_length for b in self.buckets)
+
+    @property
+    def family(self) -> str:
+        return self.buckets[0].family
+
+    @property
+    def max_prompt_length(self) -> int:
+        return self.buckets[-1].prompt_length
+
+    def bucket_for(self, prompt_length: int) -> DecoderStaticCacheRuntime:
+        for bucket in self.buckets:
+            if prompt_length <= bucket.prompt_length:
+                return bucket
+        raise BucketRangeError(
+            f"prompt length {prompt_length} exceeds the largest bucket ({self.max_prompt_length})"
+        )
+
+    def prefill_ids(self, input_ids):
+        ids = _as_ids(input_ids, self.buckets[0].engine.device)
+        if ids.shape[0] != 1:
+            raise PlanInputError(f"expected batch size 1, got {ids.shape[0]}")
+        bucket = self.bucket_for(int(ids.shape[1]))
+        logits, compact = bucket.prefill_padded(ids)
+        return logits, bucket.pad_cache(compact)
+
+    def greedy_generate(self, input_ids, *, max_new_tokens: int | None = None, sync_each_step: bool = False,
+                        use_graph: bool = True) -> torch.Tensor:
+        ids = _as_ids(input_ids, self.buckets[0].engine.device)
+        bucket = self.bucket_for(int(ids.shape[1]))
+        return bucket.greedy_generate(ids, max_new_tokens=max_new_tokens, sync_each_step=sync_each_step,
+                                      use_graph=use_graph)
+
+    def save(self, prefix):
+        from .artifact import save_runtime
+
+        paths = []
+        for bucket in self.buckets:
+            paths.extend(save_runtime(bucket, f"{prefix}.{bucket.prompt_length}"))
+        return tuple(paths)
+
+
+def compile_decoder_bucketed_state(
+    spec: DecoderSpec,
+    state: DecoderState,
+    *,
+    prompt_lengths: Sequence[int],
+    max_new_tokens: int,
+    group_size: int = 64,
+) -> DecoderBucketedRuntime:
+    widths = [int(w) for w in prompt_lengths]
+    if not widths:
+        raise CompilationError("prompt_lengths must name at least one bucket")
+    if any(w <= 0 for w in widths):
+        raise CompilationError(f"bucket widths must be positive, got {widths}")
+    if widths != sorted(set(widths)):
+        raise CompilationError(f"bucket widths must be strictly increasing, got {widths}")
+    runtimes = tuple(
+        compile_decoder_state(spec, state, prompt_length=w, max_new_tokens=max_new_tokens, group_size=group_size)
+        for w in widths
+    )
+    return DecoderBucketedRuntime(buckets=runtimes, max_new_tokens=max_new_tokens)
+
+
+def compile_decoder_bucketed(
+    model: torch.nn.Module,
+    *,
+    prompt_lengths: Sequence[int],
+    max_new_tokens: int,
+    codegen_matmul: bool = False,
+    codegen_attention: bool = False,
+    autotune: bool = False,
+    quantize: int | None = None,
+    quantize_bits: int = 4,
+    family: str | None = None,
+    target: str = TARGET,
+) -> DecoderBucketedRuntime:
+    """One plan pair per bucket over one packed state (models/decoder.py:1413-1478)."""
+
+    _check_target(target)
+    group = _check_quantize(quantize, quantize_bits)
+    spec = spec_from_model(model, require=family)
+    _check_kernel_limits(spec, group)
+    widths = [int(w) for w in prompt_lengths]
+    if widths and widths[-1] + max_new_tokens > spec.max_position:
+        raise DynamicShapeError("the largest bucket + max_new_tokens exceeds the maximum position embeddings")
+    state = pack_model_state(model, spec, group)
+    return compile_decoder_bucketed_state(spec, state, prompt_lengths=widths, max_new_tokens=max_new_tokens,
+                                          group_size=group)

@@ -304,6 +304,7 @@ def rope_kv_cache_append(
     key_start: int,
     value_start: int,
     ring_slot: int | None = None,
+    step_state: torch.Tensor | None = None,
     q_out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The decode ``rope_kv_cache_append``: returns ``q [B, Hq, D]``.
@@ -318,7 +319,7 @@ def rope_kv_cache_append(
     _, b2, kv_heads, capacity, head_dim = pair_out.shape
     if b2 != batch:
         raise ValueError("row and pair batch differ")
-    mode = 1 if ring_slot is not None else 0
+    mode = 1 if (ring_slot is not None or step_state is not None) else 0
     if mode == 0:
         if pair_in is None:
             raise ValueError("the roll needs pair_in")
@@ -330,7 +331,7 @@ def rope_kv_cache_append(
         _lib.library().aoto_hip_rope_kv_cache_append(
             _ptr(row), width, _ptr(cos_table), _ptr(sin_table), int(position), _ptr(pair_in), _ptr(pair_out),
             _ptr(q_out), batch, query_heads, kv_heads, capacity, head_dim, query_start, key_start, value_start,
-            mode, int(ring_slot or 0), _stream(),
+            mode, int(ring_slot or 0), _ptr(step_state), _stream(),
         )
     )
     return q_out
@@ -355,6 +356,7 @@ def decode_attention(
     scale: float | None = None,
     workspace: torch.Tensor | None = None,
     splits: int = 0,
+    step_state: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Single-query GQA attention: ``q [B, Hq, D]`` over ``keys/values [B, Hkv, cap, D]``."""
@@ -376,8 +378,8 @@ def decode_attention(
         mask = mask.reshape(-1, capacity).to(torch.uint8).contiguous()
         mask_stride = capacity if mask.shape[0] == batch else 0
         mask_ptr = mask
-    elif valid is None:
-        raise ValueError("pass valid= or mask=")
+    elif valid is None and step_state is None:
+        raise ValueError("pass valid=, mask= or step_state=")
     if out is None:
         out = torch.empty_like(q)
     _ready(q)
@@ -385,7 +387,7 @@ def decode_attention(
         _lib.library().aoto_hip_decode_attention(
             _ptr(q), _ptr(keys), _ptr(values), keys.stride(0), keys.stride(1), _ptr(mask_ptr), mask_stride,
             int(valid or 0), int(ring_offset), batch, query_heads, kv_heads, capacity, head_dim, float(scale),
-            int(splits), _ptr(workspace), _ptr(out), _stream(),
+            int(splits), _ptr(workspace), _ptr(step_state), _ptr(out), _stream(),
         )
     )
     return out
@@ -472,3 +474,11 @@ def argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None, history: to
         )
     )
     return out
+
+
+def step_advance(step_state: torch.Tensor, capacity: int) -> None:
+    """Advance the int32 device step state ``{position, valid, ring_offset, slot}`` by one token."""
+
+    _expect(step_state, "step_state", torch.int32, (4,))
+    _ready(step_state)
+    _lib.check(_lib.library().aoto_hip_step_advance(_ptr(step_state), int(capacity), _stream()))

@@ -33,7 +33,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 2
+#define AOTO_HIP_ABI_VERSION 3
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -135,11 +135,14 @@ int aoto_hip_rope_qkv_prefill(const void* qkv, const int64_t* positions, const v
  *   mode 0 (the reference op): pair_out = pair_in shifted down one slot with
  *          (k_rot, v) at capacity - 1; pair_in/pair_out are one layer's
  *          [2, batch, Hkv, capacity, head_dim] windows and must not overlap.
- *   mode 1 (ring): (k_rot, v) written in place at `slot` of pair_out. */
+ *   mode 1 (ring): (k_rot, v) written in place at `slot` of pair_out.
+ * step_state: NULL, or (ring mode) an int32 device array {position, valid,
+ * ring_offset, slot} read by the kernel in place of `position` and `slot`. */
 int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* cos_table, const void* sin_table,
                                   int position, const void* pair_in, void* pair_out, void* q_out, int batch,
                                   int query_heads, int kv_heads, int capacity, int head_dim, int query_start,
-                                  int key_start, int value_start, int mode, int slot, void* stream);
+                                  int key_start, int value_start, int mode, int slot,
+                                  const int32_t* step_state, void* stream);
 
 /* Bytes of the split-K workspace aoto_hip_decode_attention needs for these
  * shapes and `splits` (0 = the launcher's own choice). */
@@ -156,11 +159,19 @@ size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_he
  * workspace: NULL (one block per kv head, capacity <= 512) or a buffer of
  * aoto_hip_decode_attention_workspace() bytes, zero-filled before its first use
  * (the kernel returns its counters to zero); calls sharing one workspace must
- * be ordered on one stream. */
+ * be ordered on one stream. step_state: NULL, or the int32 device array
+ * {position, valid, ring_offset, slot} read in place of valid / ring_offset. */
 int aoto_hip_decode_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
                               int64_t kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid,
                               int ring_offset, int batch, int query_heads, int kv_heads, int capacity,
-                              int head_dim, float scale, int splits, void* workspace, void* out, void* stream);
+                              int head_dim, float scale, int splits, void* workspace,
+                              const int32_t* step_state, void* out, void* stream);
+
+/* Advance a decode loop's device step state {position, valid, ring_offset,
+ * slot} by one token (ring offset and slot wrap at capacity). The greedy loop
+ * of models/decoder.py:1054-1087 does this on the host between steps; on the
+ * device the captured step replays unchanged. */
+int aoto_hip_step_advance(int32_t* step_state, int capacity, void* stream);
 
 /* Prefill GQA attention on MFMA (the flash kernels of codegen/attention.py:68-422,
  * 671-759 and 817-1400, with the SDPA legalization's scale and safe_softmax,

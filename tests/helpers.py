@@ -72,3 +72,83 @@ def assert_bf16_parity(
     if max_ulp is not None:
         assert stats["max_ulp"] <= max_ulp, stats
     return stats
+
+
+def random_oracle_state(shape, seed: int = 0, *, std: float = 0.02, norm_std: float = 0.1, bias: bool = True) -> dict:
+    """A seeded decoder state in the oracle's format (f32 arrays of bf16 values, packed W4).
+
+    Norm weights are 1 + N(0, norm_std) and q/k/v biases N(0, std) so that a
+    dropped or misplaced term changes the outputs (HF's init would zero them).
+    """
+
+    from oracle.quant import pack_weight_bf16
+
+    rng = np.random.default_rng(seed)
+    g = shape.group_size
+    h, i, w = shape.hidden, shape.intermediate, shape.qkv_width
+    hd = shape.heads * shape.head_dim
+
+    def packed(n, k):
+        return pack_weight_bf16(bf16_normal(rng, (n, k), std), g)
+
+    def norm(n):
+        return round_bf16(np.float32(1.0) + rng.standard_normal(n).astype(np.float32) * np.float32(norm_std))
+
+    layers = []
+    for _ in range(shape.layers):
+        layers.append(
+            {
+                "qkv": packed(w, h),
+                "o": packed(h, hd),
+                "gate": packed(i, h),
+                "up": packed(i, h),
+                "down": packed(h, i),
+                "qkv_bias": bf16_normal(rng, (w,), std) if bias else None,
+                "input_norm": norm(h),
+                "post_norm": norm(h),
+            }
+        )
+    embed = bf16_normal(rng, (shape.vocab, h), std * 50)
+    return {"embed": embed, "final_norm": norm(h), "lm_head": packed(shape.vocab, h), "layers": layers}
+
+
+def state_to_device(ostate: dict, group: int):
+    """Upload an oracle-format state as the runtime's device state (same bits)."""
+
+    from aotolith_amd.decoder import DecoderState, LayerState, PackedWeight
+
+    def pw(pair):
+        return PackedWeight(torch.from_numpy(pair[0]).cuda(), to_gpu_bits(pair[1]), group)
+
+    layers = [
+        LayerState(
+            qkv=pw(l["qkv"]), o=pw(l["o"]), gate=pw(l["gate"]), up=pw(l["up"]), down=pw(l["down"]),
+            input_norm=to_gpu_bf16(l["input_norm"]), post_norm=to_gpu_bf16(l["post_norm"]),
+            qkv_bias=None if l["qkv_bias"] is None else to_gpu_bf16(l["qkv_bias"]),
+        )
+        for l in ostate["layers"]
+    ]
+    return DecoderState(embed=to_gpu_bf16(ostate["embed"]), final_norm=to_gpu_bf16(ostate["final_norm"]),
+                        lm_head=pw(ostate["lm_head"]), layers=layers)
+
+
+def runtime_spec(shape, family: str = "qwen2", bias: bool = True, max_position: int = 1 << 20):
+    from aotolith_amd.decoder import DecoderSpec
+
+    return DecoderSpec(family=family, vocab=shape.vocab, hidden=shape.hidden, intermediate=shape.intermediate,
+                       layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads, head_dim=shape.head_dim,
+                       eps=shape.eps, theta=shape.theta, qkv_bias=bias, max_position=max_position)
+
+
+def first_divergence(tokens, reference, logits_history) -> dict | None:
+    """None when the token streams agree, else the first differing step and the reference's top-2 margin."""
+
+    tokens = np.asarray(tokens).reshape(-1)
+    reference = np.asarray(reference).reshape(-1)
+    for step, (a, b) in enumerate(zip(tokens, reference)):
+        if a != b:
+            logits = np.asarray(logits_history[step], dtype=np.float64).reshape(-1)
+            top = np.sort(logits)[-2:]
+            return {"step": step, "got": int(a), "want": int(b), "margin": float(top[1] - top[0]),
+                    "got_logit": float(logits[a]), "want_logit": float(logits[b])}
+    return None
