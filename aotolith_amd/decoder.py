@@ -756,12 +756,15 @@ class DecoderStaticCacheRuntime:
         return self.decode(token, cache, valid_length)
 
     def greedy_generate(self, input_ids, *, max_new_tokens: int | None = None, sync_each_step: bool = False,
-                        use_graph: bool = True) -> torch.Tensor:
+                        use_graph: bool = True, events: dict | None = None) -> torch.Tensor:
         """Greedy tokens ``[1, steps]`` (models/decoder.py:934-951, 1054-1087).
 
         Prefill fills the ring cache in place; the first token is the argmax of
         its logits; the remaining ``steps - 1`` tokens come from device-driven
         decode steps (HIP graph replays unless ``use_graph`` is False).
+        ``events``, when given, receives ``torch.cuda.Event`` marks recorded on
+        the current stream at ``"start"``, ``"prefill"`` (first token ready) and
+        ``"end"``.
         """
 
         steps = self.max_new_tokens if max_new_tokens is None else max_new_tokens
@@ -780,14 +783,25 @@ class DecoderStaticCacheRuntime:
         length = int(ids.shape[1])
         if length > self.prompt_length:
             raise BucketRangeError(f"a {length}-token prompt does not fit the {self.prompt_length}-token plan")
+        marks = {}
+        if events is not None:
+            for key in ("start", "prefill", "end"):
+                marks[key] = torch.cuda.Event(enable_timing=True)
+            marks["start"].record()
         logits = self._prefill_ring(ids)
         engine.history_len.zero_()
         ops.argmax(logits.view(1, -1), out=engine.token, history=engine.history, history_len=engine.history_len)
         first = engine.token.clone()
+        if events is not None:
+            marks["prefill"].record()
         if sync_each_step:
             torch.cuda.synchronize()
         engine.ring_loop(steps - 1, length, first, sync_each_step=sync_each_step, use_graph=use_graph)
-        return engine.history[:steps].clone().view(1, steps)
+        tokens = engine.history[:steps].clone().view(1, steps)
+        if events is not None:
+            marks["end"].record()
+            events.update(marks)
+        return tokens
 
     def save(self, prefix):
         from .artifact import save_runtime

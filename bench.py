@@ -1,0 +1,335 @@
+"""Benchmark of the W4 g64 static-cache decode/prefill path on one MI355X.
+
+Workload: Qwen2.5-0.5B-architecture random-init model,
+W4 group-64 packed, bf16 activations, batch 1, a 128-token uniform-random
+prompt and 64 greedy tokens. One *step* is one greedy generation: prefill of
+the prompt (first token) plus 63 device-driven decode steps on a HIP graph.
+
+Printed JSON line (rank 0):
+  value            decode tok/s = 63 decode tokens per generation / their device time
+  prefill_tok_s    128 / (prefill + cache fill + argmax), device time
+  decode_tok_s_sync decode tok/s with a host sync after every token
+  roofline         the LM-head W4 GEMV (151936 x 896, RMSNorm prologue): algorithmic
+                   bytes per launch / average launch duration (HIP events on its
+                   stream, rotating weight copies > 1 GiB so HBM, not the 256 MB
+                   Infinity Cache, feeds it) against 8 TB/s
+  cpu_baseline     the CPU oracle (restated reference semantics, NumPy) on the host
+                   cores: prefill of the same prompt plus a bounded number of decode steps
+  parity           greedy tokens of the GPU run vs the CPU oracle over the sampled steps
+
+``--gpus N`` with N > 1 exits: every GPU box here has one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def qwen_spec():
+    from aotolith_amd.decoder import DecoderSpec
+
+    return DecoderSpec(family="qwen2", vocab=151936, hidden=896, intermediate=4864, layers=24, heads=14,
+                       kv_heads=2, head_dim=64, eps=1e-6, theta=1e6, qkv_bias=True, tied=True,
+                       max_position=32768)
+
+
+def llama8b_spec():
+    from aotolith_amd.decoder import DecoderSpec
+
+    return DecoderSpec(family="llama", vocab=128256, hidden=4096, intermediate=14336, layers=32, heads=32,
+                       kv_heads=8, head_dim=128, eps=1e-5, theta=5e5, qkv_bias=False, tied=False,
+                       max_position=131072)
+
+
+def gemv_bytes(n: int, k: int, group: int = 64, *, norm: bool = False, bias: bool = False,
+               paired: bool = False) -> int:
+    """Algorithmic bytes of one W4 GEMV launch: weights, scales, x, y (+ norm w, bias)."""
+
+    weights = n * k // 2 + n * (k // group) * 2
+    total = weights * (2 if paired else 1) + 2 * k + 2 * n
+    if norm:
+        total += 2 * k
+    if bias:
+        total += 2 * n
+    return total
+
+
+def step_weight_bytes(spec, group: int = 64) -> int:
+    """Algorithmic bytes of one decode token's GEMVs (the weight stream)."""
+
+    h, i = spec.hidden, spec.intermediate
+    per_layer = (
+        gemv_bytes(spec.qkv_width, h, group, norm=True, bias=spec.qkv_bias)
+        + gemv_bytes(h, spec.attention_width, group, bias=True)
+        + gemv_bytes(i, h, group, norm=True, paired=True)
+        + gemv_bytes(h, i, group, bias=True)
+    )
+    return spec.layers * per_layer + gemv_bytes(spec.vocab, h, group, norm=True)
+
+
+def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: float = 1.2e9) -> dict:
+    """Average duration of the LM-head GEMV over a rotating pool of weight copies."""
+
+    n, k, group = spec.vocab, spec.hidden, 64
+    per = gemv_bytes(n, k, group, norm=True)
+    copies = max(2, int(pool_bytes // per) + 1)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    words = [torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), generator=gen, dtype=torch.int32, device="cuda")
+             for _ in range(copies)]
+    scales = [(torch.rand((n, k // group), generator=gen, device="cuda") * 0.003).to(torch.bfloat16)
+              for _ in range(copies)]
+    x = torch.randn(k, generator=gen, device="cuda").to(torch.bfloat16)
+    norm = torch.ones(k, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream()
+    for i in range(copies):
+        ops.w4_gemv(x, words[i], scales[i], group, norm_weight=norm, eps=spec.eps, out=out)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(launches):
+        ops.w4_gemv(x, words[i % copies], scales[i % copies], group, norm_weight=norm, eps=spec.eps, out=out)
+    end.record(stream)
+    torch.cuda.synchronize()
+    avg_us = start.elapsed_time(end) * 1000.0 / launches
+    achieved = per / (avg_us * 1e-6) / 1e9
+    del words, scales
+    torch.cuda.empty_cache()
+    return {
+        "kernel": "aoto_w4_gemv (LM head 151936x896, g64, RMSNorm prologue)",
+        "bytes_per_launch": per,
+        "avg_us": avg_us,
+        "achieved": achieved,
+        "copies": copies,
+        "launches": launches,
+    }
+
+
+def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
+    """Time the CPU oracle on the same state and prompt: prefill + ``decode_steps`` decode steps."""
+
+    import numpy as np
+    import torch
+
+    from oracle.decoder import DecoderShape, OracleDecoder
+
+    state = runtime.engine.state
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def f32(t):
+        return t.detach().cpu().float().numpy()
+
+    def pair(w):
+        return (w.packed.cpu().numpy(), bits(w.scales))
+
+    ostate = {
+        "embed": f32(state.embed),
+        "final_norm": f32(state.final_norm),
+        "lm_head": pair(state.lm_head),
+        "layers": [
+            {"qkv": pair(l.qkv), "o": pair(l.o), "gate": pair(l.gate), "up": pair(l.up), "down": pair(l.down),
+             "qkv_bias": None if l.qkv_bias is None else f32(l.qkv_bias), "input_norm": f32(l.input_norm),
+             "post_norm": f32(l.post_norm)}
+            for l in state.layers
+        ],
+    }
+    shape = DecoderShape(vocab=spec.vocab, hidden=spec.hidden, intermediate=spec.intermediate, layers=spec.layers,
+                         heads=spec.heads, kv_heads=spec.kv_heads, head_dim=spec.head_dim, eps=spec.eps,
+                         theta=spec.theta)
+    oracle = OracleDecoder(shape, ostate, runtime.cache_capacity)
+    ids = np.asarray(prompt, dtype=np.int64).reshape(-1)
+    t0 = time.perf_counter()
+    oracle.warm()
+    t_setup = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    logits, compact = oracle.prefill(ids)
+    first = int(np.argmax(logits))
+    t_prefill = time.perf_counter() - t0
+    cache = oracle.pad_cache(compact)
+    tokens = [first]
+    margins = []
+    valid = ids.shape[0]
+    t0 = time.perf_counter()
+    for _ in range(decode_steps):
+        valid += 1
+        logits, cache = oracle.decode(tokens[-1], valid, cache)
+        top = np.sort(np.asarray(logits, dtype=np.float64).reshape(-1))[-2:]
+        margins.append(float(top[1] - top[0]))
+        tokens.append(int(np.argmax(logits)))
+    t_decode = time.perf_counter() - t0
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((info.get("num_threads", 1) for info in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001 - informational
+        threads = 1
+    gpu = [int(t) for t in gpu_tokens[: len(tokens)]]
+    agree = 0
+    for a, b in zip(gpu, tokens):
+        if a != b:
+            break
+        agree += 1
+    return {
+        "baseline": {
+            "value": decode_steps / t_decode,
+            "unit": "decode tok/s",
+            "cores": int(threads),
+            "kind": "port",
+            "sample": (f"CPU oracle (NumPy restatement of the reference's mlx-reference semantics, f32/f64 BLAS), "
+                       f"same packed state and prompt: prefill of {ids.shape[0]} tokens "
+                       f"({ids.shape[0] / t_prefill:.1f} tok/s) then {decode_steps} decode steps; weight "
+                       f"unpacking ({t_setup:.1f} s) excluded; host has {len(os.sched_getaffinity(0))} cores"),
+            "prefill_tok_s": ids.shape[0] / t_prefill,
+        },
+        "parity": {
+            "steps_compared": len(tokens),
+            "identical_prefix": agree,
+            "gpu_tokens": gpu,
+            "oracle_tokens": tokens,
+            "oracle_top2_margins": margins,
+        },
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10, help="timed greedy generations")
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--prompt", type=int, default=128)
+    parser.add_argument("--new", type=int, default=64)
+    parser.add_argument("--cpu-decode-steps", type=int, default=8)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-roofline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this one-GPU path "
+              "(no collectives are built; see the sharding design notes)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from aotolith_amd import ops
+    from aotolith_amd.decoder import compile_decoder_state, random_state
+
+    torch.cuda.set_device(0)
+    spec = qwen_spec()
+    print(f"[bench] building the random-init W4 state on {torch.cuda.get_device_name(0)}", file=sys.stderr,
+          flush=True)
+    state = random_state(spec, 64, seed=0)
+    runtime = compile_decoder_state(spec, state, prompt_length=args.prompt, max_new_tokens=args.new)
+    gen = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, spec.vocab, (1, args.prompt), generator=gen)
+    prompt_dev = prompt.cuda()
+
+    for _ in range(args.warmup):
+        runtime.greedy_generate(prompt_dev)
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+
+    records = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tokens = None
+    for _ in range(args.steps):
+        events: dict = {}
+        tokens = runtime.greedy_generate(prompt_dev, events=events)
+        records.append(events)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    prefill_ms = sum(e["start"].elapsed_time(e["prefill"]) for e in records) / len(records)
+    decode_ms = sum(e["prefill"].elapsed_time(e["end"]) for e in records) / len(records)
+    decode_steps = args.new - 1
+    decode_tok_s = decode_steps / (decode_ms / 1000.0)
+    prefill_tok_s = args.prompt / (prefill_ms / 1000.0)
+    print(f"[bench] timed {args.steps} generations: prefill {prefill_ms:.3f} ms, decode {decode_ms:.3f} ms",
+          file=sys.stderr, flush=True)
+
+    # decode with a host sync after every token (the reference's sync_each_step)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    sync_events: dict = {}
+    runtime.greedy_generate(prompt_dev, sync_each_step=True, events=sync_events)
+    torch.cuda.synchronize()
+    decode_sync_ms = sync_events["prefill"].elapsed_time(sync_events["end"])
+    decode_tok_s_sync = decode_steps / (decode_sync_ms / 1000.0)
+    _ = time.perf_counter() - t1
+
+    roofline = None
+    if not args.no_roofline:
+        lm = measure_lm_head_gemv(spec, torch, ops)
+        roofline = {
+            "bound": "hbm",
+            "achieved": round(lm["achieved"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(lm["achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": lm["kernel"],
+            "avg_us": round(lm["avg_us"], 3),
+            "bytes_per_launch": lm["bytes_per_launch"],
+        }
+        print(f"[bench] LM-head GEMV {lm['avg_us']:.2f} us, {lm['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+
+    baseline = None
+    parity = None
+    if not args.no_cpu_baseline:
+        print("[bench] CPU oracle baseline ...", file=sys.stderr, flush=True)
+        result = cpu_baseline(spec, runtime, prompt.numpy(), tokens.cpu().numpy().reshape(-1),
+                              args.cpu_decode_steps)
+        baseline = result["baseline"]
+        parity = result["parity"]
+
+    weight_bytes = step_weight_bytes(spec)
+    line = {
+        "metric": "decode tok/s + quant-GEMV HBM GB/s, prefill tok/s; Qwen2.5-0.5B-shape W4g64 bs1",
+        "value": round(decode_tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1000.0 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02) packed W4 g64 on the GPU, seeded q/k/v bias, "
+                "uniform-random prompt ids)",
+        "config": {
+            "workload": "qwen2.5-0.5b-shape W4g64 static-cache greedy: prompt 128, 64 new tokens, bs1 "
+                        "(one step = one generation: prefill + 63 graph-replayed decode steps)",
+            "prompt": args.prompt,
+            "new_tokens": args.new,
+            "layers": spec.layers,
+            "hidden": spec.hidden,
+            "vocab": spec.vocab,
+        },
+        "prefill_tok_s": round(prefill_tok_s, 1),
+        "decode_tok_s_sync": round(decode_tok_s_sync, 2),
+        "decode_ms_per_token": round(decode_ms / decode_steps, 4),
+        "decode_weight_stream_gbs": round(weight_bytes * decode_tok_s / 1e9, 1),
+        "decode_graph": runtime.engine.graph_error or "captured",
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+        "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

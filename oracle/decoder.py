@@ -67,6 +67,15 @@ class OracleDecoder:
         self._rounded: dict[int, np.ndarray] = {}
 
     # weights -----------------------------------------------------------------
+    def warm(self) -> None:
+        """Unpack every weight once (the f32 exact and bf16-rounded matrices)."""
+
+        self._w_exact(self.state["lm_head"])
+        for layer in self.state["layers"]:
+            for name in ("qkv", "o", "gate", "up", "down"):
+                self._w_exact(layer[name])
+                self._w_rounded(layer[name])
+
     def _w_exact(self, pair) -> np.ndarray:
         key = id(pair[0])
         if key not in self._exact:
@@ -80,6 +89,9 @@ class OracleDecoder:
         return self._rounded[key]
 
     # decode-side fused GEMV (codegen/matmul.py:542-739) -------------------------
+    # The products code * (x * s) are exact in f32; the sums here run in f32
+    # BLAS (blocked), whose error (~1e-6 relative at K = 4864) is far below the
+    # bf16 rounding every output takes.
     def _gemv(self, x, pair, *, norm=None, bias=None, up=None) -> np.ndarray:
         xv = np.asarray(x, dtype=np.float32).reshape(-1)
         if norm is not None:
