@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -82,24 +83,54 @@ int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* strea
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static std::mutex mutex;
+  static std::map<int, int> counts;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lock(mutex);
+  auto it = counts.find(device);
+  if (it != counts.end()) return it->second;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) n = 256;
+  counts[device] = n;
+  return n;
+}
+
+// Persistent GEMV blocks per CU (AOTO_GEMV_BLOCKS_PER_CU overrides; read once).
+int gemv_blocks_per_cu() {
+  static int value = [] {
+    const char* env = getenv("AOTO_GEMV_BLOCKS_PER_CU");
+    int v = env ? atoi(env) : 0;
+    return v > 0 ? v : 3;
+  }();
+  return value;
+}
+
+// Streaming GEMV instance for a reduction length: lanes per row and chunks per lane.
+bool stream_shape(int K, int* lpr, int* cpl) {
+  switch (K) {
+    // Long reductions (4864, 14336) stay on the block-staged kernel: one x copy
+    // per 256-thread block costs less than one per wave there.
+    case 896: *lpr = 4; *cpl = 7; return true;
+    case 4096: *lpr = 16; *cpl = 8; return true;
+    default: return false;
+  }
+}
+
 unsigned blocks_for(long long items, int threads) { return (unsigned)((items + threads - 1) / threads); }
 
-// Decode attention split choice: enough blocks to spread a long window over
-// the chip, at most 512 keys per block (the kernel's LDS score buffer).
-void decode_split(int batch, int kv_heads, int capacity, int requested, int* splits, int* chunk) {
-  int s = requested;
-  if (s <= 0) {
-    const int heads = batch * kv_heads;
-    s = (128 + heads - 1) / heads;
-    const int most = (capacity + 63) / 64;
-    if (s > most) s = most;
-    if (s < 1) s = 1;
-  }
+// Decode attention split choice. One block holds at most `max_chunk` keys (one
+// key row per D/64 lanes of 256 threads); longer windows split into blocks whose
+// records a merge launch combines. `requested` > 0 asks for that many splits.
+int decode_max_chunk(int head_dim) { return head_dim == 64 ? 256 : 128; }
+
+void decode_split(int head_dim, int capacity, int requested, int* splits, int* chunk) {
+  const int most = decode_max_chunk(head_dim);
+  int s = requested > 0 ? requested : (capacity + most - 1) / most;
   int c = (capacity + s - 1) / s;
-  c = (c + 15) / 16 * 16;
-  if (c > 512) {
-    c = 512;
-  }
+  if (c > most) c = most;
   s = (capacity + c - 1) / c;
   *splits = s;
   *chunk = c;
@@ -199,6 +230,28 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   if (!aligned16(x) || !aligned16(words) || (up_words && !aligned16(up_words)) ||
       (norm_weight && !aligned16(norm_weight)))
     return fail(AOTO_ERR_ARGUMENT, "w4_gemv: x, words and norm weight must be 16-byte aligned");
+  const int norm = norm_weight != nullptr;
+  const int has_bias = bias != nullptr;
+  const unsigned shared = (unsigned)((K / 8) * 16 + (K / 32) * 4);
+  int slpr = 0, scpl = 0;
+  const bool pow2_group = (group & (group - 1)) == 0;
+  if (lanes_per_row == 0 && pow2_group && stream_shape(K, &slpr, &scpl)) {
+    // Wave-persistent kernel: one wave per tile of 64/lpr rows up to the wave
+    // budget (CUs x blocks-per-CU x 4); grids smaller than the CU count use
+    // 1-wave blocks so every wave gets its own CU.
+    const long long tiles = ((long long)N + (64 / slpr) - 1) / (64 / slpr);
+    const long long budget = (long long)cu_count() * gemv_blocks_per_cu() * 4;
+    const long long waves = tiles < budget ? tiles : budget;
+    const int wpb = waves <= cu_count() ? 1 : 4;
+    const long long grid = (waves + wpb - 1) / wpb;
+    const unsigned region = (unsigned)((K / 8) * 16 + ((K / 32 + 3) / 4) * 16);
+    int shift = 0;
+    while ((32 << shift) < group) ++shift;
+    char sname[64];
+    snprintf(sname, sizeof(sname), "aoto_w4_gemv_s%dx%d_n%d_p%d_b%d", slpr, scpl, norm, paired ? 1 : 0, has_bias);
+    return launch(sname, dim3((unsigned)grid), dim3(64 * wpb), region * wpb, stream, x, words, scales, up_words,
+                  up_scales, norm_weight, eps, bias, alpha, beta, y, K, N, shift);
+  }
   int lpr = lanes_per_row;
   if (lpr == 0) {
     // Fill the chip first (>= 2 blocks per CU on 256 CUs), then keep at least two
@@ -215,9 +268,6 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
     return fail(AOTO_ERR_ARGUMENT, "w4_gemv: lanes_per_row must be 4, 8, 16, 32 or 64 (got %d)", lpr);
   const int rows_per_block = 4 * (64 / lpr);
   const unsigned blocks = (unsigned)((N + rows_per_block - 1) / rows_per_block);
-  const unsigned shared = (unsigned)((K / 8) * 16 + (K / 32) * 4);
-  const int norm = norm_weight != nullptr;
-  const int has_bias = bias != nullptr;
   char name[64];
   snprintf(name, sizeof(name), "aoto_w4_gemv_l%d_n%d_p%d_b%d", lpr, norm, paired ? 1 : 0, has_bias);
   return launch(name, dim3(blocks), dim3(256), shared, stream, x, words, scales, up_words, up_scales,
@@ -330,50 +380,90 @@ int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* co
 size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_heads, int capacity, int head_dim,
                                            int splits) {
   int s = 0, c = 0;
-  decode_split(batch, kv_heads, capacity, splits, &s, &c);
-  const size_t partials = (size_t)batch * query_heads * s * (head_dim + 2) * sizeof(float);
-  const size_t counters = (size_t)batch * kv_heads * sizeof(int);
-  return (partials + 255) / 256 * 256 + counters;
+  decode_split(head_dim, capacity, splits, &s, &c);
+  return s > 1 ? (size_t)batch * query_heads * s * (head_dim + 2) * sizeof(float) : 0;
 }
+
+namespace {
+
+// Shared checks and split choice of the two decode-attention entry points.
+int decode_attention_plan(const char* what, int batch, int query_heads, int kv_heads, int capacity, int head_dim,
+                          int splits, const void* workspace, int* s, int* chunk) {
+  if (batch <= 0 || query_heads <= 0 || kv_heads <= 0 || capacity <= 0 || query_heads % kv_heads)
+    return fail(AOTO_ERR_ARGUMENT, "%s: bad shape (Hq=%d Hkv=%d cap=%d)", what, query_heads, kv_heads, capacity);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", what, head_dim);
+  decode_split(head_dim, capacity, splits, s, chunk);
+  if (*s > 1 && workspace == nullptr)
+    return fail(AOTO_ERR_ARGUMENT, "%s: %d keys in %d splits need a workspace", what, capacity, *s);
+  return AOTO_OK;
+}
+
+int launch_merge(int rows, int splits, int head_dim, void* workspace, void* out, void* stream) {
+  return launch("aoto_decode_attention_merge", dim3(rows), dim3(128), 0, stream, (const float*)workspace, splits,
+                head_dim, out);
+}
+
+}  // namespace
 
 int aoto_hip_decode_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
                               int64_t kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid,
                               int ring_offset, int batch, int query_heads, int kv_heads, int capacity,
-                              int head_dim, float scale, int splits, void* workspace, const int32_t* step_state,
-                              void* out, void* stream) {
+                              int head_dim, float scale, int splits, void* workspace,
+                              const int32_t* step_state, void* out, void* stream) {
   if (!q || !keys || !values || !out) return fail(AOTO_ERR_ARGUMENT, "decode_attention: null pointer");
-  if (batch <= 0 || query_heads <= 0 || kv_heads <= 0 || capacity <= 0 || query_heads % kv_heads)
-    return fail(AOTO_ERR_ARGUMENT, "decode_attention: bad shape (Hq=%d Hkv=%d cap=%d)", query_heads, kv_heads,
-                capacity);
-  const int G = query_heads / kv_heads;
-  if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 7 && G != 8))
-    return fail(AOTO_ERR_UNSUPPORTED, "decode_attention: head_dim %d with %d query heads per kv head", head_dim, G);
+  int s = 0, chunk = 0;
+  if (int st = decode_attention_plan("decode_attention", batch, query_heads, kv_heads, capacity, head_dim, splits,
+                                     workspace, &s, &chunk))
+    return st;
   if (mask == nullptr && step_state == nullptr &&
       (valid < 0 || valid > capacity || ring_offset < 0 || ring_offset >= capacity))
     return fail(AOTO_ERR_ARGUMENT, "decode_attention: valid %d / ring offset %d outside capacity %d", valid,
                 ring_offset, capacity);
   if (!aligned16(q) || !aligned16(keys) || !aligned16(values) || (kv_head_stride % 8) || (kv_batch_stride % 8))
     return fail(AOTO_ERR_ARGUMENT, "decode_attention: q/keys/values must be 16-byte aligned");
-  int s = 0, chunk = 0;
-  if (workspace == nullptr) {
-    if (capacity > 512 || splits > 1)
-      return fail(AOTO_ERR_ARGUMENT, "decode_attention: %d keys need a split workspace", capacity);
-    s = 1;
-    chunk = capacity;
-  } else {
-    decode_split(batch, kv_heads, capacity, splits, &s, &chunk);
-  }
-  float* partials = static_cast<float*>(workspace);
-  int* counters = nullptr;
-  if (workspace != nullptr) {
-    const size_t pbytes = (size_t)batch * query_heads * s * (head_dim + 2) * sizeof(float);
-    counters = reinterpret_cast<int*>(static_cast<char*>(workspace) + (pbytes + 255) / 256 * 256);
-  }
   char name[64];
-  snprintf(name, sizeof(name), "aoto_decode_attention_d%d_g%d", head_dim, G);
-  return launch(name, dim3(s, batch * kv_heads), dim3(256), 0, stream, q, keys, values, (long long)kv_batch_stride,
-                (long long)kv_head_stride, mask, mask_batch_stride, valid, ring_offset, capacity, kv_heads, scale,
-                chunk, partials, counters, step_state, out);
+  snprintf(name, sizeof(name), "aoto_decode_attention_d%d", head_dim);
+  if (int st = launch(name, dim3(s, batch * query_heads), dim3(256), 0, stream, q, keys, values,
+                      (long long)kv_batch_stride, (long long)kv_head_stride, mask, mask_batch_stride, valid,
+                      ring_offset, capacity, query_heads, kv_heads, scale, chunk, (float*)workspace, step_state,
+                      out))
+    return st;
+  return s > 1 ? launch_merge(batch * query_heads, s, head_dim, workspace, out, stream) : AOTO_OK;
+}
+
+int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_start, int key_start,
+                                   int value_start, const void* cos_table, const void* sin_table, void* keys,
+                                   void* values, int64_t kv_batch_stride, int64_t kv_head_stride, int position,
+                                   int slot, int valid, int ring_offset, int batch, int query_heads, int kv_heads,
+                                   int capacity, int head_dim, float scale, int splits, void* workspace,
+                                   const int32_t* step_state, void* out, void* stream) {
+  if (!row || !cos_table || !sin_table || !keys || !values || !out)
+    return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: null pointer");
+  int s = 0, chunk = 0;
+  if (int st = decode_attention_plan("decode_rope_attention", batch, query_heads, kv_heads, capacity, head_dim,
+                                     splits, workspace, &s, &chunk))
+    return st;
+  if (query_start < 0 || key_start < 0 || value_start < 0 || query_start + query_heads * head_dim > row_width ||
+      key_start + kv_heads * head_dim > row_width || value_start + kv_heads * head_dim > row_width)
+    return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: q/k/v columns exceed the row width %d", row_width);
+  if (step_state == nullptr &&
+      (position < 0 || position >= capacity || slot < 0 || slot >= capacity || valid < 0 || valid > capacity ||
+       ring_offset < 0 || ring_offset >= capacity))
+    return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: position %d / slot %d / valid %d / offset %d outside "
+                "capacity %d", position, slot, valid, ring_offset, capacity);
+  if (!aligned16(keys) || !aligned16(values) || (kv_head_stride % 8) || (kv_batch_stride % 8) ||
+      !aligned16(row) || !aligned16(cos_table) || !aligned16(sin_table) || (row_width % 8) || (query_start % 8))
+    return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: keys/values/row/tables must be 16-byte aligned, "
+                "row width and query start multiples of 8");
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_decode_rope_attention_d%d", head_dim);
+  if (int st = launch(name, dim3(s, batch * query_heads), dim3(256), 0, stream, row, row_width, query_start,
+                      key_start, value_start, cos_table, sin_table, keys, values, (long long)kv_batch_stride,
+                      (long long)kv_head_stride, valid, ring_offset, position, slot, capacity, query_heads,
+                      kv_heads, scale, chunk, (float*)workspace, step_state, out))
+    return st;
+  return s > 1 ? launch_merge(batch * query_heads, s, head_dim, workspace, out, stream) : AOTO_OK;
 }
 
 int aoto_hip_step_advance(int32_t* step_state, int capacity, void* stream) {

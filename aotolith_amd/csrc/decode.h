@@ -97,244 +97,216 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
 // least cap - valid (the last `valid` slots of the reference's rolled window when
 // ring_offset == 0; a ring buffer rotated by ring_offset otherwise).
 //
-// With `step` non-null, valid = step[1] and ring_offset = step[2] (device-side
-// step state of a captured decode loop).
+// FUSED (the ring-buffer decode step): q is not an input. The block rotates its
+// query head and its kv head's new key straight out of the projection row
+// (`row`, table row `position`), takes the new value from the row, uses both
+// for slot `slot` instead of the cache contents, and the first query head of
+// each kv group, in the split whose key range holds `slot`, stores the new
+// (k_rot, v) there. This folds the rope_kv_cache_append node into the launch.
+// With `step` non-null, {position, valid, ring_offset, slot} come from the
+// device step state of a captured decode loop.
 //
-// Grid (splits, B*Hkv); 256 threads. Each block handles keys
-// [split*chunk, min(cap, (split+1)*chunk)) for the G query heads of one kv head:
-// LPK lanes per key (D/8 lanes, 16 B each), 64/LPK keys per wave per pass, the
-// G scores reduced over the key's lanes with shuffles, the softmax and P.V
-// in LDS/registers. With splits == 1 it writes the output; otherwise each block
-// stores (max, sum, acc[D]) per head in `partials` and the last block of a kv
-// head (an acq_rel counter in `counters`, left at zero afterwards) merges them.
-template <int D, int G>
-__device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kbase,
-                                      const uint16_t* __restrict__ vbase, long long kv_batch_stride,
-                                      long long kv_head_stride, const uint8_t* __restrict__ mask,
-                                      int mask_batch_stride, int valid, int ring_offset, int cap, int kv_heads,
-                                      float scale, int chunk, float* __restrict__ partials,
-                                      int* __restrict__ counters, const int* __restrict__ step,
-                                      uint16_t* __restrict__ out) {
+// Grid (splits, B*Hq); 256 threads; one query head per block, keys
+// [split*chunk, min(cap, (split+1)*chunk)). The decode window is tiny, so the
+// design minimizes dependent steps rather than bytes: every key row is one
+// lane's (D/64 lanes per key, 64 dims each, q in registers), so a score needs
+// no cross-lane reduction; P.V gives each thread a pair of dims and a strided
+// subset of keys. All of a block's K and V loads are independent and issued
+// together. One split writes the output; several write (max, sum, acc[D])
+// records that aoto_decode_attention_merge combines in a second launch.
+template <int D, bool FUSED>
+__device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ row,
+                                      int row_width, int query_start, int key_start, int value_start,
+                                      const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table,
+                                      uint16_t* __restrict__ kbase, uint16_t* __restrict__ vbase,
+                                      long long kv_batch_stride, long long kv_head_stride,
+                                      const uint8_t* __restrict__ mask, int mask_batch_stride, int valid,
+                                      int ring_offset, int position, int slot, int cap, int query_heads,
+                                      int kv_heads, float scale, int chunk, float* __restrict__ partials,
+                                      const int* __restrict__ step, uint16_t* __restrict__ out) {
   if (step != nullptr) {
+    position = step[0];
     valid = step[1];
     ring_offset = step[2];
+    slot = step[3];
   }
-  constexpr int LPK = D / 8;            // lanes per key
-  constexpr int KPW = 64 / LPK;         // keys per wave per pass
-  constexpr int WAVES = 4;
-  constexpr int MAXC = 512;             // keys per block
-  __shared__ float s_scores[G][MAXC];
-  __shared__ float s_red[G][WAVES];
-  __shared__ float s_acc[WAVES][G][D];
-  __shared__ int s_last;
+  constexpr int THREADS = 256;
+  constexpr int LPK = D / 64;             // lanes per key (64 dims each)
+  constexpr int KPP = THREADS / LPK;      // keys per block (one key row per D/64 lanes)
+  constexpr int PAIRS = D / 2;            // bf16 pairs per row
+  constexpr int KG = THREADS / PAIRS;     // key groups in P.V
+  constexpr int VPT = KPP / KG;           // value pairs per thread (all loaded up front)
+  __shared__ float s_p[KPP];
+  __shared__ float s_red[THREADS / 64];
+  __shared__ float s_acc[KG][D];
+  __shared__ __attribute__((aligned(16))) float s_q[D];
+  __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[D];
 
   const int split = blockIdx.x;
   const int splits = gridDim.x;
-  const int bkv = blockIdx.y;
-  const int b = bkv / kv_heads, kvh = bkv % kv_heads;
+  const int bh = blockIdx.y;
+  const int b = bh / query_heads, h = bh % query_heads;
+  const int group = query_heads / kv_heads;
+  const int kvh = h / group;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % LPK;           // which 8-element slice of the row
-  const int kslot = lane / LPK;         // which key of the wave's pass
   const int s0 = split * chunk;
-  const int s1 = min(cap, s0 + chunk);
-  const int n = max(0, s1 - s0);
+  const int n = max(0, min(cap, s0 + chunk) - s0);  // <= KPP, checked on the host
+  const int sub = threadIdx.x % LPK;      // which 64 dims of a key row
+  const int kl = threadIdx.x / LPK;       // this thread's key
+  const int d2 = threadIdx.x % PAIRS;     // P.V: this thread's dim pair
+  const int kg = threadIdx.x / PAIRS;     // P.V: keys kg, kg + KG, ...
 
-  const uint16_t* kh = kbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
-  const uint16_t* vh = vbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
-  const int head0 = kvh * G;
-  const int query_heads = kv_heads * G;
+  uint16_t* kh = kbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
+  uint16_t* vh = vbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
 
-  // q slice in registers: G heads x 8 elements, pre-multiplied by nothing
-  // (scale applies to the f32 score).
-  float qv[G][8];
+  // Every K and V load of the block is independent of the query: issue them all first.
+  const int ksl = s0 + min(kl, max(n - 1, 0));
+  uint4 kv[8];
+  {
+    const uint4* kr = reinterpret_cast<const uint4*>(kh + (size_t)ksl * D);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint4 r = reinterpret_cast<const uint4*>(q + ((size_t)b * query_heads + head0 + g) * D)[sub];
-    const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
+    for (int c = 0; c < 8; ++c) kv[c] = kr[sub * 8 + c];
+  }
+  uint32_t vv[VPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      qv[g][2 * i] = bf16_lo(raw[i]);
-      qv[g][2 * i + 1] = bf16_hi(raw[i]);
+  for (int u = 0; u < VPT; ++u) {
+    const int sl = s0 + min(kg + u * KG, max(n - 1, 0));
+    vv[u] = reinterpret_cast<const uint32_t*>(vh + (size_t)sl * D)[d2];
+  }
+
+  // Query (rotated out of the projection row when FUSED) into LDS, f32.
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    if (FUSED) {
+      const uint16_t* rrow = row + (size_t)b * row_width;
+      const uint16_t* cos_row = cos_table + (size_t)position * D;
+      const uint16_t* sin_row = sin_table + (size_t)position * D;
+      s_q[d] = round_bf16(rope_value(rrow + query_start + (size_t)h * D, cos_row, sin_row, d, D / 2));
+      s_knew[d] = (uint16_t)f32_to_bf16(rope_value(rrow + key_start + (size_t)kvh * D, cos_row, sin_row, d, D / 2));
+      s_vnew[d] = rrow[value_start + (size_t)kvh * D + d];
+    } else {
+      s_q[d] = bf16_to_f32(q[((size_t)b * query_heads + h) * D + d]);
+    }
+  }
+  __syncthreads();
+  if (FUSED && ksl == slot) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) kv[c] = reinterpret_cast<const uint4*>(s_knew)[sub * 8 + c];
+  }
+  if (FUSED) {
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+      const int sl = s0 + min(kg + u * KG, max(n - 1, 0));
+      if (sl == slot) vv[u] = reinterpret_cast<const uint32_t*>(s_vnew)[d2];
     }
   }
 
-  auto kept = [&](int s) -> bool {
-    if (mask != nullptr) return mask[(size_t)b * mask_batch_stride + s] != 0;
-    int logical = s - ring_offset;
+  auto kept = [&](int sl) -> bool {
+    if (mask != nullptr) return mask[(size_t)b * mask_batch_stride + sl] != 0;
+    int logical = sl - ring_offset;
     logical += logical < 0 ? cap : 0;
     return logical >= cap - valid;
   };
 
-  // Scores.
-  float local_max[G];
+  // Score of this thread's key (64 dims per lane).
+  float dot = 0.f;
+  const float4* qs = reinterpret_cast<const float4*>(s_q + sub * 64);
 #pragma unroll
-  for (int g = 0; g < G; ++g) local_max[g] = -INFINITY;
-  for (int base = wave * KPW; base < n; base += WAVES * KPW) {
-    const int i = base + kslot;
-    const bool in_range = i < n;
-    float part[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) part[g] = 0.f;
-    if (in_range) {
-      const uint4 r = reinterpret_cast<const uint4*>(kh + (size_t)(s0 + i) * D)[sub];
-      const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float k0 = bf16_lo(raw[j]), k1 = bf16_hi(raw[j]);
-#pragma unroll
-        for (int g = 0; g < G; ++g) part[g] = fmaf(qv[g][2 * j + 1], k1, fmaf(qv[g][2 * j], k0, part[g]));
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) part[g] = group_sum<LPK>(part[g]);
-    if (in_range && sub == 0) {
-      const bool keep = kept(s0 + i);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float sc = keep ? part[g] * scale : -INFINITY;
-        s_scores[g][i] = sc;
-        local_max[g] = fmaxf(local_max[g], sc);
-      }
-    }
+  for (int c = 0; c < 8; ++c) {
+    const float4 qa = qs[2 * c], qb = qs[2 * c + 1];
+    const uint32_t a[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+    dot = fmaf(qa.x, bf16_lo(a[0]), dot);
+    dot = fmaf(qa.y, bf16_hi(a[0]), dot);
+    dot = fmaf(qa.z, bf16_lo(a[1]), dot);
+    dot = fmaf(qa.w, bf16_hi(a[1]), dot);
+    dot = fmaf(qb.x, bf16_lo(a[2]), dot);
+    dot = fmaf(qb.y, bf16_hi(a[2]), dot);
+    dot = fmaf(qb.z, bf16_lo(a[3]), dot);
+    dot = fmaf(qb.w, bf16_hi(a[3]), dot);
   }
-  // Block max per head.
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = group_max<64>(local_max[g]);
-    if (lane == 0) s_red[g][wave] = m;
-  }
+  if (LPK == 2) dot += __shfl_xor(dot, 1, 64);
+  float sc = -INFINITY;
+  if (kl < n && kept(ksl)) sc = dot * scale;
+  if (sub == 0 && kl < n) s_p[kl] = sc;
+  float m = group_max<64>(sc);
+  if (lane == 0) s_red[wave] = m;
   __syncthreads();
-  float row_max[G];
+  float row_max = s_red[0];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = s_red[g][0];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_red[g][w]);
-    row_max[g] = m;
+  for (int w = 1; w < THREADS / 64; ++w) row_max = fmaxf(row_max, s_red[w]);
+  __syncthreads();  // s_red is reused below
+  float p_local = 0.f;
+  if (threadIdx.x < n) {
+    const float v = s_p[threadIdx.x];
+    p_local = (row_max == -INFINITY || v == -INFINITY) ? 0.f : expf(v - row_max);
+    s_p[threadIdx.x] = p_local;
   }
+  const float t = group_sum<64>(p_local);
+  if (lane == 0) s_red[wave] = t;
   __syncthreads();
-  // Exponentials and sums.
-  float local_sum[G];
+  float row_sum = 0.f;
 #pragma unroll
-  for (int g = 0; g < G; ++g) local_sum[g] = 0.f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float sc = s_scores[g][i];
-      const float p = (row_max[g] == -INFINITY || sc == -INFINITY) ? 0.f : expf(sc - row_max[g]);
-      s_scores[g][i] = p;
-      local_sum[g] += p;
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float s = group_sum<64>(local_sum[g]);
-    if (lane == 0) s_red[g][wave] = s;
-  }
-  __syncthreads();
-  float row_sum[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) s += s_red[g][w];
-    row_sum[g] = s;
-  }
-  // P.V: each lane accumulates 8 columns of its key slot's rows.
-  float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
-  for (int base = wave * KPW; base < n; base += WAVES * KPW) {
-    const int i = base + kslot;
-    if (i < n) {
-      const uint4 r = reinterpret_cast<const uint4*>(vh + (size_t)(s0 + i) * D)[sub];
-      const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = bf16_lo(raw[j]);
-        v[2 * j + 1] = bf16_hi(raw[j]);
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = s_scores[g][i];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(p, v[j], acc[g][j]);
-      }
-    }
-  }
-  // Reduce over the wave's key slots (lanes with the same `sub`), then waves.
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float a = acc[g][j];
-#pragma unroll
-      for (int off = LPK; off < 64; off <<= 1) a += __shfl_xor(a, off, 64);
-      acc[g][j] = a;
-    }
-  if (kslot == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_acc[wave][g][sub * 8 + j] = acc[g][j];
-  }
-  __syncthreads();
+  for (int w = 0; w < THREADS / 64; ++w) row_sum += s_red[w];
 
-  if (splits == 1) {
-    for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
-      const int g = e / D, d = e % D;
-      float a = 0.f;
+  // P.V over this thread's keys and dim pair.
+  float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) a += s_acc[w][g][d];
-      const float o = row_sum[g] > 0.f ? a / row_sum[g] : 0.f;
-      out[((size_t)b * query_heads + head0 + g) * D + d] = (uint16_t)f32_to_bf16(o);
-    }
-    return;
-  }
-  // Partial record per (b, head, split): [max, sum, acc[D]].
-  const int rec = D + 2;
-  for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
-    const int g = e / D, d = e % D;
-    float a = 0.f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) a += s_acc[w][g][d];
-    float* p = partials + (((size_t)b * query_heads + head0 + g) * splits + split) * rec;
-    p[2 + d] = a;
-    if (d == 0) {
-      p[0] = row_max[g];
-      p[1] = row_sum[g];
+  for (int u = 0; u < VPT; ++u) {
+    const int i = kg + u * KG;
+    if (i < n) {
+      const float pr = s_p[i];
+      a0 = fmaf(pr, bf16_lo(vv[u]), a0);
+      a1 = fmaf(pr, bf16_hi(vv[u]), a1);
     }
   }
-  __threadfence();
+  s_acc[kg][2 * d2] = a0;
+  s_acc[kg][2 * d2 + 1] = a1;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int done = __hip_atomic_fetch_add(counters + bkv, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = done == splits - 1;
-    if (s_last) __hip_atomic_store(counters + bkv, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (FUSED && h % group == 0 && slot >= s0 && slot < s0 + n && threadIdx.x < D) {
+    kh[(size_t)slot * D + threadIdx.x] = s_knew[threadIdx.x];
+    vh[(size_t)slot * D + threadIdx.x] = s_vnew[threadIdx.x];
   }
-  __syncthreads();
-  if (!s_last) return;
-  __atomic_thread_fence(__ATOMIC_ACQUIRE);
-  for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
-    const int g = e / D, d = e % D;
-    const float* p = partials + (((size_t)b * query_heads + head0 + g) * splits) * rec;
-    float m = -INFINITY;
-    for (int s = 0; s < splits; ++s) m = fmaxf(m, __builtin_nontemporal_load(p + (size_t)s * rec));
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < KG; ++g) acc += s_acc[g][d];
+    if (splits == 1) {
+      out[((size_t)b * query_heads + h) * D + d] = (uint16_t)f32_to_bf16(row_sum > 0.f ? acc / row_sum : 0.f);
+    } else {
+      float* rec = partials + (((size_t)b * query_heads + h) * splits + split) * (D + 2);
+      rec[2 + d] = acc;
+      if (d == 0) {
+        rec[0] = row_max;
+        rec[1] = row_sum;
+      }
+    }
+  }
+}
+
+// Combine the split records of aoto_decode_attention_*: one block per (b, head),
+// one thread per output column:
+//   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s; 0 when no key is kept.
+extern "C" __global__ __launch_bounds__(128) void aoto_decode_attention_merge(const float* __restrict__ partials,
+                                                                             int splits, int D,
+                                                                             uint16_t* __restrict__ out) {
+  const int bh = blockIdx.x;
+  const float* rec = partials + (size_t)bh * splits * (D + 2);
+  float m = -INFINITY;
+  for (int s = 0; s < splits; ++s) m = fmaxf(m, rec[(size_t)s * (D + 2)]);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float num = 0.f, den = 0.f;
     if (m != -INFINITY) {
       for (int s = 0; s < splits; ++s) {
-        const float ms = __builtin_nontemporal_load(p + (size_t)s * rec);
-        if (ms == -INFINITY) continue;
-        const float w = expf(ms - m);
-        den = fmaf(w, __builtin_nontemporal_load(p + (size_t)s * rec + 1), den);
-        num = fmaf(w, __builtin_nontemporal_load(p + (size_t)s * rec + 2 + d), num);
+        const float* r = rec + (size_t)s * (D + 2);
+        if (r[0] == -INFINITY) continue;
+        const float w = expf(r[0] - m);
+        den = fmaf(w, r[1], den);
+        num = fmaf(w, r[2 + d], num);
       }
     }
-    const float o = den > 0.f ? num / den : 0.f;
-    out[((size_t)b * query_heads + head0 + g) * D + d] = (uint16_t)f32_to_bf16(o);
+    out[(size_t)bh * D + d] = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
   }
 }
 
@@ -436,13 +408,25 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
 
 }  // namespace aoto
 
-#define AOTO_DECODE_ATTENTION_INSTANCE(D, G)                                                              \
-  extern "C" __global__ __launch_bounds__(256) void aoto_decode_attention_d##D##_g##G(                   \
-      const uint16_t* q, const uint16_t* kbase, const uint16_t* vbase, long long kv_batch_stride,         \
-      long long kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid, int ring_offset,   \
-      int cap, int kv_heads, float scale, int chunk, float* partials, int* counters, const int* step,     \
-      uint16_t* out) {                                                                                      \
-    aoto::decode_attention_body<D, G>(q, kbase, vbase, kv_batch_stride, kv_head_stride, mask,             \
-                                      mask_batch_stride, valid, ring_offset, cap, kv_heads, scale, chunk, \
-                                      partials, counters, step, out);                                     \
+#define AOTO_DECODE_ATTENTION_INSTANCE(D)                                                                \
+  extern "C" __global__ __launch_bounds__(256) void aoto_decode_attention_d##D(                         \
+      const uint16_t* q, uint16_t* kbase, uint16_t* vbase, long long kv_batch_stride,                    \
+      long long kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid, int ring_offset,  \
+      int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials, const int* step,  \
+      uint16_t* out) {                                                                                   \
+    aoto::decode_attention_body<D, false>(q, nullptr, 0, 0, 0, 0, nullptr, nullptr, kbase, vbase,        \
+                                          kv_batch_stride, kv_head_stride, mask, mask_batch_stride,      \
+                                          valid, ring_offset, 0, -1, cap, query_heads, kv_heads, scale,  \
+                                          chunk, partials, step, out);                                   \
+  }                                                                                                      \
+  extern "C" __global__ __launch_bounds__(256) void aoto_decode_rope_attention_d##D(                    \
+      const uint16_t* row, int row_width, int query_start, int key_start, int value_start,               \
+      const uint16_t* cos_table, const uint16_t* sin_table, uint16_t* kbase, uint16_t* vbase,            \
+      long long kv_batch_stride, long long kv_head_stride, int valid, int ring_offset, int position,     \
+      int slot, int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials,          \
+      const int* step, uint16_t* out) {                                                                  \
+    aoto::decode_attention_body<D, true>(nullptr, row, row_width, query_start, key_start, value_start,   \
+                                         cos_table, sin_table, kbase, vbase, kv_batch_stride,            \
+                                         kv_head_stride, nullptr, 0, valid, ring_offset, position, slot, \
+                                         cap, query_heads, kv_heads, scale, chunk, partials, step, out); \
   }

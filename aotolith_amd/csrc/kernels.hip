@@ -3,6 +3,7 @@
 #include "common.h"
 #include "w4_pack.h"
 #include "w4_gemv.h"
+#include "w4_gemv_stream.h"
 #include "w4_gemm.h"
 #include "decode.h"
 #include "prefill.h"
@@ -16,23 +17,21 @@ AOTO_GEMV_LPR(1, 0, 1)
 AOTO_GEMV_LPR(0, 1, 0)
 AOTO_GEMV_LPR(1, 1, 0)
 
+// Wave-persistent streaming W4 GEMV: {lanes per row} x {chunks per lane} x
+// {x vectors each lane stages, ceil(K / 512)} per reduction length
+// (896: 4x7, 4096: 16x8).
+AOTO_GEMV_STREAM_SHAPE(4, 7, 2)
+AOTO_GEMV_STREAM_SHAPE(16, 8, 8)
+
 // Prefill W4 GEMM: {n tiles per wave} x {m tiles per wave} x epilogue.
 AOTO_GEMM_EPILOGUES(1, 4)
 AOTO_GEMM_EPILOGUES(1, 8)
 AOTO_GEMM_EPILOGUES(2, 4)
 AOTO_GEMM_EPILOGUES(2, 8)
 
-// Single-query attention: head dim x query heads per kv head.
-AOTO_DECODE_ATTENTION_INSTANCE(64, 1)
-AOTO_DECODE_ATTENTION_INSTANCE(64, 2)
-AOTO_DECODE_ATTENTION_INSTANCE(64, 4)
-AOTO_DECODE_ATTENTION_INSTANCE(64, 7)
-AOTO_DECODE_ATTENTION_INSTANCE(64, 8)
-AOTO_DECODE_ATTENTION_INSTANCE(128, 1)
-AOTO_DECODE_ATTENTION_INSTANCE(128, 2)
-AOTO_DECODE_ATTENTION_INSTANCE(128, 4)
-AOTO_DECODE_ATTENTION_INSTANCE(128, 7)
-AOTO_DECODE_ATTENTION_INSTANCE(128, 8)
+// Single-query attention (plain and RoPE-fused ring step): head dim.
+AOTO_DECODE_ATTENTION_INSTANCE(64)
+AOTO_DECODE_ATTENTION_INSTANCE(128)
 
 // Prefill attention: head dim.
 AOTO_FLASH_INSTANCE(64)

@@ -1,0 +1,240 @@
+// Wave-persistent, software-pipelined form of the W4 decode GEMV (same semantics
+// and rounding points as w4_gemv.h).
+//
+// Why a second form: at decode shapes the plain kernel is latency-bound. Each
+// block stages x (and the RMSNorm statistics) behind block barriers before it
+// issues a weight load, and its loop waits for every outstanding load before
+// the first dot product. Here
+//   * a lane's whole share of a row (CPL 16-byte chunks: chunk li + LPR*j of the
+//     row, and their group scales) is loaded with unconditional, clamped loads,
+//     so the compiler counts them statically;
+//   * the first tile's loads are issued before x is staged, so the staging
+//     latency hides under them;
+//   * each wave stages x (and the norm) into its own LDS region with wave-level
+//     reductions only - no block barrier anywhere, so small grids use 1-wave
+//     blocks spread over more CUs;
+//   * waves are persistent: tile t+waves is loaded while tile t is reduced, so a
+//     wave keeps 2*CPL chunks in flight and stages x once for many rows;
+//   * nibbles become bf16 (136 + code) pairs with one v_bitop3 each (mask,
+//     bias-by-8 and the 0x4300 exponent in one three-input op), 11 VALU ops per
+//     packed word including the four v_dot2_f32_bf16.
+#pragma once
+
+#include "common.h"
+#include "w4_gemv.h"
+
+namespace aoto {
+
+// (136 + code) bf16 pairs of one nibble position pair, straight from the raw
+// word: bitop3 with table 0x6A computes (t & m) ^ (c & m) | (c & ~m) per bit for
+// m = 0x000F000F, c = 0x43084308 - the nibble, its top bit flipped (code + 8),
+// under the 0x4300 exponent.
+AOTO_DEVICE uint32_t nibble_pair(uint32_t t) {
+  return __builtin_amdgcn_bitop3_b32(t, 0x000F000Fu, 0x43084308u, 0x6A);
+}
+
+AOTO_DEVICE float chunk_dot_fast(const uint4 q, const uint4* __restrict__ xc) {
+  const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t t = words[j];
+    const uint4 xv = xc[j];
+    acc = dot2_bf16(nibble_pair(t), xv.x, acc);
+    acc = dot2_bf16(nibble_pair(t >> 4), xv.y, acc);
+    acc = dot2_bf16(nibble_pair(t >> 8), xv.z, acc);
+    acc = dot2_bf16(nibble_pair(t >> 12), xv.w, acc);
+  }
+  return acc;
+}
+
+// x (optionally RMS-normalized and rounded to bf16) staged by one wave into its
+// own LDS region, in dot2 pair order, plus per-chunk sums. All of x (and the
+// norm weight) is loaded up front - XV 16-byte vectors per lane, XV >= K/512 -
+// so staging costs one round trip. No block barrier: the wave's LDS accesses
+// are ordered among themselves.
+template <bool NORM, int XV>
+AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+                                       float eps, int K, uint4* __restrict__ xp, float* __restrict__ csum) {
+  const int lane = threadIdx.x & 63;
+  const int vecs = K >> 3;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
+  uint4 xr[XV], wr[NORM ? XV : 1];
+#pragma unroll
+  for (int i = 0; i < XV; ++i) xr[i] = xv[min(lane + 64 * i, vecs - 1)];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) wr[i] = wv[min(lane + 64 * i, vecs - 1)];
+  }
+  float ns = 1.f;
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      if (lane + 64 * i < vecs) {
+        const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = bf16_lo(raw[j]), b = bf16_hi(raw[j]);
+          ss = fmaf(a, a, ss);
+          ss = fmaf(b, b, ss);
+        }
+      }
+    }
+    ss = group_sum<64>(ss);
+    ns = 1.0f / sqrtf(ss / (float)K + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int v = lane + 64 * i;
+    const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+    float e[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      e[2 * k] = bf16_lo(raw[k]);
+      e[2 * k + 1] = bf16_hi(raw[k]);
+    }
+    if (NORM) {
+      const uint32_t wraw[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        e[2 * k] = round_bf16((ns * e[2 * k]) * bf16_lo(wraw[k]));
+        e[2 * k + 1] = round_bf16((ns * e[2 * k + 1]) * bf16_hi(wraw[k]));
+      }
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sum += e[k];
+    if (v < vecs)
+      xp[v] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
+                         pack_bf16x2(e[3], e[7]));
+    // A chunk (32 codes) is four consecutive vectors: lanes 4c .. 4c+3.
+    sum = group_sum<4>(sum);
+    if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave-persistent body: wave w of the grid handles row tiles w, w + waves, ...;
+// a tile is 64/LPR rows, LPR lanes per row, CPL chunks (16 B) per lane.
+template <int LPR, int CPL, int XV, bool NORM, bool PAIRED, bool BIAS>
+__device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
+                                    const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
+                                    const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ norm_w,
+                                    float eps, const uint16_t* __restrict__ bias, float alpha, float beta,
+                                    uint16_t* __restrict__ y, int K, int N, int group_shift) {
+  extern __shared__ uint4 lds[];
+  constexpr int RPW = 64 / LPR;  // rows per wave tile
+  const int nchunks = K >> 5;
+  const int ngroups = nchunks >> group_shift;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & (LPR - 1);
+  const int rsub = lane / LPR;
+  const int tiles = (N + RPW - 1) / RPW;
+  const int waves_per_block = blockDim.x >> 6;
+  const int total_waves = gridDim.x * waves_per_block;
+  // Per-wave LDS region: K/8 pair vectors then K/32 chunk sums.
+  const int region = (K >> 3) + ((K >> 5) + 3) / 4;
+  uint4* xp = lds + wave * region;
+  float* csum = reinterpret_cast<float*>(xp + (K >> 3));
+
+  int cidx[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) cidx[j] = min(li + LPR * j, nchunks - 1);
+
+  uint4 q[CPL], qn[CPL];
+  uint4 u[PAIRED ? CPL : 1], un[PAIRED ? CPL : 1];
+  float s[CPL], sn[CPL];
+  float us[PAIRED ? CPL : 1], usn[PAIRED ? CPL : 1];
+
+  auto load = [&](int tile, uint4* qq, float* ss, uint4* uu, float* uss) {
+    const int row = min(tile * RPW + rsub, N - 1);
+    const uint4* wrow = words + (size_t)row * nchunks;
+    const uint16_t* srow = scales + (size_t)row * ngroups;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) qq[j] = wrow[cidx[j]];
+    if (PAIRED) {
+      const uint4* urow = up_words + (size_t)row * nchunks;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) uu[j] = urow[cidx[j]];
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) ss[j] = bf16_to_f32(srow[cidx[j] >> group_shift]);
+    if (PAIRED) {
+      const uint16_t* usrow = up_scales + (size_t)row * ngroups;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) uss[j] = bf16_to_f32(usrow[cidx[j] >> group_shift]);
+    }
+  };
+
+  int tile = blockIdx.x * waves_per_block + wave;
+  if (tile >= tiles) return;
+  load(tile, q, s, u, us);
+  stage_activation_wave<NORM, XV>(x, norm_w, eps, K, xp, csum);
+
+  for (; tile < tiles; tile += total_waves) {
+    const int next = tile + total_waves;
+    if (next < tiles) load(next, qn, sn, un, usn);
+    float total = 0.f, total_up = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = li + LPR * j;
+      if (c < nchunks) {
+        const uint4* xc = xp + c * 4;
+        const float corr = 136.f * csum[c];
+        total = fmaf(chunk_dot_fast(q[j], xc) - corr, s[j], total);
+        if (PAIRED) total_up = fmaf(chunk_dot_fast(u[j], xc) - corr, us[j], total_up);
+      }
+    }
+    total = group_sum<LPR>(total);
+    if (PAIRED) total_up = group_sum<LPR>(total_up);
+    const int row = tile * RPW + rsub;
+    if (li == 0 && row < N) {
+      float out;
+      if (PAIRED) {
+        const float g = round_bf16(total);
+        out = total_up * (g / (1.0f + expf(-g)));
+      } else if (BIAS) {
+        out = beta * bf16_to_f32(bias[row]) + alpha * total;
+      } else {
+        out = total;
+      }
+      y[row] = (uint16_t)f32_to_bf16(out);
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      q[j] = qn[j];
+      s[j] = sn[j];
+      if (PAIRED) {
+        u[j] = un[j];
+        us[j] = usn[j];
+      }
+    }
+  }
+}
+
+}  // namespace aoto
+
+#define AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, NORM, PAIRED, BIAS)                                      \
+  extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void                                       \
+      aoto_w4_gemv_s##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS(                                       \
+          const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,           \
+          const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias,             \
+          float alpha, float beta, uint16_t* y, int K, int N, int group_shift) {                         \
+    aoto::w4_gemv_stream_body<LPR, CPL, XV, NORM, PAIRED, BIAS>(x, words, scales, up_words, up_scales,   \
+                                                            norm_w, eps, bias, alpha, beta, y, K, N,     \
+                                                            group_shift);                                \
+  }
+
+// The decode variants a decoder layer uses: q/k/v (norm, +bias or not), o and
+// down (+residual), paired gate/up (norm), LM head (norm), plain.
+#define AOTO_GEMV_STREAM_SHAPE(LPR, CPL, XV)          \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 1, 0, 1)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 1, 0, 0)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 0, 0, 1)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 1, 1, 0)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 0, 1, 0)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 0, 0, 0)

@@ -410,8 +410,8 @@ def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
     problems = []
     if spec.head_dim not in (64, 128):
         problems.append(f"head_dim {spec.head_dim} (attention kernels take 64 or 128)")
-    if spec.heads % spec.kv_heads or spec.heads // spec.kv_heads not in (1, 2, 4, 7, 8):
-        problems.append(f"{spec.heads}/{spec.kv_heads} query heads per kv head (1, 2, 4, 7 or 8)")
+    if spec.heads % spec.kv_heads:
+        problems.append(f"{spec.heads} query heads are not a multiple of {spec.kv_heads} kv heads")
     for name, k in (("hidden", spec.hidden), ("intermediate", spec.intermediate),
                     ("attention width", spec.attention_width)):
         if k % 64:
@@ -442,8 +442,8 @@ def decode_selections(spec: DecoderSpec) -> tuple[KernelSelection, ...]:
             _sel(base + 1, "rope_kv_cache_append", f"query_{layer}", "rope_kv_append",
                  "rotates q/k and appends (k, v) to the layer's cache window", "aoto_rope_kv_append"),
             _sel(base + 2, "attention", f"attention_{layer}", "decode_attention",
-                 f"single-query GQA ({g} query heads per kv head), split-K with in-kernel merge",
-                 f"aoto_decode_attention_d{spec.head_dim}_g{g}"),
+                 f"single-query GQA ({g} query heads per kv head), one block per query head, split-K merge "
+                 "for long windows", f"aoto_decode_attention_d{spec.head_dim}"),
             _sel(base + 3, "addmm", f"hidden_{layer}a", "w4_gemv", "packed W4 GEMV with residual epilogue",
                  _gemv_symbol(False, False, True)),
             _sel(base + 4, "matmul", f"mlp_{layer}", "w4_gemv",
@@ -535,11 +535,10 @@ class _Engine:
                        bias=layer.qkv_bias)
             pair_out = cache_out[index]
             if ring:
-                ops.rope_kv_cache_append(self.qkv.view(1, -1), self.cos, self.sin, 0, pair_out, pair_in=None,
-                                         query_heads=s.heads, query_start=0, key_start=qd, value_start=qd + kd,
-                                         step_state=self.step_state, q_out=self.q)
-                ops.decode_attention(self.q, pair_out[0], pair_out[1], scale=self.scale, workspace=self.workspace,
-                                     splits=self.attention_splits, step_state=self.step_state, out=self.attn)
+                ops.decode_rope_attention(self.qkv.view(1, -1), self.cos, self.sin, pair_out, query_heads=s.heads,
+                                          query_start=0, key_start=qd, value_start=qd + kd,
+                                          step_state=self.step_state, scale=self.scale, workspace=self.workspace,
+                                          splits=self.attention_splits, out=self.attn)
             else:
                 position = valid - 1
                 ops.rope_kv_cache_append(self.qkv.view(1, -1), self.cos, self.sin, position, pair_out,

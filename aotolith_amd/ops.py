@@ -339,10 +339,10 @@ def rope_kv_cache_append(
 
 def decode_attention_workspace(batch: int, query_heads: int, kv_heads: int, capacity: int, head_dim: int,
                                splits: int = 0, device=None) -> torch.Tensor:
-    """A zero-filled workspace for :func:`decode_attention` with these shapes."""
+    """A workspace for the split-K records of :func:`decode_attention` with these shapes."""
 
     size = _lib.library().aoto_hip_decode_attention_workspace(batch, query_heads, kv_heads, capacity, head_dim, splits)
-    return torch.zeros((size,), dtype=torch.uint8, device=device)
+    return torch.zeros((max(size, 16),), dtype=torch.uint8, device=device)
 
 
 def decode_attention(
@@ -388,6 +388,51 @@ def decode_attention(
             _ptr(q), _ptr(keys), _ptr(values), keys.stride(0), keys.stride(1), _ptr(mask_ptr), mask_stride,
             int(valid or 0), int(ring_offset), batch, query_heads, kv_heads, capacity, head_dim, float(scale),
             int(splits), _ptr(workspace), _ptr(step_state), _ptr(out), _stream(),
+        )
+    )
+    return out
+
+
+def decode_rope_attention(
+    row: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    pair: torch.Tensor,
+    *,
+    query_heads: int,
+    query_start: int,
+    key_start: int,
+    value_start: int,
+    position: int = 0,
+    slot: int = 0,
+    valid: int = 0,
+    ring_offset: int = 0,
+    step_state: torch.Tensor | None = None,
+    scale: float | None = None,
+    workspace: torch.Tensor | None = None,
+    splits: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """RoPE + in-place KV write at ``slot`` + single-query attention over ``pair [2, B, Hkv, cap, D]``."""
+
+    _expect(row, "row", BF16)
+    _expect(pair, "pair", BF16)
+    _, batch, kv_heads, capacity, head_dim = pair.shape
+    width = row.shape[-1]
+    if row.numel() != batch * width:
+        raise ValueError("row must be [B, W]")
+    if scale is None:
+        scale = float(torch.tensor(head_dim ** -0.5, dtype=torch.float32))
+    if out is None:
+        out = torch.empty((batch, query_heads, head_dim), dtype=BF16, device=row.device)
+    keys, values = pair[0], pair[1]
+    _ready(row)
+    _lib.check(
+        _lib.library().aoto_hip_decode_rope_attention(
+            _ptr(row), width, query_start, key_start, value_start, _ptr(cos_table), _ptr(sin_table), _ptr(keys),
+            _ptr(values), keys.stride(0), keys.stride(1), int(position), int(slot), int(valid), int(ring_offset),
+            batch, query_heads, kv_heads, capacity, head_dim, float(scale), int(splits), _ptr(workspace),
+            _ptr(step_state), _ptr(out), _stream(),
         )
     )
     return out

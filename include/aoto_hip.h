@@ -33,7 +33,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 3
+#define AOTO_HIP_ABI_VERSION 4
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -157,15 +157,32 @@ size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_he
  * when mask is non-null, else the last `valid` logical slots, logical slot =
  * (slot - ring_offset) mod capacity. head_dim 64 or 128; Hq / Hkv in {1,2,4,7,8}.
  * workspace: NULL (one block per kv head, capacity <= 512) or a buffer of
- * aoto_hip_decode_attention_workspace() bytes, zero-filled before its first use
- * (the kernel returns its counters to zero); calls sharing one workspace must
- * be ordered on one stream. step_state: NULL, or the int32 device array
- * {position, valid, ring_offset, slot} read in place of valid / ring_offset. */
+ * aoto_hip_decode_attention_workspace() bytes for the split-K records, which a
+ * second launch merges (splits 0 = choose: one block per kv head up to 512
+ * keys); calls sharing one workspace must be ordered on one stream.
+ * step_state: NULL, or the int32 device array {position, valid, ring_offset,
+ * slot} read in place of valid / ring_offset. */
 int aoto_hip_decode_attention(const void* q, const void* keys, const void* values, int64_t kv_batch_stride,
                               int64_t kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid,
                               int ring_offset, int batch, int query_heads, int kv_heads, int capacity,
                               int head_dim, float scale, int splits, void* workspace,
                               const int32_t* step_state, void* out, void* stream);
+
+/* Decode RoPE + KV append + attention in one launch (the ring-buffer decode
+ * step): the rope_kv_cache_append node (codegen/kv_cache.py:96-215) folded into
+ * the decode attention (codegen/attention.py:447-656). From the projection row
+ * [batch, row_width] it rotates the queries and the new key with the table row
+ * at `position`, writes (k_rot, v) in place at slot `slot` of keys/values
+ * (layout as for aoto_hip_decode_attention) and attends over the window with
+ * the new pair included; kept slots as for aoto_hip_decode_attention (valid,
+ * ring_offset). out [batch, Hq, head_dim]. step_state as above supplies
+ * {position, valid, ring_offset, slot} on the device. */
+int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_start, int key_start,
+                                   int value_start, const void* cos_table, const void* sin_table, void* keys,
+                                   void* values, int64_t kv_batch_stride, int64_t kv_head_stride, int position,
+                                   int slot, int valid, int ring_offset, int batch, int query_heads, int kv_heads,
+                                   int capacity, int head_dim, float scale, int splits, void* workspace,
+                                   const int32_t* step_state, void* out, void* stream);
 
 /* Advance a decode loop's device step state {position, valid, ring_offset,
  * slot} by one token (ring offset and slot wrap at capacity). The greedy loop

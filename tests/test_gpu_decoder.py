@@ -188,7 +188,7 @@ def test_selections_are_all_native():
         assert all(s.device_architecture == "gfx950" for s in selections)
     kinds = [s.kind for s in runtime.decode.selections]
     assert kinds.count("decode_attention") == TINY.layers
-    assert "aoto_decode_attention_d64_g2" in runtime.decode.kernel_names()
+    assert "aoto_decode_attention_d64" in runtime.decode.kernel_names()
 
 
 def test_runtime_rejects_bad_inputs():

@@ -306,3 +306,41 @@ def test_argmax_records_history():
         ops.argmax(logits, history=history, history_len=length)
     assert history.cpu().tolist()[:3] == [3, 9, 1]
     assert int(length.item()) == 3
+
+
+@pytest.mark.parametrize("hq,hkv,dim,cap,valid,offset,slot,splits", [
+    (14, 2, 64, 192, 140, 61, 60, 0),      # Qwen shape, one block per kv head
+    (14, 2, 64, 192, 191, 0, 191, 3),     # rolled layout, 3 splits + merge
+    (32, 8, 128, 2304, 1500, 700, 699, 0),  # Llama-8B window, split-K + merge
+])
+def test_decode_rope_attention_matches_append_then_attend(hq, hkv, dim, cap, valid, offset, slot, splits):
+    """The fused ring step equals rope_kv_cache_append's rotation + attention over the ring."""
+
+    rng = np.random.default_rng(cap + slot)
+    cos, sin, gcos, gsin = _tables(cap, dim, 1e6)
+    pair = bf16_normal(rng, (2, 1, hkv, cap, dim))
+    row = bf16_normal(rng, (1, (hq + 2 * hkv) * dim))
+    position = valid - 1
+    cache = pair[None]  # one layer
+    ref_q, ref_pair = oracle.rope_kv_cache_append(
+        cache, row, cos[position], sin[position], layer=0, query_heads=hq,
+        query_start=0, key_start=hq * dim, value_start=(hq + hkv) * dim,
+    )
+    ring = pair.copy()
+    ring[:, :, :, slot] = ref_pair[:, :, :, cap - 1]
+    logical = (np.arange(cap) - offset) % cap
+    keep = (logical >= cap - valid)[None, None, None, :]
+    expected = oracle.attention(ref_q, ring[0], ring[1], keep)
+    ops = _ops()
+    gpair = to_gpu_bf16(pair)
+    workspace = ops.decode_attention_workspace(1, hq, hkv, cap, dim, splits, device="cuda")
+    out = ops.decode_rope_attention(to_gpu_bf16(row), gcos, gsin, gpair, query_heads=hq, query_start=0,
+                                    key_start=hq * dim, value_start=(hq + hkv) * dim, position=position,
+                                    slot=slot, valid=valid, ring_offset=offset, workspace=workspace, splits=splits)
+    assert_bf16_parity(from_gpu_bf16(out), expected.reshape(1, hq, dim), max_ulp=2.0)
+    got = from_gpu_bf16(gpair)
+    others = np.ones(cap, dtype=bool)
+    others[slot] = False
+    np.testing.assert_array_equal(got[:, :, :, others], pair[:, :, :, others])
+    np.testing.assert_array_equal(got[1, :, :, slot], ref_pair[1, :, :, cap - 1])
+    assert_bf16_parity(got[0, :, :, slot], ref_pair[0, :, :, cap - 1], max_ulp=1.0)

@@ -154,3 +154,38 @@ def test_gemv_rejects_unsupported_group():
     with pytest.raises(UnsupportedShape):
         _ops().w4_gemv(to_gpu_bf16(bf16_normal(rng, (64,))), torch.from_numpy(packed).cuda(),
                        to_gpu_bits(scales), 16)
+
+
+STREAM_SHAPES = [
+    (151936 // 8, 896),  # LM-head rows (an eighth of the vocabulary), K = 896
+    (1000, 896),          # rows not a multiple of the 64-row tile
+    (3, 896),             # fewer rows than one tile
+    (896, 4864),          # Qwen down projection
+    (1024, 4096),         # Llama-8B K = 4096
+    (512, 14336),         # Llama-8B down projection K
+]
+
+
+@pytest.mark.parametrize("n,k", STREAM_SHAPES)
+@pytest.mark.parametrize("variant", ["plain", "norm_bias", "paired"])
+def test_gemv_stream_shapes(n, k, variant):
+    """The persistent streaming kernels (chosen for these K) against the oracle."""
+
+    from oracle.bf16 import round_bf16
+
+    rng = np.random.default_rng(n + k + len(variant))
+    _, packed, scales = _packed_case(rng, n, k)
+    x = bf16_normal(rng, (k,))
+    kwargs, gpu_kwargs = {}, {}
+    if variant == "norm_bias":
+        norm = round_bf16(np.float32(1.0) + bf16_normal(rng, (k,), 0.2))
+        bias = bf16_normal(rng, (n,), 0.5)
+        kwargs = {"norm_weight": norm, "eps": 1e-6, "bias": bias}
+        gpu_kwargs = {"norm_weight": to_gpu_bf16(norm), "eps": 1e-6, "bias": to_gpu_bf16(bias)}
+    elif variant == "paired":
+        _, up, up_s = _packed_case(rng, n, k)
+        kwargs = {"up_packed": up, "up_scales_bits": up_s}
+        gpu_kwargs = {"up": (torch.from_numpy(up).cuda(), to_gpu_bits(up_s))}
+    y = _ops().w4_gemv(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64, **gpu_kwargs)
+    expected = oracle_gemv(x, packed, scales, 64, **kwargs)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0 if variant == "paired" else 1.0)
