@@ -274,9 +274,54 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
                 norm_weight, eps, bias, alpha, beta, y, K, N, group);
 }
 
+namespace {
+
+// Prefill GEMM launch plan: tile shape and split-K count. Small grids (the
+// M = 128 prefill of a 0.5B model gives 14-76 output tiles) split the
+// reduction so at least ~256 blocks run; each slice keeps >= 2 k-steps of 64.
+struct GemmPlan {
+  int tn, tm, splits, kslice;
+};
+
+GemmPlan gemm_plan(int M, int N, int K, int tile, int splits) {
+  GemmPlan p{};
+  if (tile == 0) {
+    p.tm = M <= 64 ? 4 : 8;
+    const long long mb = (M + 16 * p.tm - 1) / (16 * p.tm);
+    p.tn = (mb * ((N + 127) / 128) >= 256) ? 2 : 1;
+  } else {
+    p.tn = tile / 10;
+    p.tm = tile % 10;
+  }
+  const long long tiles = (long long)((N + 64 * p.tn - 1) / (64 * p.tn)) * ((M + 16 * p.tm - 1) / (16 * p.tm));
+  const int ksteps = K / 64;
+  int s = splits;
+  if (s <= 0) {
+    s = 1;
+    if (tiles < 128) {
+      s = (int)((256 + tiles - 1) / tiles);
+      if (s > ksteps / 2) s = ksteps / 2;
+      if (s < 1) s = 1;
+    }
+  }
+  if (s > ksteps) s = ksteps;
+  const int steps_per = (ksteps + s - 1) / s;
+  p.kslice = steps_per * 64;
+  p.splits = (K + p.kslice - 1) / p.kslice;
+  return p;
+}
+
+}  // namespace
+
+size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  const GemmPlan p = gemm_plan(M, N, K, tile, splits);
+  return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+}
+
 int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
                      const void* residual, const void* gate, void* y, int M, int N, int K, int group,
-                     int tile, void* stream) {
+                     int tile, int splits, void* workspace, void* stream) {
   if (!x || !words || !scales || !y) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: null pointer");
   if (M <= 0 || N <= 0 || K <= 0) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: empty shape M=%d N=%d K=%d", M, N, K);
   if (K % 64 != 0 || N % 16 != 0 || group <= 0 || group % 32 != 0 || K % group != 0)
@@ -287,24 +332,25 @@ int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, co
   if (!aligned16(x) || !aligned8(y) || (bias && !aligned8(bias)) || (residual && !aligned8(residual)) ||
       (gate && !aligned8(gate)))
     return fail(AOTO_ERR_ARGUMENT, "w4_gemm: x must be 16-byte aligned, y/bias/residual/gate 8-byte aligned");
-  // tile: 0 = choose; else TN*10 + TM/4 code: 14, 18, 24, 28 (n tiles per wave, m tiles per wave).
-  int tn = 0, tm = 0;
-  if (tile == 0) {
-    tm = M <= 64 ? 4 : 8;
-    const long long mb = (M + 16 * tm - 1) / (16 * tm);
-    tn = (mb * ((N + 127) / 128) >= 256) ? 2 : 1;
-  } else {
-    tn = tile / 10;
-    tm = (tile % 10) == 4 ? 4 : 8;
-    if ((tn != 1 && tn != 2) || (tile % 10 != 4 && tile % 10 != 8))
-      return fail(AOTO_ERR_ARGUMENT, "w4_gemm: tile code %d is not one of 14, 18, 24, 28", tile);
-  }
-  const int bn = 64 * tn, bm = 16 * tm;
-  const int b = bias != nullptr, r = residual != nullptr, g = gate != nullptr;
+  if (tile != 0 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemm: tile code %d is not one of 14, 18, 24, 28", tile);
+  const GemmPlan p = gemm_plan(M, N, K, tile, splits);
+  if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemm: %d-way split-K needs a 16-byte aligned workspace of "
+                "aoto_hip_w4_gemm_workspace() bytes", p.splits);
+  const int bn = 64 * p.tn, bm = 16 * p.tm;
+  const bool split = p.splits > 1;
+  const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
   char name[64];
-  snprintf(name, sizeof(name), "aoto_w4_gemm_n%d_m%d_b%d_r%d_g%d", tn, tm, b, r, g);
-  return launch(name, dim3((N + bn - 1) / bn, (M + bm - 1) / bm), dim3(256), 0, stream, x, words, scales, bias,
-                residual, gate, y, M, N, K, group);
+  snprintf(name, sizeof(name), "aoto_w4_gemm_n%d_m%d_b%d_r%d_g%d", p.tn, p.tm, b, r, g);
+  float* partials = split ? static_cast<float*>(workspace) : nullptr;
+  if (int st = launch(name, dim3((N + bn - 1) / bn, (M + bm - 1) / bm, p.splits), dim3(256), 0, stream, x, words,
+                      scales, bias, residual, gate, y, M, N, K, group, p.kslice, partials))
+    return st;
+  if (!split) return AOTO_OK;
+  const long long quads = (long long)M * N / 4;
+  return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
+                (const float*)partials, p.splits, bias, residual, gate, y, M, N);
 }
 
 int aoto_hip_rms_norm(const void* x, const void* weight, float eps, void* out, int rows, int hidden,

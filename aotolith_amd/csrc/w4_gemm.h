@@ -43,11 +43,15 @@ AOTO_DEVICE bf16x8_v dequant_word(uint32_t w, float s) {
 constexpr int kGemmBK = 64;
 constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
 
+// Split-K: blockIdx.z selects the reduction slice [z*kslice, min(K, (z+1)*kslice));
+// with `partials` non-null the block stores its f32 tile to partials[z][m][n]
+// and aoto_w4_gemm_reduce applies the sum and the epilogue.
 template <int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE>
 __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __restrict__ words,
                              const uint16_t* __restrict__ scales, const uint16_t* __restrict__ bias,
                              const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate,
-                             uint16_t* __restrict__ Y, int M, int N, int K, int group) {
+                             uint16_t* __restrict__ Y, int M, int N, int K, int group, int kslice,
+                             float* __restrict__ partials) {
   constexpr int BM = 16 * TM;
   constexpr int BN = 64 * TN;
   constexpr int XVEC = BM * (kGemmBK / 8);        // 16-byte vectors per X tile
@@ -105,9 +109,11 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
       for (int ks = 0; ks < 2; ++ks) wr[t][ks] = words[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
   };
 
-  load_x(0);
-  load_w(0);
-  for (int k0 = 0; k0 < K; k0 += kGemmBK) {
+  const int kb = blockIdx.z * kslice;
+  const int ke = min(K, kb + kslice);
+  load_x(kb);
+  load_w(kb);
+  for (int k0 = kb; k0 < ke; k0 += kGemmBK) {
     __syncthreads();
     store_x();
     uint32_t wcur[TN][2];
@@ -123,7 +129,7 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
       for (int ks = 0; ks < 2; ++ks)
         scur[t][ks] = bf16_to_f32(scales[(size_t)wrow[t] * groups + (k0 + ks * 32) / group]);
     __syncthreads();
-    if (k0 + kGemmBK < K) {
+    if (k0 + kGemmBK < ke) {
       load_x(k0 + kGemmBK);
       load_w(k0 + kGemmBK);
     }
@@ -142,6 +148,22 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
     }
   }
 
+  if (partials != nullptr) {
+    float* part = partials + (size_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int u = 0; u < TM; ++u) {
+      const int m = m_block + u * 16 + col;
+      if (m >= M) continue;
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int n = n_wave + t * 16 + quad * 4;
+        if (n >= N) continue;
+        *reinterpret_cast<float4*>(part + (size_t)m * N + n) =
+            make_float4(acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]);
+      }
+    }
+    return;
+  }
   // Epilogue: lane holds Y[m0 + col][n0 + quad*4 + i].
 #pragma unroll
   for (int u = 0; u < TM; ++u) {
@@ -180,13 +202,61 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
   }
 }
 
+// Sum the split-K partial tiles and apply the epilogue: one thread per 4 outputs.
+// (The f32 sum of the slices replaces the single-block accumulation; each slice
+// is itself an f32 MFMA accumulation, so only the summation order differs.)
+extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
+    const float* __restrict__ partials, int splits, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate, uint16_t* __restrict__ Y, int M,
+    int N) {
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long quads = (long long)M * N / 4;
+  if (t >= quads) return;
+  const size_t e = (size_t)t * 4;
+  const int n = (int)(e % N);
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+    const float4 p = *reinterpret_cast<const float4*>(partials + (size_t)s * M * N + e);
+    v[0] += p.x;
+    v[1] += p.y;
+    v[2] += p.z;
+    v[3] += p.w;
+  }
+  if (bias != nullptr) {
+    const uint2 bb = *reinterpret_cast<const uint2*>(bias + n);
+    v[0] += bf16_lo(bb.x);
+    v[1] += bf16_hi(bb.x);
+    v[2] += bf16_lo(bb.y);
+    v[3] += bf16_hi(bb.y);
+  }
+  if (residual != nullptr) {
+    const uint2 rr = *reinterpret_cast<const uint2*>(residual + e);
+    v[0] += bf16_lo(rr.x);
+    v[1] += bf16_hi(rr.x);
+    v[2] += bf16_lo(rr.y);
+    v[3] += bf16_hi(rr.y);
+  }
+  if (gate != nullptr) {
+    const uint2 gg = *reinterpret_cast<const uint2*>(gate + e);
+    const float g[4] = {bf16_lo(gg.x), bf16_hi(gg.x), bf16_lo(gg.y), bf16_hi(gg.y)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = v[i] * (g[i] / (1.0f + expf(-g[i])));
+  }
+  uint2 o;
+  o.x = pack_bf16x2(v[0], v[1]);
+  o.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(Y + e) = o;
+}
+
 }  // namespace aoto
 
 #define AOTO_GEMM_INSTANCE(TN, TM, BIAS, RES, GATE)                                                        \
   extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_n##TN##_m##TM##_b##BIAS##_r##RES##_g##GATE( \
       const uint16_t* X, const uint32_t* words, const uint16_t* scales, const uint16_t* bias,              \
-      const uint16_t* residual, const uint16_t* gate, uint16_t* Y, int M, int N, int K, int group) {       \
-    aoto::w4_gemm_body<TN, TM, BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K, group); \
+      const uint16_t* residual, const uint16_t* gate, uint16_t* Y, int M, int N, int K, int group,          \
+      int kslice, float* partials) {                                                                        \
+    aoto::w4_gemm_body<TN, TM, BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K, group,  \
+                                                kslice, partials);                                          \
   }
 
 #define AOTO_GEMM_EPILOGUES(TN, TM)      \

@@ -166,6 +166,8 @@ def w4_matmul(
     gate: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
     tile: int = 0,
+    splits: int = 0,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Prefill W4 matmul ``[M, K] -> [M, N]`` on MFMA with one fused epilogue.
 
@@ -196,13 +198,22 @@ def w4_matmul(
         if out.numel() != m * n:
             raise ValueError(f"out has {out.numel()} elements, expected {m * n}")
     _ready(x)
+    need = gemm_workspace_bytes(m, n, k, tile, splits)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
     _lib.check(
         _lib.library().aoto_hip_w4_gemm(
             _ptr(x), _ptr(packed), _ptr(scales), _ptr(bias), _ptr(residual), _ptr(gate), _ptr(out),
-            m, n, k, group_size, int(tile), _stream(),
+            m, n, k, group_size, int(tile), int(splits), _ptr(workspace if need else None), _stream(),
         )
     )
     return out
+
+
+def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:
+    """Split-K workspace bytes :func:`w4_matmul` needs for this shape (0: no split)."""
+
+    return int(_lib.library().aoto_hip_w4_gemm_workspace(int(m), int(n), int(k), int(tile), int(splits)))
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -33,7 +33,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 4
+#define AOTO_HIP_ABI_VERSION 5
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -96,10 +96,17 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales,
  *   gate     bf16 [M, N]  -> bf16(acc * silu(gate[m][n]))
  * Limits: K % 64 == 0, N % 16 == 0, group % 32 == 0 dividing K. x 16-byte and
  * y/bias/residual/gate 8-byte aligned. tile: 0 chooses, else 14/18/24/28 (n
- * tiles x m tiles of 16 per wave). */
+ * tiles x m tiles of 16 per wave). splits: 0 chooses (small grids split the
+ * reduction), else the split-K count; a split launch stores f32 partial tiles
+ * in `workspace` (aoto_hip_w4_gemm_workspace() bytes, 16-byte aligned) and a
+ * second launch sums them and applies the epilogue. y must not alias x. */
 int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
                      const void* residual, const void* gate, void* y, int M, int N, int K, int group,
-                     int tile, void* stream);
+                     int tile, int splits, void* workspace, void* stream);
+
+/* Bytes of split-K workspace aoto_hip_w4_gemm needs for these arguments (0 when
+ * it does not split). */
+size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits);
 
 /* Row RMSNorm, out = bf16((x * rsqrt(mean(x^2) + eps)) * weight) over [rows, hidden]
  * (codegen/norm.py:75-323, _compile_normalization(kind="rms_norm");
