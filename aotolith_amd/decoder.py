@@ -1016,11 +1016,11 @@ class DecoderBucketedRuntime:
         return logits, bucket.pad_cache(compact)
 
     def greedy_generate(self, input_ids, *, max_new_tokens: int | None = None, sync_each_step: bool = False,
-                        use_graph: bool = True) -> torch.Tensor:
+                        use_graph: bool = True, events: dict | None = None) -> torch.Tensor:
         ids = _as_ids(input_ids, self.buckets[0].engine.device)
         bucket = self.bucket_for(int(ids.shape[1]))
         return bucket.greedy_generate(ids, max_new_tokens=max_new_tokens, sync_each_step=sync_each_step,
-                                      use_graph=use_graph)
+                                      use_graph=use_graph, events=events)
 
     def save(self, prefix):
         from .artifact import save_runtime

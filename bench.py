@@ -108,7 +108,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: f
     del words, scales
     torch.cuda.empty_cache()
     return {
-        "kernel": "aoto_w4_gemv (LM head 151936x896, g64, RMSNorm prologue)",
+        "kernel": f"aoto_w4_gemv (LM head {n}x{k}, g64, RMSNorm prologue)",
         "bytes_per_launch": per,
         "avg_us": avg_us,
         "achieved": achieved,
@@ -205,6 +205,55 @@ def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
     }
 
 
+def run_llama8b(args, torch, ops) -> dict:
+    """Config 5: Llama-3-8B shape, buckets {512, 2048}, 256 greedy tokens (one GPU)."""
+
+    from aotolith_amd.decoder import compile_decoder_bucketed_state, random_state
+
+    spec = llama8b_spec()
+    print("[bench] building the random-init Llama-3-8B-shape W4 state", file=sys.stderr, flush=True)
+    state = random_state(spec, 64, seed=0)
+    new = 256
+    runtime = compile_decoder_bucketed_state(spec, state, prompt_lengths=[512, 2048], max_new_tokens=new)
+    gen = torch.Generator().manual_seed(0)
+    out = {}
+    for bucket in (512, 2048):
+        prompt = torch.randint(0, spec.vocab, (1, bucket), generator=gen).cuda()
+        for _ in range(max(1, args.warmup)):
+            runtime.greedy_generate(prompt, max_new_tokens=8)
+        torch.cuda.synchronize()
+        records = []
+        for _ in range(max(1, args.steps // 5)):
+            events: dict = {}
+            runtime.greedy_generate(prompt, events=events)
+            records.append(events)
+        torch.cuda.synchronize()
+        prefill_ms = sum(e["start"].elapsed_time(e["prefill"]) for e in records) / len(records)
+        decode_ms = sum(e["prefill"].elapsed_time(e["end"]) for e in records) / len(records)
+        out[f"bucket_{bucket}"] = {
+            "prefill_tok_s": round(bucket / (prefill_ms / 1000.0), 1),
+            "prefill_gemm_tflops": round(2 * bucket * llama_params(spec) / (prefill_ms / 1000.0) / 1e12, 1),
+            "decode_tok_s": round((new - 1) / (decode_ms / 1000.0), 2),
+            "decode_ms_per_token": round(decode_ms / (new - 1), 4),
+            "decode_weight_stream_gbs": round(step_weight_bytes(spec) * (new - 1) / (decode_ms / 1000.0) / 1e9, 1),
+            "generations": len(records),
+        }
+        print(f"[bench] llama8b bucket {bucket}: {out[f'bucket_{bucket}']}", file=sys.stderr, flush=True)
+    if not args.no_roofline:
+        lm = measure_lm_head_gemv(spec, torch, ops, launches=50, pool_bytes=1.5e9)
+        out["lm_head_gemv"] = {"avg_us": round(lm["avg_us"], 2), "achieved_gbs": round(lm["achieved"], 1),
+                               "frac": round(lm["achieved"] / HBM_PEAK_GBS, 4), "bytes": lm["bytes_per_launch"]}
+    return out
+
+
+def llama_params(spec) -> int:
+    """Weight elements of the projections (the prefill GEMM work is 2 * tokens * this)."""
+
+    h, i = spec.hidden, spec.intermediate
+    per_layer = spec.qkv_width * h + h * spec.attention_width + 2 * i * h + h * i
+    return spec.layers * per_layer
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -215,6 +264,7 @@ def main() -> int:
     parser.add_argument("--cpu-decode-steps", type=int, default=8)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-roofline", action="store_true")
+    parser.add_argument("--workload", choices=("qwen0.5b", "llama8b"), default="qwen0.5b")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this one-GPU path "
@@ -227,6 +277,11 @@ def main() -> int:
     from aotolith_amd.decoder import compile_decoder_state, random_state
 
     torch.cuda.set_device(0)
+    if args.workload == "llama8b":
+        result = run_llama8b(args, torch, ops)
+        print(json.dumps({"workload": "llama-3-8b-shape W4g64 buckets {512, 2048}, 256 greedy tokens, bs1",
+                          "data": "synthetic random-init", **result}), flush=True)
+        return 0
     spec = qwen_spec()
     print(f"[bench] building the random-init W4 state on {torch.cuda.get_device_name(0)}", file=sys.stderr,
           flush=True)

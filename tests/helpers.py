@@ -152,3 +152,28 @@ def first_divergence(tokens, reference, logits_history) -> dict | None:
             return {"step": step, "got": int(a), "want": int(b), "margin": float(top[1] - top[0]),
                     "got_logit": float(logits[a]), "want_logit": float(logits[b])}
     return None
+
+
+def state_to_oracle(state) -> dict:
+    """Download a runtime device state into the oracle's format (same bits)."""
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def f32(t):
+        return t.detach().cpu().float().numpy()
+
+    def pair(w):
+        return (w.packed.cpu().numpy(), bits(w.scales))
+
+    return {
+        "embed": f32(state.embed),
+        "final_norm": f32(state.final_norm),
+        "lm_head": pair(state.lm_head),
+        "layers": [
+            {"qkv": pair(l.qkv), "o": pair(l.o), "gate": pair(l.gate), "up": pair(l.up), "down": pair(l.down),
+             "qkv_bias": None if l.qkv_bias is None else f32(l.qkv_bias), "input_norm": f32(l.input_norm),
+             "post_norm": f32(l.post_norm)}
+            for l in state.layers
+        ],
+    }
