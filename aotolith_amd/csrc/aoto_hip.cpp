@@ -103,19 +103,28 @@ int gemv_blocks_per_cu() {
   static int value = [] {
     const char* env = getenv("AOTO_GEMV_BLOCKS_PER_CU");
     int v = env ? atoi(env) : 0;
-    return v > 0 ? v : 3;
+    return v > 0 ? v : 2;
   }();
   return value;
 }
 
-// Streaming GEMV instance for a reduction length: lanes per row and chunks per lane.
-bool stream_shape(int K, int* lpr, int* cpl) {
+// Streaming GEMV instance for a reduction length: lanes per row and chunks per
+// lane (the paired gate/up form needs two weight sets in registers, so it uses
+// a narrower per-lane share at K = 896).
+bool stream_shape(int K, bool paired, int* lpr, int* cpl) {
   switch (K) {
     // Long reductions (4864, 14336) stay on the block-staged kernel: one x copy
     // per 256-thread block costs less than one per wave there.
-    case 896: *lpr = 4; *cpl = 7; return true;
-    case 4096: *lpr = 16; *cpl = 8; return true;
-    default: return false;
+    case 896:
+      *lpr = paired ? 8 : 4;
+      *cpl = paired ? 4 : 7;
+      return true;
+    case 4096:
+      *lpr = 32;
+      *cpl = 4;
+      return true;
+    default:
+      return false;
   }
 }
 
@@ -235,7 +244,7 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   const unsigned shared = (unsigned)((K / 8) * 16 + (K / 32) * 4);
   int slpr = 0, scpl = 0;
   const bool pow2_group = (group & (group - 1)) == 0;
-  if (lanes_per_row == 0 && pow2_group && stream_shape(K, &slpr, &scpl)) {
+  if (lanes_per_row == 0 && pow2_group && stream_shape(K, paired, &slpr, &scpl)) {
     // Wave-persistent kernel: one wave per tile of 64/lpr rows up to the wave
     // budget (CUs x blocks-per-CU x 4); grids smaller than the CU count use
     // 1-wave blocks so every wave gets its own CU.

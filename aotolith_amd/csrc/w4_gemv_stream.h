@@ -120,7 +120,9 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
 
 // Wave-persistent body: wave w of the grid handles row tiles w, w + waves, ...;
 // a tile is 64/LPR rows, LPR lanes per row, CPL chunks (16 B) per lane.
-template <int LPR, int CPL, int XV, bool NORM, bool PAIRED, bool BIAS>
+// XREG: after staging, each lane copies the x chunks it uses (the same CPL
+// chunks for every row it visits) into registers, so the row loop reads no LDS.
+template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                     const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
                                     const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ norm_w,
@@ -145,48 +147,53 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
 #pragma unroll
   for (int j = 0; j < CPL; ++j) cidx[j] = min(li + LPR * j, nchunks - 1);
 
-  uint4 q[CPL], qn[CPL];
-  uint4 u[PAIRED ? CPL : 1], un[PAIRED ? CPL : 1];
-  float s[CPL], sn[CPL];
-  float us[PAIRED ? CPL : 1], usn[PAIRED ? CPL : 1];
+  // Two register sets, A and B, ping-pong across tiles: the loads for the next
+  // tile go into one set while the other is consumed, so no loaded register is
+  // ever copied (a copy would force a wait on every outstanding load) and scales
+  // stay raw bf16 bits until use (a conversion right after the load would wait
+  // for it). Loads are unconditional: the tile index is clamped and the last,
+  // redundant prefetch is simply not used.
+  struct Regs {
+    uint4 q[CPL];
+    uint4 u[PAIRED ? CPL : 1];
+    uint32_t s[CPL];
+    uint32_t us[PAIRED ? CPL : 1];
+  };
+  Regs ra, rb;
 
-  auto load = [&](int tile, uint4* qq, float* ss, uint4* uu, float* uss) {
-    const int row = min(tile * RPW + rsub, N - 1);
+  auto load = [&](int tile, Regs& r) {
+    const int row = min(min(tile, tiles - 1) * RPW + rsub, N - 1);
     const uint4* wrow = words + (size_t)row * nchunks;
     const uint16_t* srow = scales + (size_t)row * ngroups;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) qq[j] = wrow[cidx[j]];
+    for (int j = 0; j < CPL; ++j) r.q[j] = wrow[cidx[j]];
     if (PAIRED) {
       const uint4* urow = up_words + (size_t)row * nchunks;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) uu[j] = urow[cidx[j]];
+      for (int j = 0; j < CPL; ++j) r.u[j] = urow[cidx[j]];
     }
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) ss[j] = bf16_to_f32(srow[cidx[j] >> group_shift]);
+    for (int j = 0; j < CPL; ++j) r.s[j] = srow[cidx[j] >> group_shift];
     if (PAIRED) {
       const uint16_t* usrow = up_scales + (size_t)row * ngroups;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) uss[j] = bf16_to_f32(usrow[cidx[j] >> group_shift]);
+      for (int j = 0; j < CPL; ++j) r.us[j] = usrow[cidx[j] >> group_shift];
     }
   };
 
-  int tile = blockIdx.x * waves_per_block + wave;
-  if (tile >= tiles) return;
-  load(tile, q, s, u, us);
-  stage_activation_wave<NORM, XV>(x, norm_w, eps, K, xp, csum);
+  uint4 xr[XREG ? CPL : 1][4];
+  float cr[XREG ? CPL : 1];
 
-  for (; tile < tiles; tile += total_waves) {
-    const int next = tile + total_waves;
-    if (next < tiles) load(next, qn, sn, un, usn);
+  auto consume = [&](int tile, const Regs& r) {
     float total = 0.f, total_up = 0.f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = li + LPR * j;
       if (c < nchunks) {
-        const uint4* xc = xp + c * 4;
-        const float corr = 136.f * csum[c];
-        total = fmaf(chunk_dot_fast(q[j], xc) - corr, s[j], total);
-        if (PAIRED) total_up = fmaf(chunk_dot_fast(u[j], xc) - corr, us[j], total_up);
+        const uint4* xc = XREG ? xr[j] : xp + c * 4;
+        const float corr = XREG ? cr[j] : 136.f * csum[c];
+        total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, bf16_to_f32(r.s[j]), total);
+        if (PAIRED) total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, bf16_to_f32(r.us[j]), total_up);
       }
     }
     total = group_sum<LPR>(total);
@@ -204,37 +211,55 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
       }
       y[row] = (uint16_t)f32_to_bf16(out);
     }
+  };
+
+  int tile = blockIdx.x * waves_per_block + wave;
+  if (tile >= tiles) return;
+  load(tile, ra);
+  stage_activation_wave<NORM, XV>(x, norm_w, eps, K, xp, csum);
+  if (XREG) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      q[j] = qn[j];
-      s[j] = sn[j];
-      if (PAIRED) {
-        u[j] = un[j];
-        us[j] = usn[j];
-      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xr[j][k] = xp[cidx[j] * 4 + k];
+      cr[j] = 136.f * csum[cidx[j]];
     }
+  }
+  while (true) {
+    load(tile + total_waves, rb);
+    consume(tile, ra);
+    tile += total_waves;
+    if (tile >= tiles) break;
+    load(tile + total_waves, ra);
+    consume(tile, rb);
+    tile += total_waves;
+    if (tile >= tiles) break;
   }
 }
 
 }  // namespace aoto
 
-#define AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, NORM, PAIRED, BIAS)                                      \
+#define AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, NORM, PAIRED, BIAS)                                \
   extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void                                       \
       aoto_w4_gemv_s##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS(                                       \
           const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,           \
           const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias,             \
           float alpha, float beta, uint16_t* y, int K, int N, int group_shift) {                         \
-    aoto::w4_gemv_stream_body<LPR, CPL, XV, NORM, PAIRED, BIAS>(x, words, scales, up_words, up_scales,   \
+    aoto::w4_gemv_stream_body<LPR, CPL, XV, XREG, NORM, PAIRED, BIAS>(x, words, scales, up_words,       \
+                                                                       up_scales,                       \
                                                             norm_w, eps, bias, alpha, beta, y, K, N,     \
                                                             group_shift);                                \
   }
 
 // The decode variants a decoder layer uses: q/k/v (norm, +bias or not), o and
 // down (+residual), paired gate/up (norm), LM head (norm), plain.
-#define AOTO_GEMV_STREAM_SHAPE(LPR, CPL, XV)          \
-  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 1, 0, 1)    \
-  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 1, 0, 0)    \
-  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 0, 0, 1)    \
-  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 1, 1, 0)    \
-  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 0, 1, 0)    \
-  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, 0, 0, 0)
+// Single-projection variants (q/k/v with or without bias, o/down residual, LM
+// head, plain) and the paired gate/up variants of one lane layout.
+#define AOTO_GEMV_STREAM_SINGLE(LPR, CPL, XV, XREG)          \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 1, 0, 1)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 1, 0, 0)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 0, 0, 1)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 0, 0, 0)
+#define AOTO_GEMV_STREAM_PAIRED(LPR, CPL, XV, XREG)          \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 1, 1, 0)    \
+  AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 0, 1, 0)
