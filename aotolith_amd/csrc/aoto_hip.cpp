@@ -108,22 +108,37 @@ int gemv_blocks_per_cu() {
   return value;
 }
 
-// Streaming GEMV instance for a reduction length: lanes per row and chunks per
-// lane (the paired gate/up form needs two weight sets in registers, so it uses
-// a narrower per-lane share at K = 896).
-bool stream_shape(int K, bool paired, int* lpr, int* cpl) {
+// Streaming GEMV instance for a reduction length and output count: lanes per
+// row, chunks per lane, and whether each lane loads its own x chunks (direct,
+// no LDS) or the wave stages x into LDS first. Short outputs (a decoder
+// layer's projections) are latency-bound and get 32-64 lanes per row with
+// direct x loads; long outputs (LM heads) get few lanes per row and one staged
+// copy of x per wave. The paired gate/up form needs two weight sets in
+// registers, so it uses a narrower per-lane share at K = 896.
+// Must agree with the instances in kernels.hip.
+struct StreamShape {
+  int lpr, cpl;
+  bool direct;
+};
+
+bool stream_shape(int K, int N, bool paired, StreamShape* s) {
+  const bool short_out = N <= 8192;
   switch (K) {
-    // Long reductions (4864, 14336) stay on the block-staged kernel: one x copy
-    // per 256-thread block costs less than one per wave there.
     case 896:
-      *lpr = paired ? 8 : 4;
-      *cpl = paired ? 4 : 7;
+      if (short_out)
+        *s = {32, 1, true};
+      else
+        *s = paired ? StreamShape{8, 4, false} : StreamShape{4, 7, false};
       return true;
     case 4096:
-      *lpr = 32;
-      *cpl = 4;
+      *s = {32, 4, false};
+      return true;
+    case 4864:
+      if (paired || !short_out) return false;
+      *s = {64, 3, true};
       return true;
     default:
+      // Other reductions (14336 ...) use the block-staged kernel.
       return false;
   }
 }
@@ -242,9 +257,10 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   const int norm = norm_weight != nullptr;
   const int has_bias = bias != nullptr;
   const unsigned shared = (unsigned)((K / 8) * 16 + (K / 32) * 4);
-  int slpr = 0, scpl = 0;
+  StreamShape ss{};
   const bool pow2_group = (group & (group - 1)) == 0;
-  if (lanes_per_row == 0 && pow2_group && stream_shape(K, paired, &slpr, &scpl)) {
+  if (lanes_per_row == 0 && pow2_group && stream_shape(K, N, paired, &ss)) {
+    const int slpr = ss.lpr, scpl = ss.cpl;
     // Wave-persistent kernel: one wave per tile of 64/lpr rows up to the wave
     // budget (CUs x blocks-per-CU x 4); grids smaller than the CU count use
     // 1-wave blocks so every wave gets its own CU.
@@ -253,7 +269,8 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
     const long long waves = tiles < budget ? tiles : budget;
     const int wpb = waves <= cu_count() ? 1 : 4;
     const long long grid = (waves + wpb - 1) / wpb;
-    const unsigned region = (unsigned)((K / 8) * 16 + ((K / 32 + 3) / 4) * 16);
+    // Direct instances read no LDS; staged ones need one region per wave.
+    const unsigned region = ss.direct ? 0u : (unsigned)((K / 8) * 16 + ((K / 32 + 3) / 4) * 16);
     int shift = 0;
     while ((32 << shift) < group) ++shift;
     char sname[64];

@@ -37,25 +37,65 @@ AOTO_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
 }
 
-// Sum over the `width` lanes of an aligned lane group (width a power of two <= 64).
+// Cross-lane moves inside 16-lane rows through DPP (a VALU operand modifier, no
+// LDS round trip): quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (quads 0<->1 of each 8), row_mirror (halves of each 16).
+template <int CTRL>
+AOTO_DEVICE float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// Sum over the `WIDTH` lanes of an aligned lane group (WIDTH a power of two <=
+// 64); every lane of the group gets the total. Up to 16 lanes it is four DPP
+// steps; wider groups add ds_swizzle-free cross-row steps through __shfl_xor.
 template <int WIDTH>
 AOTO_DEVICE float group_sum(float value) {
-#pragma unroll
-  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) value += __shfl_xor(value, offset, 64);
+  if (WIDTH >= 2) value += dpp_move<kDppXor1>(value);
+  if (WIDTH >= 4) value += dpp_move<kDppXor2>(value);
+  if (WIDTH >= 8) value += dpp_move<kDppHalfMirror>(value);
+  if (WIDTH >= 16) value += dpp_move<kDppMirror>(value);
+  if (WIDTH >= 32) value += __shfl_xor(value, 16, 64);
+  if (WIDTH >= 64) value += __shfl_xor(value, 32, 64);
   return value;
 }
 
 template <int WIDTH>
 AOTO_DEVICE float group_max(float value) {
-#pragma unroll
-  for (int offset = WIDTH / 2; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset, 64));
+  if (WIDTH >= 2) value = fmaxf(value, dpp_move<kDppXor1>(value));
+  if (WIDTH >= 4) value = fmaxf(value, dpp_move<kDppXor2>(value));
+  if (WIDTH >= 8) value = fmaxf(value, dpp_move<kDppHalfMirror>(value));
+  if (WIDTH >= 16) value = fmaxf(value, dpp_move<kDppMirror>(value));
+  if (WIDTH >= 32) value = fmaxf(value, __shfl_xor(value, 16, 64));
+  if (WIDTH >= 64) value = fmaxf(value, __shfl_xor(value, 32, 64));
   return value;
+}
+
+// Whole-wave sum / max returned uniformly: DPP within the four 16-lane rows,
+// then the four row results read with v_readlane.
+AOTO_DEVICE float wave_sum(float value) {
+  value = group_sum<16>(value);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 16)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 32)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 48));
+}
+
+AOTO_DEVICE float wave_max(float value) {
+  value = group_max<16>(value);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 0)),
+                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 32)),
+                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 48))));
 }
 
 // Block-wide sum for blocks of up to 1024 threads; every thread gets the total.
 // `scratch` needs one float per wave. Contains a barrier: call from all threads.
 AOTO_DEVICE float block_sum(float value, float* scratch) {
-  value = group_sum<64>(value);
+  value = wave_sum(value);
   const int wave = threadIdx.x >> 6;
   const int waves = (blockDim.x + 63) >> 6;
   if ((threadIdx.x & 63) == 0) scratch[wave] = value;

@@ -136,7 +136,7 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   constexpr int PAIRS = D / 2;            // bf16 pairs per row
   constexpr int KG = THREADS / PAIRS;     // key groups in P.V
   constexpr int VPT = KPP / KG;           // value pairs per thread (all loaded up front)
-  __shared__ float s_p[KPP];
+  __shared__ __attribute__((aligned(16))) float s_p[KPP];
   __shared__ float s_red[THREADS / 64];
   __shared__ float s_acc[KG][D];
   __shared__ __attribute__((aligned(16))) float s_q[D];
@@ -160,7 +160,26 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   uint16_t* kh = kbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
   uint16_t* vh = vbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
 
-  // Every K and V load of the block is independent of the query: issue them all first.
+  // Loads, in the order their results are needed (vmcnt retires in order): the
+  // query/new-key inputs first, then every K and V row of the block.
+  const int d = min((int)threadIdx.x, D - 1);
+  uint32_t qx = 0, qp = 0, kx = 0, kp = 0, cs = 0, sn = 0, vx = 0;
+  const int half = D / 2;
+  const int pd = d < half ? d + half : d - half;
+  if (FUSED) {
+    const uint16_t* rrow = row + (size_t)b * row_width;
+    const uint16_t* qh = rrow + query_start + (size_t)h * D;
+    const uint16_t* khh = rrow + key_start + (size_t)kvh * D;
+    qx = qh[d];
+    qp = qh[pd];
+    kx = khh[d];
+    kp = khh[pd];
+    cs = cos_table[(size_t)position * D + d];
+    sn = sin_table[(size_t)position * D + d];
+    vx = rrow[value_start + (size_t)kvh * D + d];
+  } else {
+    qx = q[((size_t)b * query_heads + h) * D + d];
+  }
   const int ksl = s0 + min(kl, max(n - 1, 0));
   uint4 kv[8];
   {
@@ -168,25 +187,26 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
 #pragma unroll
     for (int c = 0; c < 8; ++c) kv[c] = kr[sub * 8 + c];
   }
+  // P.V work split: thread (kg, d2) owns dims (2*d2, 2*d2+1) of keys
+  // [kg*VPT, (kg+1)*VPT), so its probabilities are one contiguous LDS run.
+  const int kbase0 = kg * VPT;
   uint32_t vv[VPT];
 #pragma unroll
   for (int u = 0; u < VPT; ++u) {
-    const int sl = s0 + min(kg + u * KG, max(n - 1, 0));
+    const int sl = s0 + min(kbase0 + u, max(n - 1, 0));
     vv[u] = reinterpret_cast<const uint32_t*>(vh + (size_t)sl * D)[d2];
   }
 
   // Query (rotated out of the projection row when FUSED) into LDS, f32.
   if (threadIdx.x < D) {
-    const int d = threadIdx.x;
     if (FUSED) {
-      const uint16_t* rrow = row + (size_t)b * row_width;
-      const uint16_t* cos_row = cos_table + (size_t)position * D;
-      const uint16_t* sin_row = sin_table + (size_t)position * D;
-      s_q[d] = round_bf16(rope_value(rrow + query_start + (size_t)h * D, cos_row, sin_row, d, D / 2));
-      s_knew[d] = (uint16_t)f32_to_bf16(rope_value(rrow + key_start + (size_t)kvh * D, cos_row, sin_row, d, D / 2));
-      s_vnew[d] = rrow[value_start + (size_t)kvh * D + d];
+      const float sign = d < half ? -1.f : 1.f;
+      const float c = bf16_to_f32(cs), sv = bf16_to_f32(sn);
+      s_q[d] = round_bf16(bf16_to_f32(qx) * c + sign * bf16_to_f32(qp) * sv);
+      s_knew[d] = (uint16_t)f32_to_bf16(bf16_to_f32(kx) * c + sign * bf16_to_f32(kp) * sv);
+      s_vnew[d] = (uint16_t)vx;
     } else {
-      s_q[d] = bf16_to_f32(q[((size_t)b * query_heads + h) * D + d]);
+      s_q[d] = bf16_to_f32(qx);
     }
   }
   __syncthreads();
@@ -197,7 +217,7 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   if (FUSED) {
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
-      const int sl = s0 + min(kg + u * KG, max(n - 1, 0));
+      const int sl = s0 + min(kbase0 + u, max(n - 1, 0));
       if (sl == slot) vv[u] = reinterpret_cast<const uint32_t*>(s_vnew)[d2];
     }
   }
@@ -225,24 +245,27 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
     dot = fmaf(qb.z, bf16_lo(a[3]), dot);
     dot = fmaf(qb.w, bf16_hi(a[3]), dot);
   }
-  if (LPK == 2) dot += __shfl_xor(dot, 1, 64);
+  if (LPK == 2) dot += dpp_move<kDppXor1>(dot);
   float sc = -INFINITY;
   if (kl < n && kept(ksl)) sc = dot * scale;
   if (sub == 0 && kl < n) s_p[kl] = sc;
-  float m = group_max<64>(sc);
+  const float m = wave_max(sc);
   if (lane == 0) s_red[wave] = m;
   __syncthreads();
   float row_max = s_red[0];
 #pragma unroll
   for (int w = 1; w < THREADS / 64; ++w) row_max = fmaxf(row_max, s_red[w]);
   __syncthreads();  // s_red is reused below
+  // Probabilities; slots past the range read as 0 in P.V.
   float p_local = 0.f;
-  if (threadIdx.x < n) {
-    const float v = s_p[threadIdx.x];
-    p_local = (row_max == -INFINITY || v == -INFINITY) ? 0.f : expf(v - row_max);
+  if (threadIdx.x < KPP) {
+    if (threadIdx.x < n) {
+      const float v = s_p[threadIdx.x];
+      p_local = (row_max == -INFINITY || v == -INFINITY) ? 0.f : expf(v - row_max);
+    }
     s_p[threadIdx.x] = p_local;
   }
-  const float t = group_sum<64>(p_local);
+  const float t = wave_sum(p_local);
   if (lane == 0) s_red[wave] = t;
   __syncthreads();
   float row_sum = 0.f;
@@ -251,13 +274,15 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
 
   // P.V over this thread's keys and dim pair.
   float a0 = 0.f, a1 = 0.f;
+  const float4* pv4 = reinterpret_cast<const float4*>(s_p + kbase0);
 #pragma unroll
-  for (int u = 0; u < VPT; ++u) {
-    const int i = kg + u * KG;
-    if (i < n) {
-      const float pr = s_p[i];
-      a0 = fmaf(pr, bf16_lo(vv[u]), a0);
-      a1 = fmaf(pr, bf16_hi(vv[u]), a1);
+  for (int u4 = 0; u4 < VPT / 4; ++u4) {
+    const float4 pr = pv4[u4];
+    const float pp[4] = {pr.x, pr.y, pr.z, pr.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a0 = fmaf(pp[e], bf16_lo(vv[u4 * 4 + e]), a0);
+      a1 = fmaf(pp[e], bf16_hi(vv[u4 * 4 + e]), a1);
     }
   }
   s_acc[kg][2 * d2] = a0;
@@ -268,7 +293,6 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
     vh[(size_t)slot * D + threadIdx.x] = s_vnew[threadIdx.x];
   }
   if (threadIdx.x < D) {
-    const int d = threadIdx.x;
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < KG; ++g) acc += s_acc[g][d];

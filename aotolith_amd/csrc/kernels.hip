@@ -18,12 +18,17 @@ AOTO_GEMV_LPR(0, 1, 0)
 AOTO_GEMV_LPR(1, 1, 0)
 
 // Wave-persistent streaming W4 GEMV: {lanes per row} x {chunks per lane} x
-// {x vectors each lane stages, ceil(K / 512)} x {x held in registers}.
-// K = 896: 4x7 single (x in 112 registers), 8x4 paired; K = 4096: 32x4.
+// {x vectors each lane stages, ceil(K / 512); 0 = each lane loads its own
+// chunks directly} x {x held in registers}.
+// K = 896: 4x7 single (x in 112 registers) for long outputs, 32x1 direct for
+// short ones (single and paired), 8x4 paired; K = 4096: 32x4; K = 4864: 64x3 direct.
 AOTO_GEMV_STREAM_SINGLE(4, 7, 2, true)
 AOTO_GEMV_STREAM_PAIRED(8, 4, 2, true)
+AOTO_GEMV_STREAM_SINGLE(32, 1, 0, true)
+AOTO_GEMV_STREAM_PAIRED(32, 1, 0, true)
 AOTO_GEMV_STREAM_SINGLE(32, 4, 8, true)
 AOTO_GEMV_STREAM_PAIRED(32, 4, 8, true)
+AOTO_GEMV_STREAM_SINGLE(64, 3, 0, true)
 
 // Prefill W4 GEMM: {n tiles per wave} x {m tiles per wave} x epilogue.
 AOTO_GEMM_EPILOGUES(1, 4)

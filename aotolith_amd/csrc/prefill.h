@@ -31,7 +31,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rms_norm(const uint16_t* 
       ss = fmaf(b, b, ss);
     }
   }
-  ss = group_sum<64>(ss);
+  ss = wave_sum(ss);
   const float ns = 1.0f / sqrtf(ss / (float)H + eps);
   for (int c = lane; c < vecs; c += 64) {
     const uint4 r = xv[c];

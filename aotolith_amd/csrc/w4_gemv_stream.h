@@ -82,7 +82,7 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
         }
       }
     }
-    ss = group_sum<64>(ss);
+    ss = wave_sum(ss);
     ns = 1.0f / sqrtf(ss / (float)K + eps);
   }
 #pragma unroll
@@ -118,10 +118,83 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Direct staging for the latency-bound shapes: the LPR lanes of a row group hold,
+// between them, every chunk of x (chunk li + LPR*j), so each lane loads just its
+// own chunks (and the norm weight's) from global memory, the RMS statistic is a
+// group sum over the LPR lanes, and the normalized pairs go straight into
+// registers - no LDS and no wave-wide staging loop.
+template <int LPR, int CPL, bool NORM>
+AOTO_DEVICE void stage_activation_direct(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+                                         float eps, int K, int li, uint4 (&xr)[CPL][4], float (&cr)[CPL]) {
+  const int nchunks = K >> 5;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
+  uint4 raw[CPL][4], wraw[NORM ? CPL : 1][4];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = min(li + LPR * j, nchunks - 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) raw[j][k] = xv[c * 4 + k];
+    if (NORM) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wraw[j][k] = wv[c * 4 + k];
+    }
+  }
+  float ns = 1.f;
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (li + LPR * j < nchunks) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float a = bf16_lo(r4[i]), b = bf16_hi(r4[i]);
+            ss = fmaf(a, a, ss);
+            ss = fmaf(b, b, ss);
+          }
+        }
+      }
+    }
+    ss = group_sum<LPR>(ss);
+    ns = 1.0f / sqrtf(ss / (float)K + eps);
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[2 * i] = bf16_lo(r4[i]);
+        e[2 * i + 1] = bf16_hi(r4[i]);
+      }
+      if (NORM) {
+        const uint32_t w4[4] = {wraw[j][k].x, wraw[j][k].y, wraw[j][k].z, wraw[j][k].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          e[2 * i] = round_bf16((ns * e[2 * i]) * bf16_lo(w4[i]));
+          e[2 * i + 1] = round_bf16((ns * e[2 * i + 1]) * bf16_hi(w4[i]));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sum += e[i];
+      xr[j][k] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
+                            pack_bf16x2(e[3], e[7]));
+    }
+    cr[j] = 136.f * sum;
+  }
+}
+
 // Wave-persistent body: wave w of the grid handles row tiles w, w + waves, ...;
 // a tile is 64/LPR rows, LPR lanes per row, CPL chunks (16 B) per lane.
 // XREG: after staging, each lane copies the x chunks it uses (the same CPL
 // chunks for every row it visits) into registers, so the row loop reads no LDS.
+// XV == 0 selects direct staging (stage_activation_direct; implies XREG).
 template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                     const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
@@ -181,8 +254,10 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     }
   };
 
-  uint4 xr[XREG ? CPL : 1][4];
-  float cr[XREG ? CPL : 1];
+  constexpr bool DIRECT = XV == 0;
+  constexpr bool INREG = XREG || DIRECT;
+  uint4 xr[INREG ? CPL : 1][4];
+  float cr[INREG ? CPL : 1];
 
   auto consume = [&](int tile, const Regs& r) {
     float total = 0.f, total_up = 0.f;
@@ -190,8 +265,8 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     for (int j = 0; j < CPL; ++j) {
       const int c = li + LPR * j;
       if (c < nchunks) {
-        const uint4* xc = XREG ? xr[j] : xp + c * 4;
-        const float corr = XREG ? cr[j] : 136.f * csum[c];
+        const uint4* xc = INREG ? xr[j] : xp + c * 4;
+        const float corr = INREG ? cr[j] : 136.f * csum[c];
         total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, bf16_to_f32(r.s[j]), total);
         if (PAIRED) total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, bf16_to_f32(r.us[j]), total_up);
       }
@@ -216,8 +291,12 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   int tile = blockIdx.x * waves_per_block + wave;
   if (tile >= tiles) return;
   load(tile, ra);
-  stage_activation_wave<NORM, XV>(x, norm_w, eps, K, xp, csum);
-  if (XREG) {
+  if (DIRECT) {
+    if constexpr (DIRECT) stage_activation_direct<LPR, CPL, NORM>(x, norm_w, eps, K, li, xr, cr);
+  } else {
+    stage_activation_wave<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
+  }
+  if (XREG && !DIRECT) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
 #pragma unroll

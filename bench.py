@@ -117,6 +117,23 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: f
     }
 
 
+def counter_traffic() -> int | None:
+    """HBM bytes per LM-head GEMV launch from the committed counter summary, or None.
+
+    The figure comes from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of
+    ``bench.py --roofline-only``, calibrated on a copy of known size; the
+    summary file records the commands and the raw counts.
+    """
+
+    path = os.path.join(ROOT, "profiles", "lm_head_gemv_qwen05b_traffic.md")
+    try:
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return int(json.loads(block)["traffic_bytes"])
+    except (OSError, IndexError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
     """Time the CPU oracle on the same state and prompt: prefill + ``decode_steps`` decode steps."""
 
@@ -265,6 +282,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-roofline", action="store_true")
     parser.add_argument("--workload", choices=("qwen0.5b", "llama8b"), default="qwen0.5b")
+    parser.add_argument("--roofline-only", action="store_true",
+                        help="only the LM-head GEMV loop, after a calibration copy of 256 MiB (for counter runs)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this one-GPU path "
@@ -277,6 +296,16 @@ def main() -> int:
     from aotolith_amd.decoder import compile_decoder_state, random_state
 
     torch.cuda.set_device(0)
+    if args.roofline_only:
+        spec = qwen_spec() if args.workload == "qwen0.5b" else llama8b_spec()
+        src = torch.empty(1 << 26, dtype=torch.int32, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        lm = measure_lm_head_gemv(spec, torch, ops, launches=20)
+        print(json.dumps({"calibration_copy_bytes": src.numel() * 4, **lm}), flush=True)
+        return 0
     if args.workload == "llama8b":
         result = run_llama8b(args, torch, ops)
         print(json.dumps({"workload": "llama-3-8b-shape W4g64 buckets {512, 2048}, 256 greedy tokens, bs1",
@@ -333,7 +362,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(lm["achieved"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": counter_traffic(),
             "kernel": lm["kernel"],
             "avg_us": round(lm["avg_us"], 3),
             "bytes_per_launch": lm["bytes_per_launch"],

@@ -160,6 +160,9 @@ STREAM_SHAPES = [
     (151936 // 8, 896),  # LM-head rows (an eighth of the vocabulary), K = 896
     (1000, 896),          # rows not a multiple of the 64-row tile
     (3, 896),             # fewer rows than one tile
+    (1152, 896),          # Qwen qkv (direct x loads, 32 lanes per row)
+    (4864, 896),          # Qwen gate/up (paired direct form)
+    (8193, 896),          # first output count past the direct-form limit
     (896, 4864),          # Qwen down projection
     (1024, 4096),         # Llama-8B K = 4096
     (512, 14336),         # Llama-8B down projection K
