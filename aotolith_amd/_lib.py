@@ -70,10 +70,14 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "aoto_hip_embedding": (_p, _p, _c_int, _c_int, _i64, _p, _p, _p),
     "aoto_hip_argmax": (_p, _c_int, _c_int, _i64, _p, _p, _p, _p),
+    "aoto_hip_w4_gemv_argmax_keys": (_c_int, _c_int, _c_int),
+    "aoto_hip_w4_gemv_argmax": (_p, _p, _p, _p, _c_float, _p, _c_int, _c_int, _c_int, _p, _c_size, _p),
+    "aoto_hip_argmax_finish": (_p, _c_int, _p, _p, _p, _p, _c_int, _p, _i64, _c_int, _p, _p, _p),
 }
 
 #: Entry points returning a size rather than a status.
-SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_decode_attention_workspace", "aoto_hip_w4_gemm_workspace"}
+SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_decode_attention_workspace", "aoto_hip_w4_gemm_workspace",
+                  "aoto_hip_w4_gemv_argmax_keys"}
 
 
 class HipBackendUnavailable(RuntimeError):

@@ -81,6 +81,7 @@ int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* strea
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 // Compute units of the current device (cached per device).
@@ -98,14 +99,14 @@ int cu_count() {
   return n;
 }
 
-// Persistent GEMV blocks per CU (AOTO_GEMV_BLOCKS_PER_CU overrides; read once).
-int gemv_blocks_per_cu() {
+// Persistent GEMV blocks per CU: the shape's own default unless
+// AOTO_GEMV_BLOCKS_PER_CU overrides it (read once).
+int gemv_blocks_per_cu(int shape_default) {
   static int value = [] {
     const char* env = getenv("AOTO_GEMV_BLOCKS_PER_CU");
-    int v = env ? atoi(env) : 0;
-    return v > 0 ? v : 2;
+    return env ? atoi(env) : 0;
   }();
-  return value;
+  return value > 0 ? value : shape_default;
 }
 
 // Streaming GEMV instance for a reduction length and output count: lanes per
@@ -119,16 +120,20 @@ int gemv_blocks_per_cu() {
 struct StreamShape {
   int lpr, cpl;
   bool direct;
+  int blocks_per_cu = 2;  // persistent 4-wave blocks per CU
 };
 
 bool stream_shape(int K, int N, bool paired, StreamShape* s) {
   const bool short_out = N <= 8192;
   switch (K) {
     case 896:
+      // Long outputs: 8 lanes x 4 chunks (32 slots for the 28 chunks of a row;
+      // the 4 spare slots repeat the last chunk), x read from LDS so the two
+      // weight register sets fit at 5 waves per SIMD, 3 blocks per CU.
       if (short_out)
         *s = {32, 1, true};
       else
-        *s = paired ? StreamShape{8, 4, false} : StreamShape{4, 7, false};
+        *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 3};
       return true;
     case 4096:
       *s = {32, 4, false};
@@ -141,6 +146,48 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s) {
       // Other reductions (14336 ...) use the block-staged kernel.
       return false;
   }
+}
+
+// Launch geometry of a streaming GEMV: one wave per tile of 64/lpr rows up to
+// the wave budget (CUs x blocks-per-CU x 4); grids no larger than the CU count
+// use 1-wave blocks so every wave gets its own CU.
+struct StreamLaunch {
+  long long grid;
+  int wpb;
+  unsigned shared;  // LDS bytes per block
+  int shift;        // log2(group / 32)
+};
+
+StreamLaunch stream_launch(const StreamShape& ss, int K, int N, int group) {
+  const long long tiles = ((long long)N + (64 / ss.lpr) - 1) / (64 / ss.lpr);
+  const long long budget = (long long)cu_count() * gemv_blocks_per_cu(ss.blocks_per_cu) * 4;
+  const long long waves = tiles < budget ? tiles : budget;
+  StreamLaunch l{};
+  l.wpb = waves <= cu_count() ? 1 : 4;
+  l.grid = (waves + l.wpb - 1) / l.wpb;
+  // Direct instances read no LDS; staged ones need one region per wave.
+  const unsigned region = ss.direct ? 0u : (unsigned)((K / 8) * 16 + ((K / 32 + 3) / 4) * 16);
+  l.shared = region * l.wpb;
+  while ((32 << l.shift) < group) ++l.shift;
+  return l;
+}
+
+// Lane layout of the LM-head GEMV with fused argmax keys: the streaming shape
+// when there is one, else a direct 64-lane form for K up to 6144.
+bool argmax_shape(int K, int N, int group, StreamShape* s) {
+  if (K % 32 != 0 || group <= 0 || group % 32 != 0 || (group & (group - 1)) != 0 || K % group != 0 ||
+      (K / group) % 2 != 0)
+    return false;
+  if (stream_shape(K, N, false, s) && !(s->direct && s->lpr == 32)) return true;
+  if (K <= 64 * 32) {
+    *s = {64, 1, true};
+    return true;
+  }
+  if (K <= 64 * 3 * 32) {
+    *s = {64, 3, true};
+    return true;
+  }
+  return false;
 }
 
 unsigned blocks_for(long long items, int threads) { return (unsigned)((items + threads - 1) / threads); }
@@ -259,24 +306,17 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   const unsigned shared = (unsigned)((K / 8) * 16 + (K / 32) * 4);
   StreamShape ss{};
   const bool pow2_group = (group & (group - 1)) == 0;
-  if (lanes_per_row == 0 && pow2_group && stream_shape(K, N, paired, &ss)) {
-    const int slpr = ss.lpr, scpl = ss.cpl;
-    // Wave-persistent kernel: one wave per tile of 64/lpr rows up to the wave
-    // budget (CUs x blocks-per-CU x 4); grids smaller than the CU count use
-    // 1-wave blocks so every wave gets its own CU.
-    const long long tiles = ((long long)N + (64 / slpr) - 1) / (64 / slpr);
-    const long long budget = (long long)cu_count() * gemv_blocks_per_cu() * 4;
-    const long long waves = tiles < budget ? tiles : budget;
-    const int wpb = waves <= cu_count() ? 1 : 4;
-    const long long grid = (waves + wpb - 1) / wpb;
-    // Direct instances read no LDS; staged ones need one region per wave.
-    const unsigned region = ss.direct ? 0u : (unsigned)((K / 8) * 16 + ((K / 32 + 3) / 4) * 16);
-    int shift = 0;
-    while ((32 << shift) < group) ++shift;
+  // The streaming form reads scales and bias as aligned 32-bit pairs.
+  const bool pairs_ok = (K / group) % 2 == 0 && aligned4(scales) && (!up_scales || aligned4(up_scales)) &&
+                        (!bias || (N % 2 == 0 && aligned4(bias)));
+  if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss)) {
+    const StreamLaunch l = stream_launch(ss, K, N, group);
     char sname[64];
-    snprintf(sname, sizeof(sname), "aoto_w4_gemv_s%dx%d_n%d_p%d_b%d", slpr, scpl, norm, paired ? 1 : 0, has_bias);
-    return launch(sname, dim3((unsigned)grid), dim3(64 * wpb), region * wpb, stream, x, words, scales, up_words,
-                  up_scales, norm_weight, eps, bias, alpha, beta, y, K, N, shift);
+    snprintf(sname, sizeof(sname), "aoto_w4_gemv_s%dx%d_n%d_p%d_b%d", ss.lpr, ss.cpl, norm, paired ? 1 : 0,
+             has_bias);
+    unsigned long long* no_keys = nullptr;
+    return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, x, words, scales, up_words,
+                  up_scales, norm_weight, eps, bias, alpha, beta, y, K, N, l.shift, l.wpb, no_keys);
   }
   int lpr = lanes_per_row;
   if (lpr == 0) {
@@ -572,6 +612,51 @@ int aoto_hip_embedding(const void* weight, const int64_t* ids, int count, int hi
   long long items = (long long)count * (hidden / 8);
   return launch("aoto_embedding", dim3(blocks_for(items, 256)), dim3(256), 0, stream, weight, ids, count, hidden,
                 (long long)vocab, out, error);
+}
+
+size_t aoto_hip_w4_gemv_argmax_keys(int K, int N, int group) {
+  StreamShape ss{};
+  if (N <= 0 || K <= 0 || !argmax_shape(K, N, group, &ss)) return 0;
+  const StreamLaunch l = stream_launch(ss, K, N, group);
+  return (size_t)(l.grid * l.wpb);
+}
+
+int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* scales, const void* norm_weight,
+                            float eps, void* y, int K, int N, int group, uint64_t* keys, size_t key_count,
+                            void* stream) {
+  if (!x || !words || !scales || !y || !keys) return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: null pointer");
+  if (N <= 0 || K <= 0) return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: empty shape K=%d N=%d", K, N);
+  StreamShape ss{};
+  if (!argmax_shape(K, N, group, &ss))
+    return fail(AOTO_ERR_UNSUPPORTED, "w4_gemv_argmax: needs K %% 32 == 0, a power-of-two group >= 32 with an "
+                "even number of groups per row, K <= 6144 (K=%d group=%d)", K, group);
+  if (!aligned16(x) || !aligned16(words) || (norm_weight && !aligned16(norm_weight)) || !aligned4(scales) ||
+      !aligned8(keys))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: x, words and norm weight must be 16-byte aligned, scales "
+                "4-byte, keys 8-byte");
+  const StreamLaunch l = stream_launch(ss, K, N, group);
+  if (key_count < (size_t)(l.grid * l.wpb))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: %zu keys given, %lld needed (aoto_hip_w4_gemv_argmax_keys)",
+                key_count, l.grid * l.wpb);
+  char sname[64];
+  snprintf(sname, sizeof(sname), "aoto_w4_gemv_s%dx%d_n%d_argmax", ss.lpr, ss.cpl, norm_weight ? 1 : 0);
+  const void* none = nullptr;
+  return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, x, words, scales, none, none,
+                norm_weight, eps, none, 1.0f, 0.0f, y, K, N, l.shift, l.wpb, keys);
+}
+
+int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_out, int64_t* history,
+                           int* history_len, int32_t* step_state, int capacity, const void* embedding,
+                           int64_t embedding_rows, int hidden, void* hidden_out, int* error, void* stream) {
+  if (!keys || !token_out || key_count <= 0) return fail(AOTO_ERR_ARGUMENT, "argmax_finish: bad arguments");
+  if ((history == nullptr) != (history_len == nullptr))
+    return fail(AOTO_ERR_ARGUMENT, "argmax_finish: a token history needs both pointers");
+  if (step_state && capacity <= 0) return fail(AOTO_ERR_ARGUMENT, "argmax_finish: step state needs a capacity");
+  if (embedding && (!hidden_out || hidden <= 0 || hidden % 8 != 0 || embedding_rows <= 0 ||
+                    !aligned16(embedding) || !aligned16(hidden_out)))
+    return fail(AOTO_ERR_ARGUMENT, "argmax_finish: the embedding gather needs 16-byte aligned rows, hidden %% 8 == 0");
+  return launch("aoto_argmax_finish", dim3(1), dim3(256), 0, stream, keys, key_count, token_out, history,
+                history_len, step_state, capacity, embedding, (long long)embedding_rows, hidden, hidden_out, error);
 }
 
 int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,

@@ -92,16 +92,45 @@ AOTO_DEVICE float wave_max(float value) {
                      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), 48))));
 }
 
-// Block-wide sum for blocks of up to 1024 threads; every thread gets the total.
-// `scratch` needs one float per wave. Contains a barrier: call from all threads.
+// Block-wide sum over a block of THREADS threads (a multiple of 64, at most
+// 1024); every thread gets the total. `scratch` needs one float per wave.
+// Contains a barrier: call from all threads. The thread count is a template
+// argument because reading blockDim costs a memory round trip.
+template <int THREADS>
 AOTO_DEVICE float block_sum(float value, float* scratch) {
   value = wave_sum(value);
   const int wave = threadIdx.x >> 6;
-  const int waves = (blockDim.x + 63) >> 6;
+  constexpr int waves = THREADS / 64;
   if ((threadIdx.x & 63) == 0) scratch[wave] = value;
   __syncthreads();
   float total = 0.f;
   for (int w = 0; w < waves; ++w) total += scratch[w];
   __syncthreads();
   return total;
+}
+
+// Order-preserving key of a bf16 value with the index in the low bits so that
+// the maximum key is the largest value and, among equal values, the first index.
+// NaN never wins.
+AOTO_DEVICE unsigned long long argmax_key(uint32_t bits16, int index) {
+  uint32_t u = bits16 & 0xFFFFu;
+  u = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+  if ((bits16 & 0x7FFFu) > 0x7F80u) u = 0;
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)index);
+}
+
+// Index encoded in an argmax key.
+AOTO_DEVICE long long argmax_key_index(unsigned long long key) {
+  return (long long)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+}
+
+AOTO_DEVICE unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+AOTO_DEVICE unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(v, off, 64);
+    v = max_u64(v, o);
+  }
+  return v;
 }

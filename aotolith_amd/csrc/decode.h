@@ -41,7 +41,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
     uint16_t* __restrict__ pair_out, uint16_t* __restrict__ q_out, int batch, int query_heads,
     int kv_heads, int cap, int D, int query_start, int key_start, int value_start, int mode, int slot,
     const int* __restrict__ step) {
-  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long tid = (long long)blockIdx.x * 256 + threadIdx.x;
   const int half = D >> 1;
   if (step != nullptr) {
     position = step[0];
@@ -319,7 +319,7 @@ extern "C" __global__ __launch_bounds__(128) void aoto_decode_attention_merge(co
   const float* rec = partials + (size_t)bh * splits * (D + 2);
   float m = -INFINITY;
   for (int s = 0; s < splits; ++s) m = fmaxf(m, rec[(size_t)s * (D + 2)]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+  for (int d = threadIdx.x; d < D; d += 128) {
     float num = 0.f, den = 0.f;
     if (m != -INFINITY) {
       for (int s = 0; s < splits; ++s) {
@@ -342,7 +342,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_embedding(
     const uint16_t* __restrict__ weight, const long long* __restrict__ ids, int count, int hidden,
     long long vocab, uint16_t* __restrict__ out, int* __restrict__ error) {
   const int vec = hidden >> 3;
-  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= (long long)count * vec) return;
   const int i = (int)(t / vec), c = (int)(t % vec);
   const long long id = ids[i];
@@ -353,26 +353,6 @@ extern "C" __global__ __launch_bounds__(256) void aoto_embedding(
     error[0] = 1;
   }
   reinterpret_cast<uint4*>(out + (size_t)i * hidden)[c] = value;
-}
-
-// Order-preserving key of a bf16 value with the index in the low bits so that
-// the maximum key is the largest value and, among equal values, the first index.
-AOTO_DEVICE unsigned long long argmax_key(uint32_t bits16, int index) {
-  uint32_t u = bits16 & 0xFFFFu;
-  u = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
-  if ((bits16 & 0x7FFFu) > 0x7F80u) u = 0;  // NaN never wins
-  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)index);
-}
-
-AOTO_DEVICE unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
-
-AOTO_DEVICE unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned long long o = __shfl_xor(v, off, 64);
-    v = max_u64(v, o);
-  }
-  return v;
 }
 
 // Greedy argmax of `rows` rows of `n` bf16 logits (first index on ties,
@@ -390,7 +370,7 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
   const bool vec = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) && (n % 8 == 0);
   if (vec) {
     const uint4* rv = reinterpret_cast<const uint4*>(row);
-    for (int c = threadIdx.x; c < n / 8; c += blockDim.x) {
+    for (int c = threadIdx.x; c < n / 8; c += 1024) {
       const uint4 r = rv[c];
       const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
@@ -400,7 +380,7 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
       }
     }
   } else {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) best = max_u64(best, argmax_key(row[i], i));
+    for (int i = threadIdx.x; i < n; i += 1024) best = max_u64(best, argmax_key(row[i], i));
   }
   best = wave_max_u64(best);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -408,8 +388,8 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
   __syncthreads();
   if (threadIdx.x == 0) {
     unsigned long long m = 0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m = max_u64(m, s_best[w]);
-    const long long token = (long long)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull));
+    for (int w = 0; w < 16; ++w) m = max_u64(m, s_best[w]);
+    const long long token = argmax_key_index(m);
     out[blockIdx.x] = token;
     if (history != nullptr && gridDim.x == 1) {
       const int at = history_len[0];
@@ -417,6 +397,55 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
       history_len[0] = at + 1;
     }
   }
+}
+
+// Finish of the fused LM-head argmax: reduce the `count` partial keys written by
+// an *_argmax streaming GEMV to the greedy token (first index on ties), store it
+// at token_out[0], and then, each when its pointer is non-null:
+//   history   append the token at history[*history_len], bump the length;
+//   step      advance the decode-loop step state {position, valid, ring_offset,
+//             slot} by one token (as aoto_step_advance);
+//   embed     gather embedding row `token` (bf16 [embed_rows, hidden]) into
+//             hidden_out - the next decode step's input - or zeros and
+//             error[0] = 1 if the token is not a row of the table.
+// One block of 256 threads; hidden % 8 == 0.
+extern "C" __global__ __launch_bounds__(256) void aoto_argmax_finish(
+    const unsigned long long* __restrict__ keys, int count, long long* __restrict__ token_out,
+    long long* __restrict__ history, int* __restrict__ history_len, int* __restrict__ step, int cap,
+    const uint16_t* __restrict__ embed, long long embed_rows, int hidden, uint16_t* __restrict__ hidden_out,
+    int* __restrict__ error) {
+  __shared__ unsigned long long s_best[4];
+  __shared__ long long s_token;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < count; i += 256) best = max_u64(best, keys[i]);
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned long long m = max_u64(max_u64(s_best[0], s_best[1]), max_u64(s_best[2], s_best[3]));
+    const long long token = argmax_key_index(m);
+    token_out[0] = token;
+    if (history != nullptr) {
+      const int at = history_len[0];
+      history[at] = token;
+      history_len[0] = at + 1;
+    }
+    if (step != nullptr) {
+      step[0] += 1;
+      step[1] += 1;
+      step[2] = step[2] + 1 == cap ? 0 : step[2] + 1;
+      step[3] = step[3] + 1 == cap ? 0 : step[3] + 1;
+    }
+    s_token = token;
+  }
+  if (embed == nullptr) return;
+  __syncthreads();
+  const long long token = s_token;
+  const bool ok = token >= 0 && token < embed_rows;
+  if (!ok && threadIdx.x == 0 && error != nullptr) error[0] = 1;
+  const uint4* src = reinterpret_cast<const uint4*>(embed + (size_t)(ok ? token : 0) * hidden);
+  uint4* dst = reinterpret_cast<uint4*>(hidden_out);
+  for (int c = threadIdx.x; c < (hidden >> 3); c += 256) dst[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
 }
 
 // Advance the decode-loop step state by one token: position and valid length

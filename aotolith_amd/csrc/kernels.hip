@@ -20,15 +20,22 @@ AOTO_GEMV_LPR(1, 1, 0)
 // Wave-persistent streaming W4 GEMV: {lanes per row} x {chunks per lane} x
 // {x vectors each lane stages, ceil(K / 512); 0 = each lane loads its own
 // chunks directly} x {x held in registers}.
-// K = 896: 4x7 single (x in 112 registers) for long outputs, 32x1 direct for
-// short ones (single and paired), 8x4 paired; K = 4096: 32x4; K = 4864: 64x3 direct.
-AOTO_GEMV_STREAM_SINGLE(4, 7, 2, true)
+// K = 896: 8x4 for long outputs (single: x read from LDS; paired: x in
+// registers), 32x1 direct for short ones (single and paired); K = 4096: 32x4;
+// K = 4864: 64x3 direct.
+AOTO_GEMV_STREAM_SINGLE(8, 4, 2, false)
 AOTO_GEMV_STREAM_PAIRED(8, 4, 2, true)
 AOTO_GEMV_STREAM_SINGLE(32, 1, 0, true)
 AOTO_GEMV_STREAM_PAIRED(32, 1, 0, true)
 AOTO_GEMV_STREAM_SINGLE(32, 4, 8, true)
 AOTO_GEMV_STREAM_PAIRED(32, 4, 8, true)
 AOTO_GEMV_STREAM_SINGLE(64, 3, 0, true)
+// LM heads with the fused greedy-argmax keys: K = 896 (8x4), K = 4096 (32x4),
+// and direct 64-lane forms for any other K up to 2048 / 6144.
+AOTO_GEMV_STREAM_ARGMAX(8, 4, 2, false)
+AOTO_GEMV_STREAM_ARGMAX(32, 4, 8, true)
+AOTO_GEMV_STREAM_ARGMAX(64, 1, 0, true)
+AOTO_GEMV_STREAM_ARGMAX(64, 3, 0, true)
 
 // Prefill W4 GEMM: {n tiles per wave} x {m tiles per wave} x epilogue.
 AOTO_GEMM_EPILOGUES(1, 4)

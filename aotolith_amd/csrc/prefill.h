@@ -55,7 +55,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope(const uint16_t* __re
                                                             const long long* __restrict__ positions,
                                                             int rows_per_position, int position_period,
                                                             uint16_t* __restrict__ out, long long rows, int D) {
-  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   if (t >= rows * D) return;
   const long long r = t / D;
   const int d = (int)(t % D);
@@ -81,7 +81,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_qkv_prefill(
     const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ pair, int batch, int M, int query_heads, int kv_heads, int D, int cap, int slot0,
     int zero_prefix) {
-  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   const int half = D >> 1;
   const int W = (query_heads + 2 * kv_heads) * D;
   const long long q_items = (long long)batch * query_heads * M * D;

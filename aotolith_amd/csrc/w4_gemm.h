@@ -209,7 +209,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
     const float* __restrict__ partials, int splits, const uint16_t* __restrict__ bias,
     const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate, uint16_t* __restrict__ Y, int M,
     int N) {
-  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   const long long quads = (long long)M * N / 4;
   if (t >= quads) return;
   const size_t e = (size_t)t * 4;

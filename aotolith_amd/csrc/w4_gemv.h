@@ -55,7 +55,7 @@ AOTO_DEVICE void stage_activation(const uint16_t* __restrict__ x, const uint16_t
   if (NORM) {
     float ss = 0.f;
     const uint4* xv = reinterpret_cast<const uint4*>(x);
-    for (int i = threadIdx.x; i < (K >> 3); i += blockDim.x) {
+    for (int i = threadIdx.x; i < (K >> 3); i += kGemvThreads) {
       const uint4 r = xv[i];
       const uint32_t v[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
@@ -65,12 +65,12 @@ AOTO_DEVICE void stage_activation(const uint16_t* __restrict__ x, const uint16_t
         ss = fmaf(b, b, ss);
       }
     }
-    ss = block_sum(ss, scratch);
+    ss = block_sum<kGemvThreads>(ss, scratch);
     ns = 1.0f / sqrtf(ss / (float)K + eps);
   }
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
-  for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
+  for (int c = threadIdx.x; c < nchunks; c += kGemvThreads) {
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

@@ -122,94 +122,110 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
 // between them, every chunk of x (chunk li + LPR*j), so each lane loads just its
 // own chunks (and the norm weight's) from global memory, the RMS statistic is a
 // group sum over the LPR lanes, and the normalized pairs go straight into
-// registers - no LDS and no wave-wide staging loop.
+// registers - no LDS and no wave-wide staging loop. Split in two so the x loads
+// can be issued before the weight loads: loads return in issue order, so the
+// norm statistic then waits for x alone, not for the weights behind it.
 template <int LPR, int CPL, bool NORM>
-AOTO_DEVICE void stage_activation_direct(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
-                                         float eps, int K, int li, uint4 (&xr)[CPL][4], float (&cr)[CPL]) {
-  const int nchunks = K >> 5;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
-  uint4 raw[CPL][4], wraw[NORM ? CPL : 1][4];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = min(li + LPR * j, nchunks - 1);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) raw[j][k] = xv[c * 4 + k];
-    if (NORM) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) wraw[j][k] = wv[c * 4 + k];
-    }
-  }
-  float ns = 1.f;
-  if (NORM) {
-    float ss = 0.f;
+struct DirectActivation {
+  uint4 raw[CPL][4];
+  uint4 wraw[NORM ? CPL : 1][4];
+
+  AOTO_DEVICE void issue(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w, int K, int li) {
+    const int nchunks = K >> 5;
+    const uint4* xv = reinterpret_cast<const uint4*>(x);
+    const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      if (li + LPR * j < nchunks) {
+      const int c = min(li + LPR * j, nchunks - 1);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
+      for (int k = 0; k < 4; ++k) raw[j][k] = xv[c * 4 + k];
+      if (NORM) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float a = bf16_lo(r4[i]), b = bf16_hi(r4[i]);
-            ss = fmaf(a, a, ss);
-            ss = fmaf(b, b, ss);
+        for (int k = 0; k < 4; ++k) wraw[j][k] = wv[c * 4 + k];
+      }
+    }
+  }
+
+  AOTO_DEVICE void finish(float eps, int K, int li, uint4 (&xr)[CPL][4], float (&cr)[CPL]) const {
+    const int nchunks = K >> 5;
+    float ns = 1.f;
+    if (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if (li + LPR * j < nchunks) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float a = bf16_lo(r4[i]), b = bf16_hi(r4[i]);
+              ss = fmaf(a, a, ss);
+              ss = fmaf(b, b, ss);
+            }
           }
         }
       }
+      ss = group_sum<LPR>(ss);
+      ns = 1.0f / sqrtf(ss / (float)K + eps);
     }
-    ss = group_sum<LPR>(ss);
-    ns = 1.0f / sqrtf(ss / (float)K + eps);
-  }
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    float sum = 0.f;
+    for (int j = 0; j < CPL; ++j) {
+      float sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
-      float e[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        e[2 * i] = bf16_lo(r4[i]);
-        e[2 * i + 1] = bf16_hi(r4[i]);
-      }
-      if (NORM) {
-        const uint32_t w4[4] = {wraw[j][k].x, wraw[j][k].y, wraw[j][k].z, wraw[j][k].w};
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
+        float e[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          e[2 * i] = round_bf16((ns * e[2 * i]) * bf16_lo(w4[i]));
-          e[2 * i + 1] = round_bf16((ns * e[2 * i + 1]) * bf16_hi(w4[i]));
+          e[2 * i] = bf16_lo(r4[i]);
+          e[2 * i + 1] = bf16_hi(r4[i]);
         }
-      }
+        if (NORM) {
+          const uint32_t w4[4] = {wraw[j][k].x, wraw[j][k].y, wraw[j][k].z, wraw[j][k].w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum += e[i];
-      xr[j][k] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
-                            pack_bf16x2(e[3], e[7]));
+          for (int i = 0; i < 4; ++i) {
+            e[2 * i] = round_bf16((ns * e[2 * i]) * bf16_lo(w4[i]));
+            e[2 * i + 1] = round_bf16((ns * e[2 * i + 1]) * bf16_hi(w4[i]));
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += e[i];
+        xr[j][k] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
+                              pack_bf16x2(e[3], e[7]));
+      }
+      cr[j] = 136.f * sum;
     }
-    cr[j] = 136.f * sum;
   }
-}
+};
 
 // Wave-persistent body: wave w of the grid handles row tiles w, w + waves, ...;
 // a tile is 64/LPR rows, LPR lanes per row, CPL chunks (16 B) per lane.
+// waves_per_block is the launch's block size / 64, passed in because reading
+// blockDim costs a memory round trip at kernel start.
 // XREG: after staging, each lane copies the x chunks it uses (the same CPL
 // chunks for every row it visits) into registers, so the row loop reads no LDS.
-// XV == 0 selects direct staging (stage_activation_direct; implies XREG).
-template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS>
+// XV == 0 selects direct staging (DirectActivation; x always in registers).
+// ARGMAX: also reduce the wave's rows to one greedy-argmax key (argmax_key of
+// the stored bf16 value and its row) and store it at keys[global wave index],
+// 0 for a wave without rows; aoto_argmax_finish reduces the keys.
+template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                     const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
                                     const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ norm_w,
                                     float eps, const uint16_t* __restrict__ bias, float alpha, float beta,
-                                    uint16_t* __restrict__ y, int K, int N, int group_shift) {
+                                    uint16_t* __restrict__ y, int K, int N, int group_shift,
+                                    int waves_per_block, unsigned long long* __restrict__ keys) {
   extern __shared__ uint4 lds[];
   constexpr int RPW = 64 / LPR;  // rows per wave tile
   const int nchunks = K >> 5;
   const int ngroups = nchunks >> group_shift;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // readfirstlane: the wave index is uniform, and saying so keeps the tile loop
+  // on scalar branches instead of exec-masked ones.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & (LPR - 1);
   const int rsub = lane / LPR;
   const int tiles = (N + RPW - 1) / RPW;
-  const int waves_per_block = blockDim.x >> 6;
   const int total_waves = gridDim.x * waves_per_block;
   // Per-wave LDS region: K/8 pair vectors then K/32 chunk sums.
   const int region = (K >> 3) + ((K >> 5) + 3) / 4;
@@ -223,21 +239,38 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   // Two register sets, A and B, ping-pong across tiles: the loads for the next
   // tile go into one set while the other is consumed, so no loaded register is
   // ever copied (a copy would force a wait on every outstanding load) and scales
-  // stay raw bf16 bits until use (a conversion right after the load would wait
-  // for it). Loads are unconditional: the tile index is clamped and the last,
-  // redundant prefetch is simply not used.
+  // stay raw bits until use (a conversion right after the load would wait for
+  // it). Loads are unconditional (row index clamped); the epilogue's bias /
+  // residual element is loaded with the row's weights, not after the reduction.
+  // A wave's last tile issues no prefetch.
+  // Scales and bias are read as the aligned 32-bit pair holding the wanted bf16
+  // (the host guarantees K/group and, with a bias, N are even, so the pair is in
+  // bounds): a 16-bit load would be zero-extended where the register sets
+  // change roles, which waits for the prefetch. With K/group even, a lane's
+  // scale half is the same for every row.
   struct Regs {
     uint4 q[CPL];
     uint4 u[PAIRED ? CPL : 1];
     uint32_t s[CPL];
     uint32_t us[PAIRED ? CPL : 1];
+    uint32_t b;
   };
+  const uint32_t* scale_words = reinterpret_cast<const uint32_t*>(scales);
+  const uint32_t* up_scale_words = reinterpret_cast<const uint32_t*>(up_scales);
+  const uint32_t* bias_words = reinterpret_cast<const uint32_t*>(bias);
+  // bf16 in the low half of a pair becomes f32 by << 16, in the high half by masking.
+  auto pair_half = [](uint32_t pair, int high) {
+    return __uint_as_float(high ? (pair & 0xFFFF0000u) : (pair << 16));
+  };
+  int shalf[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) shalf[j] = (cidx[j] >> group_shift) & 1;
   Regs ra, rb;
 
   auto load = [&](int tile, Regs& r) {
     const int row = min(min(tile, tiles - 1) * RPW + rsub, N - 1);
     const uint4* wrow = words + (size_t)row * nchunks;
-    const uint16_t* srow = scales + (size_t)row * ngroups;
+    const uint32_t* srow = scale_words + (size_t)row * (ngroups >> 1);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) r.q[j] = wrow[cidx[j]];
     if (PAIRED) {
@@ -246,12 +279,13 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
       for (int j = 0; j < CPL; ++j) r.u[j] = urow[cidx[j]];
     }
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) r.s[j] = srow[cidx[j] >> group_shift];
+    for (int j = 0; j < CPL; ++j) r.s[j] = srow[cidx[j] >> (group_shift + 1)];
     if (PAIRED) {
-      const uint16_t* usrow = up_scales + (size_t)row * ngroups;
+      const uint32_t* usrow = up_scale_words + (size_t)row * (ngroups >> 1);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) r.us[j] = usrow[cidx[j] >> group_shift];
+      for (int j = 0; j < CPL; ++j) r.us[j] = usrow[cidx[j] >> (group_shift + 1)];
     }
+    if (BIAS) r.b = bias_words[row >> 1];
   };
 
   constexpr bool DIRECT = XV == 0;
@@ -259,6 +293,7 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   uint4 xr[INREG ? CPL : 1][4];
   float cr[INREG ? CPL : 1];
 
+  unsigned long long best = 0;
   auto consume = [&](int tile, const Regs& r) {
     float total = 0.f, total_up = 0.f;
 #pragma unroll
@@ -267,8 +302,8 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
       if (c < nchunks) {
         const uint4* xc = INREG ? xr[j] : xp + c * 4;
         const float corr = INREG ? cr[j] : 136.f * csum[c];
-        total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, bf16_to_f32(r.s[j]), total);
-        if (PAIRED) total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, bf16_to_f32(r.us[j]), total_up);
+        total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, pair_half(r.s[j], shalf[j]), total);
+        if (PAIRED) total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, pair_half(r.us[j], shalf[j]), total_up);
       }
     }
     total = group_sum<LPR>(total);
@@ -280,55 +315,95 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
         const float g = round_bf16(total);
         out = total_up * (g / (1.0f + expf(-g)));
       } else if (BIAS) {
-        out = beta * bf16_to_f32(bias[row]) + alpha * total;
+        out = beta * pair_half(r.b, row & 1) + alpha * total;
       } else {
         out = total;
       }
-      y[row] = (uint16_t)f32_to_bf16(out);
+      const uint32_t bits = f32_to_bf16(out);
+      y[row] = (uint16_t)bits;
+      if (ARGMAX) best = max_u64(best, argmax_key(bits, row));
     }
   };
 
   int tile = blockIdx.x * waves_per_block + wave;
-  if (tile >= tiles) return;
-  load(tile, ra);
-  if (DIRECT) {
-    if constexpr (DIRECT) stage_activation_direct<LPR, CPL, NORM>(x, norm_w, eps, K, li, xr, cr);
-  } else {
-    stage_activation_wave<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
+  if (tile >= tiles) {
+    if (ARGMAX && lane == 0) keys[tile] = 0;
+    return;
   }
-  if (XREG && !DIRECT) {
+  if constexpr (DIRECT) {
+    DirectActivation<LPR, CPL, NORM> act;
+    act.issue(x, norm_w, K, li);
+    load(tile, ra);
+    act.finish(eps, K, li, xr, cr);
+  } else {
+    load(tile, ra);
+    stage_activation_wave<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
+    if (XREG) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
+      for (int j = 0; j < CPL; ++j) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) xr[j][k] = xp[cidx[j] * 4 + k];
-      cr[j] = 136.f * csum[cidx[j]];
+        for (int k = 0; k < 4; ++k) xr[j][k] = xp[cidx[j] * 4 + k];
+        cr[j] = 136.f * csum[cidx[j]];
+      }
     }
   }
-  while (true) {
-    load(tile + total_waves, rb);
-    consume(tile, ra);
-    tile += total_waves;
-    if (tile >= tiles) break;
-    load(tile + total_waves, ra);
-    consume(tile, rb);
-    tile += total_waves;
-    if (tile >= tiles) break;
+  // The tile count per wave is uniform, so these branches are scalar.
+  if constexpr (DIRECT) {
+    // Short outputs: a wave has one or two tiles, so its last tile issues no
+    // (redundant) prefetch - the wave would otherwise wait for it at exit.
+    while (true) {
+      if (tile + total_waves >= tiles) {
+        consume(tile, ra);
+        break;
+      }
+      load(tile + total_waves, rb);
+      consume(tile, ra);
+      tile += total_waves;
+      if (tile + total_waves >= tiles) {
+        consume(tile, rb);
+        break;
+      }
+      load(tile + total_waves, ra);
+      consume(tile, rb);
+      tile += total_waves;
+    }
+  } else {
+    // Long outputs: many tiles per wave; the prefetch is unconditional (its
+    // index clamped) so the loop has no branch between a load and its use,
+    // and the one redundant prefetch at the end is not used.
+    while (true) {
+      load(tile + total_waves, rb);
+      consume(tile, ra);
+      tile += total_waves;
+      if (tile >= tiles) break;
+      load(tile + total_waves, ra);
+      consume(tile, rb);
+      tile += total_waves;
+      if (tile >= tiles) break;
+    }
+  }
+  if (ARGMAX) {
+    best = wave_max_u64(best);
+    if (lane == 0) keys[blockIdx.x * waves_per_block + wave] = best;
   }
 }
 
 }  // namespace aoto
 
-#define AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, NORM, PAIRED, BIAS)                                \
-  extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void                                       \
-      aoto_w4_gemv_s##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS(                                       \
-          const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,           \
-          const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias,             \
-          float alpha, float beta, uint16_t* y, int K, int N, int group_shift) {                         \
-    aoto::w4_gemv_stream_body<LPR, CPL, XV, XREG, NORM, PAIRED, BIAS>(x, words, scales, up_words,       \
-                                                                       up_scales,                       \
-                                                            norm_w, eps, bias, alpha, beta, y, K, N,     \
-                                                            group_shift);                                \
+#define AOTO_GEMV_STREAM_KERNEL(NAME, LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX)                 \
+  extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void NAME(                                 \
+      const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,              \
+      const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias, float alpha,   \
+      float beta, uint16_t* y, int K, int N, int group_shift, int waves_per_block,                       \
+      unsigned long long* keys) {                                                                        \
+    aoto::w4_gemv_stream_body<LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX>(                           \
+        x, words, scales, up_words, up_scales, norm_w, eps, bias, alpha, beta, y, K, N, group_shift,     \
+        waves_per_block, keys);                                                                          \
   }
+
+#define AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, NORM, PAIRED, BIAS)                                \
+  AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS, LPR, CPL, XV,     \
+                          XREG, NORM, PAIRED, BIAS, false)
 
 // The decode variants a decoder layer uses: q/k/v (norm, +bias or not), o and
 // down (+residual), paired gate/up (norm), LM head (norm), plain.
@@ -342,3 +417,7 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
 #define AOTO_GEMV_STREAM_PAIRED(LPR, CPL, XV, XREG)          \
   AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 1, 1, 0)    \
   AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, 0, 1, 0)
+// LM head with the greedy-argmax partial keys (with or without the final norm).
+#define AOTO_GEMV_STREAM_ARGMAX(LPR, CPL, XV, XREG)                                                      \
+  AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n1_argmax, LPR, CPL, XV, XREG, 1, 0, 0, true)  \
+  AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n0_argmax, LPR, CPL, XV, XREG, 0, 0, 0, true)

@@ -16,7 +16,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_quantize(
     const void* __restrict__ src, int src_f32, int rows, int inner, int group,
     int32_t* __restrict__ packed, uint16_t* __restrict__ scales_bf16, float* __restrict__ scales_f32) {
   const int groups = inner / group;
-  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long long)rows * groups) return;
   const int row = (int)(gid / groups);
   const int g = (int)(gid - (long long)row * groups);
@@ -48,7 +48,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_dequantize(
     const int32_t* __restrict__ packed, const uint16_t* __restrict__ scales, int rows, int inner,
     int group, uint16_t* __restrict__ out) {
   const int words = inner >> 3;
-  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long long)rows * words) return;
   const int row = (int)(gid / words);
   const int w = (int)(gid - (long long)row * words);

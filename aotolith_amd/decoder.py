@@ -518,6 +518,14 @@ class _Engine:
         self.ring = torch.zeros((s.layers, 2, 1, s.kv_heads, self.capacity, s.head_dim), dtype=BF16, device=dev)
         self.history = torch.zeros((self.capacity + 1,), dtype=torch.int64, device=dev)
         self.history_len = torch.zeros((1,), dtype=torch.int32, device=dev)
+        # Greedy loop tail: the LM-head GEMV writes per-wave argmax keys and one
+        # finish kernel turns them into the token, its history entry, the next
+        # step state and the next step's embedding row (2 launches instead of
+        # GEMV + argmax + step advance + embedding), when the LM-head shape has
+        # the fused form.
+        head = self.state.lm_head
+        self.key_count = ops.argmax_key_count(s.hidden, head.packed.shape[0], head.group)
+        self.keys = (torch.empty((self.key_count,), dtype=torch.int64, device=dev) if self.key_count else None)
         self._graph = None
         self.graph_error: str | None = None
 
@@ -525,8 +533,8 @@ class _Engine:
     def _gemv(self, x, w: PackedWeight, out, **kwargs):
         return ops.w4_gemv(x, w.packed, w.scales, w.group, out=out, **kwargs)
 
-    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool):
-        """Run the per-layer decode kernels; ``hidden`` holds the embedded token."""
+    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool, lm_head: bool = True):
+        """Run the per-layer decode kernels (and the LM head); ``hidden`` holds the embedded token."""
 
         s = self.spec
         qd, kd = s.heads * s.head_dim, s.kv_heads * s.head_dim
@@ -550,8 +558,9 @@ class _Engine:
             self._gemv(self.hidden, layer.gate, self.act, norm_weight=layer.post_norm, eps=s.eps,
                        up=(layer.up.packed, layer.up.scales))
             self._gemv(self.act, layer.down, self.hidden, bias=self.hidden)
-        self._gemv(self.hidden, self.state.lm_head, self.logits.view(-1), norm_weight=self.state.final_norm,
-                   eps=s.eps)
+        if lm_head:
+            self._gemv(self.hidden, self.state.lm_head, self.logits.view(-1), norm_weight=self.state.final_norm,
+                       eps=s.eps)
 
     def decode_functional(self, token: torch.Tensor, cache: torch.Tensor, valid: int):
         """The reference decode plan: fresh logits and the rolled next cache."""
@@ -562,12 +571,32 @@ class _Engine:
         return self.logits.clone(), next_cache
 
     def _ring_step(self) -> None:
-        """One captured-loop step: token -> logits -> token, cache/step state advanced on device."""
+        """One captured-loop step: token -> logits -> token, cache/step state advanced on device.
 
-        ops.embedding(self.state.embed, self.token, out=self.hidden.view(1, -1))
-        self._decode_layers(None, self.ring, ring=True)
-        ops.argmax(self.logits.view(1, -1), out=self.token, history=self.history, history_len=self.history_len)
-        ops.step_advance(self.step_state, self.capacity)
+        With the fused tail ``hidden`` must hold the token's embedding on entry
+        (``_embed_token``), and holds the next token's on exit.
+        """
+
+        if self.keys is None:
+            ops.embedding(self.state.embed, self.token, out=self.hidden.view(1, -1))
+            self._decode_layers(None, self.ring, ring=True)
+            ops.argmax(self.logits.view(1, -1), out=self.token, history=self.history,
+                       history_len=self.history_len)
+            ops.step_advance(self.step_state, self.capacity)
+            return
+        head = self.state.lm_head
+        self._decode_layers(None, self.ring, ring=True, lm_head=False)
+        ops.w4_gemv_argmax(self.hidden, head.packed, head.scales, head.group, self.keys,
+                           norm_weight=self.state.final_norm, eps=self.spec.eps, out=self.logits.view(-1))
+        ops.argmax_finish(self.keys, self.key_count, out=self.token, history=self.history,
+                          history_len=self.history_len, step_state=self.step_state, capacity=self.capacity,
+                          embedding=self.state.embed, hidden_out=self.hidden)
+
+    def _embed_token(self) -> None:
+        """Put ``token``'s embedding in ``hidden``: the fused loop's entry condition."""
+
+        if self.keys is not None:
+            ops.embedding(self.state.embed, self.token, out=self.hidden.view(1, -1))
 
     def _ensure_graph(self) -> None:
         if self._graph is not None or self.graph_error is not None:
@@ -580,6 +609,7 @@ class _Engine:
         self.token.zero_()
         self.step_state.copy_(torch.tensor([0, 1, 1 % self.capacity, 0], dtype=torch.int32))
         self.history_len.zero_()
+        self._embed_token()
         self._ring_step()
         torch.cuda.synchronize()
         try:
@@ -603,6 +633,7 @@ class _Engine:
         self.step_state.copy_(
             torch.tensor([start_valid, start_valid + 1, 1 % self.capacity, 0], dtype=torch.int32)
         )
+        self._embed_token()
         for _ in range(steps):
             if use_graph and self._graph is not None:
                 self._graph.replay()

@@ -532,6 +532,102 @@ def argmax(logits: torch.Tensor, *, out: torch.Tensor | None = None, history: to
     return out
 
 
+def argmax_key_count(k: int, n: int, group_size: int) -> int:
+    """Keys ``w4_gemv_argmax`` writes for a ``[n, k]`` weight; 0 when the fused form does not take the shape."""
+
+    return int(_lib.library().aoto_hip_w4_gemv_argmax_keys(int(k), int(n), int(group_size)))
+
+
+def w4_gemv_argmax(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    keys: torch.Tensor,
+    *,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """LM-head GEMV (optional RMSNorm prologue) that also writes greedy-argmax keys for ``argmax_finish``.
+
+    ``keys`` is an int64 device buffer of at least ``argmax_key_count(K, N, group)`` entries.
+    Returns the bf16 logits ``[N]`` (identical to ``w4_gemv``'s).
+    """
+
+    _expect(packed, "packed", torch.int32)
+    if packed.dim() != 2:
+        raise ValueError("packed must be 2-D [N, K/8]")
+    n, words = packed.shape
+    k = words * 8
+    _expect(x, "x", BF16)
+    if x.numel() != k:
+        raise ValueError(f"x has {x.numel()} elements, the weight reduces over {k}")
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"group size {group_size} does not divide K={k}")
+    _expect(scales, "scales", BF16, (n, k // group_size))
+    _i64(keys, "keys")
+    if norm_weight is not None:
+        _expect(norm_weight, "norm_weight", BF16)
+        if norm_weight.numel() != k:
+            raise ValueError(f"norm_weight has {norm_weight.numel()} elements, expected {k}")
+    if out is None:
+        out = torch.empty((n,), dtype=BF16, device=x.device)
+    else:
+        _expect(out, "out", BF16)
+        if out.numel() != n:
+            raise ValueError(f"out has {out.numel()} elements, expected {n}")
+    _ready(x)
+    _lib.check(
+        _lib.library().aoto_hip_w4_gemv_argmax(
+            _ptr(x), _ptr(packed), _ptr(scales), _ptr(norm_weight), float(eps), _ptr(out), k, n, group_size,
+            _ptr(keys), keys.numel(), _stream(),
+        )
+    )
+    return out
+
+
+def argmax_finish(
+    keys: torch.Tensor,
+    count: int,
+    *,
+    out: torch.Tensor,
+    history: torch.Tensor | None = None,
+    history_len: torch.Tensor | None = None,
+    step_state: torch.Tensor | None = None,
+    capacity: int = 0,
+    embedding: torch.Tensor | None = None,
+    hidden_out: torch.Tensor | None = None,
+    error: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Reduce ``count`` argmax keys to the greedy token ``out[0]``; optionally append it to ``history``,
+    advance ``step_state`` and gather its ``embedding`` row into ``hidden_out``."""
+
+    _i64(keys, "keys")
+    _i64(out, "out")
+    if not 0 < count <= keys.numel():
+        raise ValueError(f"count {count} is outside (0, {keys.numel()}]")
+    if step_state is not None:
+        _expect(step_state, "step_state", torch.int32, (4,))
+    hidden = rows = 0
+    if embedding is not None:
+        _expect(embedding, "embedding", BF16)
+        rows, hidden = embedding.shape
+        if hidden_out is None or hidden_out.numel() != hidden:
+            raise ValueError("hidden_out must hold one embedding row")
+        _expect(hidden_out, "hidden_out", BF16)
+    if error is not None:
+        _expect(error, "error", torch.int32)
+    _ready(keys)
+    _lib.check(
+        _lib.library().aoto_hip_argmax_finish(
+            _ptr(keys), int(count), _ptr(out), _ptr(history), _ptr(history_len), _ptr(step_state), int(capacity),
+            _ptr(embedding), int(rows), int(hidden), _ptr(hidden_out), _ptr(error), _stream(),
+        )
+    )
+    return out
+
+
 def step_advance(step_state: torch.Tensor, capacity: int) -> None:
     """Advance the int32 device step state ``{position, valid, ring_offset, slot}`` by one token."""
 

@@ -98,6 +98,9 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: f
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    # A spin kernel holds the stream while Python enqueues every launch, so the
+    # timed launches run back to back instead of at the host's enqueue rate.
+    torch.cuda._sleep(50_000_000)
     start.record(stream)
     for i in range(launches):
         ops.w4_gemv(x, words[i % copies], scales[i % copies], group, norm_weight=norm, eps=spec.eps, out=out)

@@ -33,7 +33,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 5
+#define AOTO_HIP_ABI_VERSION 6
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -221,6 +221,28 @@ int aoto_hip_embedding(const void* weight, const int64_t* ids, int count, int hi
  * non-null (rows == 1): history[*history_len] = token, ++*history_len. */
 int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,
                     int* history_len, void* stream);
+
+/* LM-head W4 GEMV (the packed GEMV with the final RMSNorm prologue,
+ * codegen/matmul.py:542-739 with codegen/norm.py:45-72) fused with the first
+ * half of the greedy argmax that follows it (models/decoder.py:1069, 1080):
+ * y = the GEMV's bf16 logits [N] as aoto_hip_w4_gemv writes them, plus one
+ * argmax key per wave of the launch in keys[0 .. aoto_hip_w4_gemv_argmax_keys)
+ * for aoto_hip_argmax_finish. norm_weight may be null (no prologue). */
+size_t aoto_hip_w4_gemv_argmax_keys(int K, int N, int group); /* 0: shape unsupported */
+int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* scales, const void* norm_weight,
+                            float eps, void* y, int K, int N, int group, uint64_t* keys, size_t key_count,
+                            void* stream);
+
+/* Second half of the fused greedy argmax (mx.argmax, models/decoder.py:1069,
+ * 1080, first index on ties) and the loop bookkeeping around it: reduces the
+ * keys to *token_out; then, each when its pointer is non-null, appends the
+ * token to history (history[*history_len], ++*history_len), advances the decode
+ * step state like aoto_hip_step_advance, and gathers the token's embedding row
+ * (the next step's embedding take, runtime/bounds.py:104-107) into hidden_out
+ * (zeros and *error = 1 if the token is not a row of the table). */
+int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_out, int64_t* history,
+                           int* history_len, int32_t* step_state, int capacity, const void* embedding,
+                           int64_t embedding_rows, int hidden, void* hidden_out, int* error, void* stream);
 
 #ifdef __cplusplus
 }

@@ -192,3 +192,80 @@ def test_gemv_stream_shapes(n, k, variant):
     y = _ops().w4_gemv(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64, **gpu_kwargs)
     expected = oracle_gemv(x, packed, scales, 64, **kwargs)
     assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0 if variant == "paired" else 1.0)
+
+
+ARGMAX_SHAPES = [
+    (151936, 896, 64),   # Qwen LM head (staged 8x4 form)
+    (128256, 4096, 64),  # Llama-8B LM head (staged 32x4 form)
+    (3000, 4864, 64),    # direct 64x3 form
+    (512, 256, 64),      # direct 64x1 form (the small decoder tests' head)
+    (100, 896, 32),      # fewer rows than waves; group 32
+]
+
+
+@pytest.mark.parametrize("n,k,group", ARGMAX_SHAPES)
+@pytest.mark.parametrize("norm", [True, False])
+def test_gemv_argmax_matches_gemv_then_first_index_argmax(n, k, group, norm):
+    """Fused LM head + argmax: same logits as w4_gemv, the first maximal index, and the loop bookkeeping."""
+
+    from oracle.ops import argmax_first
+
+    ops = _ops()
+    count = ops.argmax_key_count(k, n, group)
+    assert count > 0
+    gen = torch.Generator(device="cuda").manual_seed(n + k + group)
+    x = torch.randn(k, generator=gen, device="cuda").to(torch.bfloat16)
+    weight = (torch.randn((n, k), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    # Row n//3 aligned with x gets the largest logit; its copy at n-1 ties it.
+    top = n // 3
+    weight[top] = (torch.sign(x.float()) * 0.05).to(torch.bfloat16)
+    weight[n - 1] = weight[top]
+    packed, scales = ops.w4_quantize(weight, group)
+    normw = (1.0 + 0.1 * torch.randn(k, generator=gen, device="cuda")).to(torch.bfloat16) if norm else None
+    keys = torch.full((count,), -7, dtype=torch.int64, device="cuda")
+    y = ops.w4_gemv_argmax(x, packed, scales, group, keys, norm_weight=normw, eps=1e-6)
+    ref = ops.w4_gemv(x, packed, scales, group, norm_weight=normw, eps=1e-6)
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+    logits = y.float().cpu().numpy()[None]
+    want = int(argmax_first(logits)[0])
+    assert want == top
+    cap = 8
+    token = torch.zeros((1,), dtype=torch.int64, device="cuda")
+    history = torch.zeros((4,), dtype=torch.int64, device="cuda")
+    history_len = torch.ones((1,), dtype=torch.int32, device="cuda")
+    step = torch.tensor([5, 6, cap - 1, cap - 1], dtype=torch.int32, device="cuda")
+    embed = torch.randn((n, 64), generator=gen, device="cuda").to(torch.bfloat16)
+    hidden = torch.empty(64, dtype=torch.bfloat16, device="cuda")
+    error = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    ops.argmax_finish(keys, count, out=token, history=history, history_len=history_len, step_state=step,
+                      capacity=cap, embedding=embed, hidden_out=hidden, error=error)
+    assert int(token.item()) == want
+    assert history.cpu().tolist()[1] == want and int(history_len.item()) == 2
+    assert step.cpu().tolist() == [6, 7, 0, 0]
+    assert torch.equal(hidden.view(torch.int16), embed[want].view(torch.int16))
+    assert int(error.item()) == 0
+
+    # A token outside the embedding table: zero row and the error flag, no fault.
+    short = embed[:top].contiguous()
+    ops.argmax_finish(keys, count, out=token, embedding=short, hidden_out=hidden, error=error)
+    assert int(token.item()) == want
+    assert int(error.item()) == 1 and not bool(hidden.float().abs().sum().item())
+
+
+def test_gemv_argmax_refuses_unsupported_shapes():
+    from aotolith_amd._lib import HipKernelError, UnsupportedShape
+
+    ops = _ops()
+    assert ops.argmax_key_count(96, 64, 32) == 0      # three groups per row: scale pairs do not fit
+    assert ops.argmax_key_count(8192, 64, 64) == 0    # K beyond the direct forms
+    keys = torch.empty((4,), dtype=torch.int64, device="cuda")
+    x = torch.zeros(896, dtype=torch.bfloat16, device="cuda")
+    packed = torch.zeros((1000, 112), dtype=torch.int32, device="cuda")
+    scales = torch.zeros((1000, 14), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(HipKernelError):   # too few keys for the launch
+        ops.w4_gemv_argmax(x, packed, scales, 64, keys)
+    with pytest.raises(UnsupportedShape):
+        ops.w4_gemv_argmax(torch.zeros(96, dtype=torch.bfloat16, device="cuda"),
+                           torch.zeros((64, 12), dtype=torch.int32, device="cuda"),
+                           torch.zeros((64, 3), dtype=torch.bfloat16, device="cuda"), 32, keys)
