@@ -21,7 +21,11 @@ __all__ = [
     "compile_llama_static_cache",
     "compile_qwen2_bucketed",
     "compile_qwen2_static_cache",
+    "load_bucketed",
+    "load_compiled_module",
     "load_runtime",
+    "read_artifact_manifest",
+    "save_compiled",
 ]
 
 
@@ -40,8 +44,9 @@ def __getattr__(name: str):
         from . import decoder
 
         return getattr(decoder, name)
-    if name == "load_runtime":
-        from .artifact import load_runtime
+    if name in ("load_runtime", "load_bucketed", "load_compiled_module", "read_artifact_manifest",
+                "save_compiled"):
+        from . import artifact
 
-        return load_runtime
+        return getattr(artifact, name)
     raise AttributeError(name)

@@ -99,6 +99,7 @@ class UnsupportedShape(HipKernelError):
 _lock = threading.RLock()
 _lib: ctypes.CDLL | None = None
 _loaded_devices: dict[int, str] = {}
+_loaded_images: dict[int, bytes] = {}
 
 
 def library() -> ctypes.CDLL:
@@ -164,6 +165,7 @@ def install_code_object(image: bytes, device: int | None = None) -> str:
         buffer = ctypes.create_string_buffer(image, len(image))
         check(library().aoto_hip_load_code_object(buffer, len(image)))
     _loaded_devices[device] = digest
+    _loaded_images[device] = bytes(image)
     return digest
 
 
@@ -187,3 +189,9 @@ def ensure_code_object(device: int | None = None) -> str:
 
 def installed_digest(device: int) -> str | None:
     return _loaded_devices.get(device)
+
+
+def installed_image(device: int) -> bytes | None:
+    """The code object installed on ``device`` by this process, if any."""
+
+    return _loaded_images.get(device)

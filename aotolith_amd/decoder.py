@@ -951,12 +951,15 @@ def compile_decoder_state(
     _check_kernel_limits(spec, group_size)
     engine = _Engine(spec, state, prompt_length, capacity, _device(), attention_splits)
     prefill, decode = _build_plans(spec, engine, prompt_length)
-    return DecoderStaticCacheRuntime(
+    runtime = DecoderStaticCacheRuntime(
         prefill=prefill, decode=decode, prompt_length=prompt_length, max_new_tokens=max_new_tokens,
         cache_capacity=capacity, num_layers=spec.layers, num_key_value_heads=spec.kv_heads,
         head_dim=spec.head_dim, family=spec.family, memory=memory, spec=spec, engine=engine,
         group_size=group_size,
     )
+    prefill.runtime = runtime
+    decode.runtime = runtime
+    return runtime
 
 
 def _check_quantize(quantize: int | None, quantize_bits: int) -> int:

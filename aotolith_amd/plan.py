@@ -44,6 +44,8 @@ class CompiledPlan:
     input_names: tuple[str, ...] = ()
     output_names: tuple[str, ...] = ()
     _lock: threading.Lock = field(default_factory=threading.Lock, repr=False)
+    #: the runtime this plan belongs to (its state and buffers); set by the compiler
+    runtime: object | None = field(default=None, repr=False, compare=False)
 
     @property
     def selections(self) -> tuple[KernelSelection, ...]:
@@ -61,6 +63,13 @@ class CompiledPlan:
             if node.selection.artifact_name:
                 seen.setdefault(node.selection.artifact_name, None)
         return tuple(seen)
+
+    def save(self, path):
+        """Write this plan as a ``.aoto`` artifact (the reference's ``CompiledModulePlan.save``)."""
+
+        from .artifact import save_compiled
+
+        return save_compiled(self, path)
 
     def __call__(self, *inputs, **kwargs):
         # Launches are enqueued in order on the caller's current stream; the lock
