@@ -61,7 +61,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "aoto_hip_decode_rope_attention": (
         _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _i64, _i64, _c_int, _c_int, _c_int, _c_int, _c_int,
-        _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _p, _p, _p, _p,
+        _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _p, _p, _p, _p, _p,
     ),
     "aoto_hip_step_advance": (_p, _c_int, _p),
     "aoto_hip_prefill_attention": (
@@ -72,7 +72,9 @@ SIGNATURES: dict[str, tuple] = {
     "aoto_hip_argmax": (_p, _c_int, _c_int, _i64, _p, _p, _p, _p),
     "aoto_hip_w4_gemv_argmax_keys": (_c_int, _c_int, _c_int),
     "aoto_hip_w4_gemv_argmax": (_p, _p, _p, _p, _c_float, _p, _c_int, _c_int, _c_int, _p, _c_size, _p),
-    "aoto_hip_argmax_finish": (_p, _c_int, _p, _p, _p, _p, _c_int, _p, _i64, _c_int, _p, _p, _p),
+    "aoto_hip_argmax_finish": (
+        _p, _c_int, _p, _p, _p, _p, _c_int, _p, _i64, _c_int, _p, _p, _p, _p, _c_int, _p, _p,
+    ),
 }
 
 #: Entry points returning a size rather than a status.

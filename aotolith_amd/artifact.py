@@ -519,7 +519,7 @@ def load_compiled_module(path: str | os.PathLike[str], *, require_device_match: 
     contents = read_artifact(path, require_device_match=require_device_match)
     runtime = _build([contents], dev, {})
     plan = runtime.prefill if contents.kind == "prefill" else runtime.decode
-    plan.runtime = runtime
+    plan._keepalive = runtime  # the caller holds only the plan
     return plan
 
 

@@ -549,7 +549,7 @@ int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_sta
                                    void* values, int64_t kv_batch_stride, int64_t kv_head_stride, int position,
                                    int slot, int valid, int ring_offset, int batch, int query_heads, int kv_heads,
                                    int capacity, int head_dim, float scale, int splits, void* workspace,
-                                   const int32_t* step_state, void* out, void* stream) {
+                                   const int32_t* step_state, const void* rope_rows, void* out, void* stream) {
   if (!row || !cos_table || !sin_table || !keys || !values || !out)
     return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: null pointer");
   int s = 0, chunk = 0;
@@ -573,7 +573,7 @@ int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_sta
   if (int st = launch(name, dim3(s, batch * query_heads), dim3(256), 0, stream, row, row_width, query_start,
                       key_start, value_start, cos_table, sin_table, keys, values, (long long)kv_batch_stride,
                       (long long)kv_head_stride, valid, ring_offset, position, slot, capacity, query_heads,
-                      kv_heads, scale, chunk, (float*)workspace, step_state, out))
+                      kv_heads, scale, chunk, (float*)workspace, step_state, rope_rows, out))
     return st;
   return s > 1 ? launch_merge(batch * query_heads, s, head_dim, workspace, out, stream) : AOTO_OK;
 }
@@ -647,7 +647,9 @@ int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* sca
 
 int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_out, int64_t* history,
                            int* history_len, int32_t* step_state, int capacity, const void* embedding,
-                           int64_t embedding_rows, int hidden, void* hidden_out, int* error, void* stream) {
+                           int64_t embedding_rows, int hidden, void* hidden_out, int* error,
+                           const void* cos_table, const void* sin_table, int head_dim, void* rope_rows,
+                           void* stream) {
   if (!keys || !token_out || key_count <= 0) return fail(AOTO_ERR_ARGUMENT, "argmax_finish: bad arguments");
   if ((history == nullptr) != (history_len == nullptr))
     return fail(AOTO_ERR_ARGUMENT, "argmax_finish: a token history needs both pointers");
@@ -655,8 +657,11 @@ int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_o
   if (embedding && (!hidden_out || hidden <= 0 || hidden % 8 != 0 || embedding_rows <= 0 ||
                     !aligned16(embedding) || !aligned16(hidden_out)))
     return fail(AOTO_ERR_ARGUMENT, "argmax_finish: the embedding gather needs 16-byte aligned rows, hidden %% 8 == 0");
+  if (rope_rows && (!step_state || !cos_table || !sin_table || head_dim <= 0))
+    return fail(AOTO_ERR_ARGUMENT, "argmax_finish: RoPE rows need the step state, both tables and head_dim");
   return launch("aoto_argmax_finish", dim3(1), dim3(256), 0, stream, keys, key_count, token_out, history,
-                history_len, step_state, capacity, embedding, (long long)embedding_rows, hidden, hidden_out, error);
+                history_len, step_state, capacity, embedding, (long long)embedding_rows, hidden, hidden_out, error,
+                cos_table, sin_table, head_dim, rope_rows);
 }
 
 int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,

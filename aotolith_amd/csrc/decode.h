@@ -123,13 +123,8 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
                                       const uint8_t* __restrict__ mask, int mask_batch_stride, int valid,
                                       int ring_offset, int position, int slot, int cap, int query_heads,
                                       int kv_heads, float scale, int chunk, float* __restrict__ partials,
-                                      const int* __restrict__ step, uint16_t* __restrict__ out) {
-  if (step != nullptr) {
-    position = step[0];
-    valid = step[1];
-    ring_offset = step[2];
-    slot = step[3];
-  }
+                                      const int* __restrict__ step, const uint16_t* __restrict__ rope_rows,
+                                      uint16_t* __restrict__ out) {
   constexpr int THREADS = 256;
   constexpr int LPK = D / 64;             // lanes per key (64 dims each)
   constexpr int KPP = THREADS / LPK;      // keys per block (one key row per D/64 lanes)
@@ -160,26 +155,9 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   uint16_t* kh = kbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
   uint16_t* vh = vbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
 
-  // Loads, in the order their results are needed (vmcnt retires in order): the
-  // query/new-key inputs first, then every K and V row of the block.
-  const int d = min((int)threadIdx.x, D - 1);
-  uint32_t qx = 0, qp = 0, kx = 0, kp = 0, cs = 0, sn = 0, vx = 0;
-  const int half = D / 2;
-  const int pd = d < half ? d + half : d - half;
-  if (FUSED) {
-    const uint16_t* rrow = row + (size_t)b * row_width;
-    const uint16_t* qh = rrow + query_start + (size_t)h * D;
-    const uint16_t* khh = rrow + key_start + (size_t)kvh * D;
-    qx = qh[d];
-    qp = qh[pd];
-    kx = khh[d];
-    kp = khh[pd];
-    cs = cos_table[(size_t)position * D + d];
-    sn = sin_table[(size_t)position * D + d];
-    vx = rrow[value_start + (size_t)kvh * D + d];
-  } else {
-    qx = q[((size_t)b * query_heads + h) * D + d];
-  }
+  // Every K and V row of the block is loaded first: those addresses do not
+  // depend on the device step state, whose read (and the RoPE table rows it
+  // selects) would otherwise hold back every other load by a round trip.
   const int ksl = s0 + min(kl, max(n - 1, 0));
   uint4 kv[8];
   {
@@ -195,6 +173,39 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   for (int u = 0; u < VPT; ++u) {
     const int sl = s0 + min(kbase0 + u, max(n - 1, 0));
     vv[u] = reinterpret_cast<const uint32_t*>(vh + (size_t)sl * D)[d2];
+  }
+  // The query / new key / new value of this head, and the RoPE rows of the
+  // position: from `rope_rows` (cos row, then sin row) when given - no
+  // dependence on the step state - else from the tables at the step's position.
+  const int d = min((int)threadIdx.x, D - 1);
+  uint32_t qx = 0, qp = 0, kx = 0, kp = 0, cs = 0, sn = 0, vx = 0;
+  const int half = D / 2;
+  const int pd = d < half ? d + half : d - half;
+  if (FUSED) {
+    const uint16_t* rrow = row + (size_t)b * row_width;
+    const uint16_t* qh = rrow + query_start + (size_t)h * D;
+    const uint16_t* khh = rrow + key_start + (size_t)kvh * D;
+    qx = qh[d];
+    qp = qh[pd];
+    kx = khh[d];
+    kp = khh[pd];
+    vx = rrow[value_start + (size_t)kvh * D + d];
+    if (rope_rows != nullptr) {
+      cs = rope_rows[d];
+      sn = rope_rows[D + d];
+    }
+  } else {
+    qx = q[((size_t)b * query_heads + h) * D + d];
+  }
+  if (step != nullptr) {
+    position = step[0];
+    valid = step[1];
+    ring_offset = step[2];
+    slot = step[3];
+  }
+  if (FUSED && rope_rows == nullptr) {
+    cs = cos_table[(size_t)position * D + d];
+    sn = sin_table[(size_t)position * D + d];
   }
 
   // Query (rotated out of the projection row when FUSED) into LDS, f32.
@@ -408,14 +419,19 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
 //   embed     gather embedding row `token` (bf16 [embed_rows, hidden]) into
 //             hidden_out - the next decode step's input - or zeros and
 //             error[0] = 1 if the token is not a row of the table.
+//   rope_rows (with step) the cos and sin rows of the advanced position
+//             (tables [cap, D]) - the next step's RoPE rows, so its attention
+//             kernels need not read the step state before loading them.
 // One block of 256 threads; hidden % 8 == 0.
 extern "C" __global__ __launch_bounds__(256) void aoto_argmax_finish(
     const unsigned long long* __restrict__ keys, int count, long long* __restrict__ token_out,
     long long* __restrict__ history, int* __restrict__ history_len, int* __restrict__ step, int cap,
     const uint16_t* __restrict__ embed, long long embed_rows, int hidden, uint16_t* __restrict__ hidden_out,
-    int* __restrict__ error) {
+    int* __restrict__ error, const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table,
+    int head_dim, uint16_t* __restrict__ rope_rows) {
   __shared__ unsigned long long s_best[4];
   __shared__ long long s_token;
+  __shared__ int s_position;
   unsigned long long best = 0;
   for (int i = threadIdx.x; i < count; i += 256) best = max_u64(best, keys[i]);
   best = wave_max_u64(best);
@@ -431,6 +447,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_argmax_finish(
       history_len[0] = at + 1;
     }
     if (step != nullptr) {
+      s_position = step[0] + 1;
       step[0] += 1;
       step[1] += 1;
       step[2] = step[2] + 1 == cap ? 0 : step[2] + 1;
@@ -438,8 +455,18 @@ extern "C" __global__ __launch_bounds__(256) void aoto_argmax_finish(
     }
     s_token = token;
   }
-  if (embed == nullptr) return;
   __syncthreads();
+  if (rope_rows != nullptr && step != nullptr) {
+    // a position past the tables (the step after the last) keeps the old rows
+    const int p = s_position;
+    if (p < cap) {
+      for (int i = threadIdx.x; i < head_dim; i += 256) {
+        rope_rows[i] = cos_table[(size_t)p * head_dim + i];
+        rope_rows[head_dim + i] = sin_table[(size_t)p * head_dim + i];
+      }
+    }
+  }
+  if (embed == nullptr) return;
   const long long token = s_token;
   const bool ok = token >= 0 && token < embed_rows;
   if (!ok && threadIdx.x == 0 && error != nullptr) error[0] = 1;
@@ -470,16 +497,17 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
     aoto::decode_attention_body<D, false>(q, nullptr, 0, 0, 0, 0, nullptr, nullptr, kbase, vbase,        \
                                           kv_batch_stride, kv_head_stride, mask, mask_batch_stride,      \
                                           valid, ring_offset, 0, -1, cap, query_heads, kv_heads, scale,  \
-                                          chunk, partials, step, out);                                   \
+                                          chunk, partials, step, nullptr, out);                          \
   }                                                                                                      \
   extern "C" __global__ __launch_bounds__(256) void aoto_decode_rope_attention_d##D(                    \
       const uint16_t* row, int row_width, int query_start, int key_start, int value_start,               \
       const uint16_t* cos_table, const uint16_t* sin_table, uint16_t* kbase, uint16_t* vbase,            \
       long long kv_batch_stride, long long kv_head_stride, int valid, int ring_offset, int position,     \
       int slot, int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials,          \
-      const int* step, uint16_t* out) {                                                                  \
+      const int* step, const uint16_t* rope_rows, uint16_t* out) {                                       \
     aoto::decode_attention_body<D, true>(nullptr, row, row_width, query_start, key_start, value_start,   \
                                          cos_table, sin_table, kbase, vbase, kv_batch_stride,            \
                                          kv_head_stride, nullptr, 0, valid, ring_offset, position, slot, \
-                                         cap, query_heads, kv_heads, scale, chunk, partials, step, out); \
+                                         cap, query_heads, kv_heads, scale, chunk, partials, step,       \
+                                         rope_rows, out);                                                \
   }

@@ -24,6 +24,8 @@ once as a HIP graph and replayed per token with no host work in between.
 
 from __future__ import annotations
 
+import contextlib
+import gc
 import os
 from collections.abc import Sequence
 from dataclasses import dataclass, field
@@ -485,6 +487,27 @@ def prefill_selections(spec: DecoderSpec) -> tuple[KernelSelection, ...]:
 
 
 # ----------------------------------------------------------------------------- engine
+@contextlib.contextmanager
+def _graph_capture(graph, pool=None):
+    """``torch.cuda.graph`` with the Python GC run first and held off until the end.
+
+    A dead reference cycle that owns another captured graph, collected while a
+    capture is underway, destroys that graph mid-capture and aborts the
+    process; torch's capture context no longer collects on entry.
+    """
+
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, pool=pool):
+            yield
+    finally:
+        if enabled:
+            gc.enable()
+
+
+# ----------------------------------------------------------------------------- engine
 @dataclass
 class _Engine:
     """Kernel sequences of one bucket over one shared state."""
@@ -526,8 +549,22 @@ class _Engine:
         head = self.state.lm_head
         self.key_count = ops.argmax_key_count(s.hidden, head.packed.shape[0], head.group)
         self.keys = (torch.empty((self.key_count,), dtype=torch.int64, device=dev) if self.key_count else None)
+        # cos/sin rows of the current decode position, kept by the finish kernel,
+        # so attention does not wait for the step state before its table loads
+        self.rope_rows = torch.zeros((2, s.head_dim), dtype=BF16, device=dev)
+        # ring prefill inputs (captured prefill graphs read these) and the graphs,
+        # one per left-pad width (the attention's key start), sharing one pool
+        self.prefill_ids = torch.zeros((1, self.prompt_length), dtype=torch.int64, device=dev)
+        self.prefill_positions = torch.zeros((1, self.prompt_length), dtype=torch.int64, device=dev)
+        self._prefill_graphs: dict[int, tuple] = {}
+        self._prefill_pool = None
+        self.prefill_graph_error: str | None = None
         self._graph = None
+        self._graphs: dict[int, object] = {}
         self.graph_error: str | None = None
+
+    #: longest run of decode steps captured in one graph
+    MAX_GRAPH_STEPS = 4
 
     # -- decode -----------------------------------------------------------------
     def _gemv(self, x, w: PackedWeight, out, **kwargs):
@@ -546,7 +583,9 @@ class _Engine:
                 ops.decode_rope_attention(self.qkv.view(1, -1), self.cos, self.sin, pair_out, query_heads=s.heads,
                                           query_start=0, key_start=qd, value_start=qd + kd,
                                           step_state=self.step_state, scale=self.scale, workspace=self.workspace,
-                                          splits=self.attention_splits, out=self.attn)
+                                          splits=self.attention_splits,
+                                          rope_rows=self.rope_rows if self.keys is not None else None,
+                                          out=self.attn)
             else:
                 position = valid - 1
                 ops.rope_kv_cache_append(self.qkv.view(1, -1), self.cos, self.sin, position, pair_out,
@@ -574,7 +613,7 @@ class _Engine:
         """One captured-loop step: token -> logits -> token, cache/step state advanced on device.
 
         With the fused tail ``hidden`` must hold the token's embedding on entry
-        (``_embed_token``), and holds the next token's on exit.
+        (``_enter_loop``), and holds the next token's on exit; ``rope_rows`` likewise.
         """
 
         if self.keys is None:
@@ -590,11 +629,14 @@ class _Engine:
                            norm_weight=self.state.final_norm, eps=self.spec.eps, out=self.logits.view(-1))
         ops.argmax_finish(self.keys, self.key_count, out=self.token, history=self.history,
                           history_len=self.history_len, step_state=self.step_state, capacity=self.capacity,
-                          embedding=self.state.embed, hidden_out=self.hidden)
+                          embedding=self.state.embed, hidden_out=self.hidden, rope_tables=(self.cos, self.sin),
+                          rope_rows=self.rope_rows)
 
-    def _embed_token(self) -> None:
-        """Put ``token``'s embedding in ``hidden``: the fused loop's entry condition."""
+    def _enter_loop(self, position: int) -> None:
+        """The loop's entry condition: the RoPE rows of ``position`` and (fused tail) ``token``'s embedding."""
 
+        self.rope_rows[0].copy_(self.cos[position])
+        self.rope_rows[1].copy_(self.sin[position])
         if self.keys is not None:
             ops.embedding(self.state.embed, self.token, out=self.hidden.view(1, -1))
 
@@ -609,17 +651,30 @@ class _Engine:
         self.token.zero_()
         self.step_state.copy_(torch.tensor([0, 1, 1 % self.capacity, 0], dtype=torch.int32))
         self.history_len.zero_()
-        self._embed_token()
+        self._enter_loop(0)
         self._ring_step()
         torch.cuda.synchronize()
         try:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                self._ring_step()
-            self._graph = graph
+            # Graphs of 1, 2, 4, ... consecutive steps: a loop of n steps replays
+            # the binary decomposition of n, so back-to-back graph launches
+            # (each with its own launch cost) are few.
+            longest = int(os.environ.get("AOTOLITH_GRAPH_STEPS", self.MAX_GRAPH_STEPS))
+            limit = min(max(1, longest), max(1, self.capacity - self.prompt_length - 1))
+            graphs = {}
+            size = 1
+            while size <= limit:
+                graph = torch.cuda.CUDAGraph()
+                with _graph_capture(graph):
+                    for _ in range(size):
+                        self._ring_step()
+                graphs[size] = graph
+                size *= 2
+            self._graphs = graphs
+            self._graph = graphs[1]
         except Exception as error:  # noqa: BLE001 - fall back to eager replay, recorded
             self.graph_error = f"{type(error).__name__}: {error}"
             self._graph = None
+            self._graphs = {}
         torch.cuda.synchronize()
 
     def ring_loop(self, steps: int, start_valid: int, first_token: torch.Tensor, *, sync_each_step: bool,
@@ -633,17 +688,85 @@ class _Engine:
         self.step_state.copy_(
             torch.tensor([start_valid, start_valid + 1, 1 % self.capacity, 0], dtype=torch.int32)
         )
-        self._embed_token()
-        for _ in range(steps):
-            if use_graph and self._graph is not None:
-                self._graph.replay()
+        self._enter_loop(start_valid)
+        remaining = steps
+        while remaining > 0:
+            if use_graph and self._graphs:
+                size = 1
+                if not sync_each_step:
+                    while size * 2 in self._graphs and size * 2 <= remaining:
+                        size *= 2
+                self._graphs[size].replay()
             else:
+                size = 1
                 self._ring_step()
+            remaining -= size
             if sync_each_step:
                 torch.cuda.synchronize()
         return self.history
 
     # -- prefill ----------------------------------------------------------------
+    #: captured ring-prefill graphs kept per engine (one per left-pad width)
+    MAX_PREFILL_GRAPHS = 8
+
+    def _ring_prefill_body(self, key_start: int) -> torch.Tensor:
+        """Prefill of ``prefill_ids`` into the ring, then the first greedy token (token, history[0])."""
+
+        slot0 = self.capacity - self.prompt_length
+        logits = self.prefill_into(self.prefill_ids, self.prefill_positions, lambda i: self.ring[i], slot0,
+                                   self.capacity, key_start=key_start)
+        self.history_len.zero_()
+        ops.argmax(logits.view(1, -1), out=self.token, history=self.history, history_len=self.history_len)
+        return logits
+
+    def _prefill_graphs_enabled(self, use_graph: bool) -> bool:
+        return (use_graph and self.prefill_graph_error is None
+                and os.environ.get("AOTOLITH_HIP_GRAPH", "1") != "0"
+                and os.environ.get("AOTOLITH_PREFILL_GRAPH", "1") != "0")
+
+    def ensure_prefill_graph(self, key_start: int, *, use_graph: bool = True) -> None:
+        """Capture the ring prefill of one left-pad width (an eager warm-up pass first).
+
+        The warm-up and the capture use whatever ``prefill_ids`` holds and
+        overwrite the ring cache and token history; a caller fills both anew.
+        """
+
+        if not self._prefill_graphs_enabled(use_graph) or key_start in self._prefill_graphs:
+            return
+        if len(self._prefill_graphs) >= self.MAX_PREFILL_GRAPHS:
+            self._prefill_graphs.pop(next(iter(self._prefill_graphs)))
+        self._ring_prefill_body(key_start)
+        torch.cuda.synchronize()
+        try:
+            if self._prefill_pool is None:
+                self._prefill_pool = torch.cuda.graph_pool_handle()
+            graph = torch.cuda.CUDAGraph()
+            with _graph_capture(graph, pool=self._prefill_pool):
+                captured = self._ring_prefill_body(key_start)
+            self._prefill_graphs[key_start] = (graph, captured)
+        except Exception as error:  # noqa: BLE001 - eager prefill stays correct, recorded
+            self.prefill_graph_error = f"{type(error).__name__}: {error}"
+        torch.cuda.synchronize()
+
+    def ring_prefill(self, ids: torch.Tensor, positions: torch.Tensor, key_start: int, *,
+                     use_graph: bool = True) -> torch.Tensor:
+        """Prefill ``ids`` (left-padded to the bucket) into the ring cache and pick the first token.
+
+        With ``use_graph`` the kernel sequence of each left-pad width is captured
+        once as a HIP graph (``ensure_prefill_graph``) and replayed, so a prefill
+        costs device time only.
+        """
+
+        self.ensure_prefill_graph(key_start, use_graph=use_graph)
+        self.prefill_ids.copy_(ids)
+        self.prefill_positions.copy_(positions)
+        entry = self._prefill_graphs.get(key_start) if self._prefill_graphs_enabled(use_graph) else None
+        if entry is None:
+            return self._ring_prefill_body(key_start)
+        graph, logits = entry
+        graph.replay()
+        return logits
+
     def prefill_into(self, ids: torch.Tensor, positions: torch.Tensor, pair_of, slot0: int, window: int, *,
                      key_start: int, mask: torch.Tensor | None = None) -> torch.Tensor:
         """Run the prefill kernels; layer ``i``'s keys/values go to ``pair_of(i)`` at ``slot0``.
@@ -803,24 +926,23 @@ class DecoderStaticCacheRuntime:
         engine = self.engine
         if steps == 0:
             return torch.zeros((1, 0), dtype=torch.int64, device=engine.device)
-        if use_graph:
-            # Capture (and its warm-up step on dummy state) must precede the
-            # prefill: the warm-up writes the ring cache and the token history.
-            engine._ensure_graph()
         ids = _as_ids(input_ids, engine.device)
         if ids.shape[0] != 1:
             raise PlanInputError(f"expected batch size 1, got {ids.shape[0]}")
         length = int(ids.shape[1])
         if length > self.prompt_length:
             raise BucketRangeError(f"a {length}-token prompt does not fit the {self.prompt_length}-token plan")
+        if use_graph:
+            # Captures (and their warm-up passes on stale inputs) precede the
+            # prefill: the warm-ups write the ring cache and the token history.
+            engine.ensure_prefill_graph(self.prompt_length - length)
+            engine._ensure_graph()
         marks = {}
         if events is not None:
             for key in ("start", "prefill", "end"):
                 marks[key] = torch.cuda.Event(enable_timing=True)
             marks["start"].record()
-        logits = self._prefill_ring(ids)
-        engine.history_len.zero_()
-        ops.argmax(logits.view(1, -1), out=engine.token, history=engine.history, history_len=engine.history_len)
+        self._prefill_ring(ids, use_graph=use_graph)
         first = engine.token.clone()
         if events is not None:
             marks["prefill"].record()
@@ -859,7 +981,9 @@ class DecoderStaticCacheRuntime:
         return footprint
 
     # -- internals ---------------------------------------------------------------
-    def _prefill_ring(self, ids: torch.Tensor) -> torch.Tensor:
+    def _prefill_ring(self, ids: torch.Tensor, *, use_graph: bool = True) -> torch.Tensor:
+        """Ring prefill of a left-padded prompt; the first token lands in ``engine.token``/``history``."""
+
         engine = self.engine
         length = int(ids.shape[1])
         padding = self.prompt_length - length
@@ -869,9 +993,7 @@ class DecoderStaticCacheRuntime:
             positions = torch.cat((zeros, torch.arange(length, dtype=torch.int64, device=ids.device)[None, :]), 1)
         else:
             positions = torch.arange(length, dtype=torch.int64, device=ids.device)[None, :]
-        slot0 = self.cache_capacity - self.prompt_length
-        return engine.prefill_into(ids, positions, lambda i: engine.ring[i], slot0, self.cache_capacity,
-                                   key_start=padding)
+        return engine.ring_prefill(ids, positions, padding, use_graph=use_graph)
 
 
 def _build_plans(spec: DecoderSpec, engine: _Engine, prompt_length: int):

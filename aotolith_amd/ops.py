@@ -422,9 +422,13 @@ def decode_rope_attention(
     scale: float | None = None,
     workspace: torch.Tensor | None = None,
     splits: int = 0,
+    rope_rows: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """RoPE + in-place KV write at ``slot`` + single-query attention over ``pair [2, B, Hkv, cap, D]``."""
+    """RoPE + in-place KV write at ``slot`` + single-query attention over ``pair [2, B, Hkv, cap, D]``.
+
+    ``rope_rows`` (bf16 ``[2, D]``: cos row, sin row of the current position) replaces the table lookup.
+    """
 
     _expect(row, "row", BF16)
     _expect(pair, "pair", BF16)
@@ -436,6 +440,8 @@ def decode_rope_attention(
         scale = float(torch.tensor(head_dim ** -0.5, dtype=torch.float32))
     if out is None:
         out = torch.empty((batch, query_heads, head_dim), dtype=BF16, device=row.device)
+    if rope_rows is not None:
+        _expect(rope_rows, "rope_rows", BF16, (2, head_dim))
     keys, values = pair[0], pair[1]
     _ready(row)
     _lib.check(
@@ -443,7 +449,7 @@ def decode_rope_attention(
             _ptr(row), width, query_start, key_start, value_start, _ptr(cos_table), _ptr(sin_table), _ptr(keys),
             _ptr(values), keys.stride(0), keys.stride(1), int(position), int(slot), int(valid), int(ring_offset),
             batch, query_heads, kv_heads, capacity, head_dim, float(scale), int(splits), _ptr(workspace),
-            _ptr(step_state), _ptr(out), _stream(),
+            _ptr(step_state), _ptr(rope_rows), _ptr(out), _stream(),
         )
     )
     return out
@@ -599,9 +605,12 @@ def argmax_finish(
     embedding: torch.Tensor | None = None,
     hidden_out: torch.Tensor | None = None,
     error: torch.Tensor | None = None,
+    rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None,
+    rope_rows: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Reduce ``count`` argmax keys to the greedy token ``out[0]``; optionally append it to ``history``,
-    advance ``step_state`` and gather its ``embedding`` row into ``hidden_out``."""
+    advance ``step_state``, gather its ``embedding`` row into ``hidden_out`` and copy the advanced
+    position's rows of ``rope_tables`` (cos, sin ``[capacity, D]``) into ``rope_rows`` ``[2, D]``."""
 
     _i64(keys, "keys")
     _i64(out, "out")
@@ -618,11 +627,22 @@ def argmax_finish(
         _expect(hidden_out, "hidden_out", BF16)
     if error is not None:
         _expect(error, "error", torch.int32)
+    cos_table = sin_table = None
+    head_dim = 0
+    if rope_rows is not None:
+        if rope_tables is None or step_state is None:
+            raise ValueError("rope_rows needs rope_tables and step_state")
+        cos_table, sin_table = rope_tables
+        head_dim = cos_table.shape[-1]
+        _expect(cos_table, "cos table", BF16, (int(capacity), head_dim))
+        _expect(sin_table, "sin table", BF16, (int(capacity), head_dim))
+        _expect(rope_rows, "rope_rows", BF16, (2, head_dim))
     _ready(keys)
     _lib.check(
         _lib.library().aoto_hip_argmax_finish(
             _ptr(keys), int(count), _ptr(out), _ptr(history), _ptr(history_len), _ptr(step_state), int(capacity),
-            _ptr(embedding), int(rows), int(hidden), _ptr(hidden_out), _ptr(error), _stream(),
+            _ptr(embedding), int(rows), int(hidden), _ptr(hidden_out), _ptr(error), _ptr(cos_table),
+            _ptr(sin_table), int(head_dim), _ptr(rope_rows), _stream(),
         )
     )
     return out

@@ -11,6 +11,7 @@ fallback, so a node that no kernel covers is a compile-time error.
 from __future__ import annotations
 
 import threading
+import weakref
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass, field
 
@@ -44,8 +45,18 @@ class CompiledPlan:
     input_names: tuple[str, ...] = ()
     output_names: tuple[str, ...] = ()
     _lock: threading.Lock = field(default_factory=threading.Lock, repr=False)
-    #: the runtime this plan belongs to (its state and buffers); set by the compiler
-    runtime: object | None = field(default=None, repr=False, compare=False)
+    _runtime_ref: object | None = field(default=None, repr=False, compare=False)
+    _keepalive: object | None = field(default=None, repr=False, compare=False)
+
+    @property
+    def runtime(self):
+        """The runtime this plan belongs to (held weakly: a runtime owns its plans)."""
+
+        return None if self._runtime_ref is None else self._runtime_ref()
+
+    @runtime.setter
+    def runtime(self, value) -> None:
+        self._runtime_ref = None if value is None else weakref.ref(value)
 
     @property
     def selections(self) -> tuple[KernelSelection, ...]:

@@ -410,6 +410,7 @@ def main() -> int:
         "decode_ms_per_token": round(decode_ms / decode_steps, 4),
         "decode_weight_stream_gbs": round(weight_bytes * decode_tok_s / 1e9, 1),
         "decode_graph": runtime.engine.graph_error or "captured",
+        "prefill_graph": runtime.engine.prefill_graph_error or "captured",
         "roofline": roofline,
         "cpu_baseline": baseline,
         "parity": parity,

@@ -33,7 +33,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 6
+#define AOTO_HIP_ABI_VERSION 7
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -183,13 +183,16 @@ int aoto_hip_decode_attention(const void* q, const void* keys, const void* value
  * (layout as for aoto_hip_decode_attention) and attends over the window with
  * the new pair included; kept slots as for aoto_hip_decode_attention (valid,
  * ring_offset). out [batch, Hq, head_dim]. step_state as above supplies
- * {position, valid, ring_offset, slot} on the device. */
+ * {position, valid, ring_offset, slot} on the device. rope_rows, when non-null,
+ * is the cos row then the sin row (2 * head_dim bf16) of the step's position,
+ * used instead of the tables (aoto_hip_argmax_finish keeps it current), so the
+ * kernel's loads do not wait for the step state. */
 int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_start, int key_start,
                                    int value_start, const void* cos_table, const void* sin_table, void* keys,
                                    void* values, int64_t kv_batch_stride, int64_t kv_head_stride, int position,
                                    int slot, int valid, int ring_offset, int batch, int query_heads, int kv_heads,
                                    int capacity, int head_dim, float scale, int splits, void* workspace,
-                                   const int32_t* step_state, void* out, void* stream);
+                                   const int32_t* step_state, const void* rope_rows, void* out, void* stream);
 
 /* Advance a decode loop's device step state {position, valid, ring_offset,
  * slot} by one token (ring offset and slot wrap at capacity). The greedy loop
@@ -239,10 +242,16 @@ int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* sca
  * token to history (history[*history_len], ++*history_len), advances the decode
  * step state like aoto_hip_step_advance, and gathers the token's embedding row
  * (the next step's embedding take, runtime/bounds.py:104-107) into hidden_out
- * (zeros and *error = 1 if the token is not a row of the table). */
+ * (zeros and *error = 1 if the token is not a row of the table), and with the
+ * step state copies the cos/sin rows of the advanced position from the tables
+ * ([capacity, head_dim] bf16) into rope_rows (2 * head_dim) for the next step's
+ * aoto_hip_decode_rope_attention (kept as is when that position is past the
+ * tables). */
 int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_out, int64_t* history,
                            int* history_len, int32_t* step_state, int capacity, const void* embedding,
-                           int64_t embedding_rows, int hidden, void* hidden_out, int* error, void* stream);
+                           int64_t embedding_rows, int hidden, void* hidden_out, int* error,
+                           const void* cos_table, const void* sin_table, int head_dim, void* rope_rows,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -110,6 +110,23 @@ def test_graph_and_eager_loops_agree_and_repeat():
     np.testing.assert_array_equal(short[0], first[0, :3])
 
 
+def test_prefill_graph_replays_match_eager():
+    """Captured ring prefills (one graph per left-pad width) replay with new ids and match eager runs."""
+
+    runtime, _ = _pair(seed=21)
+    rng = np.random.default_rng(22)
+    prompts = [rng.integers(0, TINY.vocab, n) for n in (PROMPT, PROMPT - 4, PROMPT, PROMPT - 4, PROMPT - 9)]
+    prompts.append(prompts[1])
+    for ids in prompts:
+        graphed = runtime.greedy_generate(ids).cpu().numpy()
+        torch.cuda.synchronize()
+        eager = runtime.greedy_generate(ids, use_graph=False).cpu().numpy()
+        np.testing.assert_array_equal(graphed, eager)
+    engine = runtime.engine
+    assert engine.prefill_graph_error is None
+    assert sorted(engine._prefill_graphs) == [0, 4, 9]
+
+
 def test_ring_loop_matches_the_functional_roll():
     """The ring-buffer greedy loop gives the same tokens as chaining decode_token."""
 

@@ -313,8 +313,13 @@ def test_argmax_records_history():
     (14, 2, 64, 192, 191, 0, 191, 3),     # rolled layout, 3 splits + merge
     (32, 8, 128, 2304, 1500, 700, 699, 0),  # Llama-8B window, split-K + merge
 ])
-def test_decode_rope_attention_matches_append_then_attend(hq, hkv, dim, cap, valid, offset, slot, splits):
-    """The fused ring step equals rope_kv_cache_append's rotation + attention over the ring."""
+@pytest.mark.parametrize("rows", [False, True])
+def test_decode_rope_attention_matches_append_then_attend(hq, hkv, dim, cap, valid, offset, slot, splits, rows):
+    """The fused ring step equals rope_kv_cache_append's rotation + attention over the ring.
+
+    With ``rows`` the cos/sin rows come from a [2, D] buffer and the table
+    position passed is wrong on purpose: the buffer must be what is used.
+    """
 
     rng = np.random.default_rng(cap + slot)
     cos, sin, gcos, gsin = _tables(cap, dim, 1e6)
@@ -334,9 +339,11 @@ def test_decode_rope_attention_matches_append_then_attend(hq, hkv, dim, cap, val
     ops = _ops()
     gpair = to_gpu_bf16(pair)
     workspace = ops.decode_attention_workspace(1, hq, hkv, cap, dim, splits, device="cuda")
+    rope_rows = torch.stack([gcos[position], gsin[position]]).contiguous() if rows else None
     out = ops.decode_rope_attention(to_gpu_bf16(row), gcos, gsin, gpair, query_heads=hq, query_start=0,
-                                    key_start=hq * dim, value_start=(hq + hkv) * dim, position=position,
-                                    slot=slot, valid=valid, ring_offset=offset, workspace=workspace, splits=splits)
+                                    key_start=hq * dim, value_start=(hq + hkv) * dim,
+                                    position=(position + 7) % cap if rows else position, slot=slot, valid=valid,
+                                    ring_offset=offset, workspace=workspace, splits=splits, rope_rows=rope_rows)
     assert_bf16_parity(from_gpu_bf16(out), expected.reshape(1, hq, dim), max_ulp=2.0)
     got = from_gpu_bf16(gpair)
     others = np.ones(cap, dtype=bool)

@@ -238,11 +238,17 @@ def test_gemv_argmax_matches_gemv_then_first_index_argmax(n, k, group, norm):
     embed = torch.randn((n, 64), generator=gen, device="cuda").to(torch.bfloat16)
     hidden = torch.empty(64, dtype=torch.bfloat16, device="cuda")
     error = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    cos_t = torch.randn((cap, 64), generator=gen, device="cuda").to(torch.bfloat16)
+    sin_t = torch.randn((cap, 64), generator=gen, device="cuda").to(torch.bfloat16)
+    rope_rows = torch.zeros((2, 64), dtype=torch.bfloat16, device="cuda")
     ops.argmax_finish(keys, count, out=token, history=history, history_len=history_len, step_state=step,
-                      capacity=cap, embedding=embed, hidden_out=hidden, error=error)
+                      capacity=cap, embedding=embed, hidden_out=hidden, error=error, rope_tables=(cos_t, sin_t),
+                      rope_rows=rope_rows)
     assert int(token.item()) == want
     assert history.cpu().tolist()[1] == want and int(history_len.item()) == 2
     assert step.cpu().tolist() == [6, 7, 0, 0]
+    assert torch.equal(rope_rows[0].view(torch.int16), cos_t[6].view(torch.int16))
+    assert torch.equal(rope_rows[1].view(torch.int16), sin_t[6].view(torch.int16))
     assert torch.equal(hidden.view(torch.int16), embed[want].view(torch.int16))
     assert int(error.item()) == 0
 
