@@ -563,8 +563,10 @@ class _Engine:
         self._graphs: dict[int, object] = {}
         self.graph_error: str | None = None
 
-    #: longest run of decode steps captured in one graph
-    MAX_GRAPH_STEPS = 4
+    #: longest run of decode steps captured in one graph (AOTOLITH_GRAPH_STEPS
+    #: overrides). Measured on MI355X, one-step graphs replayed back to back beat
+    #: 4- and 32-step graphs by ~25 us per token, so 1 is the default.
+    MAX_GRAPH_STEPS = 1
 
     # -- decode -----------------------------------------------------------------
     def _gemv(self, x, w: PackedWeight, out, **kwargs):
