@@ -121,6 +121,7 @@ struct StreamShape {
   int lpr, cpl;
   bool direct;
   int blocks_per_cu = 2;  // persistent 4-wave blocks per CU
+  bool block_x = false;   // x staged once per 4-wave block (aoto_w4_gemv_x* instances)
 };
 
 bool stream_shape(int K, int N, bool paired, StreamShape* s) {
@@ -136,14 +137,23 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s) {
         *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 3};
       return true;
     case 4096:
-      *s = {32, 4, false};
+      // Up to 16384 outputs (q/k/v, o, gate/up of an 8B model) a wave holds too
+      // few row tiles to amortize its own copy of x: one copy per block.
+      if (N <= 16384)
+        *s = {32, 4, false, 2, true};
+      else
+        *s = {32, 4, false};
       return true;
     case 4864:
       if (paired || !short_out) return false;
       *s = {64, 3, true};
       return true;
+    case 14336:
+      if (paired) return false;
+      *s = {64, 7, false, 2, true};
+      return true;
     default:
-      // Other reductions (14336 ...) use the block-staged kernel.
+      // Other reductions use the block-staged kernel.
       return false;
   }
 }
@@ -163,11 +173,13 @@ StreamLaunch stream_launch(const StreamShape& ss, int K, int N, int group) {
   const long long budget = (long long)cu_count() * gemv_blocks_per_cu(ss.blocks_per_cu) * 4;
   const long long waves = tiles < budget ? tiles : budget;
   StreamLaunch l{};
-  l.wpb = waves <= cu_count() ? 1 : 4;
+  // block-staged x needs full 4-wave blocks (the staging splits x over 256 threads)
+  l.wpb = (waves <= cu_count() && !ss.block_x) ? 1 : 4;
   l.grid = (waves + l.wpb - 1) / l.wpb;
-  // Direct instances read no LDS; staged ones need one region per wave.
+  // Direct instances read no LDS; staged ones need one region per wave, or one
+  // per block when x is shared.
   const unsigned region = ss.direct ? 0u : (unsigned)((K / 8) * 16 + ((K / 32 + 3) / 4) * 16);
-  l.shared = region * l.wpb;
+  l.shared = ss.block_x ? region : region * l.wpb;
   while ((32 << l.shift) < group) ++l.shift;
   return l;
 }
@@ -178,7 +190,8 @@ bool argmax_shape(int K, int N, int group, StreamShape* s) {
   if (K % 32 != 0 || group <= 0 || group % 32 != 0 || (group & (group - 1)) != 0 || K % group != 0 ||
       (K / group) % 2 != 0)
     return false;
-  if (stream_shape(K, N, false, s) && !(s->direct && s->lpr == 32)) return true;
+  // (the 32x1 direct and the block-staged shapes have no argmax instance)
+  if (stream_shape(K, N, false, s) && !(s->direct && s->lpr == 32) && !s->block_x) return true;
   if (K <= 64 * 32) {
     *s = {64, 1, true};
     return true;
@@ -312,8 +325,8 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss)) {
     const StreamLaunch l = stream_launch(ss, K, N, group);
     char sname[64];
-    snprintf(sname, sizeof(sname), "aoto_w4_gemv_s%dx%d_n%d_p%d_b%d", ss.lpr, ss.cpl, norm, paired ? 1 : 0,
-             has_bias);
+    snprintf(sname, sizeof(sname), "aoto_w4_gemv_%c%dx%d_n%d_p%d_b%d", ss.block_x ? 'x' : 's', ss.lpr, ss.cpl,
+             norm, paired ? 1 : 0, has_bias);
     unsigned long long* no_keys = nullptr;
     return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, x, words, scales, up_words,
                   up_scales, norm_weight, eps, bias, alpha, beta, y, K, N, l.shift, l.wpb, no_keys);
@@ -506,6 +519,9 @@ int decode_attention_plan(const char* what, int batch, int query_heads, int kv_h
   if (head_dim != 64 && head_dim != 128)
     return fail(AOTO_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", what, head_dim);
   decode_split(head_dim, capacity, splits, s, chunk);
+  if (*s > 1024)
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: %d keys need %d splits, more than the merge takes (1024)", what,
+                capacity, *s);
   if (*s > 1 && workspace == nullptr)
     return fail(AOTO_ERR_ARGUMENT, "%s: %d keys in %d splits need a workspace", what, capacity, *s);
   return AOTO_OK;

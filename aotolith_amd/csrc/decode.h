@@ -321,26 +321,43 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
 }
 
 // Combine the split records of aoto_decode_attention_*: one block per (b, head),
-// one thread per output column:
 //   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s; 0 when no key is kept.
+// Every load is independent of the others (split s's record is read by thread
+// s % 128, then each thread reads its column of all records with an unrolled
+// loop), so a merge costs a couple of memory round trips, not one per split.
+// splits <= kMergeMaxSplits (checked on the host).
+constexpr int kMergeMaxSplits = 1024;
 extern "C" __global__ __launch_bounds__(128) void aoto_decode_attention_merge(const float* __restrict__ partials,
                                                                              int splits, int D,
                                                                              uint16_t* __restrict__ out) {
+  __shared__ float s_w[kMergeMaxSplits];
+  __shared__ float s_red[2];
   const int bh = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float* rec = partials + (size_t)bh * splits * (D + 2);
   float m = -INFINITY;
-  for (int s = 0; s < splits; ++s) m = fmaxf(m, rec[(size_t)s * (D + 2)]);
+  for (int s = threadIdx.x; s < splits; s += 128) m = fmaxf(m, rec[(size_t)s * (D + 2)]);
+  m = wave_max(m);
+  if (lane == 0) s_red[wave] = m;
+  __syncthreads();
+  const float M = fmaxf(s_red[0], s_red[1]);
+  __syncthreads();  // s_red is reused for the denominator
+  float den = 0.f;
+  for (int s = threadIdx.x; s < splits; s += 128) {
+    const float ms = rec[(size_t)s * (D + 2)];
+    const float ls = rec[(size_t)s * (D + 2) + 1];
+    const float w = (M == -INFINITY || ms == -INFINITY) ? 0.f : expf(ms - M);
+    s_w[s] = w;
+    den = fmaf(w, ls, den);
+  }
+  den = wave_sum(den);
+  if (lane == 0) s_red[wave] = den;
+  __syncthreads();
+  den = s_red[0] + s_red[1];
   for (int d = threadIdx.x; d < D; d += 128) {
-    float num = 0.f, den = 0.f;
-    if (m != -INFINITY) {
-      for (int s = 0; s < splits; ++s) {
-        const float* r = rec + (size_t)s * (D + 2);
-        if (r[0] == -INFINITY) continue;
-        const float w = expf(r[0] - m);
-        den = fmaf(w, r[1], den);
-        num = fmaf(w, r[2 + d], num);
-      }
-    }
+    float num = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < splits; ++s) num = fmaf(s_w[s], rec[(size_t)s * (D + 2) + 2 + d], num);
     out[(size_t)bh * D + d] = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
   }
 }

@@ -30,6 +30,11 @@ AOTO_GEMV_STREAM_PAIRED(32, 1, 0, true)
 AOTO_GEMV_STREAM_SINGLE(32, 4, 8, true)
 AOTO_GEMV_STREAM_PAIRED(32, 4, 8, true)
 AOTO_GEMV_STREAM_SINGLE(64, 3, 0, true)
+// Block-staged x for long reductions with short or mid outputs: K = 4096
+// (Llama-8B q/k/v, o, gate/up) 32x4, K = 14336 (Llama-8B down) 64x7.
+AOTO_GEMV_STREAM_BLOCKX_SINGLE(32, 4, 2)
+AOTO_GEMV_STREAM_BLOCKX_PAIRED(32, 4, 2)
+AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 7, 7)
 // LM heads with the fused greedy-argmax keys: K = 896 (8x4), K = 4096 (32x4),
 // and direct 64-lane forms for any other K up to 2048 / 6144.
 AOTO_GEMV_STREAM_ARGMAX(8, 4, 2, false)

@@ -118,6 +118,74 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// x staged once per block (kGemvThreads threads) into one shared LDS region, in
+// the same layout as stage_activation_wave, with the RMS statistic reduced over
+// the block: for long reductions (K = 4096, 14336) a per-wave copy would cost
+// as many LDS writes and cache reads as the wave's share of the weights.
+// Contains barriers: every thread of the block calls it. XV >= K / (8 * 256).
+template <bool NORM, int XV>
+AOTO_DEVICE void stage_activation_block(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+                                        float eps, int K, uint4* __restrict__ xp, float* __restrict__ csum) {
+  __shared__ float scratch[kGemvThreads / 64];
+  const int vecs = K >> 3;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
+  uint4 xr[XV], wr[NORM ? XV : 1];
+#pragma unroll
+  for (int i = 0; i < XV; ++i) xr[i] = xv[min((int)threadIdx.x + kGemvThreads * i, vecs - 1)];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) wr[i] = wv[min((int)threadIdx.x + kGemvThreads * i, vecs - 1)];
+  }
+  float ns = 1.f;
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      if ((int)threadIdx.x + kGemvThreads * i < vecs) {
+        const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = bf16_lo(raw[j]), b = bf16_hi(raw[j]);
+          ss = fmaf(a, a, ss);
+          ss = fmaf(b, b, ss);
+        }
+      }
+    }
+    ss = block_sum<kGemvThreads>(ss, scratch);
+    ns = 1.0f / sqrtf(ss / (float)K + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < XV; ++i) {
+    const int v = threadIdx.x + kGemvThreads * i;
+    const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+    float e[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      e[2 * k] = bf16_lo(raw[k]);
+      e[2 * k + 1] = bf16_hi(raw[k]);
+    }
+    if (NORM) {
+      const uint32_t wraw[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        e[2 * k] = round_bf16((ns * e[2 * k]) * bf16_lo(wraw[k]));
+        e[2 * k + 1] = round_bf16((ns * e[2 * k + 1]) * bf16_hi(wraw[k]));
+      }
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sum += e[k];
+    if (v < vecs)
+      xp[v] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
+                         pack_bf16x2(e[3], e[7]));
+    // A chunk (32 codes) is four consecutive vectors: threads 4c .. 4c+3.
+    sum = group_sum<4>(sum);
+    if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
+  }
+  __syncthreads();
+}
+
 // Direct staging for the latency-bound shapes: the LPR lanes of a row group hold,
 // between them, every chunk of x (chunk li + LPR*j), so each lane loads just its
 // own chunks (and the norm weight's) from global memory, the RMS statistic is a
@@ -209,7 +277,9 @@ struct DirectActivation {
 // ARGMAX: also reduce the wave's rows to one greedy-argmax key (argmax_key of
 // the stored bf16 value and its row) and store it at keys[global wave index],
 // 0 for a wave without rows; aoto_argmax_finish reduces the keys.
-template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX>
+// BLOCKX: x staged once per block (stage_activation_block; XV >= K/2048) into
+// one LDS region the block's waves share; needs 4-wave blocks.
+template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX, bool BLOCKX = false>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                     const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
                                     const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ norm_w,
@@ -229,7 +299,7 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   const int total_waves = gridDim.x * waves_per_block;
   // Per-wave LDS region: K/8 pair vectors then K/32 chunk sums.
   const int region = (K >> 3) + ((K >> 5) + 3) / 4;
-  uint4* xp = lds + wave * region;
+  uint4* xp = lds + (BLOCKX ? 0 : wave * region);
   float* csum = reinterpret_cast<float*>(xp + (K >> 3));
 
   int cidx[CPL];
@@ -326,11 +396,18 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   };
 
   int tile = blockIdx.x * waves_per_block + wave;
+  if constexpr (BLOCKX) {
+    // every wave takes part in the block's staging barrier, tile or not
+    load(tile, ra);
+    stage_activation_block<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
+  }
   if (tile >= tiles) {
     if (ARGMAX && lane == 0) keys[tile] = 0;
     return;
   }
-  if constexpr (DIRECT) {
+  if constexpr (BLOCKX) {
+    // staged above
+  } else if constexpr (DIRECT) {
     DirectActivation<LPR, CPL, NORM> act;
     act.issue(x, norm_w, K, li);
     load(tile, ra);
@@ -390,16 +467,18 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
 
 }  // namespace aoto
 
-#define AOTO_GEMV_STREAM_KERNEL(NAME, LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX)                 \
+#define AOTO_GEMV_STREAM_KERNEL_X(NAME, LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX, BLOCKX)       \
   extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void NAME(                                 \
       const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,              \
       const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias, float alpha,   \
       float beta, uint16_t* y, int K, int N, int group_shift, int waves_per_block,                       \
       unsigned long long* keys) {                                                                        \
-    aoto::w4_gemv_stream_body<LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX>(                           \
+    aoto::w4_gemv_stream_body<LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX, BLOCKX>(                   \
         x, words, scales, up_words, up_scales, norm_w, eps, bias, alpha, beta, y, K, N, group_shift,     \
         waves_per_block, keys);                                                                          \
   }
+#define AOTO_GEMV_STREAM_KERNEL(NAME, LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX)                   \
+  AOTO_GEMV_STREAM_KERNEL_X(NAME, LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX, false)
 
 #define AOTO_GEMV_STREAM_INSTANCE(LPR, CPL, XV, XREG, NORM, PAIRED, BIAS)                                \
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS, LPR, CPL, XV,     \
@@ -421,3 +500,16 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
 #define AOTO_GEMV_STREAM_ARGMAX(LPR, CPL, XV, XREG)                                                      \
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n1_argmax, LPR, CPL, XV, XREG, 1, 0, 0, true)  \
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n0_argmax, LPR, CPL, XV, XREG, 0, 0, 0, true)
+// Block-staged forms (x shared by the block's 4 waves) for long reductions:
+// names aoto_w4_gemv_x{LPR}x{CPL}_n*_p*_b*.
+#define AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, NORM, PAIRED, BIAS)                               \
+  AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS, LPR, CPL, XV,   \
+                            false, NORM, PAIRED, BIAS, false, true)
+#define AOTO_GEMV_STREAM_BLOCKX_SINGLE(LPR, CPL, XV)          \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 1, 0, 1)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 1, 0, 0)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 0, 0, 1)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 0, 0, 0)
+#define AOTO_GEMV_STREAM_BLOCKX_PAIRED(LPR, CPL, XV)          \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 1, 1, 0)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 0, 1, 0)

@@ -164,8 +164,11 @@ STREAM_SHAPES = [
     (4864, 896),          # Qwen gate/up (paired direct form)
     (8193, 896),          # first output count past the direct-form limit
     (896, 4864),          # Qwen down projection
-    (1024, 4096),         # Llama-8B K = 4096
-    (512, 14336),         # Llama-8B down projection K
+    (1024, 4096),         # Llama-8B K = 4096 (block-staged x)
+    (6144, 4096),         # Llama-8B q/k/v rows
+    (20000, 4096),        # past the block-staged limit: per-wave staged x
+    (512, 14336),         # Llama-8B down projection K (block-staged, 64 lanes x 7 chunks)
+    (4096, 14336),        # Llama-8B down projection
 ]
 
 
@@ -191,7 +194,10 @@ def test_gemv_stream_shapes(n, k, variant):
         gpu_kwargs = {"up": (torch.from_numpy(up).cuda(), to_gpu_bits(up_s))}
     y = _ops().w4_gemv(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64, **gpu_kwargs)
     expected = oracle_gemv(x, packed, scales, 64, **kwargs)
-    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0 if variant == "paired" else 1.0)
+    # Long reductions (K = 14336) give |y| up to ~8 (paired), where one bf16 ulp
+    # exceeds the 2e-2 bar meant for O(1) outputs: scale the bar with |y|.
+    atol = 2e-2 * max(1.0, float(np.abs(expected).max()) / 4)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0 if variant == "paired" else 1.0, atol=atol)
 
 
 ARGMAX_SHAPES = [
