@@ -34,7 +34,7 @@ import numpy as np
 
 from .bf16 import round_bf16
 from .ops import argmax_first, attention, rms_norm, rms_scale, rope, rope_tables
-from .quant import dequantize_i4_bf16, dequantize_i4_exact
+from .quant import dequantize_bits_bf16, dequantize_bits_exact
 
 
 @dataclass(frozen=True)
@@ -49,6 +49,7 @@ class DecoderShape:
     eps: float
     theta: float
     group_size: int = 64
+    bits: int = 4
 
     @property
     def qkv_width(self) -> int:
@@ -79,13 +80,13 @@ class OracleDecoder:
     def _w_exact(self, pair) -> np.ndarray:
         key = id(pair[0])
         if key not in self._exact:
-            self._exact[key] = dequantize_i4_exact(pair[0], pair[1], self.shape.group_size)
+            self._exact[key] = dequantize_bits_exact(pair[0], pair[1], self.shape.group_size, self.shape.bits)
         return self._exact[key]
 
     def _w_rounded(self, pair) -> np.ndarray:
         key = id(pair[0])
         if key not in self._rounded:
-            self._rounded[key] = dequantize_i4_bf16(pair[0], pair[1], self.shape.group_size)
+            self._rounded[key] = dequantize_bits_bf16(pair[0], pair[1], self.shape.group_size, self.shape.bits)
         return self._rounded[key]
 
     # decode-side fused GEMV (codegen/matmul.py:542-739) -------------------------

@@ -13,7 +13,7 @@ from __future__ import annotations
 import numpy as np
 
 from .bf16 import round_bf16
-from .quant import dequantize_i4_bf16, dequantize_i4_exact
+from .quant import dequantize_bits_bf16, dequantize_bits_exact
 
 
 def _f32(values) -> np.ndarray:
@@ -53,8 +53,10 @@ def w4_gemv(
     beta: float = 1.0,
     up_packed=None,
     up_scales_bits=None,
+    bits: int = 4,
 ) -> np.ndarray:
-    """Packed W4 GEMV with its prologue and epilogues, one output row ``[N]``.
+    """Packed W4 (``bits=8``: W8, ``codegen/matmul.py:742-929``) GEMV with its prologue and
+    epilogues, one output row ``[N]``.
 
     Follows ``codegen/matmul.py:542-739`` (semantics
     ``runtime/mlx_ops/__init__.py:563-619``):
@@ -72,10 +74,10 @@ def w4_gemv(
     if norm_weight is not None:
         ns = rms_scale(xv, eps)[0]
         xv = round_bf16((ns * xv) * _f32(norm_weight).reshape(-1))
-    weight = dequantize_i4_exact(packed, scales_bits, group_size).astype(np.float64)
+    weight = dequantize_bits_exact(packed, scales_bits, group_size, bits).astype(np.float64)
     acc = weight @ xv.astype(np.float64)
     if up_packed is not None:
-        up = dequantize_i4_exact(up_packed, up_scales_bits, group_size).astype(np.float64)
+        up = dequantize_bits_exact(up_packed, up_scales_bits, group_size, bits).astype(np.float64)
         acc_up = up @ xv.astype(np.float64)
         gate = round_bf16(np.float32(1.0) * acc.astype(np.float32)).astype(np.float64)
         return round_bf16(acc_up.astype(np.float32).astype(np.float64) * (gate / (1.0 + np.exp(-gate))))
@@ -93,8 +95,9 @@ def w4_matmul(
     bias=None,
     residual=None,
     gate=None,
+    bits: int = 4,
 ) -> np.ndarray:
-    """Prefill W4 matmul ``[M, K] -> [M, N]`` with its fused epilogue.
+    """Prefill W4 (or W8) matmul ``[M, K] -> [M, N]`` with its fused epilogue.
 
     The reference keeps the unpack for ``M > 1`` (``passes/quantize.py:58-71``):
     the dequant kernel writes ``bf16(code * scale)`` (``codegen/quantize.py:27-63``,
@@ -108,7 +111,7 @@ def w4_matmul(
     """
 
     x64 = _f32(x).astype(np.float64)
-    weight = dequantize_i4_bf16(packed, scales_bits, group_size).astype(np.float64)
+    weight = dequantize_bits_bf16(packed, scales_bits, group_size, bits).astype(np.float64)
     acc = x64 @ weight.T
     if bias is not None:
         acc = acc + _f32(bias).astype(np.float64)[None, :]

@@ -1,4 +1,4 @@
-"""Write ``quantize_kats.json``: known-answer vectors for the int4 format.
+"""Write ``quantize_kats.json``: known-answer vectors for the int4 and int8 formats.
 
 The vectors come from the reference's own known-answer tests and from the format
 definition worked by hand in pure Python integers - nothing here calls the
@@ -11,7 +11,11 @@ oracle, so the oracle can be checked against them:
   ``rint(w * 7 / 1.5)``;
 * half-to-even rounding at scale 1 (``quantize.py:119-121`` uses ``np.rint``);
 * an all-zero group (``tests/test_quantize.py:103-107``): scale ``1 / 7``,
-  codes 0.
+  codes 0;
+* int8 (``"bits": 8``): byte order ``[-128, -1, 0, 127]`` with byte ``k`` at
+  bits ``8k`` (``tests/test_quantize.py:194-202``), a row at group 8 with scale
+  ``max|w| / 127`` (``:217-223``), half-to-even at scale 1 and an all-zero group
+  (scale ``1 / 127``).
 
 Run ``python tests/golden/make_kats.py`` to regenerate.
 """
@@ -30,6 +34,15 @@ def pack_word(codes: list[int]) -> int:
     word = 0
     for position, code in enumerate(codes):
         word |= (code & 0xF) << (4 * position)
+    return word - (1 << 32) if word >= 1 << 31 else word
+
+
+def pack_word8(codes: list[int]) -> int:
+    """Pack four signed byte codes into a signed 32-bit word, byte k at bits 8k."""
+
+    word = 0
+    for position, code in enumerate(codes):
+        word |= (code & 0xFF) << (8 * position)
     return word - (1 << 32) if word >= 1 << 31 else word
 
 
@@ -91,6 +104,51 @@ def main() -> None:
             "codes": [0] * 16,
             "word": 0,
             "scale_f32": f32(1.0 / 7.0),
+        }
+    )
+
+    codes8 = [-128, -1, 0, 127]
+    cases.append({"name": "int8_byte_order", "bits": 8, "codes": codes8, "word": pack_word8(codes8)})
+
+    row8 = [-1.0, -0.5, 0.0, 0.5, 1.0, 1.5, -1.5, 0.25]
+    scale8 = Fraction(3, 2) / 127
+    row8_codes = [max(-128, min(127, rint_half_even(Fraction(w) / scale8))) for w in row8]
+    cases.append(
+        {
+            "name": "int8_group_scale",
+            "bits": 8,
+            "weight": row8,
+            "group_size": 8,
+            "codes": row8_codes,
+            "words": [pack_word8(row8_codes[:4]), pack_word8(row8_codes[4:])],
+            "scale_f32": f32(1.5 / 127.0),
+        }
+    )
+
+    ties8 = [100.5, 3.5, 2.5, 0.5, -0.5, -2.5, 127.0, -127.0]
+    tie8_codes = [rint_half_even(Fraction(w)) for w in ties8]
+    # with max |w| = 127 the scale is exactly 1
+    cases.append(
+        {
+            "name": "int8_half_to_even",
+            "bits": 8,
+            "weight": ties8,
+            "group_size": 8,
+            "codes": tie8_codes,
+            "words": [pack_word8(tie8_codes[:4]), pack_word8(tie8_codes[4:])],
+            "scale_f32": 1.0,
+        }
+    )
+
+    cases.append(
+        {
+            "name": "int8_zero_group",
+            "bits": 8,
+            "weight": [0.0] * 8,
+            "group_size": 8,
+            "codes": [0] * 8,
+            "words": [0, 0],
+            "scale_f32": f32(1.0 / 127.0),
         }
     )
 

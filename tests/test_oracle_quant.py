@@ -166,3 +166,75 @@ def test_pack_weight_bf16_scales_are_rne_of_f32_scales() -> None:
     np.testing.assert_array_equal(packed, ref_packed)
     torch_scales = torch.from_numpy(ref_scales).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     np.testing.assert_array_equal(scales_bits, torch_scales)
+
+
+# --- eight bits (quantize.py:155-268, models/quantized.py:84-107, 165-172) ---------------
+
+
+def test_int8_byte_order_known_answer() -> None:
+    from oracle.quant import unpack_codes_int8
+
+    case = _cases()["int8_byte_order"]
+    packed = np.array([[case["word"]]], dtype=np.int32)
+    np.testing.assert_array_equal(unpack_codes_int8(packed), np.array([case["codes"]], dtype=np.int8))
+
+
+@pytest.mark.parametrize("name", ["int8_group_scale", "int8_half_to_even", "int8_zero_group"])
+def test_int8_pack_known_answers(name: str) -> None:
+    from oracle.quant import quantize_int8, unpack_codes_int8
+
+    case = _cases()[name]
+    weight = np.array([case["weight"]], dtype=np.float32)
+    packed, scales = quantize_int8(weight, case["group_size"])
+    np.testing.assert_array_equal(unpack_codes_int8(packed)[0], np.array(case["codes"], dtype=np.int8))
+    assert [int(w) for w in packed[0]] == case["words"]
+    assert float(scales[0, 0]) == case["scale_f32"]
+
+
+def test_int8_shape_scale_and_error_bound() -> None:
+    from oracle.quant import dequantize_int8, quantize_int8
+
+    weight = _weight(16, 64, seed=11)
+    weight[0, :32] *= 7.0
+    packed, scales = quantize_int8(weight, 32)
+    assert packed.dtype == np.int32 and packed.shape == (16, 16) and packed.nbytes * 4 == weight.nbytes
+    np.testing.assert_allclose(scales[0, 0], np.abs(weight[0, :32]).max() / np.float32(127.0), rtol=0)
+    error = np.abs(dequantize_int8(packed, scales, 32) - weight)
+    assert (error <= np.repeat(scales, 32, axis=1) / 2 * (1 + 1e-6)).all()
+    # 127 levels instead of 7: the residual is more than 15x smaller (reference test :205-214)
+    coarse = np.abs(dequantize_int4(*quantize_int4(weight, 32), 32) - weight).max()
+    assert error.max() < coarse / 15
+
+
+def test_int8_round_trip_and_idempotence() -> None:
+    from oracle.quant import dequantize_int8, quantize_int8, unpack_codes_int8
+
+    weight = _weight(8, 128, seed=12)
+    packed, scales = quantize_int8(weight, 64)
+    codes = unpack_codes_int8(packed)
+    assert codes.min() >= -128 and codes.max() <= 127
+    again, again_scales = quantize_int8(dequantize_int8(packed, scales, 64), 64)
+    np.testing.assert_array_equal(again, packed)
+
+
+@pytest.mark.parametrize("group_size", [0, 6, 10])
+def test_int8_rejects_groups_that_split_a_word(group_size: int) -> None:
+    from oracle.quant import quantize_int8
+
+    with pytest.raises(ValueError):
+        quantize_int8(_weight(2, 60), group_size)
+
+
+def test_int8_unpack_matches_a_torch_shift_and_wrap() -> None:
+    """The reference's torch op (models/quantized.py:84-107) restated in torch ops."""
+
+    from oracle.quant import dequantize_bits_bf16, pack_weight_bits_bf16
+
+    weight = round_bf16(_weight(6, 64, seed=13) * np.float32(0.05))
+    packed, scales_bits = pack_weight_bits_bf16(weight, 32, 8)
+    words = torch.from_numpy(packed).to(torch.int64) & 0xFFFFFFFF
+    fields = [((words >> (8 * b)) & 0xFF) for b in range(4)]
+    codes = torch.stack([torch.where(f >= 128, f - 256, f) for f in fields], dim=-1).reshape(6, -1)
+    scales = torch.from_numpy(from_bf16_bits(scales_bits)).to(torch.bfloat16)
+    ref = (codes.to(torch.bfloat16) * scales.repeat_interleave(32, dim=-1)).float().numpy()
+    np.testing.assert_array_equal(dequantize_bits_bf16(packed, scales_bits, 32, 8), ref)
