@@ -45,6 +45,13 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "aoto_hip_w4_gemm": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
     "aoto_hip_w4_gemm_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int),
+    "aoto_hip_w8_quantize": (_p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p),
+    "aoto_hip_w8_dequantize": (_p, _p, _c_int, _c_int, _c_int, _p, _p),
+    "aoto_hip_w8_gemv": (
+        _p, _p, _p, _p, _p, _p, _c_float, _p, _c_float, _c_float, _p,
+        _c_int, _c_int, _c_int, _p,
+    ),
+    "aoto_hip_w8_gemm": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
     "aoto_hip_rms_norm": (_p, _p, _c_float, _p, _c_int, _c_int, _p),
     "aoto_hip_rope": (_p, _p, _p, _p, _c_int, _c_int, _p, _i64, _c_int, _p),
     "aoto_hip_rope_qkv_prefill": (

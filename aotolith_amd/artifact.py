@@ -136,7 +136,7 @@ def state_items(state) -> list[tuple[str, Any]]:
     return items
 
 
-def state_from_items(spec, named: Mapping[str, Any], group: int):
+def state_from_items(spec, named: Mapping[str, Any], group: int, bits: int = 4):
     """Rebuild a DecoderState from ``state_items`` names (tensors already on the device)."""
 
     from .decoder import DecoderState, LayerState, PackedWeight
@@ -147,7 +147,7 @@ def state_from_items(spec, named: Mapping[str, Any], group: int):
         return named[name]
 
     def packed(prefix):
-        return PackedWeight(take(f"{prefix}.packed"), take(f"{prefix}.scales"), group)
+        return PackedWeight(take(f"{prefix}.packed"), take(f"{prefix}.scales"), group, bits)
 
     layers = []
     for i in range(spec.layers):
@@ -208,7 +208,8 @@ def write_artifact(
             "state": entries,
         },
         "compile_options": {"codegen_matmul": True, "codegen_attention": True, "autotune": False,
-                            "quantize": int(config["group_size"]), "quantize_bits": 4},
+                            "quantize": int(config["group_size"]),
+                            "quantize_bits": int(config.get("quantize_bits", 4))},
         "profile": dict(profile),
         "payload_digests": {"selections": _digest(selections_bytes), "code_object": _digest(code_object)},
         "payloads": {"selections": "selections.json", "code_object": CODE_OBJECT_ENTRY},
@@ -253,7 +254,8 @@ def save_plan(runtime, kind: str, path: str | os.PathLike[str]) -> Path:
     plan = runtime.prefill if kind == "prefill" else runtime.decode
     config = {"prompt_length": runtime.prompt_length, "max_new_tokens": runtime.max_new_tokens,
               "cache_capacity": runtime.cache_capacity, "group_size": runtime.group_size,
-              "memory": runtime.memory, "attention_splits": engine.attention_splits}
+              "quantize_bits": runtime.quantize_bits, "memory": runtime.memory,
+              "attention_splits": engine.attention_splits}
     return write_artifact(path, kind=kind, spec=runtime.spec, config=config, state=state_items(engine.state),
                           selections=plan.selections, code_object=image, profile=device_profile(engine.device))
 
@@ -480,10 +482,13 @@ def _build(contents_list: Sequence[ArtifactContents], device, state_cache: dict)
             raise ArtifactCompatibilityError("the prefill and decode artifacts hold different code objects")
     device_index = device.index if device.index is not None else 0
     _install_code_object(first.code_object, device_index)
-    key = (first.state_digest(), int(config["group_size"]))
+    bits = int(config.get("quantize_bits", 4))
+    if bits not in (4, 8):
+        raise ArtifactCompatibilityError(f"artifact records quantize_bits={bits}; this package packs 4 or 8 bits")
+    key = (first.state_digest(), int(config["group_size"]), bits)
     state = state_cache.get(key)
     if state is None:
-        state = state_from_items(spec, _device_state(first, device), int(config["group_size"]))
+        state = state_from_items(spec, _device_state(first, device), int(config["group_size"]), bits)
         state_cache[key] = state
     runtime = compile_decoder_state(
         spec, state, prompt_length=int(config["prompt_length"]), max_new_tokens=int(config["max_new_tokens"]),

@@ -398,30 +398,39 @@ size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
-int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
-                     const void* residual, const void* gate, void* y, int M, int N, int K, int group,
-                     int tile, int splits, void* workspace, void* stream) {
-  if (!x || !words || !scales || !y) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: null pointer");
-  if (M <= 0 || N <= 0 || K <= 0) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: empty shape M=%d N=%d K=%d", M, N, K);
+}  // extern "C"
+
+namespace {
+
+// The prefill GEMM of either code width (the kernels differ only in how many
+// packed words make one lane's 8-code operand).
+int packed_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* bias,
+                const void* residual, const void* gate, void* y, int M, int N, int K, int group, int tile,
+                int splits, void* workspace, void* stream) {
+  const char* what = bits == 4 ? "w4_gemm" : "w8_gemm";
+  if (!x || !words || !scales || !y) return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(AOTO_ERR_ARGUMENT, "%s: empty shape M=%d N=%d K=%d", what, M, N, K);
   if (K % 64 != 0 || N % 16 != 0 || group <= 0 || group % 32 != 0 || K % group != 0)
-    return fail(AOTO_ERR_UNSUPPORTED, "w4_gemm: needs K %% 64 == 0, N %% 16 == 0, group %% 32 == 0 dividing K "
-                "(M=%d N=%d K=%d group=%d)", M, N, K, group);
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: needs K %% 64 == 0, N %% 16 == 0, group %% 32 == 0 dividing K "
+                "(M=%d N=%d K=%d group=%d)", what, M, N, K, group);
   const int epilogues = (bias != nullptr) + (residual != nullptr) + (gate != nullptr);
-  if (epilogues > 1) return fail(AOTO_ERR_ARGUMENT, "w4_gemm: at most one of bias, residual, gate");
+  if (epilogues > 1) return fail(AOTO_ERR_ARGUMENT, "%s: at most one of bias, residual, gate", what);
   if (!aligned16(x) || !aligned8(y) || (bias && !aligned8(bias)) || (residual && !aligned8(residual)) ||
-      (gate && !aligned8(gate)))
-    return fail(AOTO_ERR_ARGUMENT, "w4_gemm: x must be 16-byte aligned, y/bias/residual/gate 8-byte aligned");
+      (gate && !aligned8(gate)) || (bits == 8 && !aligned8(words)))
+    return fail(AOTO_ERR_ARGUMENT, "%s: x must be 16-byte aligned, y/bias/residual/gate%s 8-byte aligned", what,
+                bits == 8 ? "/words" : "");
   if (tile != 0 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
-    return fail(AOTO_ERR_ARGUMENT, "w4_gemm: tile code %d is not one of 14, 18, 24, 28", tile);
+    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 14, 18, 24, 28", what, tile);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits);
   if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
-    return fail(AOTO_ERR_ARGUMENT, "w4_gemm: %d-way split-K needs a 16-byte aligned workspace of "
-                "aoto_hip_w4_gemm_workspace() bytes", p.splits);
+    return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
+                "aoto_hip_w4_gemm_workspace() bytes", what, p.splits);
   const int bn = 64 * p.tn, bm = 16 * p.tm;
   const bool split = p.splits > 1;
   const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
   char name[64];
-  snprintf(name, sizeof(name), "aoto_w4_gemm_n%d_m%d_b%d_r%d_g%d", p.tn, p.tm, b, r, g);
+  snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_b%d_r%d_g%d", bits, p.tn, p.tm, b, r, g);
   float* partials = split ? static_cast<float*>(workspace) : nullptr;
   if (int st = launch(name, dim3((N + bn - 1) / bn, (M + bm - 1) / bm, p.splits), dim3(256), 0, stream, x, words,
                       scales, bias, residual, gate, y, M, N, K, group, p.kslice, partials))
@@ -430,6 +439,81 @@ int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, co
   const long long quads = (long long)M * N / 4;
   return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
                 (const float*)partials, p.splits, bias, residual, gate, y, M, N);
+}
+
+}  // namespace
+
+extern "C" {
+
+int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
+                     const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                     int tile, int splits, void* workspace, void* stream) {
+  return packed_gemm(4, x, words, scales, bias, residual, gate, y, M, N, K, group, tile, splits, workspace,
+                     stream);
+}
+
+int aoto_hip_w8_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
+                     const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                     int tile, int splits, void* workspace, void* stream) {
+  return packed_gemm(8, x, words, scales, bias, residual, gate, y, M, N, K, group, tile, splits, workspace,
+                     stream);
+}
+
+int aoto_hip_w8_quantize(const void* weight, int weight_is_f32, int rows, int inner, int group,
+                         int32_t* packed, void* scales_bf16, float* scales_f32, void* stream) {
+  if (!weight || !packed || !scales_bf16) return fail(AOTO_ERR_ARGUMENT, "w8_quantize: null pointer");
+  if (rows <= 0 || inner <= 0) return fail(AOTO_ERR_ARGUMENT, "w8_quantize: empty shape %dx%d", rows, inner);
+  if (group <= 0 || group % 4 != 0 || inner % group != 0)
+    return fail(AOTO_ERR_ARGUMENT, "w8_quantize: group %d must be a positive multiple of 4 dividing %d",
+                group, inner);
+  const long long tasks = (long long)rows * (inner / group);
+  return launch("aoto_w8_quantize", dim3(blocks_for(tasks, 256)), dim3(256), 0, stream, weight, weight_is_f32,
+                rows, inner, group, packed, scales_bf16, scales_f32);
+}
+
+int aoto_hip_w8_dequantize(const int32_t* packed, const void* scales, int rows, int inner, int group,
+                           void* out, void* stream) {
+  if (!packed || !scales || !out) return fail(AOTO_ERR_ARGUMENT, "w8_dequantize: null pointer");
+  if (rows <= 0 || inner <= 0 || inner % 4 != 0)
+    return fail(AOTO_ERR_ARGUMENT, "w8_dequantize: bad shape %dx%d", rows, inner);
+  if (group <= 0 || group % 4 != 0 || inner % group != 0)
+    return fail(AOTO_ERR_ARGUMENT, "w8_dequantize: bad group %d for inner %d", group, inner);
+  if (!aligned8(out)) return fail(AOTO_ERR_ARGUMENT, "w8_dequantize: output must be 8-byte aligned");
+  const long long words = (long long)rows * (inner / 4);
+  return launch("aoto_w8_dequantize", dim3(blocks_for(words, 256)), dim3(256), 0, stream, packed, scales, rows,
+                inner, group, out);
+}
+
+int aoto_hip_w8_gemv(const void* x, const int32_t* words, const void* scales, const int32_t* up_words,
+                     const void* up_scales, const void* norm_weight, float eps, const void* bias, float alpha,
+                     float beta, void* y, int K, int N, int group, void* stream) {
+  if (!x || !words || !scales || !y) return fail(AOTO_ERR_ARGUMENT, "w8_gemv: null pointer");
+  if ((up_words == nullptr) != (up_scales == nullptr))
+    return fail(AOTO_ERR_ARGUMENT, "w8_gemv: paired projection needs both up_words and up_scales");
+  const bool paired = up_words != nullptr;
+  if (paired && bias != nullptr) return fail(AOTO_ERR_ARGUMENT, "w8_gemv: the paired epilogue takes no bias");
+  if (N <= 0 || K <= 0) return fail(AOTO_ERR_ARGUMENT, "w8_gemv: empty shape K=%d N=%d", K, N);
+  if (K % 16 != 0 || group <= 0 || group % 16 != 0 || K % group != 0 || K > 32768)
+    return fail(AOTO_ERR_UNSUPPORTED, "w8_gemv: needs K %% 16 == 0, group %% 16 == 0 dividing K, K <= 32768 "
+                "(K=%d group=%d)", K, group);
+  if (!aligned16(x) || !aligned16(words) || (up_words && !aligned16(up_words)) ||
+      (norm_weight && !aligned16(norm_weight)))
+    return fail(AOTO_ERR_ARGUMENT, "w8_gemv: x, words and norm weight must be 16-byte aligned");
+  // A wave holds R rows x U chunks of 16 codes per lane in flight: U covers the
+  // row's chunks in one pass where it can (up to 4), R fills the rest of 4.
+  const int chunks = K / 16;
+  const int u = chunks <= 64 ? 1 : (chunks <= 128 ? 2 : 4);
+  const int r = 4 / u;
+  const int waves_needed = (N + r - 1) / r;
+  const long long blocks_needed = (waves_needed + 3) / 4;
+  const long long cap = (long long)cu_count() * 4;
+  const unsigned blocks = (unsigned)(blocks_needed < cap ? blocks_needed : cap);
+  const unsigned shared = (unsigned)(chunks * 32 + chunks * 4);
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_w8_gemv_r%du%d_n%d_p%d_b%d", r, u, norm_weight != nullptr ? 1 : 0,
+           paired ? 1 : 0, bias != nullptr ? 1 : 0);
+  return launch(name, dim3(blocks), dim3(256), shared, stream, x, words, scales, up_words, up_scales,
+                norm_weight, eps, bias, alpha, beta, y, K, N, group);
 }
 
 int aoto_hip_rms_norm(const void* x, const void* weight, float eps, void* out, int rows, int hidden,

@@ -1,10 +1,11 @@
-// The gfx950 code object of the W4 decoder path: every kernel the C ABI
+// The gfx950 code object of the W4 (and W8) decoder path: every kernel the C ABI
 // (include/aoto_hip.h) launches, as extern "C" symbols looked up by name.
 #include "common.h"
 #include "w4_pack.h"
 #include "w4_gemv.h"
 #include "w4_gemv_stream.h"
 #include "w4_gemm.h"
+#include "w8.h"
 #include "decode.h"
 #include "prefill.h"
 #include "flash_attention.h"
@@ -42,11 +43,21 @@ AOTO_GEMV_STREAM_ARGMAX(32, 4, 8, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 1, 0, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 3, 0, true)
 
-// Prefill W4 GEMM: {n tiles per wave} x {m tiles per wave} x epilogue.
-AOTO_GEMM_EPILOGUES(1, 4)
-AOTO_GEMM_EPILOGUES(1, 8)
-AOTO_GEMM_EPILOGUES(2, 4)
-AOTO_GEMM_EPILOGUES(2, 8)
+// Prefill GEMM: {code width} x {n tiles per wave} x {m tiles per wave} x epilogue.
+AOTO_GEMM_EPILOGUES(4, 1, 4)
+AOTO_GEMM_EPILOGUES(4, 1, 8)
+AOTO_GEMM_EPILOGUES(4, 2, 4)
+AOTO_GEMM_EPILOGUES(4, 2, 8)
+AOTO_GEMM_EPILOGUES(8, 1, 4)
+AOTO_GEMM_EPILOGUES(8, 1, 8)
+AOTO_GEMM_EPILOGUES(8, 2, 4)
+AOTO_GEMM_EPILOGUES(8, 2, 8)
+
+// Eight-bit decode GEMV: {rows per wave} x {chunks per lane per pass}, with
+// the decoder's epilogues (rms-norm prologue, paired gate/up, bias/residual).
+AOTO_GEMV_W8_SHAPE(4, 1)
+AOTO_GEMV_W8_SHAPE(2, 2)
+AOTO_GEMV_W8_SHAPE(1, 4)
 
 // Single-query attention (plain and RoPE-fused ring step): head dim.
 AOTO_DECODE_ATTENTION_INSTANCE(64)

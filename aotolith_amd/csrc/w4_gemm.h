@@ -20,6 +20,10 @@
 // staged in LDS (rows padded by 16 B) and shared by the four waves; each wave
 // dequantizes only its own words, once, and reuses them for all TM row tiles
 // (TM = 8 keeps the dequant VALU work under the MFMA time).
+//
+// The eight-bit form (BITS = 8, the reference's quantize_bits=8 weights: four
+// codes per int32 word, byte k of word j = code 4j+k) is the same kernel with
+// two words (one 8-byte load) per lane operand instead of one.
 #pragma once
 
 #include "common.h"
@@ -40,14 +44,30 @@ AOTO_DEVICE bf16x8_v dequant_word(uint32_t w, float s) {
   return out;
 }
 
+// Eight bf16(code * s) values of two eight-bit words (bytes 0..3 of lo, then hi).
+AOTO_DEVICE bf16x8_v dequant_word(uint2 w, float s) {
+  bf16x8_v out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    out[j] = (__bf16)((float)((int)(w.x << (24 - 8 * j)) >> 24) * s);
+    out[4 + j] = (__bf16)((float)((int)(w.y << (24 - 8 * j)) >> 24) * s);
+  }
+  return out;
+}
+
+// The unit of packed weight that holds one lane's 8 consecutive codes.
+template <int BITS> struct GemmWord;
+template <> struct GemmWord<4> { using type = uint32_t; };
+template <> struct GemmWord<8> { using type = uint2; };
+
 constexpr int kGemmBK = 64;
 constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
 
 // Split-K: blockIdx.z selects the reduction slice [z*kslice, min(K, (z+1)*kslice));
 // with `partials` non-null the block stores its f32 tile to partials[z][m][n]
 // and aoto_w4_gemm_reduce applies the sum and the epilogue.
-template <int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE>
-__device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __restrict__ words,
+template <int BITS, int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE>
+__device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename GemmWord<BITS>::type* __restrict__ words,
                              const uint16_t* __restrict__ scales, const uint16_t* __restrict__ bias,
                              const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate,
                              uint16_t* __restrict__ Y, int M, int N, int K, int group, int kslice,
@@ -62,7 +82,8 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
   const int n_block = blockIdx.x * BN;
   const int m_block = blockIdx.y * BM;
   const int n_wave = n_block + wave * (16 * TN);
-  const int kw = K >> 3;           // words per weight row
+  using Word = typename GemmWord<BITS>::type;
+  const int kw = K >> 3;           // 8-code units per weight row
   const int groups = K / group;
   const int col = lane & 15;       // n (A) / m (B, C) within a tile
   const int quad = lane >> 4;      // k block of 8 (A, B) / n block of 4 (C)
@@ -79,7 +100,7 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
   for (int t = 0; t < TN; ++t) wrow[t] = min(n_wave + t * 16 + col, N - 1);
 
   uint4 xr[XPT];
-  uint32_t wr[TN][2];
+  Word wr[TN][2];
   auto load_x = [&](int k0) {
 #pragma unroll
     for (int v = 0; v < XPT; ++v) {
@@ -116,7 +137,7 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const uint32_t* __r
   for (int k0 = kb; k0 < ke; k0 += kGemmBK) {
     __syncthreads();
     store_x();
-    uint32_t wcur[TN][2];
+    Word wcur[TN][2];
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       wcur[t][0] = wr[t][0];
@@ -250,17 +271,18 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
 
 }  // namespace aoto
 
-#define AOTO_GEMM_INSTANCE(TN, TM, BIAS, RES, GATE)                                                        \
-  extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_n##TN##_m##TM##_b##BIAS##_r##RES##_g##GATE( \
-      const uint16_t* X, const uint32_t* words, const uint16_t* scales, const uint16_t* bias,              \
-      const uint16_t* residual, const uint16_t* gate, uint16_t* Y, int M, int N, int K, int group,          \
-      int kslice, float* partials) {                                                                        \
-    aoto::w4_gemm_body<TN, TM, BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K, group,  \
-                                                kslice, partials);                                          \
+#define AOTO_GEMM_INSTANCE(BITS, TN, TM, BIAS, RES, GATE)                                                  \
+  extern "C" __global__ __launch_bounds__(256) void                                                         \
+      aoto_w##BITS##_gemm_n##TN##_m##TM##_b##BIAS##_r##RES##_g##GATE(                                       \
+          const uint16_t* X, const aoto::GemmWord<BITS>::type* words, const uint16_t* scales,               \
+          const uint16_t* bias, const uint16_t* residual, const uint16_t* gate, uint16_t* Y, int M, int N,  \
+          int K, int group, int kslice, float* partials) {                                                  \
+    aoto::w4_gemm_body<BITS, TN, TM, BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K,   \
+                                                      group, kslice, partials);                             \
   }
 
-#define AOTO_GEMM_EPILOGUES(TN, TM)      \
-  AOTO_GEMM_INSTANCE(TN, TM, 0, 0, 0)    \
-  AOTO_GEMM_INSTANCE(TN, TM, 1, 0, 0)    \
-  AOTO_GEMM_INSTANCE(TN, TM, 0, 1, 0)    \
-  AOTO_GEMM_INSTANCE(TN, TM, 0, 0, 1)
+#define AOTO_GEMM_EPILOGUES(BITS, TN, TM)      \
+  AOTO_GEMM_INSTANCE(BITS, TN, TM, 0, 0, 0)    \
+  AOTO_GEMM_INSTANCE(BITS, TN, TM, 1, 0, 0)    \
+  AOTO_GEMM_INSTANCE(BITS, TN, TM, 0, 1, 0)    \
+  AOTO_GEMM_INSTANCE(BITS, TN, TM, 0, 0, 1)

@@ -1,4 +1,4 @@
-"""Static-KV-cache W4 decoder runtime for the hip-gfx950 target.
+"""Static-KV-cache W4 (and W8) decoder runtime for the hip-gfx950 target.
 
 The host-side mirror of the reference's static-cache adapter
 (``models/decoder.py``): the same cache ABI, the same plan pair per prompt
@@ -15,6 +15,9 @@ decode  (per layer)   W4 GEMV (norm prologue, bias) -> RoPE + KV append
                       -> split-K decode attention -> W4 GEMV (+residual)
                       -> paired gate/up W4 GEMV (norm, silu) -> W4 GEMV (+residual);
                       LM-head GEMV (norm), argmax.
+
+With ``quantize_bits=8`` every W4 kernel above is its eight-bit counterpart
+(int8 packer, GEMV and GEMM) and the LM head's argmax runs as its own kernel.
 
 ``decode_token`` keeps the reference's functional contract (the cache it
 returns is the input window rolled by one slot). ``greedy_generate`` runs the
@@ -175,11 +178,13 @@ def spec_from_model(model: torch.nn.Module, *, require: str | None = None) -> De
 # ----------------------------------------------------------------------------- state
 @dataclass
 class PackedWeight:
-    """A W4 weight in the reference's format: int32 words [N, K/8], bf16 scales [N, K/g]."""
+    """A packed weight in the reference's format: int32 words [N, K/8] (``bits=8``:
+    [N, K/4]), bf16 scales [N, K/g]."""
 
     packed: torch.Tensor
     scales: torch.Tensor
     group: int
+    bits: int = 4
 
     @property
     def out_features(self) -> int:
@@ -187,7 +192,7 @@ class PackedWeight:
 
     @property
     def in_features(self) -> int:
-        return int(self.packed.shape[1]) * 8
+        return int(self.packed.shape[1]) * ops.CODES_PER_WORD[self.bits]
 
     @property
     def nbytes(self) -> int:
@@ -226,6 +231,22 @@ class DecoderState:
         return out
 
     @property
+    def weights(self) -> list[PackedWeight]:
+        out = [self.lm_head]
+        for layer in self.layers:
+            out += [layer.qkv, layer.o, layer.gate, layer.up, layer.down]
+        return out
+
+    @property
+    def bits(self) -> int:
+        """The code width of every packed weight (4 or 8); mixed widths are refused."""
+
+        widths = {w.bits for w in self.weights}
+        if len(widths) != 1:
+            raise CompilationError(f"a decoder state packs every weight at one width, found {sorted(widths)}")
+        return widths.pop()
+
+    @property
     def nbytes(self) -> int:
         seen = {}
         for tensor in self.tensors():
@@ -242,18 +263,19 @@ def _device() -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
-def _pack(weight: torch.Tensor, group: int, device) -> PackedWeight:
+def _pack(weight: torch.Tensor, group: int, device, bits: int = 4) -> PackedWeight:
     w = weight.detach().to(device=device)
     if w.dtype not in (BF16, torch.float32):
         w = w.to(BF16)
-    packed, scales = ops.w4_quantize(w.contiguous(), group)
-    return PackedWeight(packed, scales, group)
+    packed, scales = ops.quantize(w.contiguous(), group, bits)
+    return PackedWeight(packed, scales, group, bits)
 
 
-def pack_model_state(model: torch.nn.Module, spec: DecoderSpec, group: int) -> DecoderState:
+def pack_model_state(model: torch.nn.Module, spec: DecoderSpec, group: int, bits: int = 4) -> DecoderState:
     """Pack an HF model's projections on the GPU (models/decoder.py:640-698).
 
-    The packer is the bit-exact gfx950 quantizer (symmetric int4, bf16 scales);
+    The packer is the bit-exact gfx950 quantizer (symmetric int4, or int8 with
+    ``bits=8`` as models/decoder.py:651 picks pack_weight_int8; bf16 scales);
     the q/k/v projections are concatenated into one packed weight, the embedding
     and norms stay bf16, and any bias besides q/k/v is refused.
     """
@@ -284,11 +306,11 @@ def pack_model_state(model: torch.nn.Module, spec: DecoderSpec, group: int) -> D
             bias = dev(torch.cat((attention.q_proj.bias, attention.k_proj.bias, attention.v_proj.bias), dim=0))
         layers.append(
             LayerState(
-                qkv=_pack(qkv, group, device),
-                o=_pack(attention.o_proj.weight, group, device),
-                gate=_pack(mlp.gate_proj.weight, group, device),
-                up=_pack(mlp.up_proj.weight, group, device),
-                down=_pack(mlp.down_proj.weight, group, device),
+                qkv=_pack(qkv, group, device, bits),
+                o=_pack(attention.o_proj.weight, group, device, bits),
+                gate=_pack(mlp.gate_proj.weight, group, device, bits),
+                up=_pack(mlp.up_proj.weight, group, device, bits),
+                down=_pack(mlp.down_proj.weight, group, device, bits),
                 input_norm=dev(layer.input_layernorm.weight),
                 post_norm=dev(layer.post_attention_layernorm.weight),
                 qkv_bias=bias,
@@ -300,13 +322,13 @@ def pack_model_state(model: torch.nn.Module, spec: DecoderSpec, group: int) -> D
     return DecoderState(
         embed=dev(model.model.embed_tokens.weight),
         final_norm=dev(model.model.norm.weight),
-        lm_head=_pack(model.lm_head.weight, group, device),
+        lm_head=_pack(model.lm_head.weight, group, device, bits),
         layers=layers,
     )
 
 
 def random_state(spec: DecoderSpec, group: int = 64, *, seed: int = 0, std: float = 0.02,
-                 norm_std: float = 0.0) -> DecoderState:
+                 norm_std: float = 0.0, bits: int = 4) -> DecoderState:
     """A seeded random-init state built directly on the GPU, one tensor at a time.
 
     Weights and biases ~ N(0, std) in bf16 (q/k/v biases seeded, unlike HF's
@@ -328,7 +350,7 @@ def random_state(spec: DecoderSpec, group: int = 64, *, seed: int = 0, std: floa
 
     def packed(n, k):
         w = normal(n, k)
-        out = _pack(w, group, device)
+        out = _pack(w, group, device, bits)
         del w
         return out
 
@@ -348,7 +370,7 @@ def random_state(spec: DecoderSpec, group: int = 64, *, seed: int = 0, std: floa
             )
         )
     embed = normal(spec.vocab, h)
-    lm_head = _pack(embed, group, device) if spec.tied else packed(spec.vocab, h)
+    lm_head = _pack(embed, group, device, bits) if spec.tied else packed(spec.vocab, h)
     return DecoderState(embed=embed, final_norm=norm(h), lm_head=lm_head, layers=layers)
 
 
@@ -404,8 +426,8 @@ def _sel(index: int, op: str, output: str, kind: str, reason: str, artifact: str
     )
 
 
-def _gemv_symbol(norm: bool, paired: bool, bias: bool) -> str:
-    return f"aoto_w4_gemv_n{int(norm)}_p{int(paired)}_b{int(bias)}"
+def _gemv_symbol(norm: bool, paired: bool, bias: bool, bits: int = 4) -> str:
+    return f"aoto_w{bits}_gemv_n{int(norm)}_p{int(paired)}_b{int(bias)}"
 
 
 def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
@@ -430,59 +452,63 @@ def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
         )
 
 
-def decode_selections(spec: DecoderSpec) -> tuple[KernelSelection, ...]:
+def decode_selections(spec: DecoderSpec, bits: int = 4) -> tuple[KernelSelection, ...]:
     """The decode plan's nodes after the reference's fusions (passes/fusion.py, passes/cache.py)."""
 
+    w, kind = f"W{bits}", f"w{bits}_gemv"
     out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather by device token", "aoto_embedding")]
     g = spec.heads // spec.kv_heads
     for layer in range(spec.layers):
         base = len(out)
         out += [
-            _sel(base, "addmm", f"qkv_{layer}", "w4_gemv",
-                 "packed W4 GEMV (M=1) with RMSNorm prologue" + (" and q/k/v bias epilogue" if spec.qkv_bias else ""),
-                 _gemv_symbol(True, False, spec.qkv_bias)),
+            _sel(base, "addmm", f"qkv_{layer}", kind,
+                 f"packed {w} GEMV (M=1) with RMSNorm prologue"
+                 + (" and q/k/v bias epilogue" if spec.qkv_bias else ""),
+                 _gemv_symbol(True, False, spec.qkv_bias, bits)),
             _sel(base + 1, "rope_kv_cache_append", f"query_{layer}", "rope_kv_append",
                  "rotates q/k and appends (k, v) to the layer's cache window", "aoto_rope_kv_append"),
             _sel(base + 2, "attention", f"attention_{layer}", "decode_attention",
                  f"single-query GQA ({g} query heads per kv head), one block per query head, split-K merge "
                  "for long windows", f"aoto_decode_attention_d{spec.head_dim}"),
-            _sel(base + 3, "addmm", f"hidden_{layer}a", "w4_gemv", "packed W4 GEMV with residual epilogue",
-                 _gemv_symbol(False, False, True)),
-            _sel(base + 4, "matmul", f"mlp_{layer}", "w4_gemv",
-                 "paired gate/up W4 GEMV with RMSNorm prologue and silu_mul_paired epilogue",
-                 _gemv_symbol(True, True, False)),
-            _sel(base + 5, "addmm", f"hidden_{layer}b", "w4_gemv", "packed W4 GEMV with residual epilogue",
-                 _gemv_symbol(False, False, True)),
+            _sel(base + 3, "addmm", f"hidden_{layer}a", kind, f"packed {w} GEMV with residual epilogue",
+                 _gemv_symbol(False, False, True, bits)),
+            _sel(base + 4, "matmul", f"mlp_{layer}", kind,
+                 f"paired gate/up {w} GEMV with RMSNorm prologue and silu_mul_paired epilogue",
+                 _gemv_symbol(True, True, False, bits)),
+            _sel(base + 5, "addmm", f"hidden_{layer}b", kind, f"packed {w} GEMV with residual epilogue",
+                 _gemv_symbol(False, False, True, bits)),
         ]
     n = len(out)
-    out.append(_sel(n, "matmul", "logits", "w4_gemv", "LM-head W4 GEMV with final RMSNorm prologue",
-                    _gemv_symbol(True, False, False)))
+    out.append(_sel(n, "matmul", "logits", kind, f"LM-head {w} GEMV with final RMSNorm prologue",
+                    _gemv_symbol(True, False, False, bits)))
     return tuple(out)
 
 
-def prefill_selections(spec: DecoderSpec) -> tuple[KernelSelection, ...]:
+def prefill_selections(spec: DecoderSpec, bits: int = 4) -> tuple[KernelSelection, ...]:
+    w, kind, gemm = f"W{bits}", f"w{bits}_gemm", f"aoto_w{bits}_gemm"
     out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather", "aoto_embedding")]
     for layer in range(spec.layers):
         base = len(out)
         out += [
             _sel(base, "rms_norm", f"norm_{layer}a", "rms_norm", "row RMSNorm", "aoto_rms_norm"),
-            _sel(base + 1, "addmm" if spec.qkv_bias else "matmul", f"qkv_{layer}", "w4_gemm",
-                 "fused-dequant W4 GEMM on bf16 MFMA" + (" with q/k/v bias epilogue" if spec.qkv_bias else ""),
-                 "aoto_w4_gemm"),
+            _sel(base + 1, "addmm" if spec.qkv_bias else "matmul", f"qkv_{layer}", kind,
+                 f"fused-dequant {w} GEMM on bf16 MFMA" + (" with q/k/v bias epilogue" if spec.qkv_bias else ""),
+                 gemm),
             _sel(base + 2, "rope", f"rope_{layer}", "rope_qkv_prefill",
                  "RoPE of q and k fused with the layer's cache fill", "aoto_rope_qkv_prefill"),
             _sel(base + 3, "attention", f"attention_{layer}", "flash_attention",
                  "causal + left-pad masked GQA flash attention on MFMA",
                  f"aoto_flash_attention_d{spec.head_dim}"),
-            _sel(base + 4, "addmm", f"hidden_{layer}a", "w4_gemm", "W4 GEMM with residual epilogue", "aoto_w4_gemm"),
+            _sel(base + 4, "addmm", f"hidden_{layer}a", kind, f"{w} GEMM with residual epilogue", gemm),
             _sel(base + 5, "rms_norm", f"norm_{layer}b", "rms_norm", "row RMSNorm", "aoto_rms_norm"),
-            _sel(base + 6, "matmul", f"gate_{layer}", "w4_gemm", "W4 GEMM", "aoto_w4_gemm"),
-            _sel(base + 7, "matmul", f"up_{layer}", "w4_gemm", "W4 GEMM with silu_mul epilogue", "aoto_w4_gemm"),
-            _sel(base + 8, "addmm", f"hidden_{layer}b", "w4_gemm", "W4 GEMM with residual epilogue", "aoto_w4_gemm"),
+            _sel(base + 6, "matmul", f"gate_{layer}", kind, f"{w} GEMM", gemm),
+            _sel(base + 7, "matmul", f"up_{layer}", kind, f"{w} GEMM with silu_mul epilogue", gemm),
+            _sel(base + 8, "addmm", f"hidden_{layer}b", kind, f"{w} GEMM with residual epilogue", gemm),
         ]
     n = len(out)
-    out.append(_sel(n, "matmul", "logits", "w4_gemv", "LM-head W4 GEMV on the last row with final RMSNorm prologue",
-                    _gemv_symbol(True, False, False)))
+    out.append(_sel(n, "matmul", "logits", f"w{bits}_gemv",
+                    f"LM-head {w} GEMV on the last row with final RMSNorm prologue",
+                    _gemv_symbol(True, False, False, bits)))
     return tuple(out)
 
 
@@ -547,7 +573,8 @@ class _Engine:
         # GEMV + argmax + step advance + embedding), when the LM-head shape has
         # the fused form.
         head = self.state.lm_head
-        self.key_count = ops.argmax_key_count(s.hidden, head.packed.shape[0], head.group)
+        self.key_count = (ops.argmax_key_count(s.hidden, head.packed.shape[0], head.group)
+                          if head.bits == 4 else 0)
         self.keys = (torch.empty((self.key_count,), dtype=torch.int64, device=dev) if self.key_count else None)
         # cos/sin rows of the current decode position, kept by the finish kernel,
         # so attention does not wait for the step state before its table loads
@@ -570,7 +597,13 @@ class _Engine:
 
     # -- decode -----------------------------------------------------------------
     def _gemv(self, x, w: PackedWeight, out, **kwargs):
-        return ops.w4_gemv(x, w.packed, w.scales, w.group, out=out, **kwargs)
+        gemv = ops.w4_gemv if w.bits == 4 else ops.w8_gemv
+        return gemv(x, w.packed, w.scales, w.group, out=out, **kwargs)
+
+    @staticmethod
+    def _matmul(x, w: PackedWeight, **kwargs):
+        matmul = ops.w4_matmul if w.bits == 4 else ops.w8_matmul
+        return matmul(x, w.packed, w.scales, w.group, **kwargs)
 
     def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool, lm_head: bool = True):
         """Run the per-layer decode kernels (and the LM head); ``hidden`` holds the embedded token."""
@@ -789,8 +822,7 @@ class _Engine:
         ops.embedding(self.state.embed, ids.reshape(-1), out=x)
         for index, layer in enumerate(self.state.layers):
             ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
-            ops.w4_matmul(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, bias=layer.qkv_bias,
-                          out=qkv.view(m, -1))
+            self._matmul(xn, layer.qkv, bias=layer.qkv_bias, out=qkv.view(m, -1))
             pair = pair_of(index)
             ops.rope_qkv_prefill(qkv, positions.reshape(1, -1), self.cos, self.sin, pair, query_heads=s.heads,
                                  kv_heads=s.kv_heads, head_dim=s.head_dim, slot0=slot0, zero_prefix=True, q_out=q)
@@ -800,11 +832,11 @@ class _Engine:
                 ops.prefill_attention(q, keys, values, mask=mask, scale=self.scale, out=attn)
             else:
                 ops.prefill_attention(q, keys, values, causal=True, key_start=key_start, scale=self.scale, out=attn)
-            ops.w4_matmul(attn.view(m, -1), layer.o.packed, layer.o.scales, layer.o.group, residual=x, out=x)
+            self._matmul(attn.view(m, -1), layer.o, residual=x, out=x)
             ops.rms_norm(x, layer.post_norm, s.eps, out=xn)
-            ops.w4_matmul(xn, layer.gate.packed, layer.gate.scales, layer.gate.group, out=gate)
-            ops.w4_matmul(xn, layer.up.packed, layer.up.scales, layer.up.group, gate=gate, out=act)
-            ops.w4_matmul(act, layer.down.packed, layer.down.scales, layer.down.group, residual=x, out=x)
+            self._matmul(xn, layer.gate, out=gate)
+            self._matmul(xn, layer.up, gate=gate, out=act)
+            self._matmul(act, layer.down, residual=x, out=x)
         logits = torch.empty((1, 1, s.vocab), dtype=BF16, device=dev)
         self._gemv(x[m - 1], self.state.lm_head, logits.view(-1), norm_weight=self.state.final_norm, eps=s.eps)
         return logits
@@ -856,6 +888,7 @@ class DecoderStaticCacheRuntime:
     spec: DecoderSpec
     engine: _Engine
     group_size: int
+    quantize_bits: int = 4
 
     # -- reference API -----------------------------------------------------------
     def prefill_ids(self, input_ids):
@@ -1030,8 +1063,9 @@ def _build_plans(spec: DecoderSpec, engine: _Engine, prompt_length: int):
             raise PlanInputError(f"expected a bf16 device cache of shape {expected}, got {tuple(cache.shape)}")
         return engine.decode_functional(token, cache.contiguous(), int(valid_length))
 
-    p_sel = prefill_selections(spec)
-    d_sel = decode_selections(spec)
+    bits = engine.state.bits
+    p_sel = prefill_selections(spec, bits)
+    d_sel = decode_selections(spec, bits)
     require_native(p_sel, "prefill plan")
     require_native(d_sel, "decode plan")
     prefill = CompiledPlan("prefill", tuple(PlanNode(s) for s in p_sel), run_prefill,
@@ -1073,13 +1107,16 @@ def compile_decoder_state(
             f"prompt_length + max_new_tokens exceeds the model's maximum position embeddings ({spec.max_position})"
         )
     _check_kernel_limits(spec, group_size)
+    bits = state.bits
+    if any(w.group != group_size for w in state.weights):
+        raise CompilationError(f"the state's packed weights are not all grouped by {group_size}")
     engine = _Engine(spec, state, prompt_length, capacity, _device(), attention_splits)
     prefill, decode = _build_plans(spec, engine, prompt_length)
     runtime = DecoderStaticCacheRuntime(
         prefill=prefill, decode=decode, prompt_length=prompt_length, max_new_tokens=max_new_tokens,
         cache_capacity=capacity, num_layers=spec.layers, num_key_value_heads=spec.kv_heads,
         head_dim=spec.head_dim, family=spec.family, memory=memory, spec=spec, engine=engine,
-        group_size=group_size,
+        group_size=group_size, quantize_bits=bits,
     )
     prefill.runtime = runtime
     decode.runtime = runtime
@@ -1087,15 +1124,16 @@ def compile_decoder_state(
 
 
 def _check_quantize(quantize: int | None, quantize_bits: int) -> int:
+    """``quantize`` is the group size and ``quantize_bits`` the width (models/decoder.py:1406-1425)."""
+
     if quantize_bits not in (4, 8):
-        raise CompilationError(f"quantize_bits must be 4 or 8, got {quantize_bits!r}")
+        raise CompilationError(f"quantize_bits must be 4 or 8, got {quantize_bits!r}",
+                               hint="four bits packs eight codes a word, eight bits packs four")
     if quantize is None:
         raise CompilationError(
-            f"the {TARGET} target compiles the weight-only W4 path: pass quantize=<group size> (e.g. 64)",
+            f"the {TARGET} target compiles the weight-only packed path: pass quantize=<group size> (e.g. 64)",
             hint="dense bf16 projections are not part of this backend",
         )
-    if quantize_bits != 4:
-        raise CompilationError(f"the {TARGET} target packs 4-bit weights; quantize_bits={quantize_bits}")
     return int(quantize)
 
 
@@ -1126,7 +1164,7 @@ def compile_decoder_static_cache(
             f"({spec.max_position})"
         )
     _check_kernel_limits(spec, group)
-    state = pack_model_state(model, spec, group)
+    state = pack_model_state(model, spec, group, quantize_bits)
     return compile_decoder_state(spec, state, prompt_length=prompt_length, max_new_tokens=max_new_tokens,
                                  group_size=group, memory=memory)
 
@@ -1233,6 +1271,6 @@ def compile_decoder_bucketed(
     widths = [int(w) for w in prompt_lengths]
     if widths and widths[-1] + max_new_tokens > spec.max_position:
         raise DynamicShapeError("the largest bucket + max_new_tokens exceeds the maximum position embeddings")
-    state = pack_model_state(model, spec, group)
+    state = pack_model_state(model, spec, group, quantize_bits)
     return compile_decoder_bucketed_state(spec, state, prompt_lengths=widths, max_new_tokens=max_new_tokens,
                                           group_size=group)

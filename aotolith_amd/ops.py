@@ -42,26 +42,26 @@ def _ready(tensor: torch.Tensor) -> None:
     _lib.ensure_code_object(tensor.device.index)
 
 
-def w4_quantize(weight: torch.Tensor, group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
-    """Pack a ``[out, in]`` bf16/f32 weight: ``(int32 [out, in/8], bf16 scales [out, in/group])``.
+#: codes per packed int32 word of each width
+CODES_PER_WORD = {4: 8, 8: 4}
 
-    Bit-exact with the reference packer (``quantize.py:95-152``,
-    ``models/quantized.py:133-163``).
-    """
 
+def _quantize(weight: torch.Tensor, group_size: int, bits: int) -> tuple[torch.Tensor, torch.Tensor]:
+    per_word = CODES_PER_WORD[bits]
     if weight.dim() != 2:
         raise ValueError(f"a quantized weight must be 2-D, got {tuple(weight.shape)}")
     if weight.dtype not in (BF16, torch.float32):
         raise TypeError(f"weight must be bf16 or f32, got {weight.dtype}")
     _expect(weight, "weight", weight.dtype)
     rows, inner = weight.shape
-    if group_size <= 0 or group_size % 8 or inner % group_size:
-        raise ValueError(f"group size {group_size} must be a positive multiple of 8 dividing {inner}")
+    if group_size <= 0 or group_size % per_word or inner % group_size:
+        raise ValueError(f"group size {group_size} must be a positive multiple of {per_word} dividing {inner}")
     _ready(weight)
-    packed = torch.empty((rows, inner // 8), dtype=torch.int32, device=weight.device)
+    packed = torch.empty((rows, inner // per_word), dtype=torch.int32, device=weight.device)
     scales = torch.empty((rows, inner // group_size), dtype=BF16, device=weight.device)
+    entry = _lib.library().aoto_hip_w4_quantize if bits == 4 else _lib.library().aoto_hip_w8_quantize
     _lib.check(
-        _lib.library().aoto_hip_w4_quantize(
+        entry(
             _ptr(weight), int(weight.dtype == torch.float32), rows, inner, group_size,
             _ptr(packed), _ptr(scales), None, _stream(),
         )
@@ -69,52 +69,83 @@ def w4_quantize(weight: torch.Tensor, group_size: int = 64) -> tuple[torch.Tenso
     return packed, scales
 
 
-def w4_dequantize(packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
-    """``bf16(code * scale)`` ``[out, in]`` (``models/quantized.py:61-82``)."""
+def w4_quantize(weight: torch.Tensor, group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Pack a ``[out, in]`` bf16/f32 weight: ``(int32 [out, in/8], bf16 scales [out, in/group])``.
 
+    Bit-exact with the reference packer (``quantize.py:95-152``,
+    ``models/quantized.py:133-163``).
+    """
+
+    return _quantize(weight, group_size, 4)
+
+
+def w8_quantize(weight: torch.Tensor, group_size: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """Eight-bit pack: ``(int32 [out, in/4], bf16 scales [out, in/group])``.
+
+    Bit-exact with ``quantize_int8`` (``quantize.py:155-172``) and
+    ``pack_weight_int8`` (``models/quantized.py:166-172``).
+    """
+
+    return _quantize(weight, group_size, 8)
+
+
+def quantize(weight: torch.Tensor, group_size: int = 64, bits: int = 4) -> tuple[torch.Tensor, torch.Tensor]:
+    """:func:`w4_quantize` or :func:`w8_quantize` by width."""
+
+    if bits not in CODES_PER_WORD:
+        raise ValueError(f"bits must be 4 or 8, got {bits!r}")
+    return _quantize(weight, group_size, bits)
+
+
+def _dequantize(packed: torch.Tensor, scales: torch.Tensor, group_size: int, bits: int) -> torch.Tensor:
     _expect(packed, "packed", torch.int32)
     if packed.dim() != 2:
         raise ValueError("packed must be 2-D")
     rows, words = packed.shape
-    inner = words * 8
+    inner = words * CODES_PER_WORD[bits]
+    if group_size <= 0 or inner % group_size:
+        raise ValueError(f"group size {group_size} does not divide {inner}")
     _expect(scales, "scales", BF16, (rows, inner // group_size))
     _ready(packed)
     out = torch.empty((rows, inner), dtype=BF16, device=packed.device)
-    _lib.check(
-        _lib.library().aoto_hip_w4_dequantize(
-            _ptr(packed), _ptr(scales), rows, inner, group_size, _ptr(out), _stream()
-        )
-    )
+    entry = _lib.library().aoto_hip_w4_dequantize if bits == 4 else _lib.library().aoto_hip_w8_dequantize
+    _lib.check(entry(_ptr(packed), _ptr(scales), rows, inner, group_size, _ptr(out), _stream()))
     return out
 
 
-def w4_gemv(
+def w4_dequantize(packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
+    """``bf16(code * scale)`` ``[out, in]`` (``models/quantized.py:61-82``)."""
+
+    return _dequantize(packed, scales, group_size, 4)
+
+
+def w8_dequantize(packed: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
+    """``bf16(code * scale)`` of an eight-bit pack (``models/quantized.py:84-107``)."""
+
+    return _dequantize(packed, scales, group_size, 8)
+
+
+def _gemv(
+    bits: int,
     x: torch.Tensor,
     packed: torch.Tensor,
     scales: torch.Tensor,
     group_size: int,
-    *,
-    norm_weight: torch.Tensor | None = None,
-    eps: float = 1e-6,
-    bias: torch.Tensor | None = None,
-    alpha: float = 1.0,
-    beta: float = 1.0,
-    up: tuple[torch.Tensor, torch.Tensor] | None = None,
-    out: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None,
+    eps: float,
+    bias: torch.Tensor | None,
+    alpha: float,
+    beta: float,
+    up: tuple[torch.Tensor, torch.Tensor] | None,
+    out: torch.Tensor | None,
     lanes_per_row: int = 0,
 ) -> torch.Tensor:
-    """Decode GEMV ``y[N] = W4[N, K] @ x[K]`` with the fused prologue/epilogues.
-
-    ``norm_weight``: RMSNorm prologue; ``bias``: addmm epilogue
-    ``bf16(beta * bias + alpha * acc)``; ``up``: ``(packed, scales)`` of the up
-    projection for the paired ``silu_mul`` epilogue (``packed`` is then gate).
-    """
-
+    per_word = CODES_PER_WORD[bits]
     _expect(packed, "packed", torch.int32)
     if packed.dim() != 2:
-        raise ValueError("packed must be 2-D [N, K/8]")
+        raise ValueError(f"packed must be 2-D [N, K/{per_word}]")
     n, words = packed.shape
-    k = words * 8
+    k = words * per_word
     if x.numel() != k:
         raise ValueError(f"x has {x.numel()} elements, the weight reduces over {k}")
     _expect(x, "x", BF16)
@@ -141,18 +172,116 @@ def w4_gemv(
         if out.numel() != n:
             raise ValueError(f"out has {out.numel()} elements, expected {n}")
     _ready(x)
-    _lib.check(
-        _lib.library().aoto_hip_w4_gemv(
-            _ptr(x), _ptr(packed), _ptr(scales), _ptr(up_packed), _ptr(up_scales), _ptr(norm_weight),
-            float(eps), _ptr(bias), float(alpha), float(beta), _ptr(out), k, n, group_size,
-            int(lanes_per_row), _stream(),
-        )
-    )
+    lib = _lib.library()
+    args = (_ptr(x), _ptr(packed), _ptr(scales), _ptr(up_packed), _ptr(up_scales), _ptr(norm_weight),
+            float(eps), _ptr(bias), float(alpha), float(beta), _ptr(out), k, n, group_size)
+    if bits == 4:
+        _lib.check(lib.aoto_hip_w4_gemv(*args, int(lanes_per_row), _stream()))
+    else:
+        _lib.check(lib.aoto_hip_w8_gemv(*args, _stream()))
     return out
+
+
+def w4_gemv(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    *,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
+    bias: torch.Tensor | None = None,
+    alpha: float = 1.0,
+    beta: float = 1.0,
+    up: tuple[torch.Tensor, torch.Tensor] | None = None,
+    out: torch.Tensor | None = None,
+    lanes_per_row: int = 0,
+) -> torch.Tensor:
+    """Decode GEMV ``y[N] = W4[N, K] @ x[K]`` with the fused prologue/epilogues.
+
+    ``norm_weight``: RMSNorm prologue; ``bias``: addmm epilogue
+    ``bf16(beta * bias + alpha * acc)``; ``up``: ``(packed, scales)`` of the up
+    projection for the paired ``silu_mul`` epilogue (``packed`` is then gate).
+    """
+
+    return _gemv(4, x, packed, scales, group_size, norm_weight, eps, bias, alpha, beta, up, out, lanes_per_row)
+
+
+def w8_gemv(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    *,
+    norm_weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
+    bias: torch.Tensor | None = None,
+    alpha: float = 1.0,
+    beta: float = 1.0,
+    up: tuple[torch.Tensor, torch.Tensor] | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`w4_gemv` over an eight-bit pack ``int32 [N, K/4]``
+    (``codegen/matmul.py:742-929``)."""
+
+    return _gemv(8, x, packed, scales, group_size, norm_weight, eps, bias, alpha, beta, up, out)
 
 
 def _i64(tensor: torch.Tensor, name: str) -> None:
     _expect(tensor, name, torch.int64)
+
+
+def _matmul(
+    bits: int,
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    bias: torch.Tensor | None,
+    residual: torch.Tensor | None,
+    gate: torch.Tensor | None,
+    out: torch.Tensor | None,
+    tile: int,
+    splits: int,
+    workspace: torch.Tensor | None,
+) -> torch.Tensor:
+    per_word = CODES_PER_WORD[bits]
+    _expect(packed, "packed", torch.int32)
+    if packed.dim() != 2:
+        raise ValueError(f"packed must be 2-D [N, K/{per_word}]")
+    n, words = packed.shape
+    k = words * per_word
+    _expect(x, "x", BF16)
+    if x.shape[-1] != k:
+        raise ValueError(f"x has last dimension {x.shape[-1]}, the weight reduces over {k}")
+    m = x.numel() // k
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"group size {group_size} does not divide K={k}")
+    _expect(scales, "scales", BF16, (n, k // group_size))
+    for name, tensor, numel in (("bias", bias, n), ("residual", residual, m * n), ("gate", gate, m * n)):
+        if tensor is not None:
+            _expect(tensor, name, BF16)
+            if tensor.numel() != numel:
+                raise ValueError(f"{name} has {tensor.numel()} elements, expected {numel}")
+    shape = tuple(x.shape[:-1]) + (n,)
+    if out is None:
+        out = torch.empty(shape, dtype=BF16, device=x.device)
+    else:
+        _expect(out, "out", BF16)
+        if out.numel() != m * n:
+            raise ValueError(f"out has {out.numel()} elements, expected {m * n}")
+    _ready(x)
+    need = gemm_workspace_bytes(m, n, k, tile, splits)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
+    entry = _lib.library().aoto_hip_w4_gemm if bits == 4 else _lib.library().aoto_hip_w8_gemm
+    _lib.check(
+        entry(
+            _ptr(x), _ptr(packed), _ptr(scales), _ptr(bias), _ptr(residual), _ptr(gate), _ptr(out),
+            m, n, k, group_size, int(tile), int(splits), _ptr(workspace if need else None), _stream(),
+        )
+    )
+    return out
 
 
 def w4_matmul(
@@ -175,39 +304,26 @@ def w4_matmul(
     (``silu_mul``: ``bf16(acc * silu(gate))``), as the reference's prefill GEMM.
     """
 
-    _expect(packed, "packed", torch.int32)
-    if packed.dim() != 2:
-        raise ValueError("packed must be 2-D [N, K/8]")
-    n, words = packed.shape
-    k = words * 8
-    _expect(x, "x", BF16)
-    if x.shape[-1] != k:
-        raise ValueError(f"x has last dimension {x.shape[-1]}, the weight reduces over {k}")
-    m = x.numel() // k
-    _expect(scales, "scales", BF16, (n, k // group_size))
-    for name, tensor, numel in (("bias", bias, n), ("residual", residual, m * n), ("gate", gate, m * n)):
-        if tensor is not None:
-            _expect(tensor, name, BF16)
-            if tensor.numel() != numel:
-                raise ValueError(f"{name} has {tensor.numel()} elements, expected {numel}")
-    shape = tuple(x.shape[:-1]) + (n,)
-    if out is None:
-        out = torch.empty(shape, dtype=BF16, device=x.device)
-    else:
-        _expect(out, "out", BF16)
-        if out.numel() != m * n:
-            raise ValueError(f"out has {out.numel()} elements, expected {m * n}")
-    _ready(x)
-    need = gemm_workspace_bytes(m, n, k, tile, splits)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
-    _lib.check(
-        _lib.library().aoto_hip_w4_gemm(
-            _ptr(x), _ptr(packed), _ptr(scales), _ptr(bias), _ptr(residual), _ptr(gate), _ptr(out),
-            m, n, k, group_size, int(tile), int(splits), _ptr(workspace if need else None), _stream(),
-        )
-    )
-    return out
+    return _matmul(4, x, packed, scales, group_size, bias, residual, gate, out, tile, splits, workspace)
+
+
+def w8_matmul(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    *,
+    bias: torch.Tensor | None = None,
+    residual: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    tile: int = 0,
+    splits: int = 0,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`w4_matmul` over an eight-bit pack ``int32 [N, K/4]``."""
+
+    return _matmul(8, x, packed, scales, group_size, bias, residual, gate, out, tile, splits, workspace)
 
 
 def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:

@@ -11,7 +11,9 @@
  *
  * bf16 tensors are passed as void* to 16-bit storage; int4 weights are the
  * reference's packed format: int32 words [N, K/8] (code 8j+k of a row at bits 4k
- * of word j, two's complement) with bf16 group scales [N, K/group].
+ * of word j, two's complement) with bf16 group scales [N, K/group]. int8
+ * weights (the aoto_hip_w8_* entry points) are int32 words [N, K/4], code 4j+k
+ * at bits 8k of word j, with the same bf16 group scales.
  *
  * Each declaration cites the reference (aotolith 0.68.0, src/aotolith/...)
  * interface it replaces: there, every kernel is an MSL source string emitted per
@@ -33,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 7
+#define AOTO_HIP_ABI_VERSION 8
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -107,6 +109,38 @@ int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, co
 /* Bytes of split-K workspace aoto_hip_w4_gemm needs for these arguments (0 when
  * it does not split). */
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits);
+
+/* Symmetric int8 group quantizer + packer, bit-exact with quantize.py:155-172
+ * (quantize_int8: scale = max|w| / 127, an all-zero group 1/127, codes
+ * clip(rint(w / scale), -128, 127)) and the bf16 scale cast of
+ * models/quantized.py:133-172 (pack_weight_int8). Arguments as
+ * aoto_hip_w4_quantize; group % 4 == 0. packed: int32 [rows, inner/4]. */
+int aoto_hip_w8_quantize(const void* weight, int weight_is_f32, int rows, int inner, int group,
+                         int32_t* packed, void* scales_bf16, float* scales_f32, void* stream);
+
+/* bf16(code * scale) of an int8 pack: the dequantize_i8 op in the scales'
+ * dtype (models/quantized.py:84-107; Metal kernel codegen/quantize.py:66-99,
+ * 155-190). out: bf16 [rows, inner], 8-byte aligned. */
+int aoto_hip_w8_dequantize(const int32_t* packed, const void* scales, int rows, int inner,
+                           int group, void* out, void* stream);
+
+/* Decode GEMV over a packed int8 weight, one activation row (M == 1): the
+ * eight-bit emitter _emit_quantized_gemv_int8_source (codegen/matmul.py:742-929)
+ * with the same prologue and epilogues as aoto_hip_w4_gemv (words are int32
+ * [N, K/4]). Limits: K % 16 == 0, group % 16 == 0 dividing K, K <= 32768. */
+int aoto_hip_w8_gemv(const void* x, const int32_t* words, const void* scales,
+                     const int32_t* up_words, const void* up_scales, const void* norm_weight,
+                     float eps, const void* bias, float alpha, float beta, void* y, int K, int N,
+                     int group, void* stream);
+
+/* Prefill GEMM over a packed int8 weight: aoto_hip_w4_gemm with words int32
+ * [N, K/4] (8-byte aligned); the reference's prefill pair for eight bits is
+ * dequantize_i8 (codegen/quantize.py:155-190) feeding the same tiled GEMM.
+ * Same limits, tile codes, split-K and workspace (aoto_hip_w4_gemm_workspace()
+ * bytes: the plan does not depend on the code width). */
+int aoto_hip_w8_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
+                     const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                     int tile, int splits, void* workspace, void* stream);
 
 /* Row RMSNorm, out = bf16((x * rsqrt(mean(x^2) + eps)) * weight) over [rows, hidden]
  * (codegen/norm.py:75-323, _compile_normalization(kind="rms_norm");

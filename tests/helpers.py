@@ -81,15 +81,16 @@ def random_oracle_state(shape, seed: int = 0, *, std: float = 0.02, norm_std: fl
     dropped or misplaced term changes the outputs (HF's init would zero them).
     """
 
-    from oracle.quant import pack_weight_bf16
+    from oracle.quant import pack_weight_bits_bf16
 
     rng = np.random.default_rng(seed)
     g = shape.group_size
+    bits = getattr(shape, "bits", 4)
     h, i, w = shape.hidden, shape.intermediate, shape.qkv_width
     hd = shape.heads * shape.head_dim
 
     def packed(n, k):
-        return pack_weight_bf16(bf16_normal(rng, (n, k), std), g)
+        return pack_weight_bits_bf16(bf16_normal(rng, (n, k), std), g, bits)
 
     def norm(n):
         return round_bf16(np.float32(1.0) + rng.standard_normal(n).astype(np.float32) * np.float32(norm_std))
@@ -112,13 +113,13 @@ def random_oracle_state(shape, seed: int = 0, *, std: float = 0.02, norm_std: fl
     return {"embed": embed, "final_norm": norm(h), "lm_head": packed(shape.vocab, h), "layers": layers}
 
 
-def state_to_device(ostate: dict, group: int):
+def state_to_device(ostate: dict, group: int, bits: int = 4):
     """Upload an oracle-format state as the runtime's device state (same bits)."""
 
     from aotolith_amd.decoder import DecoderState, LayerState, PackedWeight
 
     def pw(pair):
-        return PackedWeight(torch.from_numpy(pair[0]).cuda(), to_gpu_bits(pair[1]), group)
+        return PackedWeight(torch.from_numpy(pair[0]).cuda(), to_gpu_bits(pair[1]), group, bits)
 
     layers = [
         LayerState(
