@@ -2,9 +2,10 @@
 
 Target name: ``"hip-gfx950"``. Kernels are hand-written HIP for CDNA4, built into
 one gfx950 code object and reached through the C ABI of ``include/aoto_hip.h``
-from torch-ROCm tensors. The public names mirror the reference's static-cache
-API (``compile_qwen2_static_cache``, ``compile_llama_static_cache`` and their
-bucketed forms) with ``target="hip-gfx950"``.
+from torch-ROCm tensors. The public names mirror the reference's API with
+``target="hip-gfx950"``: the static-cache decoders (``compile_qwen2_static_cache``,
+``compile_llama_static_cache`` and their bucketed forms) and the general
+``compile_callable`` / ``compile_module`` graph compilers.
 """
 
 from __future__ import annotations
@@ -15,6 +16,8 @@ from .plan import TARGET
 __all__ = [
     "TARGET",
     "__version__",
+    "compile_callable",
+    "compile_module",
     "compile_decoder_static_cache",
     "compile_decoder_bucketed",
     "compile_llama_bucketed",
@@ -44,6 +47,10 @@ def __getattr__(name: str):
         from . import decoder
 
         return getattr(decoder, name)
+    if name in ("compile_callable", "compile_module", "CompiledModulePlan", "CompilationResult"):
+        from . import compiler
+
+        return getattr(compiler, name)
     if name in ("load_runtime", "load_bucketed", "load_compiled_module", "read_artifact_manifest",
                 "save_compiled"):
         from . import artifact

@@ -82,6 +82,14 @@ SIGNATURES: dict[str, tuple] = {
     "aoto_hip_argmax_finish": (
         _p, _c_int, _p, _p, _p, _p, _c_int, _p, _i64, _c_int, _p, _p, _p, _p, _c_int, _p, _p,
     ),
+    "aoto_hip_generic_elementwise": (_c_int, _p, _p, _p, _p, ctypes.c_double, _p),
+    "aoto_hip_generic_reduce": (_c_int, _p, _p, _p),
+    "aoto_hip_generic_matmul": (_p, _p, _p, _p, _c_float, _c_float, _p),
+    "aoto_hip_generic_index": (_p, _p, _c_int, _p, _p, _p),
+    "aoto_hip_generic_copy": (_p, _p, _p),
+    "aoto_hip_generic_fill": (_p, ctypes.c_double, ctypes.c_double, _p),
+    "aoto_hip_generic_rms_norm": (_p, _p, _p, _c_float, _c_int, _p),
+    "aoto_hip_generic_attention": (_p, _p, _p, _p, _p, _c_int, _c_float, _p),
 }
 
 #: Entry points returning a size rather than a status.

@@ -17,6 +17,7 @@
 #include <unordered_map>
 
 #include "aoto_hip.h"
+#include "generic_args.h"
 
 namespace {
 
@@ -774,4 +775,422 @@ int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int
                 history_len);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------- generic graph kernels
+namespace {
+
+bool valid_dtype(int dt) { return dt >= AOTO_DT_F32 && dt <= AOTO_DT_I8; }
+bool float_dtype(int dt) { return dt == AOTO_DT_F32 || dt == AOTO_DT_BF16; }
+
+long long numel(const aoto_tensor* t) {
+  long long n = 1;
+  for (int d = 0; d < t->ndim; ++d) n *= t->shape[d];
+  return n;
+}
+
+int check_tensor(const char* what, const char* name, const aoto_tensor* t, bool allow_scalar) {
+  if (t == nullptr) return fail(AOTO_ERR_ARGUMENT, "%s: %s is null", what, name);
+  if (t->ndim < 0 || t->ndim > AOTO_MAX_DIMS)
+    return fail(AOTO_ERR_ARGUMENT, "%s: %s has %d dims (at most %d)", what, name, t->ndim, AOTO_MAX_DIMS);
+  if (t->data == nullptr) {
+    if (allow_scalar && t->ndim == 0) return AOTO_OK;
+    return fail(AOTO_ERR_ARGUMENT, "%s: %s has no data", what, name);
+  }
+  if (!valid_dtype(t->dtype)) return fail(AOTO_ERR_ARGUMENT, "%s: %s has element type %d", what, name, t->dtype);
+  for (int d = 0; d < t->ndim; ++d)
+    if (t->shape[d] < 0) return fail(AOTO_ERR_ARGUMENT, "%s: %s has a negative extent", what, name);
+  return AOTO_OK;
+}
+
+bool contiguous(const aoto_tensor* t) {
+  long long expect = 1;
+  for (int d = t->ndim - 1; d >= 0; --d) {
+    if (t->shape[d] != 1 && t->strides[d] != expect) return false;
+    expect *= t->shape[d];
+  }
+  return true;
+}
+
+// Right-aligned numpy broadcast of `t` onto `out`'s shape: element strides per output dim.
+int broadcast_operand(const char* what, const char* name, const aoto_tensor* t, const aoto_tensor* out,
+                      aoto::Operand* o) {
+  memset(o, 0, sizeof(*o));
+  if (t == nullptr) return AOTO_OK;
+  if (int s = check_tensor(what, name, t, true)) return s;
+  o->data = t->data;
+  o->dtype = t->dtype;
+  o->value = t->value;
+  if (t->data == nullptr) return AOTO_OK;
+  if (t->ndim > out->ndim) return fail(AOTO_ERR_ARGUMENT, "%s: %s has more dims than the output", what, name);
+  const int shift = out->ndim - t->ndim;
+  for (int d = 0; d < t->ndim; ++d) {
+    const long long ext = t->shape[d], oext = out->shape[d + shift];
+    if (ext == oext)
+      o->strides[d + shift] = ext == 1 ? 0 : t->strides[d];
+    else if (ext == 1)
+      o->strides[d + shift] = 0;
+    else
+      return fail(AOTO_ERR_ARGUMENT, "%s: %s dim %d (%lld) does not broadcast to %lld", what, name, d, ext, oext);
+  }
+  return AOTO_OK;
+}
+
+unsigned grid_for(long long total) {
+  long long blocks = (total + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 8192) blocks = 8192;
+  return (unsigned)blocks;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aoto_hip_generic_elementwise(int op, const aoto_tensor* out, const aoto_tensor* a, const aoto_tensor* b,
+                                 const aoto_tensor* c, double alpha, void* stream) {
+  const char* what = "generic_elementwise";
+  if (int s = check_tensor(what, "out", out, false)) return s;
+  if (!contiguous(out)) return fail(AOTO_ERR_ARGUMENT, "%s: out must be contiguous", what);
+  const int arity = op == AOTO_EW_WHERE ? 3 : (op >= AOTO_EW_ADD && op != AOTO_EW_ISNAN ? 2 : 1);
+  if (op < 0 || (op > AOTO_EW_BITWISE_NOT && op < AOTO_EW_ADD) || (op > AOTO_EW_LOG_OR && op < AOTO_EW_EQ) ||
+      (op > AOTO_EW_ISNAN && op != AOTO_EW_WHERE))
+    return fail(AOTO_ERR_ARGUMENT, "%s: unknown op %d", what, op);
+  if (a == nullptr || (arity >= 2 && b == nullptr) || (arity == 3 && c == nullptr))
+    return fail(AOTO_ERR_ARGUMENT, "%s: op %d takes %d operands", what, op, arity);
+  if (op == AOTO_EW_BITWISE_NOT && out->dtype == AOTO_DT_BOOL) op = AOTO_EW_LOGICAL_NOT;  // ~ of bool is not
+  aoto::EwArgs args;
+  memset(&args, 0, sizeof(args));
+  if (int s = broadcast_operand(what, "a", a, out, &args.in[0])) return s;
+  if (int s = broadcast_operand(what, "b", arity >= 2 ? b : nullptr, out, &args.in[1])) return s;
+  if (int s = broadcast_operand(what, "c", arity == 3 ? c : nullptr, out, &args.in[2])) return s;
+  const bool compare = op >= AOTO_EW_EQ && op <= AOTO_EW_ISNAN;
+  if (compare) {
+    if (out->dtype != AOTO_DT_BOOL) return fail(AOTO_ERR_ARGUMENT, "%s: a comparison writes bool", what);
+    args.domain = 2;
+  } else if (op == AOTO_EW_WHERE) {
+    args.domain = 3;
+  } else if (float_dtype(out->dtype)) {
+    if (op == AOTO_EW_LOGICAL_NOT || op == AOTO_EW_BITWISE_NOT || (op >= AOTO_EW_BIT_AND && op <= AOTO_EW_LOG_OR))
+      return fail(AOTO_ERR_ARGUMENT, "%s: op %d has no floating-point form", what, op);
+    args.domain = 0;
+  } else {
+    const bool int_ok = op == AOTO_EW_CAST || op == AOTO_EW_NEG || op == AOTO_EW_ABS || op == AOTO_EW_LOGICAL_NOT ||
+                        op == AOTO_EW_BITWISE_NOT || op == AOTO_EW_ADD || op == AOTO_EW_SUB || op == AOTO_EW_MUL ||
+                        op == AOTO_EW_DIV_TRUNC || op == AOTO_EW_DIV_FLOOR || op == AOTO_EW_MAXIMUM ||
+                        op == AOTO_EW_MINIMUM || op == AOTO_EW_REMAINDER || (op >= AOTO_EW_BIT_AND && op <= AOTO_EW_LOG_OR);
+    if (!int_ok) return fail(AOTO_ERR_ARGUMENT, "%s: op %d has no integer form", what, op);
+    // a float operand cast to an integer output truncates: load it as float
+    args.domain = (op == AOTO_EW_CAST && a->data && float_dtype(a->dtype)) ? 0 : 1;
+  }
+  args.op = op;
+  args.ndim = out->ndim;
+  args.out_dtype = out->dtype;
+  args.total = numel(out);
+  for (int d = 0; d < out->ndim; ++d) args.shape[d] = out->shape[d];
+  args.out = out->data;
+  args.alpha = alpha;
+  if (args.total == 0) return AOTO_OK;
+  return launch("aoto_generic_elementwise", dim3(grid_for(args.total)), dim3(256), 0, stream, args);
+}
+
+int aoto_hip_generic_reduce(int op, const aoto_tensor* out, const aoto_tensor* in, void* stream) {
+  const char* what = "generic_reduce";
+  if (int s = check_tensor(what, "in", in, false)) return s;
+  if (int s = check_tensor(what, "out", out, false)) return s;
+  if (op < AOTO_RED_SUM || op > AOTO_RED_CUMSUM) return fail(AOTO_ERR_ARGUMENT, "%s: unknown op %d", what, op);
+  if (in->ndim < 1) return fail(AOTO_ERR_ARGUMENT, "%s: the input needs a dim to reduce", what);
+  const long long len = in->shape[in->ndim - 1];
+  const long long total = numel(in);
+  const long long rows = len > 0 ? total / len : 0;
+  // the leading dims of `in` must collapse to one row stride
+  long long row_stride = 0;
+  {
+    long long expect = -1, extent = 1;
+    for (int d = in->ndim - 2; d >= 0; --d) {
+      if (in->shape[d] == 1) continue;
+      if (expect >= 0 && in->strides[d] != expect)
+        return fail(AOTO_ERR_ARGUMENT, "%s: the leading dims of the input do not collapse to one stride", what);
+      if (expect < 0) row_stride = in->strides[d];
+      expect = in->strides[d] * in->shape[d];
+      extent *= in->shape[d];
+    }
+    (void)extent;
+  }
+  const bool full = op == AOTO_RED_SOFTMAX || op == AOTO_RED_LOG_SOFTMAX || op == AOTO_RED_CUMSUM;
+  if (!contiguous(out) || numel(out) != (full ? total : rows))
+    return fail(AOTO_ERR_ARGUMENT, "%s: out must be contiguous with %lld elements", what, full ? total : rows);
+  aoto::ReduceArgs args;
+  memset(&args, 0, sizeof(args));
+  args.op = op;
+  const bool int_out = !float_dtype(out->dtype);
+  args.domain = (op == AOTO_RED_SUM || op == AOTO_RED_AMAX || op == AOTO_RED_AMIN || op == AOTO_RED_CUMSUM) && int_out
+                    ? 1
+                    : 0;
+  if ((op == AOTO_RED_MEAN || op == AOTO_RED_SOFTMAX || op == AOTO_RED_LOG_SOFTMAX) && int_out)
+    return fail(AOTO_ERR_ARGUMENT, "%s: op %d writes a floating-point output", what, op);
+  if (op == AOTO_RED_CUMSUM && len > 256 * 4096)
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: cumsum rows longer than 1048576", what);
+  args.in_dtype = in->dtype;
+  args.out_dtype = out->dtype;
+  args.rows = rows;
+  args.len = len;
+  args.in = in->data;
+  args.in_row_stride = row_stride;
+  args.in_elem_stride = in->strides[in->ndim - 1];
+  args.out = out->data;
+  args.out_row_stride = full ? len : 1;
+  args.out_elem_stride = 1;
+  if (rows == 0) return AOTO_OK;
+  if (len == 0) {
+    if (full) return AOTO_OK;
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: reducing an empty dim", what);
+  }
+  const unsigned grid = (unsigned)(rows < 65536 ? rows : 65536);
+  return launch("aoto_generic_reduce", dim3(grid), dim3(256), 0, stream, args);
+}
+
+int aoto_hip_generic_matmul(const aoto_tensor* out, const aoto_tensor* a, const aoto_tensor* b,
+                            const aoto_tensor* bias, float alpha, float beta, void* stream) {
+  const char* what = "generic_matmul";
+  if (int s = check_tensor(what, "a", a, false)) return s;
+  if (int s = check_tensor(what, "b", b, false)) return s;
+  if (int s = check_tensor(what, "out", out, false)) return s;
+  if (a->ndim != 3 || b->ndim != 3 || out->ndim != 3)
+    return fail(AOTO_ERR_ARGUMENT, "%s: a, b and out must be 3-D [batch, rows, cols]", what);
+  const long long B = out->shape[0], M = out->shape[1], N = out->shape[2], K = a->shape[2];
+  if ((a->shape[0] != B && a->shape[0] != 1) || (b->shape[0] != B && b->shape[0] != 1) || a->shape[1] != M ||
+      b->shape[1] != K || b->shape[2] != N)
+    return fail(AOTO_ERR_ARGUMENT, "%s: shapes [%lld,%lld,%lld] x [%lld,%lld,%lld] -> [%lld,%lld,%lld] disagree", what,
+                (long long)a->shape[0], (long long)a->shape[1], (long long)a->shape[2], (long long)b->shape[0],
+                (long long)b->shape[1], (long long)b->shape[2], B, M, N);
+  if (!float_dtype(a->dtype) || !float_dtype(b->dtype) || !float_dtype(out->dtype))
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: f32 / bf16 operands only", what);
+  if (B > 65535 || (M + 63) / 64 > 65535) return fail(AOTO_ERR_UNSUPPORTED, "%s: grid too large", what);
+  aoto::GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.a = a->data;
+  g.b = b->data;
+  g.c = out->data;
+  g.a_dtype = a->dtype;
+  g.b_dtype = b->dtype;
+  g.c_dtype = out->dtype;
+  g.batch = B;
+  g.m = M;
+  g.n = N;
+  g.k = K;
+  g.sa_b = a->shape[0] == 1 ? 0 : a->strides[0];
+  g.sa_m = a->strides[1];
+  g.sa_k = a->strides[2];
+  g.sb_b = b->shape[0] == 1 ? 0 : b->strides[0];
+  g.sb_k = b->strides[1];
+  g.sb_n = b->strides[2];
+  g.sc_b = out->strides[0];
+  g.sc_m = out->strides[1];
+  g.sc_n = out->strides[2];
+  g.alpha = alpha;
+  g.beta = beta;
+  if (bias != nullptr) {
+    aoto::Operand o;
+    if (int s = broadcast_operand(what, "bias", bias, out, &o)) return s;
+    if (o.data == nullptr) return fail(AOTO_ERR_ARGUMENT, "%s: bias needs data", what);
+    g.bias = o.data;
+    g.bias_dtype = o.dtype;
+    g.sbias_b = o.strides[0];
+    g.sbias_m = o.strides[1];
+    g.sbias_n = o.strides[2];
+  }
+  if (B == 0 || M == 0 || N == 0) return AOTO_OK;
+  return launch("aoto_generic_gemm", dim3((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)B),
+                dim3(256), 0, stream, g);
+}
+
+int aoto_hip_generic_index(const aoto_tensor* out, const aoto_tensor* src, int nidx,
+                           const aoto_tensor* const* indices, int* error, void* stream) {
+  const char* what = "generic_index";
+  if (int s = check_tensor(what, "src", src, false)) return s;
+  if (int s = check_tensor(what, "out", out, false)) return s;
+  if (nidx < 1 || nidx > 4 || nidx > src->ndim || indices == nullptr)
+    return fail(AOTO_ERR_ARGUMENT, "%s: 1..4 index tensors over the source's leading dims", what);
+  if (!contiguous(src) || !contiguous(out) || src->dtype != out->dtype)
+    return fail(AOTO_ERR_ARGUMENT, "%s: src and out must be contiguous and of one element type", what);
+  const int rest = src->ndim - nidx;
+  const int bdims = out->ndim - rest;
+  if (bdims < 0 || bdims > AOTO_MAX_DIMS) return fail(AOTO_ERR_ARGUMENT, "%s: output rank does not fit", what);
+  long long inner = 1;
+  for (int d = 0; d < rest; ++d) {
+    if (out->shape[bdims + d] != src->shape[nidx + d])
+      return fail(AOTO_ERR_ARGUMENT, "%s: trailing dims of out and src differ", what);
+    inner *= src->shape[nidx + d];
+  }
+  aoto::IndexArgs args;
+  memset(&args, 0, sizeof(args));
+  args.src = src->data;
+  args.dtype = src->dtype;
+  args.nidx = nidx;
+  args.bdims = bdims;
+  for (int d = 0; d < bdims; ++d) args.bshape[d] = out->shape[d];
+  aoto_tensor bshape_view;
+  memset(&bshape_view, 0, sizeof(bshape_view));
+  bshape_view.ndim = bdims;
+  for (int d = 0; d < bdims; ++d) bshape_view.shape[d] = out->shape[d];
+  for (int j = 0; j < nidx; ++j) {
+    const aoto_tensor* ix = indices[j];
+    if (int s = check_tensor(what, "index", ix, false)) return s;
+    if (float_dtype(ix->dtype)) return fail(AOTO_ERR_ARGUMENT, "%s: index tensors must be integer or bool", what);
+    aoto::Operand o;
+    if (int s = broadcast_operand(what, "index", ix, &bshape_view, &o)) return s;
+    args.idx[j] = ix->data;
+    args.idx_dtype[j] = ix->dtype;
+    for (int d = 0; d < bdims; ++d) args.idx_strides[j][d] = o.strides[d];
+    args.dim_size[j] = src->shape[j];
+    args.src_stride[j] = src->strides[j];
+  }
+  args.inner = inner;
+  args.total = numel(out);
+  args.out = out->data;
+  args.error = error;
+  if (args.total == 0) return AOTO_OK;
+  return launch("aoto_generic_index", dim3(grid_for(args.total)), dim3(256), 0, stream, args);
+}
+
+int aoto_hip_generic_copy(const aoto_tensor* dst, const aoto_tensor* src, void* stream) {
+  const char* what = "generic_copy";
+  if (int s = check_tensor(what, "src", src, false)) return s;
+  if (int s = check_tensor(what, "dst", dst, false)) return s;
+  if (src->ndim != dst->ndim) return fail(AOTO_ERR_ARGUMENT, "%s: src and dst ranks differ", what);
+  aoto::CopyArgs args;
+  memset(&args, 0, sizeof(args));
+  for (int d = 0; d < dst->ndim; ++d) {
+    if (src->shape[d] != dst->shape[d]) return fail(AOTO_ERR_ARGUMENT, "%s: src and dst shapes differ", what);
+    args.shape[d] = dst->shape[d];
+    args.src_strides[d] = src->strides[d];
+    args.dst_strides[d] = dst->strides[d];
+  }
+  args.src = src->data;
+  args.dst = dst->data;
+  args.src_dtype = src->dtype;
+  args.dst_dtype = dst->dtype;
+  args.ndim = dst->ndim;
+  args.total = numel(dst);
+  if (args.total == 0) return AOTO_OK;
+  return launch("aoto_generic_copy", dim3(grid_for(args.total)), dim3(256), 0, stream, args);
+}
+
+int aoto_hip_generic_fill(const aoto_tensor* dst, double start, double step, void* stream) {
+  const char* what = "generic_fill";
+  if (int s = check_tensor(what, "dst", dst, false)) return s;
+  if (!contiguous(dst)) return fail(AOTO_ERR_ARGUMENT, "%s: dst must be contiguous", what);
+  aoto::FillArgs args;
+  memset(&args, 0, sizeof(args));
+  args.dst = dst->data;
+  args.dtype = dst->dtype;
+  args.integer = float_dtype(dst->dtype) ? 0 : 1;
+  args.total = numel(dst);
+  args.start = start;
+  args.step = step;
+  args.start_i = (long long)start;
+  args.step_i = (long long)step;
+  if (args.total == 0) return AOTO_OK;
+  return launch("aoto_generic_fill", dim3(grid_for(args.total)), dim3(256), 0, stream, args);
+}
+
+int aoto_hip_generic_rms_norm(const aoto_tensor* out, const aoto_tensor* x, const aoto_tensor* weight, float eps,
+                              int mid_dtype, void* stream) {
+  const char* what = "generic_rms_norm";
+  if (int s = check_tensor(what, "x", x, false)) return s;
+  if (int s = check_tensor(what, "out", out, false)) return s;
+  if (x->ndim < 1 || !contiguous(x) || !contiguous(out) || numel(x) != numel(out))
+    return fail(AOTO_ERR_ARGUMENT, "%s: x and out must be contiguous and of one size", what);
+  if (!float_dtype(x->dtype) || !float_dtype(out->dtype) || !float_dtype(mid_dtype))
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: f32 / bf16 only", what);
+  const long long hidden = x->shape[x->ndim - 1];
+  aoto::RmsArgs args;
+  memset(&args, 0, sizeof(args));
+  if (weight != nullptr) {
+    if (int s = check_tensor(what, "weight", weight, false)) return s;
+    if (numel(weight) != hidden || !contiguous(weight) || !float_dtype(weight->dtype))
+      return fail(AOTO_ERR_ARGUMENT, "%s: weight must be a contiguous float vector of %lld", what, hidden);
+    args.w = weight->data;
+    args.w_dtype = weight->dtype;
+    args.has_weight = 1;
+  }
+  args.x = x->data;
+  args.out = out->data;
+  args.x_dtype = x->dtype;
+  args.mid_dtype = mid_dtype;
+  args.out_dtype = out->dtype;
+  args.hidden = hidden;
+  args.rows = hidden > 0 ? numel(x) / hidden : 0;
+  args.eps = eps;
+  if (args.rows == 0) return AOTO_OK;
+  const unsigned grid = (unsigned)(args.rows < 65536 ? args.rows : 65536);
+  return launch("aoto_generic_rms_norm", dim3(grid), dim3(256), 0, stream, args);
+}
+
+int aoto_hip_generic_attention(const aoto_tensor* out, const aoto_tensor* q, const aoto_tensor* k,
+                               const aoto_tensor* v, const aoto_tensor* mask, int causal, float scale,
+                               void* stream) {
+  const char* what = "generic_attention";
+  if (int s = check_tensor(what, "q", q, false)) return s;
+  if (int s = check_tensor(what, "k", k, false)) return s;
+  if (int s = check_tensor(what, "v", v, false)) return s;
+  if (int s = check_tensor(what, "out", out, false)) return s;
+  if (q->ndim != 4 || k->ndim != 4 || v->ndim != 4 || out->ndim != 4)
+    return fail(AOTO_ERR_ARGUMENT, "%s: q, k, v, out must be 4-D [batch, heads, tokens, dim]", what);
+  const long long B = q->shape[0], H = q->shape[1], Lq = q->shape[2], D = q->shape[3];
+  const long long Hk = k->shape[1], Lk = k->shape[2], Dv = v->shape[3];
+  if (k->shape[0] != B || v->shape[0] != B || v->shape[1] != Hk || v->shape[2] != Lk || k->shape[3] != D ||
+      Hk <= 0 || H % Hk != 0)
+    return fail(AOTO_ERR_ARGUMENT, "%s: q/k/v shapes disagree", what);
+  if (out->shape[0] != B || out->shape[1] != H || out->shape[2] != Lq || out->shape[3] != Dv || !contiguous(out))
+    return fail(AOTO_ERR_ARGUMENT, "%s: out must be contiguous [B, H, Lq, Dv]", what);
+  if (Lk > 8192) return fail(AOTO_ERR_UNSUPPORTED, "%s: at most 8192 keys (got %lld)", what, Lk);
+  if (B * H > 65535 || Lq > 2147483647LL) return fail(AOTO_ERR_UNSUPPORTED, "%s: grid too large", what);
+  if (!float_dtype(q->dtype) || !float_dtype(k->dtype) || !float_dtype(v->dtype) || !float_dtype(out->dtype))
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: f32 / bf16 only", what);
+  aoto::AttnArgs args;
+  memset(&args, 0, sizeof(args));
+  args.q = q->data;
+  args.k = k->data;
+  args.v = v->data;
+  args.out = out->data;
+  args.q_dtype = q->dtype;
+  args.k_dtype = k->dtype;
+  args.v_dtype = v->dtype;
+  args.out_dtype = out->dtype;
+  args.causal = causal;
+  args.batch = (int)B;
+  args.heads = (int)H;
+  args.kv_heads = (int)Hk;
+  args.lq = (int)Lq;
+  args.lk = (int)Lk;
+  args.d = (int)D;
+  args.dv = (int)Dv;
+  for (int d = 0; d < 4; ++d) {
+    args.qs[d] = q->strides[d];
+    args.ks[d] = k->strides[d];
+    args.vs[d] = v->strides[d];
+  }
+  if (mask != nullptr) {
+    aoto_tensor shape4;
+    memset(&shape4, 0, sizeof(shape4));
+    shape4.ndim = 4;
+    shape4.shape[0] = B;
+    shape4.shape[1] = H;
+    shape4.shape[2] = Lq;
+    shape4.shape[3] = Lk;
+    aoto::Operand o;
+    if (int s = broadcast_operand(what, "mask", mask, &shape4, &o)) return s;
+    if (o.data == nullptr) return fail(AOTO_ERR_ARGUMENT, "%s: mask needs data", what);
+    if (o.dtype != AOTO_DT_BOOL && !float_dtype(o.dtype))
+      return fail(AOTO_ERR_ARGUMENT, "%s: mask must be bool or float", what);
+    args.mask = o.data;
+    args.mask_dtype = o.dtype;
+    for (int d = 0; d < 4; ++d) args.ms[d] = o.strides[d];
+  }
+  args.scale = scale;
+  if (B == 0 || H == 0 || Lq == 0) return AOTO_OK;
+  return launch("aoto_generic_attention", dim3((unsigned)Lq, (unsigned)(B * H)), dim3(256), 0, stream, args);
+}
 }  // extern "C"

@@ -63,6 +63,7 @@ def build(verbose: bool = False) -> tuple[str, str]:
             "-fPIC",
             "-shared",
             "-I" + INCLUDE,
+            "-I" + CSRC,
             os.path.join(CSRC, "aoto_hip.cpp"),
             "-o",
             tmp_lib,

@@ -6,6 +6,7 @@
 #include "w4_gemv_stream.h"
 #include "w4_gemm.h"
 #include "w8.h"
+#include "generic.h"
 #include "decode.h"
 #include "prefill.h"
 #include "flash_attention.h"

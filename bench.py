@@ -52,10 +52,10 @@ def llama8b_spec():
 
 
 def gemv_bytes(n: int, k: int, group: int = 64, *, norm: bool = False, bias: bool = False,
-               paired: bool = False) -> int:
-    """Algorithmic bytes of one W4 GEMV launch: weights, scales, x, y (+ norm w, bias)."""
+               paired: bool = False, bits: int = 4) -> int:
+    """Algorithmic bytes of one packed GEMV launch: weights, scales, x, y (+ norm w, bias)."""
 
-    weights = n * k // 2 + n * (k // group) * 2
+    weights = n * k * bits // 8 + n * (k // group) * 2
     total = weights * (2 if paired else 1) + 2 * k + 2 * n
     if norm:
         total += 2 * k
@@ -64,28 +64,31 @@ def gemv_bytes(n: int, k: int, group: int = 64, *, norm: bool = False, bias: boo
     return total
 
 
-def step_weight_bytes(spec, group: int = 64) -> int:
+def step_weight_bytes(spec, group: int = 64, bits: int = 4) -> int:
     """Algorithmic bytes of one decode token's GEMVs (the weight stream)."""
 
     h, i = spec.hidden, spec.intermediate
     per_layer = (
-        gemv_bytes(spec.qkv_width, h, group, norm=True, bias=spec.qkv_bias)
-        + gemv_bytes(h, spec.attention_width, group, bias=True)
-        + gemv_bytes(i, h, group, norm=True, paired=True)
-        + gemv_bytes(h, i, group, bias=True)
+        gemv_bytes(spec.qkv_width, h, group, norm=True, bias=spec.qkv_bias, bits=bits)
+        + gemv_bytes(h, spec.attention_width, group, bias=True, bits=bits)
+        + gemv_bytes(i, h, group, norm=True, paired=True, bits=bits)
+        + gemv_bytes(h, i, group, bias=True, bits=bits)
     )
-    return spec.layers * per_layer + gemv_bytes(spec.vocab, h, group, norm=True)
+    return spec.layers * per_layer + gemv_bytes(spec.vocab, h, group, norm=True, bits=bits)
 
 
-def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: float = 1.2e9) -> dict:
+def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: float = 1.2e9,
+                         bits: int = 4) -> dict:
     """Average duration of the LM-head GEMV over a rotating pool of weight copies."""
 
     n, k, group = spec.vocab, spec.hidden, 64
-    per = gemv_bytes(n, k, group, norm=True)
+    per = gemv_bytes(n, k, group, norm=True, bits=bits)
     copies = max(2, int(pool_bytes // per) + 1)
+    gemv = ops.w4_gemv if bits == 4 else ops.w8_gemv
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1)
-    words = [torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), generator=gen, dtype=torch.int32, device="cuda")
+    words = [torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k * bits // 32), generator=gen, dtype=torch.int32,
+                           device="cuda")
              for _ in range(copies)]
     scales = [(torch.rand((n, k // group), generator=gen, device="cuda") * 0.003).to(torch.bfloat16)
               for _ in range(copies)]
@@ -94,7 +97,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: f
     out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
     stream = torch.cuda.current_stream()
     for i in range(copies):
-        ops.w4_gemv(x, words[i], scales[i], group, norm_weight=norm, eps=spec.eps, out=out)
+        gemv(x, words[i], scales[i], group, norm_weight=norm, eps=spec.eps, out=out)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -103,7 +106,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: f
     torch.cuda._sleep(50_000_000)
     start.record(stream)
     for i in range(launches):
-        ops.w4_gemv(x, words[i % copies], scales[i % copies], group, norm_weight=norm, eps=spec.eps, out=out)
+        gemv(x, words[i % copies], scales[i % copies], group, norm_weight=norm, eps=spec.eps, out=out)
     end.record(stream)
     torch.cuda.synchronize()
     avg_us = start.elapsed_time(end) * 1000.0 / launches
@@ -111,7 +114,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 200, pool_bytes: f
     del words, scales
     torch.cuda.empty_cache()
     return {
-        "kernel": f"aoto_w4_gemv (LM head {n}x{k}, g64, RMSNorm prologue)",
+        "kernel": f"aoto_w{bits}_gemv (LM head {n}x{k}, g64, RMSNorm prologue)",
         "bytes_per_launch": per,
         "avg_us": avg_us,
         "achieved": achieved,
@@ -169,7 +172,7 @@ def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
     }
     shape = DecoderShape(vocab=spec.vocab, hidden=spec.hidden, intermediate=spec.intermediate, layers=spec.layers,
                          heads=spec.heads, kv_heads=spec.kv_heads, head_dim=spec.head_dim, eps=spec.eps,
-                         theta=spec.theta)
+                         theta=spec.theta, bits=runtime.quantize_bits)
     oracle = OracleDecoder(shape, ostate, runtime.cache_capacity)
     ids = np.asarray(prompt, dtype=np.int64).reshape(-1)
     t0 = time.perf_counter()
@@ -285,6 +288,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-roofline", action="store_true")
     parser.add_argument("--workload", choices=("qwen0.5b", "llama8b"), default="qwen0.5b")
+    parser.add_argument("--bits", type=int, choices=(4, 8), default=4,
+                        help="weight code width of the qwen0.5b workload (8: the quantize_bits=8 variant)")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the LM-head GEMV loop, after a calibration copy of 256 MiB (for counter runs)")
     args = parser.parse_args()
@@ -306,7 +311,7 @@ def main() -> int:
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        lm = measure_lm_head_gemv(spec, torch, ops, launches=20)
+        lm = measure_lm_head_gemv(spec, torch, ops, launches=20, bits=args.bits)
         print(json.dumps({"calibration_copy_bytes": src.numel() * 4, **lm}), flush=True)
         return 0
     if args.workload == "llama8b":
@@ -315,9 +320,10 @@ def main() -> int:
                           "data": "synthetic random-init", **result}), flush=True)
         return 0
     spec = qwen_spec()
-    print(f"[bench] building the random-init W4 state on {torch.cuda.get_device_name(0)}", file=sys.stderr,
+    bits = args.bits
+    print(f"[bench] building the random-init W{bits} state on {torch.cuda.get_device_name(0)}", file=sys.stderr,
           flush=True)
-    state = random_state(spec, 64, seed=0)
+    state = random_state(spec, 64, seed=0, bits=bits)
     runtime = compile_decoder_state(spec, state, prompt_length=args.prompt, max_new_tokens=args.new)
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, spec.vocab, (1, args.prompt), generator=gen)
@@ -358,14 +364,14 @@ def main() -> int:
 
     roofline = None
     if not args.no_roofline:
-        lm = measure_lm_head_gemv(spec, torch, ops)
+        lm = measure_lm_head_gemv(spec, torch, ops, bits=bits)
         roofline = {
             "bound": "hbm",
             "achieved": round(lm["achieved"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(lm["achieved"] / HBM_PEAK_GBS, 4),
-            "traffic": counter_traffic(),
+            "traffic": counter_traffic() if bits == 4 else None,
             "kernel": lm["kernel"],
             "avg_us": round(lm["avg_us"], 3),
             "bytes_per_launch": lm["bytes_per_launch"],
@@ -381,9 +387,9 @@ def main() -> int:
         baseline = result["baseline"]
         parity = result["parity"]
 
-    weight_bytes = step_weight_bytes(spec)
+    weight_bytes = step_weight_bytes(spec, bits=bits)
     line = {
-        "metric": "decode tok/s + quant-GEMV HBM GB/s, prefill tok/s; Qwen2.5-0.5B-shape W4g64 bs1",
+        "metric": f"decode tok/s + quant-GEMV HBM GB/s, prefill tok/s; Qwen2.5-0.5B-shape W{bits}g64 bs1",
         "value": round(decode_tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -394,10 +400,10 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init weights N(0,0.02) packed W4 g64 on the GPU, seeded q/k/v bias, "
+        "data": f"synthetic (random-init weights N(0,0.02) packed W{bits} g64 on the GPU, seeded q/k/v bias, "
                 "uniform-random prompt ids)",
         "config": {
-            "workload": "qwen2.5-0.5b-shape W4g64 static-cache greedy: prompt 128, 64 new tokens, bs1 "
+            "workload": f"qwen2.5-0.5b-shape W{bits}g64 static-cache greedy: prompt 128, 64 new tokens, bs1 "
                         "(one step = one generation: prefill + 63 graph-replayed decode steps)",
             "prompt": args.prompt,
             "new_tokens": args.new,

@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 8
+#define AOTO_HIP_ABI_VERSION 9
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -286,6 +286,142 @@ int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_o
                            int64_t embedding_rows, int hidden, void* hidden_out, int* error,
                            const void* cos_table, const void* sin_table, int head_dim, void* rope_rows,
                            void* stream);
+
+/* ---------------------------------------------------------------- generic graph kernels
+ *
+ * The compile_callable / compile_module plans (compiler.py:301-405 of the
+ * reference: torch capture -> lowered graph -> one kernel per node) run on
+ * these launchers. Tensors are described by aoto_tensor: a device pointer,
+ * element type, shape and element strides (stride 0 broadcasts); data == NULL
+ * with ndim 0 is a scalar operand holding `value`. Outputs are written through
+ * their strides; shapes must match the op's rules (checked on the host). */
+
+#define AOTO_MAX_DIMS 8
+
+#define AOTO_DT_F32 0
+#define AOTO_DT_BF16 1
+#define AOTO_DT_I64 2
+#define AOTO_DT_I32 3
+#define AOTO_DT_BOOL 4
+#define AOTO_DT_U8 5
+#define AOTO_DT_I8 6
+
+typedef struct aoto_tensor {
+  void* data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[AOTO_MAX_DIMS];
+  int64_t strides[AOTO_MAX_DIMS];
+  double value;
+} aoto_tensor;
+
+/* Elementwise ops (runtime/mlx_ops/__init__.py:239-620 semantics): codes below
+ * AOTO_EW_ADD take one operand, AOTO_EW_ADD..AOTO_EW_ISNAN two (ISNAN one),
+ * AOTO_EW_WHERE three (cond, x, y). Float results compute in f32 and round
+ * once to the output type; integer/bool outputs compute in int64; comparisons
+ * compare exactly and write bool. */
+#define AOTO_EW_CAST 0
+#define AOTO_EW_NEG 1
+#define AOTO_EW_ABS 2
+#define AOTO_EW_RECIPROCAL 3
+#define AOTO_EW_SQRT 4
+#define AOTO_EW_RSQRT 5
+#define AOTO_EW_EXP 6
+#define AOTO_EW_LOG 7
+#define AOTO_EW_SIGMOID 8
+#define AOTO_EW_SILU 9
+#define AOTO_EW_TANH 10
+#define AOTO_EW_COS 11
+#define AOTO_EW_SIN 12
+#define AOTO_EW_RELU 13
+#define AOTO_EW_GELU 14
+#define AOTO_EW_GELU_TANH 15
+#define AOTO_EW_ERF 16
+#define AOTO_EW_FLOOR 17
+#define AOTO_EW_CEIL 18
+#define AOTO_EW_LOG1P 19
+#define AOTO_EW_EXPM1 20
+#define AOTO_EW_LOGICAL_NOT 21
+#define AOTO_EW_BITWISE_NOT 22
+#define AOTO_EW_ADD 32
+#define AOTO_EW_SUB 33
+#define AOTO_EW_MUL 34
+#define AOTO_EW_DIV 35
+#define AOTO_EW_DIV_TRUNC 36
+#define AOTO_EW_DIV_FLOOR 37
+#define AOTO_EW_POW 38
+#define AOTO_EW_MAXIMUM 39
+#define AOTO_EW_MINIMUM 40
+#define AOTO_EW_REMAINDER 41
+#define AOTO_EW_BIT_AND 42
+#define AOTO_EW_BIT_OR 43
+#define AOTO_EW_BIT_XOR 44
+#define AOTO_EW_LOG_AND 45
+#define AOTO_EW_LOG_OR 46
+#define AOTO_EW_EQ 48
+#define AOTO_EW_NE 49
+#define AOTO_EW_LT 50
+#define AOTO_EW_LE 51
+#define AOTO_EW_GT 52
+#define AOTO_EW_GE 53
+#define AOTO_EW_ISNAN 54
+#define AOTO_EW_WHERE 64
+
+/* out (contiguous) = op(a, b, c) with numpy broadcasting of a, b, c to out's
+ * shape; alpha scales b for ADD/SUB; unused operands may be NULL. */
+int aoto_hip_generic_elementwise(int op, const aoto_tensor* out, const aoto_tensor* a, const aoto_tensor* b,
+                                 const aoto_tensor* c, double alpha, void* stream);
+
+/* Row reductions and scans over the last dim of `in` (its leading dims must
+ * collapse to one stride): SUM, MEAN, AMAX, AMIN, ANY, ALL, ARGMAX, ARGMIN
+ * write out[rows]; SOFTMAX, LOG_SOFTMAX, CUMSUM write out[rows, len].
+ * (runtime/mlx_ops/__init__.py reductions; softmax in f32.) */
+#define AOTO_RED_SUM 0
+#define AOTO_RED_MEAN 1
+#define AOTO_RED_AMAX 2
+#define AOTO_RED_AMIN 3
+#define AOTO_RED_ANY 4
+#define AOTO_RED_ALL 5
+#define AOTO_RED_ARGMAX 6
+#define AOTO_RED_ARGMIN 7
+#define AOTO_RED_SOFTMAX 8
+#define AOTO_RED_LOG_SOFTMAX 9
+#define AOTO_RED_CUMSUM 10
+int aoto_hip_generic_reduce(int op, const aoto_tensor* out, const aoto_tensor* in, void* stream);
+
+/* out[b] = alpha * a[b] . b[b] + beta * bias (bias broadcast by its strides,
+ * or NULL); a [B, M, K], b [B, K, N], out [B, M, N], any strides, f32
+ * accumulation (mm / bmm / addmm of the lowered graph). */
+int aoto_hip_generic_matmul(const aoto_tensor* out, const aoto_tensor* a, const aoto_tensor* b,
+                            const aoto_tensor* bias, float alpha, float beta, void* stream);
+
+/* Advanced indexing of a contiguous source by index tensors over its leading
+ * nidx dims (embedding, index.Tensor): the indices broadcast to out's leading
+ * dims, the source's remaining dims follow. An index outside [-size, size)
+ * sets *error (when non-NULL) to 1 and yields zeros. */
+int aoto_hip_generic_index(const aoto_tensor* out, const aoto_tensor* src, int nidx,
+                           const aoto_tensor* const* indices, int* error, void* stream);
+
+/* dst = src (same shape, any strides, element-type conversion). */
+int aoto_hip_generic_copy(const aoto_tensor* dst, const aoto_tensor* src, void* stream);
+
+/* Contiguous dst[i] = start + i * step (step 0: a fill). */
+int aoto_hip_generic_fill(const aoto_tensor* dst, double start, double step, void* stream);
+
+/* The HF RMSNorm chain folded into one kernel (legalize/attention.py:332-525):
+ * out = weight * cast_mid(float(x) * rsqrt(mean(float(x)^2) + eps)) over the
+ * last dim of a contiguous x; weight may be NULL; mid_dtype is the element
+ * type the normalized value is cast to before the weight multiply. */
+int aoto_hip_generic_rms_norm(const aoto_tensor* out, const aoto_tensor* x, const aoto_tensor* weight, float eps,
+                              int mid_dtype, void* stream);
+
+/* scaled_dot_product_attention (legalize/attention.py:105-170): q [B, H, Lq, D],
+ * k [B, Hk, Lk, D], v [B, Hk, Lk, Dv] (H % Hk == 0), mask broadcast to
+ * [B, H, Lq, Lk] (bool keep / float additive) or NULL, is_causal; out
+ * [B, H, Lq, Dv] contiguous; Lk <= 8192. Fully masked rows give zeros. */
+int aoto_hip_generic_attention(const aoto_tensor* out, const aoto_tensor* q, const aoto_tensor* k,
+                               const aoto_tensor* v, const aoto_tensor* mask, int causal, float scale,
+                               void* stream);
 
 #ifdef __cplusplus
 }
