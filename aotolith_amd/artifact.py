@@ -54,10 +54,10 @@ from .selection import KernelBenchmark, KernelSelection
 ARTIFACT_FORMAT = "aotolith"
 FORMAT_VERSION = 6
 _SUPPORTED_FORMAT_VERSIONS = (6,)
-KINDS = ("prefill", "decode")
+KINDS = ("prefill", "decode", "graph")
 CODE_OBJECT_ENTRY = "code/gfx950.hsaco"
 _ZIP_TIMESTAMP = (1980, 1, 1, 0, 0, 0)
-_DTYPES = {"bfloat16": 2, "int32": 4, "int64": 8, "float32": 4}
+_DTYPES = {"bfloat16": 2, "int32": 4, "int64": 8, "float32": 4, "bool": 1, "uint8": 1, "int8": 1}
 _REQUIRED = ("entrypoint", "compile_options", "profile", "payload_digests", "payloads")
 
 
@@ -105,7 +105,8 @@ def _decode_selection(d: Mapping[str, Any]) -> KernelSelection:
 def _tensor_bytes(tensor) -> tuple[bytes, str, list[int]]:
     import torch
 
-    names = {torch.bfloat16: "bfloat16", torch.int32: "int32", torch.int64: "int64", torch.float32: "float32"}
+    names = {torch.bfloat16: "bfloat16", torch.int32: "int32", torch.int64: "int64", torch.float32: "float32",
+             torch.bool: "bool", torch.uint8: "uint8", torch.int8: "int8"}
     if tensor.dtype not in names:
         raise ArtifactError(f"cannot store a {tensor.dtype} state tensor")
     host = tensor.detach().to("cpu").contiguous()
@@ -172,8 +173,13 @@ def write_artifact(
     selections: Sequence[KernelSelection],
     code_object: bytes,
     profile: Mapping[str, Any],
+    graph: Mapping[str, Any] | None = None,
 ) -> Path:
-    """Write one plan's archive. ``state`` is ``(name, tensor)`` pairs (any device)."""
+    """Write one plan's archive. ``state`` is ``(name, tensor)`` pairs (any device).
+
+    Decoder plans carry their ``spec`` and ``config``; a graph plan (``kind``
+    ``"graph"``) carries its encoded lowered graph instead of a spec.
+    """
 
     if kind not in KINDS:
         raise ArtifactError(f"unknown plan kind {kind!r}; expected one of {KINDS}")
@@ -202,13 +208,14 @@ def write_artifact(
         "target": TARGET,
         "entrypoint": {
             "kind": kind,
-            "plan": "static_cache_decoder",
-            "spec": dataclasses.asdict(spec),
+            "plan": "graph" if kind == "graph" else "static_cache_decoder",
+            "spec": None if spec is None else dataclasses.asdict(spec),
             "config": dict(config),
             "state": entries,
+            **({"graph": dict(graph)} if graph is not None else {}),
         },
         "compile_options": {"codegen_matmul": True, "codegen_attention": True, "autotune": False,
-                            "quantize": int(config["group_size"]),
+                            "quantize": config.get("group_size"),
                             "quantize_bits": int(config.get("quantize_bits", 4))},
         "profile": dict(profile),
         "payload_digests": {"selections": _digest(selections_bytes), "code_object": _digest(code_object)},
@@ -441,7 +448,8 @@ def _install_code_object(image: bytes, device: int) -> None:
 def _device_state(contents: ArtifactContents, device) -> dict[str, Any]:
     import torch
 
-    dtypes = {"bfloat16": torch.bfloat16, "int32": torch.int32, "int64": torch.int64, "float32": torch.float32}
+    dtypes = {"bfloat16": torch.bfloat16, "int32": torch.int32, "int64": torch.int64, "float32": torch.float32,
+              "bool": torch.bool, "uint8": torch.uint8, "int8": torch.int8}
     tensors: dict[str, Any] = {}
     by_file: dict[str, Any] = {}
     files = {e["name"]: e["file"] for e in contents.manifest["entrypoint"]["state"]}
@@ -522,6 +530,8 @@ def load_compiled_module(path: str | os.PathLike[str], *, require_device_match: 
 
     dev = _torch_device(device)
     contents = read_artifact(path, require_device_match=require_device_match)
+    if contents.kind == "graph":
+        return _load_graph(contents, dev)
     runtime = _build([contents], dev, {})
     plan = runtime.prefill if contents.kind == "prefill" else runtime.decode
     plan._keepalive = runtime  # the caller holds only the plan
@@ -582,12 +592,163 @@ def load_bucketed(prefix: str | os.PathLike[str], *, prompt_lengths: Sequence[in
 
 
 def save_compiled(compiled, path: str | os.PathLike[str]) -> Path:
-    """Save a compiled plan (``runtime.prefill`` / ``runtime.decode``) as one artifact (artifact.py:82-269)."""
+    """Save a compiled plan as one artifact (artifact.py:82-269).
 
+    Takes ``runtime.prefill`` / ``runtime.decode`` of a static-cache runtime, or
+    the result of ``compile_callable`` / ``compile_module``.
+    """
+
+    from .compiler import CompilationResult, CompiledModulePlan
+
+    if isinstance(compiled, (CompilationResult, CompiledModulePlan)):
+        return save_graph_plan(compiled, path)
     runtime = getattr(compiled, "runtime", None)
     if runtime is None or getattr(compiled, "name", None) not in KINDS:
         raise ArtifactError("save_compiled takes the prefill or decode plan of a compiled static-cache runtime")
     return save_plan(runtime, compiled.name, path)
+
+
+# ----------------------------------------------------------------------------- graph plans
+def _encode_value(value):
+    import torch
+
+    from .graph import Ref
+
+    if isinstance(value, Ref):
+        return {"ref": value.name}
+    if isinstance(value, torch.dtype):
+        return {"dtype": str(value)}
+    if isinstance(value, torch.device):
+        return {"device": str(value)}
+    if isinstance(value, (torch.layout, torch.memory_format)):
+        return {"torch": str(value)}
+    if isinstance(value, tuple):
+        return {"tuple": [_encode_value(v) for v in value]}
+    if isinstance(value, list):
+        return [_encode_value(v) for v in value]
+    if isinstance(value, dict):
+        return {"map": {str(k): _encode_value(v) for k, v in value.items()}}
+    if value is None or isinstance(value, (bool, int, float, str)):
+        return value
+    raise ArtifactError(f"cannot store a graph argument of type {type(value).__name__}")
+
+
+def _torch_attr(text: str):
+    import torch
+
+    name = text.removeprefix("torch.")
+    value = getattr(torch, name, None)
+    if value is None:
+        raise ArtifactCompatibilityError(f"unknown torch constant {text!r} in the stored graph")
+    return value
+
+
+def _decode_value(value):
+    import torch
+
+    from .graph import Ref
+
+    if isinstance(value, list):
+        return [_decode_value(v) for v in value]
+    if isinstance(value, dict):
+        if "ref" in value:
+            return Ref(str(value["ref"]))
+        if "dtype" in value:
+            return _torch_attr(value["dtype"])
+        if "device" in value:
+            return torch.device(value["device"])
+        if "torch" in value:
+            return _torch_attr(value["torch"])
+        if "tuple" in value:
+            return tuple(_decode_value(v) for v in value["tuple"])
+        if "map" in value:
+            return {k: _decode_value(v) for k, v in value["map"].items()}
+        raise ArtifactCompatibilityError(f"malformed stored graph value {value!r}")
+    return value
+
+
+def encode_graph(graph) -> dict[str, Any]:
+    """The lowered graph as JSON-safe data (node records, inputs, outputs; state goes to payloads)."""
+
+    return {
+        "inputs": list(graph.inputs),
+        "input_meta": {k: {"shape": list(shape), "dtype": str(dtype)} for k, (shape, dtype) in
+                       graph.input_meta.items()},
+        "state_names": list(graph.state_names),
+        "state_labels": dict(graph.state_labels),
+        "nodes": [{"name": n.name, "op": n.op, "args": _encode_value(tuple(n.args)),
+                   "kwargs": _encode_value(dict(n.kwargs)), "shape": None if n.shape is None else list(n.shape),
+                   "dtype": None if n.dtype is None else str(n.dtype)} for n in graph.nodes],
+        "outputs": _encode_value(list(graph.outputs)),
+    }
+
+
+def decode_graph(data: Mapping[str, Any], state: Mapping[str, Any]):
+    from .graph import LoweredGraph, Node
+
+    try:
+        nodes = [Node(str(n["name"]), str(n["op"]), tuple(_decode_value(n["args"])), dict(_decode_value(n["kwargs"])),
+                      None if n["shape"] is None else tuple(int(d) for d in n["shape"]),
+                      None if n["dtype"] is None else _torch_attr(n["dtype"])) for n in data["nodes"]]
+        meta = {k: (tuple(int(d) for d in v["shape"]), _torch_attr(v["dtype"])) for k, v in data["input_meta"].items()}
+        names = [str(n) for n in data["state_names"]]
+        return LoweredGraph(inputs=[str(i) for i in data["inputs"]], input_meta=meta, state_names=names,
+                            state={n: state[n] for n in names}, nodes=nodes, outputs=list(_decode_value(data["outputs"])),
+                            state_labels={str(k): str(v) for k, v in data.get("state_labels", {}).items()})
+    except (KeyError, TypeError, ValueError) as error:
+        raise ArtifactCompatibilityError(f"stored graph is malformed: {error}") from error
+
+
+def save_graph_plan(compiled, path: str | os.PathLike[str]) -> Path:
+    """Save a ``compile_callable`` / ``compile_module`` result (artifact.py:82-269 for graph plans)."""
+
+    import torch
+
+    from . import _lib
+    from .compiler import CompiledModulePlan
+
+    result = compiled.compilation if isinstance(compiled, CompiledModulePlan) else compiled
+    graph = result.lowered_graph
+    runner = result.plan._keepalive
+    device = runner.device
+    image = _lib.installed_image(device.index if device.index is not None else 0)
+    if image is None:
+        _lib.ensure_code_object(device.index)
+        image = _lib.installed_image(device.index)
+    config: dict[str, Any] = {"entry": "module" if isinstance(compiled, CompiledModulePlan) else "callable",
+                              "name": result.plan.name}
+    if isinstance(compiled, CompiledModulePlan):
+        config.update({"input_count": compiled.input_count, "state_names": list(compiled.state_names),
+                       "tensor_kwarg_names": list(compiled.tensor_kwarg_names)})
+    state = [(name, runner.state[name] if isinstance(runner.state[name], torch.Tensor)
+              else torch.as_tensor(runner.state[name])) for name in graph.state_names]
+    return write_artifact(path, kind="graph", spec=None, config=config, state=state,
+                          selections=result.plan.selections, code_object=image, profile=device_profile(device),
+                          graph=encode_graph(graph))
+
+
+def _load_graph(contents: ArtifactContents, device):
+    from .compiler import CompilationResult, CompiledModulePlan
+    from .graph_ops import build_graph_plan
+
+    _install_code_object(contents.code_object, device.index if device.index is not None else 0)
+    entry = contents.manifest["entrypoint"]
+    state = _device_state(contents, device)
+    graph = decode_graph(entry.get("graph") or {}, state)
+    config = entry["config"]
+    plan, runner = build_graph_plan(graph, name=str(config.get("name", "graph")))
+    plan._keepalive = runner
+    rebuilt = [_encode_selection(s) for s in plan.selections]
+    stored = [_encode_selection(s) for s in contents.selections]
+    if rebuilt != stored:
+        raise ArtifactCompatibilityError("the rebuilt graph plan selects different kernels than the artifact records",
+                                         hint="the artifact was written by another version of this package")
+    result = CompilationResult(plan=plan, input_graph=graph, lowered_graph=graph)
+    if config.get("entry") != "module":
+        return result
+    return CompiledModulePlan(compilation=result, input_count=int(config["input_count"]),
+                              state_names=tuple(config.get("state_names", ())),
+                              tensor_kwarg_names=tuple(config.get("tensor_kwarg_names", ())), _runner=runner)
 
 
 __all__ = [
@@ -600,6 +761,7 @@ __all__ = [
     "read_artifact",
     "read_artifact_manifest",
     "save_compiled",
+    "save_graph_plan",
     "save_plan",
     "save_runtime",
     "write_artifact",

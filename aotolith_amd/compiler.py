@@ -52,6 +52,13 @@ class CompilationResult:
     def __call__(self, *inputs, verify_index_bounds: bool = True, memory: str = "latency"):
         return self.plan(*inputs, verify_index_bounds=verify_index_bounds, memory=memory)
 
+    def save(self, path):
+        """Write the plan as a ``.aoto`` artifact (gfx950 code object, graph, bound state)."""
+
+        from .artifact import save_compiled
+
+        return save_compiled(self, path)
+
     def prepare(self, memory: str = "latency") -> dict:
         """Everything is built at compile time; report what a call does."""
 
@@ -92,6 +99,13 @@ class CompiledModulePlan:
 
     def prepare(self, memory: str = "latency") -> dict:
         return self.compilation.prepare(memory)
+
+    def save(self, path):
+        """Write the plan as a ``.aoto`` artifact; ``load_compiled_module`` reloads it in any process."""
+
+        from .artifact import save_compiled
+
+        return save_compiled(self, path)
 
     def __call__(self, *inputs, verify_index_bounds: bool = True, memory: str = "latency", **tensor_kwargs):
         if len(inputs) != self.input_count:

@@ -145,3 +145,54 @@ def test_unsupported_targets_and_training_mode_are_refused():
     model = tiny_llama(10).train()
     with pytest.raises(CompilationError):
         aoto.compile_module(model, (config1_ids(),))
+
+
+def test_module_plan_artifact_reloads_here_and_in_a_fresh_process(tmp_path):
+    import json
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    import aotolith_amd as aoto
+    from aotolith_amd import load_compiled_module, read_artifact_manifest
+
+    model = module_case(tiny_llama(12))
+    ids = config1_ids(13)
+    plan = aoto.compile_module(model, (ids,), target="hip-gfx950")
+    (logits,) = plan(ids)
+    path = plan.save(tmp_path / "tiny.aoto")
+    manifest = read_artifact_manifest(path)
+    assert manifest["entrypoint"]["kind"] == "graph" and manifest["profile"]["architecture"] == "gfx950"
+    loaded = load_compiled_module(path)
+    assert loaded.selections == plan.selections and loaded.state_names == plan.state_names
+    (again,) = loaded(ids)
+    assert torch.equal(again.cpu(), logits.cpu())
+    root = Path(__file__).resolve().parents[1]
+    script = ("import json, sys, torch\n"
+              "from aotolith_amd import load_compiled_module\n"
+              "plan = load_compiled_module(sys.argv[1])\n"
+              "ids = torch.tensor(json.loads(sys.argv[2]), dtype=torch.int64)\n"
+              "(out,) = plan(ids)\n"
+              "print(json.dumps(out.cpu().flatten().tolist()))\n")
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([str(root), env.get("PYTHONPATH", "")])
+    print(f"[graph-artifact] fresh process loading {path}", flush=True)
+    done = subprocess.run([sys.executable, "-c", script, str(path), json.dumps(ids.tolist())], capture_output=True,
+                          text=True, env=env, timeout=240)
+    assert done.returncode == 0, done.stderr[-2000:]
+    fresh = torch.tensor(json.loads(done.stdout.strip().splitlines()[-1]))
+    assert torch.equal(fresh, logits.cpu().flatten())
+
+
+def test_callable_artifact_round_trip(tmp_path):
+    import aotolith_amd as aoto
+    from aotolith_amd import load_compiled_module
+    from tests.graph_cases import indexing
+
+    inputs = [c for c in CASES if c[0] == "indexing"][0][2]()
+    result = aoto.compile_callable(indexing, inputs)
+    want = result.plan(*inputs)
+    loaded = load_compiled_module(result.save(tmp_path / "indexing.aoto"))
+    got = loaded.plan(*inputs)
+    assert all(torch.equal(a.cpu(), b.cpu()) for a, b in zip(got, want))

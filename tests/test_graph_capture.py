@@ -95,3 +95,24 @@ def test_capture_refuses_data_dependent_control_flow():
 
     with pytest.raises(CompilationError):
         capture(branchy, (torch.ones(3),))
+
+
+def test_graph_encoding_round_trips_through_json():
+    """The artifact's graph record (aotolith_amd.artifact.encode_graph) decodes to the same graph."""
+
+    import json
+
+    from aotolith_amd.artifact import decode_graph, encode_graph
+    from aotolith_amd.graph import capture
+
+    model = module_case(tiny_llama(11))
+    graph = capture(model, (config1_ids(12),))
+    text = json.dumps(encode_graph(graph), sort_keys=True)
+    again = decode_graph(json.loads(text), graph.state)
+    assert again.inputs == graph.inputs and again.input_meta == graph.input_meta
+    assert again.state_names == graph.state_names and again.outputs == graph.outputs
+    assert [(n.name, n.op, n.args, n.kwargs, n.shape, n.dtype) for n in again.nodes] == \
+        [(n.name, n.op, n.args, n.kwargs, n.shape, n.dtype) for n in graph.nodes]
+    ids = config1_ids(13)
+    np.testing.assert_array_equal(GraphOracle(again).run({graph.inputs[0]: ids})[0],
+                                  GraphOracle(graph).run({graph.inputs[0]: ids})[0])
