@@ -131,11 +131,12 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s) {
     case 896:
       // Long outputs: 8 lanes x 4 chunks (32 slots for the 28 chunks of a row;
       // the 4 spare slots repeat the last chunk), x read from LDS so the two
-      // weight register sets fit at 5 waves per SIMD, 3 blocks per CU.
+      // weight register sets fit; 4 blocks per CU (measured in one process
+      // against 3 and 5: 14.3 vs 15.6 / 14.6 us for the 151936-row LM head).
       if (short_out)
         *s = {32, 1, true};
       else
-        *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 3};
+        *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 4};
       return true;
     case 4096:
       // Up to 16384 outputs (q/k/v, o, gate/up of an 8B model) a wave holds too

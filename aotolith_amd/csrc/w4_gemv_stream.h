@@ -366,15 +366,19 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   unsigned long long best = 0;
   auto consume = [&](int tile, const Regs& r) {
     float total = 0.f, total_up = 0.f;
+    // Branch-free over the chunks: a lane past the row's last chunk computes on
+    // the clamped (in-bounds) chunk and weights it by zero. An exec-masked
+    // branch here would hide the per-set load waits from the compiler's wait
+    // placement, which then waits for the next tile's prefetch at the loop head.
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = li + LPR * j;
-      if (c < nchunks) {
-        const uint4* xc = INREG ? xr[j] : xp + c * 4;
-        const float corr = INREG ? cr[j] : 136.f * csum[c];
-        total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, pair_half(r.s[j], shalf[j]), total);
-        if (PAIRED) total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, pair_half(r.us[j], shalf[j]), total_up);
-      }
+      const bool valid = li + LPR * j < nchunks;
+      const int c = cidx[j];
+      const uint4* xc = INREG ? xr[j] : xp + c * 4;
+      const float corr = INREG ? cr[j] : 136.f * csum[c];
+      total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, valid ? pair_half(r.s[j], shalf[j]) : 0.f, total);
+      if (PAIRED)
+        total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, valid ? pair_half(r.us[j], shalf[j]) : 0.f, total_up);
     }
     total = group_sum<LPR>(total);
     if (PAIRED) total_up = group_sum<LPR>(total_up);
@@ -445,19 +449,27 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
       tile += total_waves;
     }
   } else {
-    // Long outputs: many tiles per wave; the prefetch is unconditional (its
-    // index clamped) so the loop has no branch between a load and its use,
-    // and the one redundant prefetch at the end is not used.
-    while (true) {
+    // Long outputs: many tiles per wave. The trip count is computed up front
+    // (uniform), so the loop has one exit and no branch between a load and its
+    // use; the prefetch is unconditional (index clamped), and the one redundant
+    // prefetch at the end is not used. A loop with an exit in the middle lets
+    // the compiler's wait placement merge a path on which the other register
+    // set is still in flight into the loop head, which then waits for every
+    // outstanding load before issuing the next prefetch.
+    // The scheduling barriers keep each prefetch ahead of the math on the
+    // other set (the scheduler would otherwise start the math first, and the
+    // prefetch would wait behind the current set's loads).
+    const int mine = (tiles - tile + total_waves - 1) / total_waves;
+    for (int i = 0; i + 2 <= mine; i += 2) {
       load(tile + total_waves, rb);
+      __builtin_amdgcn_sched_barrier(0);
       consume(tile, ra);
-      tile += total_waves;
-      if (tile >= tiles) break;
-      load(tile + total_waves, ra);
-      consume(tile, rb);
-      tile += total_waves;
-      if (tile >= tiles) break;
+      load(tile + 2 * total_waves, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(tile + total_waves, rb);
+      tile += 2 * total_waves;
     }
+    if (mine & 1) consume(tile, ra);
   }
   if (ARGMAX) {
     best = wave_max_u64(best);
