@@ -225,8 +225,8 @@ bool argmax_shape(int K, int N, int group, StreamShape* s) {
 
 unsigned blocks_for(long long items, int threads) { return (unsigned)((items + threads - 1) / threads); }
 
-// Decode attention split choice. One block holds at most `max_chunk` keys (one
-// key row per D/64 lanes of 256 threads); longer windows split into blocks whose
+// Decode attention split choice. One block holds at most `max_chunk` keys (8
+// wave loads of 64/(D/8) rows per wave, 4 waves); longer windows split into blocks whose
 // records a merge launch combines. `requested` > 0 asks for that many splits.
 int decode_max_chunk(int head_dim) { return head_dim == 64 ? 256 : 128; }
 

@@ -106,15 +106,24 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
 // With `step` non-null, {position, valid, ring_offset, slot} come from the
 // device step state of a captured decode loop.
 //
-// Grid (splits, B*Hq); 256 threads; one query head per block, keys
-// [split*chunk, min(cap, (split+1)*chunk)). The decode window is tiny, so the
-// design minimizes dependent steps rather than bytes: every key row is one
-// lane's (D/64 lanes per key, 64 dims each, q in registers), so a score needs
-// no cross-lane reduction; P.V gives each thread a pair of dims and a strided
-// subset of keys. All of a block's K and V loads are independent and issued
-// together. One split writes the output; several write (max, sum, acc[D])
-// records that aoto_decode_attention_merge combines in a second launch.
-template <int D, bool FUSED>
+// Grid (splits, B*Hq); 256 threads (4 waves); one query head per block, keys
+// [split*chunk, min(cap, (split+1)*chunk)), chunk <= 16384 / D (256 keys at
+// D = 64, 128 at D = 128). The window is tiny, so the design minimizes dependent
+// steps and keeps every load coalesced:
+// * a key row is D/8 lanes, 16 bytes (8 dims) each, so one wave load reads
+//   64/(D/8) consecutive rows - 1 KB contiguous - of K or V;
+// * wave w owns a contiguous run of the split's keys; its K and V chunks, the
+//   query (and, FUSED, the new key/value and RoPE rows) are all loaded up
+//   front, the small loads first so the RoPE can start while K and V land;
+// * a score is 4 bf16 dot2 per lane and a DPP sum over the row's D/8 lanes;
+//   each wave keeps its own softmax (max m_w, sum l_w, unnormalized P.V over its
+//   keys, 8 dims per lane), so the block meets at one barrier, where D threads
+//   combine the waves' records (the same rescaling the split merge uses).
+// ROWS: the RoPE rows come from `rope_rows` (no dependence on the step state);
+// otherwise from the tables at the position. One split writes the output;
+// several write (max, sum, acc[D]) records that aoto_decode_attention_merge
+// combines in a second launch.
+template <int D, bool FUSED, bool ROWS>
 __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ row,
                                       int row_width, int query_start, int key_start, int value_start,
                                       const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table,
@@ -125,18 +134,13 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
                                       int kv_heads, float scale, int chunk, float* __restrict__ partials,
                                       const int* __restrict__ step, const uint16_t* __restrict__ rope_rows,
                                       uint16_t* __restrict__ out) {
-  constexpr int THREADS = 256;
-  constexpr int LPK = D / 64;             // lanes per key (64 dims each)
-  constexpr int KPP = THREADS / LPK;      // keys per block (one key row per D/64 lanes)
-  constexpr int PAIRS = D / 2;            // bf16 pairs per row
-  constexpr int KG = THREADS / PAIRS;     // key groups in P.V
-  constexpr int VPT = KPP / KG;           // value pairs per thread (all loaded up front)
-  __shared__ __attribute__((aligned(16))) float s_p[KPP];
-  __shared__ float s_red[THREADS / 64];
-  __shared__ float s_acc[KG][D];
-  __shared__ __attribute__((aligned(16))) float s_q[D];
-  __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vnew[D];
+  constexpr int WAVES = 4;
+  constexpr int LPK = D / 8;                    // lanes per key row (8 dims each)
+  constexpr int KPI = 64 / LPK;                 // key rows per wave load
+  constexpr int J = 16384 / D / (WAVES * KPI);  // loads per wave at the largest chunk
+  constexpr int HALF_LANES = LPK / 2;           // lanes holding the first half of a row
+  __shared__ __attribute__((aligned(16))) float s_acc[WAVES][64][8];
+  __shared__ float s_m[WAVES], s_l[WAVES];
 
   const int split = blockIdx.x;
   const int splits = gridDim.x;
@@ -145,91 +149,88 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   const int group = query_heads / kv_heads;
   const int kvh = h / group;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPK;                   // dims [8*sub, 8*sub + 8)
+  const int kin = lane / LPK;                   // key within a wave load
   const int s0 = split * chunk;
-  const int n = max(0, min(cap, s0 + chunk) - s0);  // <= KPP, checked on the host
-  const int sub = threadIdx.x % LPK;      // which 64 dims of a key row
-  const int kl = threadIdx.x / LPK;       // this thread's key
-  const int d2 = threadIdx.x % PAIRS;     // P.V: this thread's dim pair
-  const int kg = threadIdx.x / PAIRS;     // P.V: keys kg, kg + KG, ...
+  const int n = max(0, min(cap, s0 + chunk) - s0);  // <= KPI * J * WAVES, checked on the host
+  const int loads = (n + WAVES * KPI - 1) / (WAVES * KPI);  // wave loads per wave, <= J
+  const int wfirst = wave * loads * KPI;        // this wave's first key (split-relative)
 
   uint16_t* kh = kbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
   uint16_t* vh = vbase + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
 
-  // Every K and V row of the block is loaded first: those addresses do not
-  // depend on the device step state, whose read (and the RoPE table rows it
-  // selects) would otherwise hold back every other load by a round trip.
-  const int ksl = s0 + min(kl, max(n - 1, 0));
-  uint4 kv[8];
-  {
-    const uint4* kr = reinterpret_cast<const uint4*>(kh + (size_t)ksl * D);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) kv[c] = kr[sub * 8 + c];
-  }
-  // P.V work split: thread (kg, d2) owns dims (2*d2, 2*d2+1) of keys
-  // [kg*VPT, (kg+1)*VPT), so its probabilities are one contiguous LDS run.
-  const int kbase0 = kg * VPT;
-  uint32_t vv[VPT];
-#pragma unroll
-  for (int u = 0; u < VPT; ++u) {
-    const int sl = s0 + min(kbase0 + u, max(n - 1, 0));
-    vv[u] = reinterpret_cast<const uint32_t*>(vh + (size_t)sl * D)[d2];
-  }
-  // The query / new key / new value of this head, and the RoPE rows of the
-  // position: from `rope_rows` (cos row, then sin row) when given - no
-  // dependence on the step state - else from the tables at the step's position.
-  const int d = min((int)threadIdx.x, D - 1);
-  uint32_t qx = 0, qp = 0, kx = 0, kp = 0, cs = 0, sn = 0, vx = 0;
-  const int half = D / 2;
-  const int pd = d < half ? d + half : d - half;
+  // Small loads first: the query chunk (and its RoPE partner), the new key /
+  // value chunks and the RoPE rows (from `rope_rows` when given, so nothing
+  // waits on the device step state), then K and V.
+  const int psub = (sub + HALF_LANES) % LPK;    // partner chunk: dims d +- D/2
+  uint4 qc, qpc = make_uint4(0, 0, 0, 0), kc = qpc, kpc = qpc, vc = qpc, cc = qpc, sc = qpc;
   if (FUSED) {
     const uint16_t* rrow = row + (size_t)b * row_width;
-    const uint16_t* qh = rrow + query_start + (size_t)h * D;
-    const uint16_t* khh = rrow + key_start + (size_t)kvh * D;
-    qx = qh[d];
-    qp = qh[pd];
-    kx = khh[d];
-    kp = khh[pd];
-    vx = rrow[value_start + (size_t)kvh * D + d];
-    if (rope_rows != nullptr) {
-      cs = rope_rows[d];
-      sn = rope_rows[D + d];
+    const uint4* qh = reinterpret_cast<const uint4*>(rrow + query_start + (size_t)h * D);
+    const uint4* khh = reinterpret_cast<const uint4*>(rrow + key_start + (size_t)kvh * D);
+    qc = qh[sub];
+    qpc = qh[psub];
+    kc = khh[sub];
+    kpc = khh[psub];
+    vc = reinterpret_cast<const uint4*>(rrow + value_start + (size_t)kvh * D)[sub];
+    if (ROWS) {
+      cc = reinterpret_cast<const uint4*>(rope_rows)[sub];
+      sc = reinterpret_cast<const uint4*>(rope_rows + D)[sub];
     }
   } else {
-    qx = q[((size_t)b * query_heads + h) * D + d];
+    qc = reinterpret_cast<const uint4*>(q + ((size_t)b * query_heads + h) * D)[sub];
   }
+  // Keep these ahead of K and V: loads complete in issue order, so the RoPE's
+  // wait then leaves K and V in flight.
+  __builtin_amdgcn_sched_barrier(0);
+  // K then V chunks of this wave's keys (the last row repeats past n). All J
+  // loads are issued, with no branch between them, so the wait before the
+  // RoPE covers only the small loads; loads past `loads` are never used.
+  uint4 kq[J], vq[J];
+  const int last = max(n - 1, 0);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int key = s0 + min(wfirst + j * KPI + kin, last);
+    kq[j] = reinterpret_cast<const uint4*>(kh + (size_t)key * D)[sub];
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int key = s0 + min(wfirst + j * KPI + kin, last);
+    vq[j] = reinterpret_cast<const uint4*>(vh + (size_t)key * D)[sub];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   if (step != nullptr) {
     position = step[0];
     valid = step[1];
     ring_offset = step[2];
     slot = step[3];
   }
-  if (FUSED && rope_rows == nullptr) {
-    cs = cos_table[(size_t)position * D + d];
-    sn = sin_table[(size_t)position * D + d];
+  if (FUSED && !ROWS) {
+    cc = reinterpret_cast<const uint4*>(cos_table + (size_t)position * D)[sub];
+    sc = reinterpret_cast<const uint4*>(sin_table + (size_t)position * D)[sub];
   }
-
-  // Query (rotated out of the projection row when FUSED) into LDS, f32.
-  if (threadIdx.x < D) {
+  // RoPE of the query (and new key) for this lane's 8 dims, f32, one rounding
+  // to bf16 (codegen/kv_cache.py:144-159), packed as bf16 pairs for dot2.
+  uint32_t qw[4], knew[4];
+  {
+    const uint32_t qa[4] = {qc.x, qc.y, qc.z, qc.w};
     if (FUSED) {
-      const float sign = d < half ? -1.f : 1.f;
-      const float c = bf16_to_f32(cs), sv = bf16_to_f32(sn);
-      s_q[d] = round_bf16(bf16_to_f32(qx) * c + sign * bf16_to_f32(qp) * sv);
-      s_knew[d] = (uint16_t)f32_to_bf16(bf16_to_f32(kx) * c + sign * bf16_to_f32(kp) * sv);
-      s_vnew[d] = (uint16_t)vx;
+      const uint32_t qp[4] = {qpc.x, qpc.y, qpc.z, qpc.w}, ka[4] = {kc.x, kc.y, kc.z, kc.w};
+      const uint32_t kp[4] = {kpc.x, kpc.y, kpc.z, kpc.w};
+      const uint32_t ca[4] = {cc.x, cc.y, cc.z, cc.w}, sa[4] = {sc.x, sc.y, sc.z, sc.w};
+      const float sign = sub < HALF_LANES ? -1.f : 1.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float c0 = bf16_lo(ca[i]), c1 = bf16_hi(ca[i]), s0v = bf16_lo(sa[i]), s1v = bf16_hi(sa[i]);
+        qw[i] = pack_bf16x2(bf16_lo(qa[i]) * c0 + sign * bf16_lo(qp[i]) * s0v,
+                            bf16_hi(qa[i]) * c1 + sign * bf16_hi(qp[i]) * s1v);
+        knew[i] = pack_bf16x2(bf16_lo(ka[i]) * c0 + sign * bf16_lo(kp[i]) * s0v,
+                              bf16_hi(ka[i]) * c1 + sign * bf16_hi(kp[i]) * s1v);
+      }
     } else {
-      s_q[d] = bf16_to_f32(qx);
-    }
-  }
-  __syncthreads();
-  if (FUSED && ksl == slot) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) kv[c] = reinterpret_cast<const uint4*>(s_knew)[sub * 8 + c];
-  }
-  if (FUSED) {
-#pragma unroll
-    for (int u = 0; u < VPT; ++u) {
-      const int sl = s0 + min(kbase0 + u, max(n - 1, 0));
-      if (sl == slot) vv[u] = reinterpret_cast<const uint32_t*>(s_vnew)[d2];
+      for (int i = 0; i < 4; ++i) qw[i] = qa[i];
     }
   }
 
@@ -240,81 +241,107 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
     return logical >= cap - valid;
   };
 
-  // Score of this thread's key (64 dims per lane).
-  float dot = 0.f;
-  const float4* qs = reinterpret_cast<const float4*>(s_q + sub * 64);
+  // Scores of this wave's keys; the slot being written uses the new key.
+  float score[J];
+  float wmax = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const float4 qa = qs[2 * c], qb = qs[2 * c + 1];
-    const uint32_t a[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
-    dot = fmaf(qa.x, bf16_lo(a[0]), dot);
-    dot = fmaf(qa.y, bf16_hi(a[0]), dot);
-    dot = fmaf(qa.z, bf16_lo(a[1]), dot);
-    dot = fmaf(qa.w, bf16_hi(a[1]), dot);
-    dot = fmaf(qb.x, bf16_lo(a[2]), dot);
-    dot = fmaf(qb.y, bf16_hi(a[2]), dot);
-    dot = fmaf(qb.z, bf16_lo(a[3]), dot);
-    dot = fmaf(qb.w, bf16_hi(a[3]), dot);
-  }
-  if (LPK == 2) dot += dpp_move<kDppXor1>(dot);
-  float sc = -INFINITY;
-  if (kl < n && kept(ksl)) sc = dot * scale;
-  if (sub == 0 && kl < n) s_p[kl] = sc;
-  const float m = wave_max(sc);
-  if (lane == 0) s_red[wave] = m;
-  __syncthreads();
-  float row_max = s_red[0];
-#pragma unroll
-  for (int w = 1; w < THREADS / 64; ++w) row_max = fmaxf(row_max, s_red[w]);
-  __syncthreads();  // s_red is reused below
-  // Probabilities; slots past the range read as 0 in P.V.
-  float p_local = 0.f;
-  if (threadIdx.x < KPP) {
-    if (threadIdx.x < n) {
-      const float v = s_p[threadIdx.x];
-      p_local = (row_max == -INFINITY || v == -INFINITY) ? 0.f : expf(v - row_max);
+  for (int j = 0; j < J; ++j) {
+    score[j] = -INFINITY;
+    if (j < loads) {
+      const int rel = wfirst + j * KPI + kin;
+      const int key = s0 + min(rel, last);
+      uint4 k = kq[j];
+      if (FUSED) {
+        const bool mine = key == slot;
+        k.x = mine ? knew[0] : k.x;
+        k.y = mine ? knew[1] : k.y;
+        k.z = mine ? knew[2] : k.z;
+        k.w = mine ? knew[3] : k.w;
+      }
+      float dot = dot2_bf16(k.x, qw[0], 0.f);
+      dot = dot2_bf16(k.y, qw[1], dot);
+      dot = dot2_bf16(k.z, qw[2], dot);
+      dot = dot2_bf16(k.w, qw[3], dot);
+      dot = group_sum<LPK>(dot);
+      score[j] = (rel < n && kept(key)) ? dot * scale : -INFINITY;
+      wmax = fmaxf(wmax, score[j]);
     }
-    s_p[threadIdx.x] = p_local;
   }
-  const float t = wave_sum(p_local);
-  if (lane == 0) s_red[wave] = t;
-  __syncthreads();
-  float row_sum = 0.f;
-#pragma unroll
-  for (int w = 0; w < THREADS / 64; ++w) row_sum += s_red[w];
+  const float m = wave_max(wmax);
 
-  // P.V over this thread's keys and dim pair.
-  float a0 = 0.f, a1 = 0.f;
-  const float4* pv4 = reinterpret_cast<const float4*>(s_p + kbase0);
+  // This wave's probabilities, their sum and its P.V over 8 dims per lane.
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
 #pragma unroll
-  for (int u4 = 0; u4 < VPT / 4; ++u4) {
-    const float4 pr = pv4[u4];
-    const float pp[4] = {pr.x, pr.y, pr.z, pr.w};
+  for (int j = 0; j < J; ++j) {
+    if (j < loads) {
+      const float pj = (m == -INFINITY || score[j] == -INFINITY) ? 0.f : expf(score[j] - m);
+      lsum += pj;
+      uint4 v = vq[j];
+      if (FUSED) {
+        const int key = s0 + min(wfirst + j * KPI + kin, last);
+        const bool mine = key == slot;
+        v.x = mine ? vc.x : v.x;
+        v.y = mine ? vc.y : v.y;
+        v.z = mine ? vc.z : v.z;
+        v.w = mine ? vc.w : v.w;
+      }
+      const uint32_t va[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      a0 = fmaf(pp[e], bf16_lo(vv[u4 * 4 + e]), a0);
-      a1 = fmaf(pp[e], bf16_hi(vv[u4 * 4 + e]), a1);
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = fmaf(pj, bf16_lo(va[i]), acc[2 * i]);
+        acc[2 * i + 1] = fmaf(pj, bf16_hi(va[i]), acc[2 * i + 1]);
+      }
     }
   }
-  s_acc[kg][2 * d2] = a0;
-  s_acc[kg][2 * d2 + 1] = a1;
-  __syncthreads();
-  if (FUSED && h % group == 0 && slot >= s0 && slot < s0 + n && threadIdx.x < D) {
-    kh[(size_t)slot * D + threadIdx.x] = s_knew[threadIdx.x];
-    vh[(size_t)slot * D + threadIdx.x] = s_vnew[threadIdx.x];
+  // Each key's probability sits in all LPK lanes of its row: count it once.
+  const float l = wave_sum(sub == 0 ? lsum : 0.f);
+  reinterpret_cast<float4*>(s_acc[wave][lane])[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  reinterpret_cast<float4*>(s_acc[wave][lane])[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
   }
-  if (threadIdx.x < D) {
-    float acc = 0.f;
+  // The first query head of each kv group stores the new (k_rot, v) row.
+  if (FUSED && h % group == 0) {
 #pragma unroll
-    for (int g = 0; g < KG; ++g) acc += s_acc[g][d];
+    for (int j = 0; j < J; ++j) {
+      const int rel = wfirst + j * KPI + kin;
+      if (j < loads && rel < n && s0 + rel == slot) {
+        reinterpret_cast<uint4*>(kh + (size_t)slot * D)[sub] = make_uint4(knew[0], knew[1], knew[2], knew[3]);
+        reinterpret_cast<uint4*>(vh + (size_t)slot * D)[sub] = vc;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Combine the waves: M = max m_w, sum = sum e^(m_w - M) l_w, acc likewise.
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    float mw[WAVES], big = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      mw[w] = s_m[w];
+      big = fmaxf(big, mw[w]);
+    }
+    float total = 0.f, sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const float f = (mw[w] == -INFINITY) ? 0.f : expf(mw[w] - big);
+      float part = 0.f;
+#pragma unroll
+      for (int r = 0; r < KPI; ++r) part += s_acc[w][r * LPK + d / 8][d % 8];
+      total = fmaf(f, part, total);
+      sum = fmaf(f, s_l[w], sum);
+    }
     if (splits == 1) {
-      out[((size_t)b * query_heads + h) * D + d] = (uint16_t)f32_to_bf16(row_sum > 0.f ? acc / row_sum : 0.f);
+      out[((size_t)b * query_heads + h) * D + d] = (uint16_t)f32_to_bf16(sum > 0.f ? total / sum : 0.f);
     } else {
       float* rec = partials + (((size_t)b * query_heads + h) * splits + split) * (D + 2);
-      rec[2 + d] = acc;
+      rec[2 + d] = total;
       if (d == 0) {
-        rec[0] = row_max;
-        rec[1] = row_sum;
+        rec[0] = big;
+        rec[1] = sum;
       }
     }
   }
@@ -511,10 +538,10 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
       long long kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid, int ring_offset,  \
       int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials, const int* step,  \
       uint16_t* out) {                                                                                   \
-    aoto::decode_attention_body<D, false>(q, nullptr, 0, 0, 0, 0, nullptr, nullptr, kbase, vbase,        \
-                                          kv_batch_stride, kv_head_stride, mask, mask_batch_stride,      \
-                                          valid, ring_offset, 0, -1, cap, query_heads, kv_heads, scale,  \
-                                          chunk, partials, step, nullptr, out);                          \
+    aoto::decode_attention_body<D, false, false>(q, nullptr, 0, 0, 0, 0, nullptr, nullptr, kbase, vbase, \
+                                                 kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
+                                                 valid, ring_offset, 0, -1, cap, query_heads, kv_heads,    \
+                                                 scale, chunk, partials, step, nullptr, out);              \
   }                                                                                                      \
   extern "C" __global__ __launch_bounds__(256) void aoto_decode_rope_attention_d##D(                    \
       const uint16_t* row, int row_width, int query_start, int key_start, int value_start,               \
@@ -522,9 +549,16 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
       long long kv_batch_stride, long long kv_head_stride, int valid, int ring_offset, int position,     \
       int slot, int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials,          \
       const int* step, const uint16_t* rope_rows, uint16_t* out) {                                       \
-    aoto::decode_attention_body<D, true>(nullptr, row, row_width, query_start, key_start, value_start,   \
-                                         cos_table, sin_table, kbase, vbase, kv_batch_stride,            \
-                                         kv_head_stride, nullptr, 0, valid, ring_offset, position, slot, \
-                                         cap, query_heads, kv_heads, scale, chunk, partials, step,       \
-                                         rope_rows, out);                                                \
+    if (rope_rows != nullptr)                                                                            \
+      aoto::decode_attention_body<D, true, true>(nullptr, row, row_width, query_start, key_start,        \
+                                                 value_start, cos_table, sin_table, kbase, vbase,       \
+                                                 kv_batch_stride, kv_head_stride, nullptr, 0, valid,    \
+                                                 ring_offset, position, slot, cap, query_heads,         \
+                                                 kv_heads, scale, chunk, partials, step, rope_rows, out); \
+    else                                                                                                 \
+      aoto::decode_attention_body<D, true, false>(nullptr, row, row_width, query_start, key_start,       \
+                                                  value_start, cos_table, sin_table, kbase, vbase,      \
+                                                  kv_batch_stride, kv_head_stride, nullptr, 0, valid,   \
+                                                  ring_offset, position, slot, cap, query_heads,        \
+                                                  kv_heads, scale, chunk, partials, step, nullptr, out); \
   }
