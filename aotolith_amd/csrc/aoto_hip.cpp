@@ -141,9 +141,23 @@ struct StreamShape {
   bool direct;
   int blocks_per_cu = 2;  // persistent 4-wave blocks per CU
   bool block_x = false;   // x staged once per 4-wave block (aoto_w4_gemv_x* instances)
+  int rows = 0;           // > 0: the multi-row direct form, rows per lane (aoto_w4_gemv_r* instances)
 };
 
-bool stream_shape(int K, int N, bool paired, StreamShape* s) {
+// Rows per lane of the multi-row direct GEMV; AOTO_GEMV_ROWS overrides the
+// shape's default (0 selects the streaming form) where that instance exists.
+int gemv_rows(int lpr, int shape_default) {
+  static const int value = [] {
+    const char* env = getenv("AOTO_GEMV_ROWS");
+    return env ? atoi(env) : -1;
+  }();
+  if (value < 0) return shape_default;
+  if (value == 0) return 0;
+  const bool exists = lpr == 32 && (value == 2 || value == 4);
+  return exists ? value : shape_default;
+}
+
+bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) {
   const bool short_out = N <= 8192;
   switch (K) {
     case 896:
@@ -151,9 +165,14 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s) {
       // the 4 spare slots repeat the last chunk), x read from LDS so the two
       // weight register sets fit; 4 blocks per CU (measured in one process
       // against 3 and 5: 14.3 vs 15.6 / 14.6 us for the 151936-row LM head).
-      if (short_out)
+      // Short outputs: the multi-row direct form where one normalized copy of x
+      // serves several rows (paired gate/up: 4 rows per lane, 3.9 vs 4.3 us for
+      // Qwen's 2 x 4864 rows; normed q/k/v: 2, 2.45 vs 2.6 us); without a norm
+      // prologue (o projection) the streaming form is as fast (2.0 us).
+      if (short_out) {
         *s = {32, 1, true};
-      else
+        s->rows = gemv_rows(32, paired ? 4 : (norm ? 2 : 0));
+      } else
         *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 4};
       return true;
     case 4096:
@@ -211,7 +230,10 @@ bool argmax_shape(int K, int N, int group, StreamShape* s) {
       (K / group) % 2 != 0)
     return false;
   // (the 32x1 direct and the block-staged shapes have no argmax instance)
-  if (stream_shape(K, N, false, s) && !(s->direct && s->lpr == 32) && !s->block_x) return true;
+  if (stream_shape(K, N, false, s) && !(s->direct && s->lpr == 32) && !s->block_x) {
+    s->rows = 0;  // the argmax instances are streaming ones
+    return true;
+  }
   if (K <= 64 * 32) {
     *s = {64, 1, true};
     return true;
@@ -342,6 +364,19 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   // The streaming form reads scales and bias as aligned 32-bit pairs.
   const bool pairs_ok = (K / group) % 2 == 0 && aligned4(scales) && (!up_scales || aligned4(up_scales)) &&
                         (!bias || (N % 2 == 0 && aligned4(bias)));
+  if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss, norm) && ss.rows > 0) {
+    // one 1-wave block per tile of (64 / lpr) * rows rows
+    const int rows_per_wave = (64 / ss.lpr) * ss.rows;
+    const unsigned grid = (unsigned)((N + rows_per_wave - 1) / rows_per_wave);
+    int shift = 0;
+    while ((32 << shift) < group) ++shift;
+    char rname[64];
+    snprintf(rname, sizeof(rname), "aoto_w4_gemv_r%dx%dx%d_n%d_p%d_b%d", ss.lpr, ss.cpl, ss.rows, norm,
+             paired ? 1 : 0, has_bias);
+    const int one_wave = 1;
+    return launch(rname, dim3(grid), dim3(64), 0u, stream, x, words, scales, up_words, up_scales, norm_weight,
+                  eps, bias, alpha, beta, y, K, N, shift, one_wave);
+  }
   if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss)) {
     const StreamLaunch l = stream_launch(ss, K, N, group);
     char sname[64];

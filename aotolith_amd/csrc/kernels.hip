@@ -4,6 +4,7 @@
 #include "w4_pack.h"
 #include "w4_gemv.h"
 #include "w4_gemv_stream.h"
+#include "w4_gemv_rows.h"
 #include "w4_gemm.h"
 #include "w8.h"
 #include "generic.h"
@@ -33,6 +34,12 @@ AOTO_GEMV_STREAM_PAIRED(32, 1, 0, true)
 AOTO_GEMV_STREAM_SINGLE(32, 4, 8, true)
 AOTO_GEMV_STREAM_PAIRED(32, 4, 8, true)
 AOTO_GEMV_STREAM_SINGLE(64, 3, 0, true)
+// Multi-row direct GEMV for a decoder layer's short outputs at K = 896:
+// {lanes per row} x {chunks per lane} x {rows per lane}. (Measured and not
+// kept: 8 rows per lane at K = 896, and 2 or 4 rows of the 64x3 layout at
+// K = 4864, no faster than the streaming form.)
+AOTO_GEMV_ROWS_SHAPE(32, 1, 2)
+AOTO_GEMV_ROWS_SHAPE(32, 1, 4)
 // Block-staged x for long reductions with short or mid outputs: K = 4096
 // (Llama-8B q/k/v, o, gate/up) 32x4, K = 14336 (Llama-8B down) 64x7.
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(32, 4, 2)

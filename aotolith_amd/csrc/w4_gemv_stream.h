@@ -48,6 +48,36 @@ AOTO_DEVICE float chunk_dot_fast(const uint4 q, const uint4* __restrict__ xc) {
   return acc;
 }
 
+// One 16-byte vector of x, bf16 pairs (e0,e1) .. (e6,e7): with NORM scaled by
+// the RMS factor ns and multiplied by the norm weight's vector, each product
+// rounded once to bf16; repacked in dot2 pair order {(e0,e4), (e1,e5), (e2,e6),
+// (e3,e7)}. Returns `sum` plus the (rounded) values, added in element order.
+template <bool NORM>
+AOTO_DEVICE float pack_x8(const uint4 raw, const uint4 w, float ns, uint4& out, float sum = 0.f) {
+  const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
+  if (NORM) {
+    const uint32_t wr[4] = {w.x, w.y, w.z, w.w};
+    float lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo[k] = (ns * bf16_lo(r[k])) * bf16_lo(wr[k]);
+      hi[k] = (ns * bf16_hi(r[k])) * bf16_hi(wr[k]);
+    }
+    // element 2k is lo[k], 2k+1 is hi[k]
+    out = make_uint4(cvt_pk_bf16(lo[0], lo[2]), cvt_pk_bf16(hi[0], hi[2]), cvt_pk_bf16(lo[1], lo[3]),
+                     cvt_pk_bf16(hi[1], hi[3]));
+  } else {
+    out = make_uint4(__builtin_amdgcn_perm(r[2], r[0], 0x05040100u), __builtin_amdgcn_perm(r[2], r[0], 0x07060302u),
+                     __builtin_amdgcn_perm(r[3], r[1], 0x05040100u), __builtin_amdgcn_perm(r[3], r[1], 0x07060302u));
+  }
+  const uint32_t o[4] = {out.x, out.y, out.z, out.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sum += bf16_lo(o[k]);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sum += bf16_hi(o[k]);
+  return sum;
+}
+
 // x (optionally RMS-normalized and rounded to bf16) staged by one wave into its
 // own LDS region, in dot2 pair order, plus per-chunk sums. All of x (and the
 // norm weight) is loaded up front - XV 16-byte vectors per lane, XV >= K/512 -
@@ -88,27 +118,9 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
 #pragma unroll
   for (int i = 0; i < XV; ++i) {
     const int v = lane + 64 * i;
-    const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-    float e[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      e[2 * k] = bf16_lo(raw[k]);
-      e[2 * k + 1] = bf16_hi(raw[k]);
-    }
-    if (NORM) {
-      const uint32_t wraw[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        e[2 * k] = round_bf16((ns * e[2 * k]) * bf16_lo(wraw[k]));
-        e[2 * k + 1] = round_bf16((ns * e[2 * k + 1]) * bf16_hi(wraw[k]));
-      }
-    }
-    float sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) sum += e[k];
-    if (v < vecs)
-      xp[v] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
-                         pack_bf16x2(e[3], e[7]));
+    uint4 packed;
+    float sum = pack_x8<NORM>(xr[i], wr[NORM ? i : 0], ns, packed);
+    if (v < vecs) xp[v] = packed;
     // A chunk (32 codes) is four consecutive vectors: lanes 4c .. 4c+3.
     sum = group_sum<4>(sum);
     if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
@@ -158,27 +170,9 @@ AOTO_DEVICE void stage_activation_block(const uint16_t* __restrict__ x, const ui
 #pragma unroll
   for (int i = 0; i < XV; ++i) {
     const int v = threadIdx.x + kGemvThreads * i;
-    const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-    float e[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      e[2 * k] = bf16_lo(raw[k]);
-      e[2 * k + 1] = bf16_hi(raw[k]);
-    }
-    if (NORM) {
-      const uint32_t wraw[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        e[2 * k] = round_bf16((ns * e[2 * k]) * bf16_lo(wraw[k]));
-        e[2 * k + 1] = round_bf16((ns * e[2 * k + 1]) * bf16_hi(wraw[k]));
-      }
-    }
-    float sum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) sum += e[k];
-    if (v < vecs)
-      xp[v] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
-                         pack_bf16x2(e[3], e[7]));
+    uint4 packed;
+    float sum = pack_x8<NORM>(xr[i], wr[NORM ? i : 0], ns, packed);
+    if (v < vecs) xp[v] = packed;
     // A chunk (32 codes) is four consecutive vectors: threads 4c .. 4c+3.
     sum = group_sum<4>(sum);
     if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
@@ -241,27 +235,7 @@ struct DirectActivation {
     for (int j = 0; j < CPL; ++j) {
       float sum = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
-        float e[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          e[2 * i] = bf16_lo(r4[i]);
-          e[2 * i + 1] = bf16_hi(r4[i]);
-        }
-        if (NORM) {
-          const uint32_t w4[4] = {wraw[j][k].x, wraw[j][k].y, wraw[j][k].z, wraw[j][k].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            e[2 * i] = round_bf16((ns * e[2 * i]) * bf16_lo(w4[i]));
-            e[2 * i + 1] = round_bf16((ns * e[2 * i + 1]) * bf16_hi(w4[i]));
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sum += e[i];
-        xr[j][k] = make_uint4(pack_bf16x2(e[0], e[4]), pack_bf16x2(e[1], e[5]), pack_bf16x2(e[2], e[6]),
-                              pack_bf16x2(e[3], e[7]));
-      }
+      for (int k = 0; k < 4; ++k) sum = pack_x8<NORM>(raw[j][k], wraw[NORM ? j : 0][k], ns, xr[j][k], sum);
       cr[j] = 136.f * sum;
     }
   }
