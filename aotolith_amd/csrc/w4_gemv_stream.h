@@ -51,9 +51,12 @@ AOTO_DEVICE float chunk_dot_fast(const uint4 q, const uint4* __restrict__ xc) {
 // One 16-byte vector of x, bf16 pairs (e0,e1) .. (e6,e7): with NORM scaled by
 // the RMS factor ns and multiplied by the norm weight's vector, each product
 // rounded once to bf16; repacked in dot2 pair order {(e0,e4), (e1,e5), (e2,e6),
-// (e3,e7)}. Returns `sum` plus the (rounded) values, added in element order.
+// (e3,e7)}. Returns `corr` plus 136 times the (rounded) values - the offset the
+// (136 + code) weight pairs add to a dot product - accumulated with dot2
+// against the bf16 pair (136, 136) (each product 136 * x is exact).
+constexpr uint32_t kBf16Pair136 = 0x43084308u;
 template <bool NORM>
-AOTO_DEVICE float pack_x8(const uint4 raw, const uint4 w, float ns, uint4& out, float sum = 0.f) {
+AOTO_DEVICE float pack_x8(const uint4 raw, const uint4 w, float ns, uint4& out, float corr = 0.f) {
   const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
   if (NORM) {
     const uint32_t wr[4] = {w.x, w.y, w.z, w.w};
@@ -70,16 +73,24 @@ AOTO_DEVICE float pack_x8(const uint4 raw, const uint4 w, float ns, uint4& out, 
     out = make_uint4(__builtin_amdgcn_perm(r[2], r[0], 0x05040100u), __builtin_amdgcn_perm(r[2], r[0], 0x07060302u),
                      __builtin_amdgcn_perm(r[3], r[1], 0x05040100u), __builtin_amdgcn_perm(r[3], r[1], 0x07060302u));
   }
-  const uint32_t o[4] = {out.x, out.y, out.z, out.w};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) sum += bf16_lo(o[k]);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) sum += bf16_hi(o[k]);
-  return sum;
+  corr = dot2_bf16(out.x, kBf16Pair136, corr);
+  corr = dot2_bf16(out.y, kBf16Pair136, corr);
+  corr = dot2_bf16(out.z, kBf16Pair136, corr);
+  return dot2_bf16(out.w, kBf16Pair136, corr);
+}
+
+// Sum of squares of the eight bf16 values of a 16-byte vector (each square is
+// exact in f32), accumulated with dot2.
+AOTO_DEVICE float sum_squares8(const uint4 raw, float ss) {
+  ss = dot2_bf16(raw.x, raw.x, ss);
+  ss = dot2_bf16(raw.y, raw.y, ss);
+  ss = dot2_bf16(raw.z, raw.z, ss);
+  return dot2_bf16(raw.w, raw.w, ss);
 }
 
 // x (optionally RMS-normalized and rounded to bf16) staged by one wave into its
-// own LDS region, in dot2 pair order, plus per-chunk sums. All of x (and the
+// own LDS region, in dot2 pair order, plus per-chunk offsets (136 x the chunk's
+// sum, pack_x8). All of x (and the
 // norm weight) is loaded up front - XV 16-byte vectors per lane, XV >= K/512 -
 // so staging costs one round trip. No block barrier: the wave's LDS accesses
 // are ordered among themselves.
@@ -101,17 +112,8 @@ AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uin
   if (NORM) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < XV; ++i) {
-      if (lane + 64 * i < vecs) {
-        const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = bf16_lo(raw[j]), b = bf16_hi(raw[j]);
-          ss = fmaf(a, a, ss);
-          ss = fmaf(b, b, ss);
-        }
-      }
-    }
+    for (int i = 0; i < XV; ++i)
+      if (lane + 64 * i < vecs) ss = sum_squares8(xr[i], ss);
     ss = wave_sum(ss);
     ns = 1.0f / sqrtf(ss / (float)K + eps);
   }
@@ -153,17 +155,8 @@ AOTO_DEVICE void stage_activation_block(const uint16_t* __restrict__ x, const ui
   if (NORM) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < XV; ++i) {
-      if ((int)threadIdx.x + kGemvThreads * i < vecs) {
-        const uint32_t raw[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = bf16_lo(raw[j]), b = bf16_hi(raw[j]);
-          ss = fmaf(a, a, ss);
-          ss = fmaf(b, b, ss);
-        }
-      }
-    }
+    for (int i = 0; i < XV; ++i)
+      if ((int)threadIdx.x + kGemvThreads * i < vecs) ss = sum_squares8(xr[i], ss);
     ss = block_sum<kGemvThreads>(ss, scratch);
     ns = 1.0f / sqrtf(ss / (float)K + eps);
   }
@@ -217,15 +210,7 @@ struct DirectActivation {
       for (int j = 0; j < CPL; ++j) {
         if (li + LPR * j < nchunks) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint32_t r4[4] = {raw[j][k].x, raw[j][k].y, raw[j][k].z, raw[j][k].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float a = bf16_lo(r4[i]), b = bf16_hi(r4[i]);
-              ss = fmaf(a, a, ss);
-              ss = fmaf(b, b, ss);
-            }
-          }
+          for (int k = 0; k < 4; ++k) ss = sum_squares8(raw[j][k], ss);
         }
       }
       ss = group_sum<LPR>(ss);
@@ -236,7 +221,7 @@ struct DirectActivation {
       float sum = 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) sum = pack_x8<NORM>(raw[j][k], wraw[NORM ? j : 0][k], ns, xr[j][k], sum);
-      cr[j] = 136.f * sum;
+      cr[j] = sum;
     }
   }
 };
@@ -349,7 +334,7 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
       const bool valid = li + LPR * j < nchunks;
       const int c = cidx[j];
       const uint4* xc = INREG ? xr[j] : xp + c * 4;
-      const float corr = INREG ? cr[j] : 136.f * csum[c];
+      const float corr = INREG ? cr[j] : csum[c];
       total = fmaf(chunk_dot_fast(r.q[j], xc) - corr, valid ? pair_half(r.s[j], shalf[j]) : 0.f, total);
       if (PAIRED)
         total_up = fmaf(chunk_dot_fast(r.u[j], xc) - corr, valid ? pair_half(r.us[j], shalf[j]) : 0.f, total_up);
@@ -398,7 +383,7 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
       for (int j = 0; j < CPL; ++j) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) xr[j][k] = xp[cidx[j] * 4 + k];
-        cr[j] = 136.f * csum[cidx[j]];
+        cr[j] = csum[cidx[j]];
       }
     }
   }
