@@ -362,6 +362,7 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   if constexpr (BLOCKX) {
     // every wave takes part in the block's staging barrier, tile or not
     load(tile, ra);
+    __builtin_amdgcn_sched_barrier(0);  // the first tile's loads ahead of the staging
     stage_activation_block<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
   }
   if (tile >= tiles) {
@@ -374,9 +375,15 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     DirectActivation<LPR, CPL, NORM> act;
     act.issue(x, norm_w, K, li);
     load(tile, ra);
+    __builtin_amdgcn_sched_barrier(0);  // x, then every load of the first tile, then the math
     act.finish(eps, K, li, xr, cr);
   } else {
     load(tile, ra);
+    // Keep every load of the first tile ahead of the staging code: the
+    // scheduler otherwise sinks some of them behind the wait for x, which costs
+    // a memory round trip per wave and leaves the loop's entry waits
+    // conservative.
+    __builtin_amdgcn_sched_barrier(0);
     stage_activation_wave<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
     if (XREG) {
 #pragma unroll
