@@ -252,6 +252,22 @@ unsigned blocks_for(long long items, int threads) { return (unsigned)((items + t
 // records a merge launch combines. `requested` > 0 asks for that many splits.
 int decode_max_chunk(int head_dim) { return head_dim == 64 ? 256 : 128; }
 
+// Block size and loads per wave of a decode-attention launch: 4 waves, each
+// issuing J wave loads (512/D key rows each) of K and of V; J is the smallest
+// instance (2, 4, 6 or 8) that covers the chunk, so no load is idle when the
+// chunk is a multiple of 4 * 2 * 512/D keys (Qwen's 192-key window: J = 6,
+// 4.38 us against 4.63 for J = 8 on MI355X).
+struct AttnShape {
+  int waves, loads;
+};
+AttnShape attention_shape(int head_dim, int chunk) {
+  const int waves = 4;
+  const int per_load = waves * (512 / head_dim);
+  int j = (chunk + per_load - 1) / per_load;
+  j = j < 2 ? 2 : j + (j & 1);
+  return {waves, j};
+}
+
 void decode_split(int head_dim, int capacity, int requested, int* splits, int* chunk) {
   const int most = decode_max_chunk(head_dim);
   int s = requested > 0 ? requested : (capacity + most - 1) / most;
@@ -690,8 +706,9 @@ int aoto_hip_decode_attention(const void* q, const void* keys, const void* value
   if (!aligned16(q) || !aligned16(keys) || !aligned16(values) || (kv_head_stride % 8) || (kv_batch_stride % 8))
     return fail(AOTO_ERR_ARGUMENT, "decode_attention: q/keys/values must be 16-byte aligned");
   char name[64];
-  snprintf(name, sizeof(name), "aoto_decode_attention_d%d", head_dim);
-  if (int st = launch(name, dim3(s, batch * query_heads), dim3(256), 0, stream, q, keys, values,
+  const AttnShape as = attention_shape(head_dim, chunk);
+  snprintf(name, sizeof(name), "aoto_decode_attention_d%d_w%dj%d", head_dim, as.waves, as.loads);
+  if (int st = launch(name, dim3(s, batch * query_heads), dim3(64 * as.waves), 0, stream, q, keys, values,
                       (long long)kv_batch_stride, (long long)kv_head_stride, mask, mask_batch_stride, valid,
                       ring_offset, capacity, query_heads, kv_heads, scale, chunk, (float*)workspace, step_state,
                       out))
@@ -724,8 +741,10 @@ int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_sta
     return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: keys/values/row/tables must be 16-byte aligned, "
                 "row width and query start multiples of 8");
   char name[64];
-  snprintf(name, sizeof(name), "aoto_decode_rope_attention_d%d", head_dim);
-  if (int st = launch(name, dim3(s, batch * query_heads), dim3(256), 0, stream, row, row_width, query_start,
+  const AttnShape as = attention_shape(head_dim, chunk);
+  snprintf(name, sizeof(name), "aoto_decode_rope_attention_d%d_w%dj%d", head_dim, as.waves, as.loads);
+  if (int st = launch(name, dim3(s, batch * query_heads), dim3(64 * as.waves), 0, stream, row, row_width,
+                      query_start,
                       key_start, value_start, cos_table, sin_table, keys, values, (long long)kv_batch_stride,
                       (long long)kv_head_stride, valid, ring_offset, position, slot, capacity, query_heads,
                       kv_heads, scale, chunk, (float*)workspace, step_state, rope_rows, out))

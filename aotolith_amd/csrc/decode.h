@@ -106,10 +106,11 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
 // With `step` non-null, {position, valid, ring_offset, slot} come from the
 // device step state of a captured decode loop.
 //
-// Grid (splits, B*Hq); 256 threads (4 waves); one query head per block, keys
-// [split*chunk, min(cap, (split+1)*chunk)), chunk <= 16384 / D (256 keys at
-// D = 64, 128 at D = 128). The window is tiny, so the design minimizes dependent
-// steps and keeps every load coalesced:
+// Grid (splits, B*Hq); WAVES waves per block; one query head per block, keys
+// [split*chunk, min(cap, (split+1)*chunk)), chunk <= WAVES * J * 512 / D (each
+// wave issues J wave loads of K and J of V; the host picks the instance whose
+// J fits the chunk with no idle loads). The window is tiny, so the design
+// minimizes dependent steps and keeps every load coalesced:
 // * a key row is D/8 lanes, 16 bytes (8 dims) each, so one wave load reads
 //   64/(D/8) consecutive rows - 1 KB contiguous - of K or V;
 // * wave w owns a contiguous run of the split's keys; its K and V chunks, the
@@ -117,13 +118,15 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rope_kv_append(
 //   front, the small loads first so the RoPE can start while K and V land;
 // * a score is 4 bf16 dot2 per lane and a DPP sum over the row's D/8 lanes;
 //   each wave keeps its own softmax (max m_w, sum l_w, unnormalized P.V over its
-//   keys, 8 dims per lane), so the block meets at one barrier, where D threads
-//   combine the waves' records (the same rescaling the split merge uses).
+//   keys, 8 dims per lane; at D = 64 the two keys of a 16-lane row are summed
+//   with one DPP move first), so the block meets at one barrier, where D
+//   threads combine the waves' records (the same rescaling the split merge
+//   uses).
 // ROWS: the RoPE rows come from `rope_rows` (no dependence on the step state);
 // otherwise from the tables at the position. One split writes the output;
 // several write (max, sum, acc[D]) records that aoto_decode_attention_merge
 // combines in a second launch.
-template <int D, bool FUSED, bool ROWS>
+template <int D, int WAVES, int J, bool FUSED, bool ROWS>
 __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ row,
                                       int row_width, int query_start, int key_start, int value_start,
                                       const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table,
@@ -134,12 +137,12 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
                                       int kv_heads, float scale, int chunk, float* __restrict__ partials,
                                       const int* __restrict__ step, const uint16_t* __restrict__ rope_rows,
                                       uint16_t* __restrict__ out) {
-  constexpr int WAVES = 4;
   constexpr int LPK = D / 8;                    // lanes per key row (8 dims each)
   constexpr int KPI = 64 / LPK;                 // key rows per wave load
-  constexpr int J = 16384 / D / (WAVES * KPI);  // loads per wave at the largest chunk
   constexpr int HALF_LANES = LPK / 2;           // lanes holding the first half of a row
-  __shared__ __attribute__((aligned(16))) float s_acc[WAVES][64][8];
+  constexpr int SLOTS = 4 * LPK;                // P.V records per wave (4 key lanes per dim)
+  static_assert(KPI == 4 || KPI == 8, "D = 64 or 128");
+  __shared__ __attribute__((aligned(16))) float s_acc[WAVES][SLOTS][8];
   __shared__ float s_m[WAVES], s_l[WAVES];
 
   const int split = blockIdx.x;
@@ -296,8 +299,17 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
   }
   // Each key's probability sits in all LPK lanes of its row: count it once.
   const float l = wave_sum(sub == 0 ? lsum : 0.f);
-  reinterpret_cast<float4*>(s_acc[wave][lane])[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  reinterpret_cast<float4*>(s_acc[wave][lane])[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  // Four records per dim: at D = 64 (two key rows per 16-lane row) the rows'
+  // pairs are summed first (row_ror:8, i.e. lane ^ 8).
+  if (KPI == 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += dpp_move<0x128>(acc[e]);
+  }
+  if (KPI == 4 || (lane & 8) == 0) {
+    const int rec = (lane >> 4) * LPK + sub;
+    reinterpret_cast<float4*>(s_acc[wave][rec])[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    reinterpret_cast<float4*>(s_acc[wave][rec])[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
   if (lane == 0) {
     s_m[wave] = m;
     s_l[wave] = l;
@@ -330,7 +342,7 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
       const float f = (mw[w] == -INFINITY) ? 0.f : expf(mw[w] - big);
       float part = 0.f;
 #pragma unroll
-      for (int r = 0; r < KPI; ++r) part += s_acc[w][r * LPK + d / 8][d % 8];
+      for (int r = 0; r < 4; ++r) part += s_acc[w][r * LPK + d / 8][d % 8];
       total = fmaf(f, part, total);
       sum = fmaf(f, s_l[w], sum);
     }
@@ -532,33 +544,39 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
 
 }  // namespace aoto
 
-#define AOTO_DECODE_ATTENTION_INSTANCE(D)                                                                \
-  extern "C" __global__ __launch_bounds__(256) void aoto_decode_attention_d##D(                         \
+// aoto_decode_attention_d{D}_w{WAVES}j{J} and aoto_decode_rope_attention_d{D}_w{WAVES}j{J}.
+#define AOTO_DECODE_ATTENTION_INSTANCE(D, WAVES, J)                                                       \
+  extern "C" __global__ __launch_bounds__(64 * WAVES) void aoto_decode_attention_d##D##_w##WAVES##j##J(  \
       const uint16_t* q, uint16_t* kbase, uint16_t* vbase, long long kv_batch_stride,                    \
       long long kv_head_stride, const uint8_t* mask, int mask_batch_stride, int valid, int ring_offset,  \
       int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials, const int* step,  \
       uint16_t* out) {                                                                                   \
-    aoto::decode_attention_body<D, false, false>(q, nullptr, 0, 0, 0, 0, nullptr, nullptr, kbase, vbase, \
-                                                 kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
-                                                 valid, ring_offset, 0, -1, cap, query_heads, kv_heads,    \
-                                                 scale, chunk, partials, step, nullptr, out);              \
+    aoto::decode_attention_body<D, WAVES, J, false, false>(                                              \
+        q, nullptr, 0, 0, 0, 0, nullptr, nullptr, kbase, vbase, kv_batch_stride, kv_head_stride, mask,  \
+        mask_batch_stride, valid, ring_offset, 0, -1, cap, query_heads, kv_heads, scale, chunk, partials, \
+        step, nullptr, out);                                                                             \
   }                                                                                                      \
-  extern "C" __global__ __launch_bounds__(256) void aoto_decode_rope_attention_d##D(                    \
-      const uint16_t* row, int row_width, int query_start, int key_start, int value_start,               \
-      const uint16_t* cos_table, const uint16_t* sin_table, uint16_t* kbase, uint16_t* vbase,            \
-      long long kv_batch_stride, long long kv_head_stride, int valid, int ring_offset, int position,     \
-      int slot, int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials,          \
-      const int* step, const uint16_t* rope_rows, uint16_t* out) {                                       \
+  extern "C" __global__ __launch_bounds__(64 * WAVES) void                                               \
+      aoto_decode_rope_attention_d##D##_w##WAVES##j##J(                                                  \
+          const uint16_t* row, int row_width, int query_start, int key_start, int value_start,           \
+          const uint16_t* cos_table, const uint16_t* sin_table, uint16_t* kbase, uint16_t* vbase,        \
+          long long kv_batch_stride, long long kv_head_stride, int valid, int ring_offset, int position, \
+          int slot, int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials,      \
+          const int* step, const uint16_t* rope_rows, uint16_t* out) {                                   \
     if (rope_rows != nullptr)                                                                            \
-      aoto::decode_attention_body<D, true, true>(nullptr, row, row_width, query_start, key_start,        \
-                                                 value_start, cos_table, sin_table, kbase, vbase,       \
-                                                 kv_batch_stride, kv_head_stride, nullptr, 0, valid,    \
-                                                 ring_offset, position, slot, cap, query_heads,         \
-                                                 kv_heads, scale, chunk, partials, step, rope_rows, out); \
+      aoto::decode_attention_body<D, WAVES, J, true, true>(                                              \
+          nullptr, row, row_width, query_start, key_start, value_start, cos_table, sin_table, kbase,     \
+          vbase, kv_batch_stride, kv_head_stride, nullptr, 0, valid, ring_offset, position, slot, cap,   \
+          query_heads, kv_heads, scale, chunk, partials, step, rope_rows, out);                          \
     else                                                                                                 \
-      aoto::decode_attention_body<D, true, false>(nullptr, row, row_width, query_start, key_start,       \
-                                                  value_start, cos_table, sin_table, kbase, vbase,      \
-                                                  kv_batch_stride, kv_head_stride, nullptr, 0, valid,   \
-                                                  ring_offset, position, slot, cap, query_heads,        \
-                                                  kv_heads, scale, chunk, partials, step, nullptr, out); \
+      aoto::decode_attention_body<D, WAVES, J, true, false>(                                             \
+          nullptr, row, row_width, query_start, key_start, value_start, cos_table, sin_table, kbase,     \
+          vbase, kv_batch_stride, kv_head_stride, nullptr, 0, valid, ring_offset, position, slot, cap,   \
+          query_heads, kv_heads, scale, chunk, partials, step, nullptr, out);                            \
   }
+// Every loads-per-wave count of one head size and block size.
+#define AOTO_DECODE_ATTENTION_SHAPES(D, WAVES, J1, J2, J3, J4) \
+  AOTO_DECODE_ATTENTION_INSTANCE(D, WAVES, J1)                 \
+  AOTO_DECODE_ATTENTION_INSTANCE(D, WAVES, J2)                 \
+  AOTO_DECODE_ATTENTION_INSTANCE(D, WAVES, J3)                 \
+  AOTO_DECODE_ATTENTION_INSTANCE(D, WAVES, J4)
