@@ -57,17 +57,39 @@ constexpr int kDppXor2 = 0x4E;
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppMirror = 0x140;
 
+// The pair {value of lane l & ~16, value of lane l | 16} (permlane16_swap of a
+// register with itself: rows 0/1 and 2/3 exchange) and the same across the
+// wave's halves (permlane32_swap): lane l ^ 16 / l ^ 32 without an LDS round
+// trip. Lane layout checked on gfx950.
+AOTO_DEVICE float xor16_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+AOTO_DEVICE float xor32_sum(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+AOTO_DEVICE float xor16_max(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+AOTO_DEVICE float xor32_max(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
 // Sum over the `WIDTH` lanes of an aligned lane group (WIDTH a power of two <=
 // 64); every lane of the group gets the total. Up to 16 lanes it is four DPP
-// steps; wider groups add ds_swizzle-free cross-row steps through __shfl_xor.
+// steps; wider groups add permlane swaps across rows and halves. Each step adds
+// a lane's value and its partner's (l ^ 1, 2, 4 or 8 by DPP, then l ^ 16, 32).
 template <int WIDTH>
 AOTO_DEVICE float group_sum(float value) {
   if (WIDTH >= 2) value += dpp_move<kDppXor1>(value);
   if (WIDTH >= 4) value += dpp_move<kDppXor2>(value);
   if (WIDTH >= 8) value += dpp_move<kDppHalfMirror>(value);
   if (WIDTH >= 16) value += dpp_move<kDppMirror>(value);
-  if (WIDTH >= 32) value += __shfl_xor(value, 16, 64);
-  if (WIDTH >= 64) value += __shfl_xor(value, 32, 64);
+  if (WIDTH >= 32) value = xor16_sum(value);
+  if (WIDTH >= 64) value = xor32_sum(value);
   return value;
 }
 
@@ -77,8 +99,8 @@ AOTO_DEVICE float group_max(float value) {
   if (WIDTH >= 4) value = fmaxf(value, dpp_move<kDppXor2>(value));
   if (WIDTH >= 8) value = fmaxf(value, dpp_move<kDppHalfMirror>(value));
   if (WIDTH >= 16) value = fmaxf(value, dpp_move<kDppMirror>(value));
-  if (WIDTH >= 32) value = fmaxf(value, __shfl_xor(value, 16, 64));
-  if (WIDTH >= 64) value = fmaxf(value, __shfl_xor(value, 32, 64));
+  if (WIDTH >= 32) value = xor16_max(value);
+  if (WIDTH >= 64) value = xor32_max(value);
   return value;
 }
 

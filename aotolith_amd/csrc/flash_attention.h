@@ -126,8 +126,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
         tile_max = fmaxf(tile_max, sc);
       }
     }
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, 64));
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, 64));
+    tile_max = xor32_max(xor16_max(tile_max));
     const float new_max = fmaxf(run_max, tile_max);
     const float correction = (new_max == -INFINITY) ? 1.f : expf(run_max - new_max);
     float tile_sum = 0.f;
@@ -140,8 +139,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
         tile_sum += e;
         p[st][i] = (__bf16)e;
       }
-    tile_sum += __shfl_xor(tile_sum, 16, 64);
-    tile_sum += __shfl_xor(tile_sum, 32, 64);
+    tile_sum = xor32_sum(xor16_sum(tile_sum));
     run_sum = run_sum * correction + tile_sum;
     run_max = new_max;
 #pragma unroll
