@@ -301,7 +301,18 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     const uint4* wrow = words + (size_t)row * nchunks;
     const uint32_t* srow = scale_words + (size_t)row * (ngroups >> 1);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) r.q[j] = wrow[cidx[j]];
+    for (int j = 0; j < CPL; ++j) {
+      if (ARGMAX) {
+        // The greedy loop's LM head streams 68 MB per token once: non-temporal
+        // loads keep it from evicting the layer weights the next token reads
+        // again (+0.7% decode tok/s on the Qwen2-0.5B loop, same head time).
+        typedef unsigned v4u __attribute__((ext_vector_type(4)));
+        const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wrow + cidx[j]));
+        r.q[j] = make_uint4(t.x, t.y, t.z, t.w);
+      } else {
+        r.q[j] = wrow[cidx[j]];
+      }
+    }
     if (PAIRED) {
       const uint4* urow = up_words + (size_t)row * nchunks;
 #pragma unroll
