@@ -831,8 +831,9 @@ int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_o
   if (embedding && (!hidden_out || hidden <= 0 || hidden % 8 != 0 || embedding_rows <= 0 ||
                     !aligned16(embedding) || !aligned16(hidden_out)))
     return fail(AOTO_ERR_ARGUMENT, "argmax_finish: the embedding gather needs 16-byte aligned rows, hidden %% 8 == 0");
-  if (rope_rows && (!step_state || !cos_table || !sin_table || head_dim <= 0))
-    return fail(AOTO_ERR_ARGUMENT, "argmax_finish: RoPE rows need the step state, both tables and head_dim");
+  if (rope_rows && (!step_state || !cos_table || !sin_table || head_dim <= 0 || head_dim > 256))
+    return fail(AOTO_ERR_ARGUMENT, "argmax_finish: RoPE rows need the step state, both tables and "
+                "0 < head_dim <= 256");
   return launch("aoto_argmax_finish", dim3(1), dim3(256), 0, stream, keys, key_count, token_out, history,
                 history_len, step_state, capacity, embedding, (long long)embedding_rows, hidden, hidden_out, error,
                 cos_table, sin_table, head_dim, rope_rows);

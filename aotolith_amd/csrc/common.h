@@ -156,11 +156,29 @@ AOTO_DEVICE long long argmax_key_index(unsigned long long key) {
 
 AOTO_DEVICE unsigned long long max_u64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
 
+// Whole-wave maximum of a 64-bit key, every lane gets it: the two halves move
+// together through the same DPP steps as group_max, then permlane swaps across
+// rows and halves (no LDS round trip).
+template <int CTRL>
+AOTO_DEVICE unsigned long long dpp_move_u64(unsigned long long v) {
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((unsigned long long)hi << 32) | lo;
+}
 AOTO_DEVICE unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned long long o = __shfl_xor(v, off, 64);
-    v = max_u64(v, o);
+  v = max_u64(v, dpp_move_u64<kDppXor1>(v));
+  v = max_u64(v, dpp_move_u64<kDppXor2>(v));
+  v = max_u64(v, dpp_move_u64<kDppHalfMirror>(v));
+  v = max_u64(v, dpp_move_u64<kDppMirror>(v));
+  {
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    v = max_u64(((unsigned long long)hi[0] << 32) | lo[0], ((unsigned long long)hi[1] << 32) | lo[1]);
+  }
+  {
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+    v = max_u64(((unsigned long long)hi[0] << 32) | lo[0], ((unsigned long long)hi[1] << 32) | lo[1]);
   }
   return v;
 }

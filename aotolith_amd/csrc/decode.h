@@ -486,44 +486,62 @@ extern "C" __global__ __launch_bounds__(256) void aoto_argmax_finish(
     int* __restrict__ error, const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table,
     int head_dim, uint16_t* __restrict__ rope_rows) {
   __shared__ unsigned long long s_best[4];
-  __shared__ long long s_token;
-  __shared__ int s_position;
+  constexpr int kUnroll = 16;  // keys per thread loaded at once (count <= 4096)
+  // Everything that does not depend on the token is read up front, in parallel
+  // with the keys: the step state, the history length and the next position's
+  // RoPE rows.
+  int st[4] = {0, 0, 0, 0};
+  if (step != nullptr) {
+    st[0] = step[0];
+    st[1] = step[1];
+    st[2] = step[2];
+    st[3] = step[3];
+  }
+  const int at = history != nullptr ? history_len[0] : 0;
+  const int p = st[0] + 1;
+  // a position past the tables (the step after the last) keeps the old rows
+  const bool rows = rope_rows != nullptr && step != nullptr && p < cap && (int)threadIdx.x < head_dim;
+  uint16_t cs = 0, sn = 0;
+  if (rows) {
+    cs = cos_table[(size_t)p * head_dim + threadIdx.x];
+    sn = sin_table[(size_t)p * head_dim + threadIdx.x];
+  }
   unsigned long long best = 0;
-  for (int i = threadIdx.x; i < count; i += 256) best = max_u64(best, keys[i]);
+  if (count <= 256 * kUnroll) {
+    unsigned long long v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      v[u] = i < count ? keys[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) best = max_u64(best, v[u]);
+  } else {
+    for (int i = threadIdx.x; i < count; i += 256) best = max_u64(best, keys[i]);
+  }
   best = wave_max_u64(best);
   if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+  if (rows) {
+    rope_rows[threadIdx.x] = cs;
+    rope_rows[head_dim + threadIdx.x] = sn;
+  }
   __syncthreads();
+  const unsigned long long m = max_u64(max_u64(s_best[0], s_best[1]), max_u64(s_best[2], s_best[3]));
+  const long long token = argmax_key_index(m);
   if (threadIdx.x == 0) {
-    const unsigned long long m = max_u64(max_u64(s_best[0], s_best[1]), max_u64(s_best[2], s_best[3]));
-    const long long token = argmax_key_index(m);
     token_out[0] = token;
     if (history != nullptr) {
-      const int at = history_len[0];
       history[at] = token;
       history_len[0] = at + 1;
     }
     if (step != nullptr) {
-      s_position = step[0] + 1;
-      step[0] += 1;
-      step[1] += 1;
-      step[2] = step[2] + 1 == cap ? 0 : step[2] + 1;
-      step[3] = step[3] + 1 == cap ? 0 : step[3] + 1;
-    }
-    s_token = token;
-  }
-  __syncthreads();
-  if (rope_rows != nullptr && step != nullptr) {
-    // a position past the tables (the step after the last) keeps the old rows
-    const int p = s_position;
-    if (p < cap) {
-      for (int i = threadIdx.x; i < head_dim; i += 256) {
-        rope_rows[i] = cos_table[(size_t)p * head_dim + i];
-        rope_rows[head_dim + i] = sin_table[(size_t)p * head_dim + i];
-      }
+      step[0] = st[0] + 1;
+      step[1] = st[1] + 1;
+      step[2] = st[2] + 1 == cap ? 0 : st[2] + 1;
+      step[3] = st[3] + 1 == cap ? 0 : st[3] + 1;
     }
   }
   if (embed == nullptr) return;
-  const long long token = s_token;
   const bool ok = token >= 0 && token < embed_rows;
   if (!ok && threadIdx.x == 0 && error != nullptr) error[0] = 1;
   const uint4* src = reinterpret_cast<const uint4*>(embed + (size_t)(ok ? token : 0) * hidden);

@@ -295,9 +295,9 @@ int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* sca
  * (the next step's embedding take, runtime/bounds.py:104-107) into hidden_out
  * (zeros and *error = 1 if the token is not a row of the table), and with the
  * step state copies the cos/sin rows of the advanced position from the tables
- * ([capacity, head_dim] bf16) into rope_rows (2 * head_dim) for the next step's
- * aoto_hip_decode_rope_attention (kept as is when that position is past the
- * tables). */
+ * ([capacity, head_dim] bf16, head_dim <= 256) into rope_rows (2 * head_dim)
+ * for the next step's aoto_hip_decode_rope_attention (kept as is when that
+ * position is past the tables). */
 int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_out, int64_t* history,
                            int* history_len, int32_t* step_state, int capacity, const void* embedding,
                            int64_t embedding_rows, int hidden, void* hidden_out, int* error,
