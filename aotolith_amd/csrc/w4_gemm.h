@@ -101,6 +101,7 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
 
   uint4 xr[XPT];
   Word wr[TN][2];
+  uint16_t sr[TN][2];  // the scales of wr, loaded with it (a load at use would cost a round trip per k-step)
   auto load_x = [&](int k0) {
 #pragma unroll
     for (int v = 0; v < XPT; ++v) {
@@ -127,7 +128,10 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
 #pragma unroll
     for (int t = 0; t < TN; ++t)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) wr[t][ks] = words[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
+      for (int ks = 0; ks < 2; ++ks) {
+        wr[t][ks] = words[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
+        sr[t][ks] = scales[(size_t)wrow[t] * groups + (k0 + ks * 32) / group];
+      }
   };
 
   const int kb = blockIdx.z * kslice;
@@ -147,8 +151,7 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
 #pragma unroll
     for (int t = 0; t < TN; ++t)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        scur[t][ks] = bf16_to_f32(scales[(size_t)wrow[t] * groups + (k0 + ks * 32) / group]);
+      for (int ks = 0; ks < 2; ++ks) scur[t][ks] = bf16_to_f32(sr[t][ks]);
     __syncthreads();
     if (k0 + kGemmBK < ke) {
       load_x(k0 + kGemmBK);
