@@ -52,6 +52,9 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, _c_int, _c_int, _p,
     ),
     "aoto_hip_w8_gemm": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
+    "aoto_hip_w4_gemm_gate_up": (_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
+    "aoto_hip_w8_gemm_gate_up": (_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
+    "aoto_hip_w4_gemm_gate_up_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int),
     "aoto_hip_rms_norm": (_p, _p, _c_float, _p, _c_int, _c_int, _p),
     "aoto_hip_rope": (_p, _p, _p, _p, _c_int, _c_int, _p, _i64, _c_int, _p),
     "aoto_hip_rope_qkv_prefill": (
@@ -97,7 +100,7 @@ SIGNATURES: dict[str, tuple] = {
 
 #: Entry points returning a size rather than a status.
 SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_decode_attention_workspace", "aoto_hip_w4_gemm_workspace",
-                  "aoto_hip_w4_gemv_argmax_keys"}
+                  "aoto_hip_w4_gemm_gate_up_workspace", "aoto_hip_w4_gemv_argmax_keys"}
 
 
 class HipBackendUnavailable(RuntimeError):

@@ -469,17 +469,28 @@ size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
+size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits) {
+  return 2 * aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
+}
+
 }  // extern "C"
 
 namespace {
 
 // The prefill GEMM of either code width (the kernels differ only in how many
 // packed words make one lane's 8-code operand).
+// With up_words / up_scales (the gate/up entry points) the launch is the paired
+// form: `words` is the gate projection, y = bf16(up * silu(bf16(gate))).
 int packed_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* bias,
                 const void* residual, const void* gate, void* y, int M, int N, int K, int group, int tile,
-                int splits, void* workspace, void* stream) {
-  const char* what = bits == 4 ? "w4_gemm" : "w8_gemm";
-  if (!x || !words || !scales || !y) return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
+                int splits, void* workspace, void* stream, const int32_t* up_words = nullptr,
+                const void* up_scales = nullptr) {
+  const bool paired = up_words != nullptr;
+  const char* what = paired ? (bits == 4 ? "w4_gemm_gate_up" : "w8_gemm_gate_up") : (bits == 4 ? "w4_gemm" : "w8_gemm");
+  if (!x || !words || !scales || !y || (paired && !up_scales))
+    return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
+  if (paired && (bias || residual || gate)) return fail(AOTO_ERR_ARGUMENT, "%s: no other epilogue", what);
+  if (paired && bits == 8 && !aligned8(up_words)) return fail(AOTO_ERR_ARGUMENT, "%s: words 8-byte aligned", what);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(AOTO_ERR_ARGUMENT, "%s: empty shape M=%d N=%d K=%d", what, M, N, K);
   if (K % 64 != 0 || N % 16 != 0 || group <= 0 || group % 32 != 0 || K % group != 0)
@@ -496,18 +507,28 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   const GemmPlan p = gemm_plan(M, N, K, tile, splits);
   if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
     return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
-                "aoto_hip_w4_gemm_workspace() bytes", what, p.splits);
+                "aoto_hip_w4_gemm%s_workspace() bytes", what, p.splits, paired ? "_gate_up" : "");
   const int bn = 64 * p.tn, bm = 16 * p.tm;
   const bool split = p.splits > 1;
-  const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
-  char name[64];
-  snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_b%d_r%d_g%d", bits, p.tn, p.tm, b, r, g);
+  const dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, p.splits);
   float* partials = split ? static_cast<float*>(workspace) : nullptr;
-  if (int st = launch(name, dim3((N + bn - 1) / bn, (M + bm - 1) / bm, p.splits), dim3(256), 0, stream, x, words,
-                      scales, bias, residual, gate, y, M, N, K, group, p.kslice, partials))
+  const long long quads = (long long)M * N / 4;
+  char name[64];
+  if (paired) {
+    snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_paired", bits, p.tn, p.tm);
+    if (int st = launch(name, grid, dim3(256), 0, stream, x, words, scales, up_words, up_scales, y, M, N, K, group,
+                        p.kslice, partials))
+      return st;
+    if (!split) return AOTO_OK;
+    return launch("aoto_w4_gemm_reduce_paired", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
+                  (const float*)partials, p.splits, y, M, N);
+  }
+  const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
+  snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_b%d_r%d_g%d", bits, p.tn, p.tm, b, r, g);
+  if (int st = launch(name, grid, dim3(256), 0, stream, x, words, scales, bias, residual, gate, y, M, N, K, group,
+                      p.kslice, partials))
     return st;
   if (!split) return AOTO_OK;
-  const long long quads = (long long)M * N / 4;
   return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
                 (const float*)partials, p.splits, bias, residual, gate, y, M, N);
 }
@@ -528,6 +549,22 @@ int aoto_hip_w8_gemm(const void* x, const int32_t* words, const void* scales, co
                      int tile, int splits, void* workspace, void* stream) {
   return packed_gemm(8, x, words, scales, bias, residual, gate, y, M, N, K, group, tile, splits, workspace,
                      stream);
+}
+
+int aoto_hip_w4_gemm_gate_up(const void* x, const int32_t* gate_words, const void* gate_scales,
+                             const int32_t* up_words, const void* up_scales, void* y, int M, int N, int K,
+                             int group, int tile, int splits, void* workspace, void* stream) {
+  if (!up_words) return fail(AOTO_ERR_ARGUMENT, "w4_gemm_gate_up: null pointer");
+  return packed_gemm(4, x, gate_words, gate_scales, nullptr, nullptr, nullptr, y, M, N, K, group, tile, splits,
+                     workspace, stream, up_words, up_scales);
+}
+
+int aoto_hip_w8_gemm_gate_up(const void* x, const int32_t* gate_words, const void* gate_scales,
+                             const int32_t* up_words, const void* up_scales, void* y, int M, int N, int K,
+                             int group, int tile, int splits, void* workspace, void* stream) {
+  if (!up_words) return fail(AOTO_ERR_ARGUMENT, "w8_gemm_gate_up: null pointer");
+  return packed_gemm(8, x, gate_words, gate_scales, nullptr, nullptr, nullptr, y, M, N, K, group, tile, splits,
+                     workspace, stream, up_words, up_scales);
 }
 
 int aoto_hip_w8_quantize(const void* weight, int weight_is_f32, int rows, int inner, int group,

@@ -61,6 +61,15 @@ AOTO_GEMM_EPILOGUES(8, 1, 4)
 AOTO_GEMM_EPILOGUES(8, 1, 8)
 AOTO_GEMM_EPILOGUES(8, 2, 4)
 AOTO_GEMM_EPILOGUES(8, 2, 8)
+// The MLP's gate/up pair in one pass: {code width} x {n tiles} x {m tiles}.
+AOTO_GEMM_PAIRED_INSTANCE(4, 1, 4)
+AOTO_GEMM_PAIRED_INSTANCE(4, 1, 8)
+AOTO_GEMM_PAIRED_INSTANCE(4, 2, 4)
+AOTO_GEMM_PAIRED_INSTANCE(4, 2, 8)
+AOTO_GEMM_PAIRED_INSTANCE(8, 1, 4)
+AOTO_GEMM_PAIRED_INSTANCE(8, 1, 8)
+AOTO_GEMM_PAIRED_INSTANCE(8, 2, 4)
+AOTO_GEMM_PAIRED_INSTANCE(8, 2, 8)
 
 // Eight-bit decode GEMV: {rows per wave} x {chunks per lane per pass}, with
 // the decoder's epilogues (rms-norm prologue, paired gate/up, bias/residual).

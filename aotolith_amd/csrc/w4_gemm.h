@@ -66,12 +66,22 @@ constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
 // Split-K: blockIdx.z selects the reduction slice [z*kslice, min(K, (z+1)*kslice));
 // with `partials` non-null the block stores its f32 tile to partials[z][m][n]
 // and aoto_w4_gemm_reduce applies the sum and the epilogue.
-template <int BITS, int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE>
+// PAIRED: the MLP's gate and up projections in one pass (the decode path's
+// paired GEMV, at M > 1): the block also holds the up weight's words for the
+// same columns, accumulates both against the one staged X tile and stores
+// bf16(up * silu(bf16(gate))) - the values the gate GEMM followed by the up
+// GEMM with the gate epilogue produce, with one launch and one read of X.
+// Split partials are gate at partials[z], up at partials[splits + z]
+// (aoto_w4_gemm_reduce_paired).
+template <int BITS, int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE, bool PAIRED = false>
 __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename GemmWord<BITS>::type* __restrict__ words,
                              const uint16_t* __restrict__ scales, const uint16_t* __restrict__ bias,
                              const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate,
                              uint16_t* __restrict__ Y, int M, int N, int K, int group, int kslice,
-                             float* __restrict__ partials) {
+                             float* __restrict__ partials,
+                             const typename GemmWord<BITS>::type* __restrict__ up_words = nullptr,
+                             const uint16_t* __restrict__ up_scales = nullptr) {
+  static_assert(!(PAIRED && (BIAS || RESIDUAL || GATE)), "the paired form has its own epilogue");
   constexpr int BM = 16 * TM;
   constexpr int BN = 64 * TN;
   constexpr int XVEC = BM * (kGemmBK / 8);        // 16-byte vectors per X tile
@@ -88,11 +98,14 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   const int col = lane & 15;       // n (A) / m (B, C) within a tile
   const int quad = lane >> 4;      // k block of 8 (A, B) / n block of 4 (C)
 
-  f32x4_v acc[TN][TM];
+  constexpr int NP = PAIRED ? 2 : 1;  // weight matrices: gate (or the only one), up
+  f32x4_v acc[NP][TN][TM];
 #pragma unroll
-  for (int t = 0; t < TN; ++t)
+  for (int p = 0; p < NP; ++p)
 #pragma unroll
-    for (int u = 0; u < TM; ++u) acc[t][u] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int u = 0; u < TM; ++u) acc[p][t][u] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 
   // Rows of W this lane reads (clamped: rows past N compute garbage that is never stored).
   int wrow[TN];
@@ -100,8 +113,8 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   for (int t = 0; t < TN; ++t) wrow[t] = min(n_wave + t * 16 + col, N - 1);
 
   uint4 xr[XPT];
-  Word wr[TN][2];
-  uint16_t sr[TN][2];  // the scales of wr, loaded with it (a load at use would cost a round trip per k-step)
+  Word wr[NP][TN][2];
+  uint16_t sr[NP][TN][2];  // the scales of wr, loaded with it (a load at use would cost a round trip per k-step)
   auto load_x = [&](int k0) {
 #pragma unroll
     for (int v = 0; v < XPT; ++v) {
@@ -126,12 +139,17 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   };
   auto load_w = [&](int k0) {
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
+    for (int p = 0; p < NP; ++p) {
+      const Word* wm = p == 0 ? words : up_words;
+      const uint16_t* sm = p == 0 ? scales : up_scales;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        wr[t][ks] = words[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
-        sr[t][ks] = scales[(size_t)wrow[t] * groups + (k0 + ks * 32) / group];
-      }
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          wr[p][t][ks] = wm[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
+          sr[p][t][ks] = sm[(size_t)wrow[t] * groups + (k0 + ks * 32) / group];
+        }
+    }
   };
 
   const int kb = blockIdx.z * kslice;
@@ -141,17 +159,17 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   for (int k0 = kb; k0 < ke; k0 += kGemmBK) {
     __syncthreads();
     store_x();
-    Word wcur[TN][2];
+    Word wcur[NP][TN][2];
+    float scur[NP][TN][2];
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      wcur[t][0] = wr[t][0];
-      wcur[t][1] = wr[t][1];
-    }
-    float scur[TN][2];
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
+      for (int t = 0; t < TN; ++t)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) scur[t][ks] = bf16_to_f32(sr[t][ks]);
+        for (int ks = 0; ks < 2; ++ks) {
+          wcur[p][t][ks] = wr[p][t][ks];
+          scur[p][t][ks] = bf16_to_f32(sr[p][t][ks]);
+        }
     __syncthreads();
     if (k0 + kGemmBK < ke) {
       load_x(k0 + kGemmBK);
@@ -159,31 +177,39 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      bf16x8_v a[TN];
+      bf16x8_v a[NP][TN];
 #pragma unroll
-      for (int t = 0; t < TN; ++t) a[t] = dequant_word(wcur[t][ks], scur[t][ks]);
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) a[p][t] = dequant_word(wcur[p][t][ks], scur[p][t][ks]);
 #pragma unroll
       for (int u = 0; u < TM; ++u) {
         const bf16x8_v b =
             *reinterpret_cast<const bf16x8_v*>(xs + (u * 16 + col) * kGemmLdsStride + ks * 32 + quad * 8);
 #pragma unroll
-        for (int t = 0; t < TN; ++t) acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b, acc[t][u], 0, 0, 0);
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int t = 0; t < TN; ++t)
+            acc[p][t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][t], b, acc[p][t][u], 0, 0, 0);
       }
     }
   }
 
   if (partials != nullptr) {
-    float* part = partials + (size_t)blockIdx.z * M * N;
 #pragma unroll
-    for (int u = 0; u < TM; ++u) {
-      const int m = m_block + u * 16 + col;
-      if (m >= M) continue;
+    for (int p = 0; p < NP; ++p) {
+      float* part = partials + ((size_t)p * gridDim.z + blockIdx.z) * M * N;
 #pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        const int n = n_wave + t * 16 + quad * 4;
-        if (n >= N) continue;
-        *reinterpret_cast<float4*>(part + (size_t)m * N + n) =
-            make_float4(acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]);
+      for (int u = 0; u < TM; ++u) {
+        const int m = m_block + u * 16 + col;
+        if (m >= M) continue;
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          const int n = n_wave + t * 16 + quad * 4;
+          if (n >= N) continue;
+          *reinterpret_cast<float4*>(part + (size_t)m * N + n) =
+              make_float4(acc[p][t][u][0], acc[p][t][u][1], acc[p][t][u][2], acc[p][t][u][3]);
+        }
       }
     }
     return;
@@ -197,7 +223,15 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
     for (int t = 0; t < TN; ++t) {
       const int n = n_wave + t * 16 + quad * 4;
       if (n >= N) continue;
-      float v[4] = {acc[t][u][0], acc[t][u][1], acc[t][u][2], acc[t][u][3]};
+      float v[4] = {acc[0][t][u][0], acc[0][t][u][1], acc[0][t][u][2], acc[0][t][u][3]};
+      if (PAIRED) {
+        // gate rounded to bf16 as the gate GEMM stores it, then the up epilogue
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g = round_bf16(v[i]);
+          v[i] = acc[1][t][u][i] * (g / (1.0f + expf(-g)));
+        }
+      }
       if (BIAS) {
         const uint2 bb = *reinterpret_cast<const uint2*>(bias + n);
         v[0] += bf16_lo(bb.x);
@@ -272,6 +306,41 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
   *reinterpret_cast<uint2*>(Y + e) = o;
 }
 
+
+// The paired form's split-K sum: gate = sum of partials[0 .. splits), up = sum
+// of partials[splits .. 2 * splits), y = bf16(up * silu(bf16(gate))), one thread
+// per 4 outputs (the gate's rounding and the up epilogue of the unpaired pair).
+extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_paired(const float* __restrict__ partials,
+                                                                             int splits, uint16_t* __restrict__ Y,
+                                                                             int M, int N) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long quads = (long long)M * N / 4;
+  if (t >= quads) return;
+  const size_t e = (size_t)t * 4;
+  float g[4] = {0.f, 0.f, 0.f, 0.f}, v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+    const float4 p = *reinterpret_cast<const float4*>(partials + (size_t)s * M * N + e);
+    const float4 q = *reinterpret_cast<const float4*>(partials + (size_t)(splits + s) * M * N + e);
+    g[0] += p.x;
+    g[1] += p.y;
+    g[2] += p.z;
+    g[3] += p.w;
+    v[0] += q.x;
+    v[1] += q.y;
+    v[2] += q.z;
+    v[3] += q.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float gr = round_bf16(g[i]);
+    v[i] = v[i] * (gr / (1.0f + expf(-gr)));
+  }
+  uint2 o;
+  o.x = pack_bf16x2(v[0], v[1]);
+  o.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(Y + e) = o;
+}
+
 }  // namespace aoto
 
 #define AOTO_GEMM_INSTANCE(BITS, TN, TM, BIAS, RES, GATE)                                                  \
@@ -289,3 +358,13 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
   AOTO_GEMM_INSTANCE(BITS, TN, TM, 1, 0, 0)    \
   AOTO_GEMM_INSTANCE(BITS, TN, TM, 0, 1, 0)    \
   AOTO_GEMM_INSTANCE(BITS, TN, TM, 0, 0, 1)
+// aoto_w{BITS}_gemm_n{TN}_m{TM}_paired: the gate/up pair in one pass.
+#define AOTO_GEMM_PAIRED_INSTANCE(BITS, TN, TM)                                                           \
+  extern "C" __global__ __launch_bounds__(256) void aoto_w##BITS##_gemm_n##TN##_m##TM##_paired(            \
+      const uint16_t* X, const aoto::GemmWord<BITS>::type* words, const uint16_t* scales,                  \
+      const aoto::GemmWord<BITS>::type* up_words, const uint16_t* up_scales, uint16_t* Y, int M, int N,    \
+      int K, int group, int kslice, float* partials) {                                                     \
+    aoto::w4_gemm_body<BITS, TN, TM, false, false, false, true>(X, words, scales, nullptr, nullptr,       \
+                                                                nullptr, Y, M, N, K, group, kslice,       \
+                                                                partials, up_words, up_scales);           \
+  }

@@ -332,6 +332,72 @@ def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0)
     return int(_lib.library().aoto_hip_w4_gemm_workspace(int(m), int(n), int(k), int(tile), int(splits)))
 
 
+def gate_up_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:
+    """Split-K workspace bytes :func:`w4_matmul_gate_up` needs (gate and up partials; 0: no split)."""
+
+    return int(_lib.library().aoto_hip_w4_gemm_gate_up_workspace(int(m), int(n), int(k), int(tile), int(splits)))
+
+
+def _matmul_gate_up(bits, x, gate_packed, gate_scales, up_packed, up_scales, group_size, out, tile, splits,
+                    workspace):
+    per_word = CODES_PER_WORD[bits]
+    _expect(gate_packed, "gate_packed", torch.int32)
+    if gate_packed.dim() != 2:
+        raise ValueError(f"gate_packed must be 2-D [N, K/{per_word}]")
+    n, words = gate_packed.shape
+    k = words * per_word
+    _expect(up_packed, "up_packed", torch.int32, (n, words))
+    _expect(x, "x", BF16)
+    if x.shape[-1] != k:
+        raise ValueError(f"x has last dimension {x.shape[-1]}, the weights reduce over {k}")
+    m = x.numel() // k
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"group size {group_size} does not divide K={k}")
+    _expect(gate_scales, "gate_scales", BF16, (n, k // group_size))
+    _expect(up_scales, "up_scales", BF16, (n, k // group_size))
+    shape = tuple(x.shape[:-1]) + (n,)
+    if out is None:
+        out = torch.empty(shape, dtype=BF16, device=x.device)
+    else:
+        _expect(out, "out", BF16)
+        if out.numel() != m * n:
+            raise ValueError(f"out has {out.numel()} elements, expected {m * n}")
+    _ready(x)
+    need = gate_up_workspace_bytes(m, n, k, tile, splits)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
+    lib = _lib.library()
+    entry = lib.aoto_hip_w4_gemm_gate_up if bits == 4 else lib.aoto_hip_w8_gemm_gate_up
+    _lib.check(
+        entry(
+            _ptr(x), _ptr(gate_packed), _ptr(gate_scales), _ptr(up_packed), _ptr(up_scales), _ptr(out),
+            m, n, k, group_size, int(tile), int(splits), _ptr(workspace if need else None), _stream(),
+        )
+    )
+    return out
+
+
+def w4_matmul_gate_up(x, gate_packed, gate_scales, up_packed, up_scales, group_size, *, out=None, tile=0,
+                      splits=0, workspace=None):
+    """Prefill MLP ``bf16(up(x) * silu(bf16(gate(x))))`` ``[M, K] -> [M, N]`` in one pass over x.
+
+    The same values as ``w4_matmul(x, gate)`` followed by ``w4_matmul(x, up, gate=...)``
+    (the reference's gate GEMM and silu_mul-epilogue up GEMM), up to the f32
+    summation order of the split reduction.
+    """
+
+    return _matmul_gate_up(4, x, gate_packed, gate_scales, up_packed, up_scales, group_size, out, tile, splits,
+                           workspace)
+
+
+def w8_matmul_gate_up(x, gate_packed, gate_scales, up_packed, up_scales, group_size, *, out=None, tile=0,
+                      splits=0, workspace=None):
+    """:func:`w4_matmul_gate_up` over int8 packs (words ``[N, K/4]``)."""
+
+    return _matmul_gate_up(8, x, gate_packed, gate_scales, up_packed, up_scales, group_size, out, tile, splits,
+                           workspace)
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """Row RMSNorm over the last dimension, ``bf16((x * rsqrt(mean(x^2) + eps)) * w)``."""
 

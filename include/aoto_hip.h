@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 10
+#define AOTO_HIP_ABI_VERSION 11
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -141,6 +141,23 @@ int aoto_hip_w8_gemv(const void* x, const int32_t* words, const void* scales,
 int aoto_hip_w8_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
                      const void* residual, const void* gate, void* y, int M, int N, int K, int group,
                      int tile, int splits, void* workspace, void* stream);
+
+/* The prefill MLP's gate and up projections in one pass: y[M, N] =
+ * bf16(up . x * silu(bf16(gate . x))) - the reference's gate GEMM followed by
+ * the up GEMM with the silu_mul epilogue (codegen/matmul.py:1443-1471,
+ * 1721-1742; passes/fusion.py:406-498), with X read once. gate/up words and
+ * scales as aoto_hip_w4_gemm (int4) / aoto_hip_w8_gemm (int8), both [N, K].
+ * Limits, tile and splits as aoto_hip_w4_gemm; a split launch needs
+ * aoto_hip_w4_gemm_gate_up_workspace() bytes (gate and up partials). */
+int aoto_hip_w4_gemm_gate_up(const void* x, const int32_t* gate_words, const void* gate_scales,
+                             const int32_t* up_words, const void* up_scales, void* y, int M, int N, int K,
+                             int group, int tile, int splits, void* workspace, void* stream);
+int aoto_hip_w8_gemm_gate_up(const void* x, const int32_t* gate_words, const void* gate_scales,
+                             const int32_t* up_words, const void* up_scales, void* y, int M, int N, int K,
+                             int group, int tile, int splits, void* workspace, void* stream);
+
+/* Bytes of split-K workspace the gate/up entry points need (0 when unsplit). */
+size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits);
 
 /* Row RMSNorm, out = bf16((x * rsqrt(mean(x^2) + eps)) * weight) over [rows, hidden]
  * (codegen/norm.py:75-323, _compile_normalization(kind="rms_norm");

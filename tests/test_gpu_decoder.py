@@ -216,8 +216,11 @@ def test_bucketed_runtime_dispatches_by_length():
 
 
 def test_selections_are_all_native():
+    from aotolith_amd.decoder import _prefill_pairs_gate_up
+
     runtime, _ = _pair(seed=17)
-    for plan, per_layer in ((runtime.decode, 6), (runtime.prefill, 9)):
+    paired = _prefill_pairs_gate_up(PROMPT, TINY)
+    for plan, per_layer in ((runtime.decode, 6), (runtime.prefill, 8 if paired else 9)):
         selections = plan.selections
         assert all(s.is_native and s.implementation == "hip_kernel" for s in selections)
         assert len(selections) == 2 + per_layer * TINY.layers
@@ -225,6 +228,7 @@ def test_selections_are_all_native():
     kinds = [s.kind for s in runtime.decode.selections]
     assert kinds.count("decode_attention") == TINY.layers
     assert "aoto_decode_attention_d64" in runtime.decode.kernel_names()
+    assert ("aoto_w4_gemm_gate_up" in runtime.prefill.kernel_names()) == paired
 
 
 def test_runtime_rejects_bad_inputs():

@@ -449,3 +449,52 @@ def test_decode_attention_o_refuses_large_windows():
         ops.decode_attention_o(torch.zeros(18 * 64, dtype=torch.bfloat16, device="cuda"), pair[0, 0, 0],
                                pair[0, 0, 0], pair, step, *_gpu_packed(packed, scales), 64,
                                torch.zeros(64, dtype=torch.bfloat16, device="cuda"), query_heads=14)
+
+
+GATE_UP_CASES = [
+    (128, 4864, 896, 64, 0),    # Qwen prefill MLP (auto plan: split-K)
+    (16, 4864, 896, 64, 0),     # config 2, M = 16
+    (200, 1152, 896, 32, 0),    # ragged M, group 32
+    (512, 2048, 512, 128, 0),   # several m blocks, no split
+    (96, 896, 4864, 64, 5),     # forced 5-way split
+    (64, 512, 256, 64, 1),      # forced single pass
+]
+
+
+@pytest.mark.parametrize("m,n,k,group,splits", GATE_UP_CASES)
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gemm_gate_up_matches_gate_then_up(m, n, k, group, splits, bits):
+    """The paired prefill MLP GEMM: bit-identical to the gate GEMM followed by the up
+    GEMM with the silu_mul epilogue under the same plan, and within the bars of the
+    oracle's two-step result."""
+
+    from oracle.quant import pack_weight_bits_bf16
+
+    rng = np.random.default_rng(m * 3 + n + k + bits + splits)
+    gate_w = bf16_normal(rng, (n, k), 0.02)
+    up_w = bf16_normal(rng, (n, k), 0.02)
+    gp, gs = pack_weight_bits_bf16(gate_w, group, bits)
+    upk, us = pack_weight_bits_bf16(up_w, group, bits)
+    x = bf16_normal(rng, (m, k))
+    ops = _ops()
+    matmul = ops.w4_matmul if bits == 4 else ops.w8_matmul
+    gate_up = ops.w4_matmul_gate_up if bits == 4 else ops.w8_matmul_gate_up
+    xg = to_gpu_bf16(x)
+    g_gpu, u_gpu = _gpu_packed(gp, gs), _gpu_packed(upk, us)
+    y = gate_up(xg, *g_gpu, *u_gpu, group, splits=splits)
+    gate = matmul(xg, *g_gpu, group, splits=splits)
+    two_step = matmul(xg, *u_gpu, group, gate=gate, splits=splits)
+    assert torch.equal(y.view(torch.int16), two_step.view(torch.int16))
+    want_gate = round_bf16(oracle.w4_matmul(x, gp, gs, group, bits=bits))
+    expected = oracle.w4_matmul(x, upk, us, group, gate=want_gate, bits=bits)
+    atol = 2e-2 * max(1.0, float(np.abs(expected).max()) / 4)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0, atol=atol)
+
+
+def test_gemm_gate_up_rejects_mismatched_weights():
+    ops = _ops()
+    x = torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda")
+    gp = torch.zeros((64, 32), dtype=torch.int32, device="cuda")
+    gs = torch.zeros((64, 4), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.w4_matmul_gate_up(x, gp, gs, torch.zeros((32, 32), dtype=torch.int32, device="cuda"), gs, 64)
