@@ -436,7 +436,11 @@ struct GemmPlan {
 GemmPlan gemm_plan(int M, int N, int K, int tile, int splits) {
   GemmPlan p{};
   if (tile == 0) {
-    p.tm = M <= 64 ? 4 : 8;
+    // 64-row blocks up to M = 256: the latency-bound prefill GEMMs of a small
+    // model run 10-20% faster with twice the blocks (Qwen2-0.5B at M = 128:
+    // q/k/v 10.4 -> 9.6 us, o 10.1 -> 8.8, down 18.4 -> 14.8, gate/up 22.0 ->
+    // 18.9 including the split-K reduce); 128-row blocks beyond.
+    p.tm = M <= 256 ? 4 : 8;
     const long long mb = (M + 16 * p.tm - 1) / (16 * p.tm);
     p.tn = (mb * ((N + 127) / 128) >= 256) ? 2 : 1;
   } else {

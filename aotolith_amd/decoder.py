@@ -488,15 +488,16 @@ def _prefill_pairs_gate_up(tokens: int, spec: DecoderSpec) -> bool:
     """Whether a prefill of ``tokens`` rows runs the MLP's gate and up projections as
     one paired GEMM (one pass over x, one launch) instead of the reference's two.
 
-    Paired where the GEMM plan is latency-bound, i.e. splits the reduction (the
-    Qwen2-0.5B 128-token prefill: 58.5k -> 69.6k tok/s on MI355X); the two GEMMs
-    where it is MFMA-bound (Llama-3-8B buckets: 21.3k / 28.3k tok/s against
-    20.0k / 26.2k paired). ``AOTOLITH_PREFILL_GATE_UP=0`` keeps the two GEMMs.
+    Paired for short prefills (at most 256 rows), where the GEMMs are latency-bound
+    (the Qwen2-0.5B 128-token prefill: 58.5k -> 69.6k tok/s on MI355X); the two
+    GEMMs for longer ones, where they are MFMA-bound (Llama-3-8B 512 / 2048-token
+    buckets: 21.3k / 28.3k tok/s against 20.0k / 26.2k paired).
+    ``AOTOLITH_PREFILL_GATE_UP=0`` keeps the two GEMMs.
     """
 
     if os.environ.get("AOTOLITH_PREFILL_GATE_UP", "1") == "0":
         return False
-    return ops.gemm_workspace_bytes(tokens, spec.intermediate, spec.hidden) > 0
+    return tokens <= 256
 
 
 def prefill_selections(spec: DecoderSpec, bits: int = 4, tokens: int = 128) -> tuple[KernelSelection, ...]:
