@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
@@ -283,6 +284,69 @@ def run_llama8b(args, torch, ops) -> dict:
     return out
 
 
+def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> dict:
+    """One decoder layer's prefill projections at ``tokens`` rows, timed alone.
+
+    q/k/v (+bias when the model has it), o (+residual), gate/up (two GEMMs, or the
+    paired one where the decoder pairs them) and down (+residual) on random packed
+    weights, each the median of 3 rounds of ``launches`` back-to-back launches
+    between HIP events; TFLOP/s = 2 * tokens * N * K / duration (for counter runs:
+    MFMA utilization against the bf16 peak).
+    """
+
+    from aotolith_amd.decoder import _prefill_pairs_gate_up
+
+    dev = "cuda"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    def packed(n, k):
+        w = (torch.randn(n, k, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        return ops.w4_quantize(w, 64)
+
+    h, i = spec.hidden, spec.intermediate
+    x_h = torch.randn(tokens, h, generator=gen, device=dev).to(torch.bfloat16)
+    x_a = torch.randn(tokens, spec.attention_width, generator=gen, device=dev).to(torch.bfloat16)
+    x_i = torch.randn(tokens, i, generator=gen, device=dev).to(torch.bfloat16)
+    res = torch.randn(tokens, h, generator=gen, device=dev).to(torch.bfloat16)
+    qkv_w, o_w, gate_w, up_w, down_w = (packed(spec.qkv_width, h), packed(h, spec.attention_width), packed(i, h),
+                                         packed(i, h), packed(h, i))
+    bias = torch.randn(spec.qkv_width, generator=gen, device=dev).to(torch.bfloat16) if spec.qkv_bias else None
+    out_q = torch.empty(tokens, spec.qkv_width, device=dev, dtype=torch.bfloat16)
+    out_h = torch.empty(tokens, h, device=dev, dtype=torch.bfloat16)
+    out_i = torch.empty(tokens, i, device=dev, dtype=torch.bfloat16)
+    gate = torch.empty_like(out_i)
+    paired = _prefill_pairs_gate_up(tokens, spec)
+    cases = [
+        ("qkv", spec.qkv_width, h, lambda: ops.w4_matmul(x_h, *qkv_w, 64, bias=bias, out=out_q)),
+        ("o", h, spec.attention_width, lambda: ops.w4_matmul(x_a, *o_w, 64, residual=res, out=out_h)),
+    ]
+    if paired:
+        cases.append(("gate_up", 2 * i, h, lambda: ops.w4_matmul_gate_up(x_h, *gate_w, *up_w, 64, out=out_i)))
+    else:
+        cases.append(("gate", i, h, lambda: ops.w4_matmul(x_h, *gate_w, 64, out=gate)))
+        cases.append(("up", i, h, lambda: ops.w4_matmul(x_h, *up_w, 64, gate=gate, out=out_i)))
+    cases.append(("down", h, i, lambda: ops.w4_matmul(x_i, *down_w, 64, residual=res, out=out_h)))
+    out = {}
+    for name, n, k, run in cases:
+        run()
+        torch.cuda.synchronize()
+        rounds = []
+        for _ in range(3):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(launches):
+                run()
+            end.record()
+            torch.cuda.synchronize()
+            rounds.append(start.elapsed_time(end) * 1000.0 / launches)
+        us = sorted(rounds)[1]
+        tflops = 2.0 * tokens * n * k / (us * 1e-6) / 1e12
+        out[name] = {"M": tokens, "N": n, "K": k, "us": round(us, 2), "tflops": round(tflops, 1),
+                     "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    return out
+
+
 def llama_params(spec) -> int:
     """Weight elements of the projections (the prefill GEMM work is 2 * tokens * this)."""
 
@@ -306,6 +370,8 @@ def main() -> int:
                         help="weight code width of the qwen0.5b workload (8: the quantize_bits=8 variant)")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the LM-head GEMV loop, after a calibration copy of 256 MiB (for counter runs)")
+    parser.add_argument("--prefill-gemm-only", type=int, default=0, metavar="TOKENS",
+                        help="only one layer's prefill GEMMs at TOKENS rows (for MFMA counter runs)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported on this one-GPU path "
@@ -327,6 +393,12 @@ def main() -> int:
         torch.cuda.synchronize()
         lm = measure_lm_head_gemv(spec, torch, ops, bits=args.bits)
         print(json.dumps({"calibration_copy_bytes": src.numel() * 4, **lm}), flush=True)
+        return 0
+    if args.prefill_gemm_only:
+        spec = qwen_spec() if args.workload == "qwen0.5b" else llama8b_spec()
+        gemms = measure_prefill_gemms(spec, torch, ops, args.prefill_gemm_only)
+        print(json.dumps({"workload": f"{args.workload} prefill GEMMs", "tokens": args.prefill_gemm_only,
+                          "peak_tflops": MFMA_BF16_PEAK_TFLOPS, **gemms}), flush=True)
         return 0
     if args.workload == "llama8b":
         result = run_llama8b(args, torch, ops)
