@@ -289,9 +289,9 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> 
 
     q/k/v (+bias when the model has it), o (+residual), gate/up (two GEMMs, or the
     paired one where the decoder pairs them) and down (+residual) on random packed
-    weights, each the median of 3 rounds of ``launches`` back-to-back launches
-    between HIP events; TFLOP/s = 2 * tokens * N * K / duration (for counter runs:
-    MFMA utilization against the bf16 peak).
+    weights, each the median of 3 replays of a HIP graph of ``launches`` launches
+    (no host overhead between them) between HIP events; TFLOP/s = 2 * tokens * N * K
+    / duration (for counter runs: MFMA utilization against the bf16 peak).
     """
 
     from aotolith_amd.decoder import _prefill_pairs_gate_up
@@ -329,14 +329,19 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> 
     cases.append(("down", h, i, lambda: ops.w4_matmul(x_i, *down_w, 64, residual=res, out=out_h)))
     out = {}
     for name, n, k, run in cases:
-        run()
+        run()  # allocates any split-K workspace outside the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(launches):
+                run()
+        graph.replay()
         torch.cuda.synchronize()
         rounds = []
         for _ in range(3):
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
-            for _ in range(launches):
-                run()
+            graph.replay()
             end.record()
             torch.cuda.synchronize()
             rounds.append(start.elapsed_time(end) * 1000.0 / launches)
