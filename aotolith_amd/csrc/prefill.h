@@ -10,6 +10,9 @@ namespace aoto {
 // Row RMSNorm (codegen/norm.py:75-323; runtime/mlx_ops/normalization.py:73-119):
 //   out[r] = bf16((x[r] * rsqrt(mean(x[r]^2) + eps)) * w), f32 statistics.
 // One wave per row, 4 rows per 256-thread block; H % 8 == 0 (16-byte vectors).
+// Rows of up to 64 * kRmsVecs vectors (H <= 8192) are held in registers: x and w
+// are loaded once, together, so the normalization needs no second round trip.
+constexpr int kRmsVecs = 16;
 extern "C" __global__ __launch_bounds__(256) void aoto_rms_norm(const uint16_t* __restrict__ x,
                                                                 const uint16_t* __restrict__ w, float eps,
                                                                 uint16_t* __restrict__ out, int rows, int H) {
@@ -20,9 +23,16 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rms_norm(const uint16_t* 
   const uint4* wv = reinterpret_cast<const uint4*>(w);
   uint4* ov = reinterpret_cast<uint4*>(out + (size_t)row * H);
   const int vecs = H >> 3;
-  float ss = 0.f;
-  for (int c = lane; c < vecs; c += 64) {
-    const uint4 r = xv[c];
+  auto normalized = [&](const uint4 r, const uint4 q, float ns) {
+    const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
+    const uint32_t wr[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = cvt_pk_bf16((ns * bf16_lo(raw[j])) * bf16_lo(wr[j]), (ns * bf16_hi(raw[j])) * bf16_hi(wr[j]));
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  auto squares = [](const uint4 r, float ss) {
     const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -30,20 +40,35 @@ extern "C" __global__ __launch_bounds__(256) void aoto_rms_norm(const uint16_t* 
       ss = fmaf(a, a, ss);
       ss = fmaf(b, b, ss);
     }
+    return ss;
+  };
+  float ss = 0.f;
+  if (vecs <= 64 * kRmsVecs) {
+    uint4 xr[kRmsVecs], wr[kRmsVecs];
+#pragma unroll
+    for (int i = 0; i < kRmsVecs; ++i) {
+      const int c = lane + 64 * i;
+      if (c < vecs) {
+        xr[i] = xv[c];
+        wr[i] = wv[c];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRmsVecs; ++i)
+      if (lane + 64 * i < vecs) ss = squares(xr[i], ss);
+    ss = wave_sum(ss);
+    const float ns = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < kRmsVecs; ++i) {
+      const int c = lane + 64 * i;
+      if (c < vecs) ov[c] = normalized(xr[i], wr[i], ns);
+    }
+    return;
   }
+  for (int c = lane; c < vecs; c += 64) ss = squares(xv[c], ss);
   ss = wave_sum(ss);
   const float ns = 1.0f / sqrtf(ss / (float)H + eps);
-  for (int c = lane; c < vecs; c += 64) {
-    const uint4 r = xv[c];
-    const uint4 q = wv[c];
-    const uint32_t raw[4] = {r.x, r.y, r.z, r.w};
-    const uint32_t wr[4] = {q.x, q.y, q.z, q.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o[j] = pack_bf16x2((ns * bf16_lo(raw[j])) * bf16_lo(wr[j]), (ns * bf16_hi(raw[j])) * bf16_hi(wr[j]));
-    ov[c] = make_uint4(o[0], o[1], o[2], o[3]);
-  }
+  for (int c = lane; c < vecs; c += 64) ov[c] = normalized(xv[c], wv[c], ns);
 }
 
 // Standalone RoPE over [rows][D] head rows (runtime/mlx_ops/__init__.py:276-280):
