@@ -260,6 +260,39 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   }
 }
 
+// v += partials[s][e .. e+4) for s = 0 .. splits-1, added in split order; the
+// loads are issued eight splits at a time (a loop that waits for each split's
+// load costs a memory round trip per split).
+AOTO_DEVICE void sum_partials(const float* __restrict__ partials, int splits, size_t stride, size_t e,
+                              float (&v)[4]) {
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float4 p[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) p[u] = *reinterpret_cast<const float4*>(partials + (size_t)(s + u) * stride + e);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      v[0] += p[u].x;
+      v[1] += p[u].y;
+      v[2] += p[u].z;
+      v[3] += p[u].w;
+    }
+  }
+  float4 p[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (s + u < splits) p[u] = *reinterpret_cast<const float4*>(partials + (size_t)(s + u) * stride + e);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    if (s + u < splits) {
+      v[0] += p[u].x;
+      v[1] += p[u].y;
+      v[2] += p[u].z;
+      v[3] += p[u].w;
+    }
+  }
+}
+
 // Sum the split-K partial tiles and apply the epilogue: one thread per 4 outputs.
 // (The f32 sum of the slices replaces the single-block accumulation; each slice
 // is itself an f32 MFMA accumulation, so only the summation order differs.)
@@ -273,13 +306,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
   const size_t e = (size_t)t * 4;
   const int n = (int)(e % N);
   float v[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) {
-    const float4 p = *reinterpret_cast<const float4*>(partials + (size_t)s * M * N + e);
-    v[0] += p.x;
-    v[1] += p.y;
-    v[2] += p.z;
-    v[3] += p.w;
-  }
+  sum_partials(partials, splits, (size_t)M * N, e, v);
   if (bias != nullptr) {
     const uint2 bb = *reinterpret_cast<const uint2*>(bias + n);
     v[0] += bf16_lo(bb.x);
@@ -318,18 +345,8 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_paired(con
   if (t >= quads) return;
   const size_t e = (size_t)t * 4;
   float g[4] = {0.f, 0.f, 0.f, 0.f}, v[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) {
-    const float4 p = *reinterpret_cast<const float4*>(partials + (size_t)s * M * N + e);
-    const float4 q = *reinterpret_cast<const float4*>(partials + (size_t)(splits + s) * M * N + e);
-    g[0] += p.x;
-    g[1] += p.y;
-    g[2] += p.z;
-    g[3] += p.w;
-    v[0] += q.x;
-    v[1] += q.y;
-    v[2] += q.z;
-    v[3] += q.w;
-  }
+  sum_partials(partials, splits, (size_t)M * N, e, g);
+  sum_partials(partials + (size_t)splits * M * N, splits, (size_t)M * N, e, v);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float gr = round_bf16(g[i]);
