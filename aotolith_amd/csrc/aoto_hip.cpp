@@ -268,9 +268,17 @@ AttnShape attention_shape(int head_dim, int chunk) {
   return {waves, j};
 }
 
-void decode_split(int head_dim, int capacity, int requested, int* splits, int* chunk) {
+void decode_split(int head_dim, int capacity, int requested, long long rows, int* splits, int* chunk) {
   const int most = decode_max_chunk(head_dim);
   int s = requested > 0 ? requested : (capacity + most - 1) / most;
+  if (requested <= 0 && s > 1) {
+    // A window that needs a merge launch anyway is spread over ~1152 blocks,
+    // chunks of at least 32 keys (Llama-8B, 32 heads: 768-key window 657 ->
+    // 680 tok/s with 24 splits, 2304-key window 614 -> 624 with 36).
+    const long long want = (1152 + rows - 1) / rows;
+    const int finest = (capacity + 31) / 32;
+    if (want > s) s = (int)(want < finest ? want : finest);
+  }
   int c = (capacity + s - 1) / s;
   if (c > most) c = most;
   s = (capacity + c - 1) / c;
@@ -709,7 +717,7 @@ int aoto_hip_rope_kv_cache_append(const void* row, int row_width, const void* co
 size_t aoto_hip_decode_attention_workspace(int batch, int query_heads, int kv_heads, int capacity, int head_dim,
                                            int splits) {
   int s = 0, c = 0;
-  decode_split(head_dim, capacity, splits, &s, &c);
+  decode_split(head_dim, capacity, splits, (long long)batch * query_heads, &s, &c);
   return s > 1 ? (size_t)batch * query_heads * s * (head_dim + 2) * sizeof(float) : 0;
 }
 
@@ -722,7 +730,7 @@ int decode_attention_plan(const char* what, int batch, int query_heads, int kv_h
     return fail(AOTO_ERR_ARGUMENT, "%s: bad shape (Hq=%d Hkv=%d cap=%d)", what, query_heads, kv_heads, capacity);
   if (head_dim != 64 && head_dim != 128)
     return fail(AOTO_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", what, head_dim);
-  decode_split(head_dim, capacity, splits, s, chunk);
+  decode_split(head_dim, capacity, splits, (long long)batch * query_heads, s, chunk);
   if (*s > 1024)
     return fail(AOTO_ERR_UNSUPPORTED, "%s: %d keys need %d splits, more than the merge takes (1024)", what,
                 capacity, *s);
