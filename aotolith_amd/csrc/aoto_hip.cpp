@@ -459,7 +459,7 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits) {
     p.tm = tile % 10;
   }
   const long long tiles = (long long)((N + 64 * p.tn - 1) / (64 * p.tn)) * ((M + 16 * p.tm - 1) / (16 * p.tm));
-  const int ksteps = K / 64;
+  const int ksteps = (K + 127) / 128;  // the kernel's k-steps (the last may be half)
   int s = splits;
   if (s <= 0) {
     // Split the reduction of small grids: up to 256 rows, to ~256 blocks when
@@ -470,13 +470,12 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits) {
     s = 1;
     if (tiles < few) {
       s = (int)((target + tiles - 1) / tiles);
-      if (s > ksteps / 2) s = ksteps / 2;
       if (s < 1) s = 1;
     }
   }
   if (s > ksteps) s = ksteps;
   const int steps_per = (ksteps + s - 1) / s;
-  p.kslice = steps_per * 64;
+  p.kslice = steps_per * 128;
   p.splits = (K + p.kslice - 1) / p.kslice;
   return p;
 }
@@ -510,7 +509,6 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   if (!x || !words || !scales || !y || (paired && !up_scales))
     return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
   if (paired && (bias || residual || gate)) return fail(AOTO_ERR_ARGUMENT, "%s: no other epilogue", what);
-  if (paired && bits == 8 && !aligned8(up_words)) return fail(AOTO_ERR_ARGUMENT, "%s: words 8-byte aligned", what);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(AOTO_ERR_ARGUMENT, "%s: empty shape M=%d N=%d K=%d", what, M, N, K);
   if (K % 64 != 0 || N % 16 != 0 || group <= 0 || group % 32 != 0 || K % group != 0)
@@ -519,9 +517,9 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   const int epilogues = (bias != nullptr) + (residual != nullptr) + (gate != nullptr);
   if (epilogues > 1) return fail(AOTO_ERR_ARGUMENT, "%s: at most one of bias, residual, gate", what);
   if (!aligned16(x) || !aligned8(y) || (bias && !aligned8(bias)) || (residual && !aligned8(residual)) ||
-      (gate && !aligned8(gate)) || (bits == 8 && !aligned8(words)))
-    return fail(AOTO_ERR_ARGUMENT, "%s: x must be 16-byte aligned, y/bias/residual/gate%s 8-byte aligned", what,
-                bits == 8 ? "/words" : "");
+      (gate && !aligned8(gate)) || !aligned16(words) || (paired && !aligned16(up_words)))
+    return fail(AOTO_ERR_ARGUMENT, "%s: x and words must be 16-byte aligned, y/bias/residual/gate 8-byte aligned",
+                what);
   if (tile != 0 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 14, 18, 24, 28", what, tile);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits);

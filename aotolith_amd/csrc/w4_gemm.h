@@ -26,6 +26,8 @@
 // two words (one 8-byte load) per lane operand instead of one.
 #pragma once
 
+#include <utility>
+
 #include "common.h"
 
 namespace aoto {
@@ -60,8 +62,25 @@ template <int BITS> struct GemmWord;
 template <> struct GemmWord<4> { using type = uint32_t; };
 template <> struct GemmWord<8> { using type = uint2; };
 
-constexpr int kGemmBK = 64;
+constexpr int kGemmBK = 128;                 // k per step: 16 packed words of a weight row
 constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
+
+// k-steps whose loads are in flight. The 64-row tiles serve the prefills of up
+// to 256 rows, whose blocks do little MFMA work per k-step; the 128-row tiles
+// have the MFMA work to cover one step of prefetch and the registers for little more.
+constexpr int gemm_depth(int tm) { return tm <= 4 ? 3 : 2; }
+
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order: the
+// step index is a constant in each call, so register arrays indexed by it stay
+// in registers whatever the unroller decides.
+template <int... I, class F>
+AOTO_DEVICE void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+AOTO_DEVICE void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
 
 // Split-K: blockIdx.z selects the reduction slice [z*kslice, min(K, (z+1)*kslice));
 // with `partials` non-null the block stores its f32 tile to partials[z][m][n]
@@ -73,7 +92,14 @@ constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
 // GEMM with the gate epilogue produce, with one launch and one read of X.
 // Split partials are gate at partials[z], up at partials[splits + z]
 // (aoto_w4_gemm_reduce_paired).
-template <int BITS, int TN, int TM, bool BIAS, bool RESIDUAL, bool GATE, bool PAIRED = false>
+//
+// k order within a step: the 128 k of a step are 16 eight-code units; lane
+// quad q holds units 4q .. 4q+3 of its weight row (one 16-byte load for 4-bit
+// codes, one scale: 32 aligned k never straddle a group) and the j-th product
+// of the step takes unit 4q + j from every lane - for both operands, so the
+// sum over k is the same, only its order differs. A step past K (K = 64 mod
+// 128) zeroes the codes of quads 2 and 3.
+template <int BITS, int TN, int TM, int DEPTH, bool BIAS, bool RESIDUAL, bool GATE, bool PAIRED = false>
 __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename GemmWord<BITS>::type* __restrict__ words,
                              const uint16_t* __restrict__ scales, const uint16_t* __restrict__ bias,
                              const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate,
@@ -86,7 +112,9 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   constexpr int BN = 64 * TN;
   constexpr int XVEC = BM * (kGemmBK / 8);        // 16-byte vectors per X tile
   constexpr int XPT = (XVEC + 255) / 256;         // per thread
-  __shared__ __attribute__((aligned(16))) uint16_t xs[BM * kGemmLdsStride];
+  constexpr int NP = PAIRED ? 2 : 1;              // weight matrices: gate (or the only one), up
+  constexpr int WV = BITS / 4;                    // 16-byte vectors per lane's 4 units
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2 * BM * kGemmLdsStride];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_block = blockIdx.x * BN;
@@ -95,10 +123,10 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
   using Word = typename GemmWord<BITS>::type;
   const int kw = K >> 3;           // 8-code units per weight row
   const int groups = K / group;
+  const float inv_g32 = 32.0f / (float)group;  // 32-k chunks -> group: exact for the chunk counts here
   const int col = lane & 15;       // n (A) / m (B, C) within a tile
-  const int quad = lane >> 4;      // k block of 8 (A, B) / n block of 4 (C)
+  const int quad = lane >> 4;      // unit block of 4 (A, B) / n block of 4 (C)
 
-  constexpr int NP = PAIRED ? 2 : 1;  // weight matrices: gate (or the only one), up
   f32x4_v acc[NP][TN][TM];
 #pragma unroll
   for (int p = 0; p < NP; ++p)
@@ -112,87 +140,113 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
 #pragma unroll
   for (int t = 0; t < TN; ++t) wrow[t] = min(n_wave + t * 16 + col, N - 1);
 
-  uint4 xr[XPT];
-  Word wr[NP][TN][2];
-  uint16_t sr[NP][TN][2];  // the scales of wr, loaded with it (a load at use would cost a round trip per k-step)
-  auto load_x = [&](int k0) {
+  // DEPTH slots of loads in flight: every load is unconditional (a step past the
+  // block's slice re-reads its last step, a cache hit), so the wait for a slot
+  // is an exact count of the loads issued after it. Native vector types: a HIP
+  // uint4 struct copied from global memory lowers to a memcpy through a stack slot.
+  typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+  u32x4_v xr[DEPTH][XPT];
+  u32x4_v wr[DEPTH][NP][TN][WV];
+  uint16_t sr[DEPTH][NP][TN];
+  auto load = [&](auto slot_c, int k0) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int v = 0; v < XPT; ++v) {
-      const int idx = threadIdx.x + v * 256;
-      xr[v] = make_uint4(0, 0, 0, 0);
-      if (idx < XVEC) {
-        const int r = idx / (kGemmBK / 8), c = idx % (kGemmBK / 8);
-        const int m = m_block + r;
-        if (m < M) xr[v] = reinterpret_cast<const uint4*>(X + (size_t)m * K + k0)[c];
-      }
+      const int idx = min((int)threadIdx.x + v * 256, XVEC - 1);
+      const int r = idx / (kGemmBK / 8), c = idx % (kGemmBK / 8);
+      const int m = min(m_block + r, M - 1);  // rows past M feed outputs that are never stored
+      int k = k0 + c * 8;
+      k = k < K ? k : k - kGemmBK / 2;         // the half step's upper half: any finite X (codes are 0)
+      xr[slot][v] = *reinterpret_cast<const u32x4_v*>(X + (size_t)m * K + k);
     }
-  };
-  auto store_x = [&]() {
-#pragma unroll
-    for (int v = 0; v < XPT; ++v) {
-      const int idx = threadIdx.x + v * 256;
-      if (idx < XVEC) {
-        const int r = idx / (kGemmBK / 8), c = idx % (kGemmBK / 8);
-        *reinterpret_cast<uint4*>(xs + r * kGemmLdsStride + c * 8) = xr[v];
-      }
-    }
-  };
-  auto load_w = [&](int k0) {
+    const int ku = (k0 >> 3) + 4 * quad;      // this lane's first unit
+    const int kuc = ku < kw ? ku : ku - 8;    // (half step: in-bounds, zeroed below)
+    const int sidx = (int)(((float)(ku >> 2) + 0.5f) * inv_g32);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const Word* wm = p == 0 ? words : up_words;
       const uint16_t* sm = p == 0 ? scales : up_scales;
 #pragma unroll
-      for (int t = 0; t < TN; ++t)
+      for (int t = 0; t < TN; ++t) {
+        const u32x4_v* src = reinterpret_cast<const u32x4_v*>(wm + (size_t)wrow[t] * kw + kuc);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          wr[p][t][ks] = wm[(size_t)wrow[t] * kw + (k0 >> 3) + ks * 4 + quad];
-          sr[p][t][ks] = sm[(size_t)wrow[t] * groups + (k0 + ks * 32) / group];
-        }
+        for (int e = 0; e < WV; ++e) wr[slot][p][t][e] = src[e];
+        sr[slot][p][t] = sm[(size_t)wrow[t] * groups + min(sidx, groups - 1)];
+      }
+    }
+  };
+  auto store_x = [&](auto slot_c, uint16_t* buf) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+#pragma unroll
+    for (int v = 0; v < XPT; ++v) {
+      const int idx = threadIdx.x + v * 256;
+      if (idx < XVEC) {
+        const int r = idx / (kGemmBK / 8), c = idx % (kGemmBK / 8);
+        *reinterpret_cast<u32x4_v*>(buf + r * kGemmLdsStride + c * 8) = xr[slot][v];
+      }
     }
   };
 
   const int kb = blockIdx.z * kslice;
   const int ke = min(K, kb + kslice);
-  load_x(kb);
-  load_w(kb);
-  for (int k0 = kb; k0 < ke; k0 += kGemmBK) {
-    __syncthreads();
-    store_x();
-    Word wcur[NP][TN][2];
-    float scur[NP][TN][2];
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          wcur[p][t][ks] = wr[p][t][ks];
-          scur[p][t][ks] = bf16_to_f32(sr[p][t][ks]);
-        }
-    __syncthreads();
-    if (k0 + kGemmBK < ke) {
-      load_x(k0 + kGemmBK);
-      load_w(k0 + kGemmBK);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8_v a[NP][TN];
-#pragma unroll
-      for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int t = 0; t < TN; ++t) a[p][t] = dequant_word(wcur[p][t][ks], scur[p][t][ks]);
-#pragma unroll
-      for (int u = 0; u < TM; ++u) {
-        const bf16x8_v b =
-            *reinterpret_cast<const bf16x8_v*>(xs + (u * 16 + col) * kGemmLdsStride + ks * 32 + quad * 8);
+  const int steps = (ke - kb + kGemmBK - 1) / kGemmBK;
+  // The loop starts DEPTH - 1 steps early with the compute skipped, so every
+  // slot is loaded inside the loop: with a separate prologue the registers it
+  // loads and the ones the loop carries differ, and the wait count at the loop
+  // head falls back to the prologue's latest load (one step of prefetch).
+  // s0 = 1 - DEPTH (mod DEPTH): sub-step d loads step s0 + d + DEPTH - 1 into
+  // slot d and computes step s0 + d from slot (d + 1) % DEPTH. X tiles are
+  // double-buffered in LDS: one barrier per step orders the store of step s
+  // before its reads and the reads of step s - 2 before the store that reuses
+  // their buffer.
+  for (int s0 = 1 - DEPTH; s0 < steps; s0 += DEPTH) {
+    static_for<DEPTH>([&](auto d_c) __attribute__((always_inline)) {
+      constexpr int d = decltype(d_c)::value;
+      constexpr int cs = (d + 1) % DEPTH;
+      const int s = s0 + d;
+      load(d_c, kb + min(s + DEPTH - 1, steps - 1) * kGemmBK);
+      if (s >= 0 && s < steps) {
+        uint16_t* buf = xs + (s & 1) * (BM * kGemmLdsStride);
+        store_x(std::integral_constant<int, cs>{}, buf);
+        // this lane's units past K (the half step) contribute zero codes
+        const bool live = kb + s * kGemmBK + 32 * quad < ke;
+        float scur[NP][TN];
 #pragma unroll
         for (int p = 0; p < NP; ++p)
 #pragma unroll
-          for (int t = 0; t < TN; ++t)
-            acc[p][t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][t], b, acc[p][t][u], 0, 0, 0);
+          for (int t = 0; t < TN; ++t) scur[p][t] = bf16_to_f32(sr[cs][p][t]);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // all TM operands read before the products (one LDS round trip, not TM)
+          bf16x8_v b[TM];
+#pragma unroll
+          for (int u = 0; u < TM; ++u)
+            b[u] = *reinterpret_cast<const bf16x8_v*>(buf + (u * 16 + col) * kGemmLdsStride + (4 * quad + j) * 8);
+          bf16x8_v a[NP][TN];
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+              Word w;
+              if constexpr (BITS == 4) {
+                w = live ? wr[cs][p][t][0][j] : 0u;
+              } else {
+                const u32x4_v& h = wr[cs][p][t][j >> 1];
+                w = live ? make_uint2(h[(j & 1) * 2], h[(j & 1) * 2 + 1]) : make_uint2(0u, 0u);
+              }
+              a[p][t] = dequant_word(w, scur[p][t]);
+            }
+#pragma unroll
+          for (int u = 0; u < TM; ++u)
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+              for (int t = 0; t < TN; ++t)
+                acc[p][t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][t], b[u], acc[p][t][u], 0, 0, 0);
+        }
       }
-    }
+    });
   }
 
   if (partials != nullptr) {
@@ -366,7 +420,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_paired(con
           const uint16_t* X, const aoto::GemmWord<BITS>::type* words, const uint16_t* scales,               \
           const uint16_t* bias, const uint16_t* residual, const uint16_t* gate, uint16_t* Y, int M, int N,  \
           int K, int group, int kslice, float* partials) {                                                  \
-    aoto::w4_gemm_body<BITS, TN, TM, BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K,   \
+    aoto::w4_gemm_body<BITS, TN, TM, aoto::gemm_depth(TM), BIAS, RES, GATE>(X, words, scales, bias, residual, gate, Y, M, N, K,   \
                                                       group, kslice, partials);                             \
   }
 
@@ -381,7 +435,7 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_paired(con
       const uint16_t* X, const aoto::GemmWord<BITS>::type* words, const uint16_t* scales,                  \
       const aoto::GemmWord<BITS>::type* up_words, const uint16_t* up_scales, uint16_t* Y, int M, int N,    \
       int K, int group, int kslice, float* partials) {                                                     \
-    aoto::w4_gemm_body<BITS, TN, TM, false, false, false, true>(X, words, scales, nullptr, nullptr,       \
+    aoto::w4_gemm_body<BITS, TN, TM, aoto::gemm_depth(TM), false, false, false, true>(X, words, scales, nullptr, nullptr,       \
                                                                 nullptr, Y, M, N, K, group, kslice,       \
                                                                 partials, up_words, up_scales);           \
   }

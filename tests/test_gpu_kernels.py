@@ -45,6 +45,8 @@ GEMM_CASES = [
     (1, 896, 896, 64),      # a single row through the GEMM
     (200, 1152, 896, 32),   # ragged M, group 32
     (300, 2048, 512, 128),  # group 128, several m blocks
+    (40, 640, 192, 64),     # K = 64 mod 128: the last 128-k step is half
+    (130, 1152, 960, 32),   # half last step with group 32, ragged M
 ]
 
 
@@ -458,6 +460,8 @@ GATE_UP_CASES = [
     (512, 2048, 512, 128, 0),   # several m blocks, no split
     (96, 896, 4864, 64, 5),     # forced 5-way split
     (64, 512, 256, 64, 1),      # forced single pass
+    (72, 512, 320, 64, 0),      # half last 128-k step
+    (64, 640, 960, 64, 3),      # half last step inside a 3-way split
 ]
 
 
