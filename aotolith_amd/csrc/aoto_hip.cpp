@@ -441,19 +441,19 @@ struct GemmPlan {
   int tn, tm, splits, kslice;
 };
 
-GemmPlan gemm_plan(int M, int N, int K, int tile, int splits) {
+GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
   if (tile == 0) {
-    // 64-row blocks up to M = 256: the latency-bound prefill GEMMs of a small
-    // model run 10-20% faster with twice the blocks (Qwen2-0.5B at M = 128:
-    // q/k/v 10.4 -> 9.6 us, o 10.1 -> 8.8, down 18.4 -> 14.8, gate/up 22.0 ->
-    // 18.9 including the split-K reduce); 128-row blocks beyond.
-    p.tm = M <= 256 ? 4 : 8;
+    // 64-row blocks up to M = 128 (the latency-bound prefill of a small model
+    // wants the blocks), 128-row blocks beyond: measured on MI355X with the
+    // 128-k step kernel, M = 256: gate/up 114 -> 83 us, down 84 -> 58 us.
+    p.tm = M <= 128 ? 4 : 8;
     const long long mb = (M + 16 * p.tm - 1) / (16 * p.tm);
-    // Beyond 256 rows, 128-column blocks (the Llama-8B 512-token o and down
-    // projections: 64-column blocks ran 1.5-2.5x slower than 128-column ones
-    // with a 4-way split).
-    p.tn = (M > 256 || mb * ((N + 127) / 128) >= 256) ? 2 : 1;
+    // 128-column blocks with 128-row blocks, except for the paired gate/up,
+    // whose two accumulator sets fit one wave's registers only at 64 columns
+    // (Llama-8B shapes, gate/up at M = 512 / 2048: 161 / 571 us at 64 columns,
+    // 183 / 638 at 128).
+    p.tn = !paired && (p.tm == 8 || mb * ((N + 127) / 128) >= 256) ? 2 : 1;
   } else {
     p.tn = tile / 10;
     p.tm = tile % 10;
@@ -484,12 +484,14 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits) {
 
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  const GemmPlan p = gemm_plan(M, N, K, tile, splits);
+  const GemmPlan p = gemm_plan(M, N, K, tile, splits, false);
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits) {
-  return 2 * aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  const GemmPlan p = gemm_plan(M, N, K, tile, splits, true);
+  return p.splits > 1 ? 2 * (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
 }  // extern "C"
@@ -522,7 +524,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
                 what);
   if (tile != 0 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 14, 18, 24, 28", what, tile);
-  const GemmPlan p = gemm_plan(M, N, K, tile, splits);
+  const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
   if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
     return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
                 "aoto_hip_w4_gemm%s_workspace() bytes", what, p.splits, paired ? "_gate_up" : "");

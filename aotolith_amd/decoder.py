@@ -488,16 +488,15 @@ def _prefill_pairs_gate_up(tokens: int, spec: DecoderSpec) -> bool:
     """Whether a prefill of ``tokens`` rows runs the MLP's gate and up projections as
     one paired GEMM (one pass over x, one launch) instead of the reference's two.
 
-    Paired for short prefills (at most 256 rows), where the GEMMs are latency-bound
-    (the Qwen2-0.5B 128-token prefill: 58.5k -> 69.6k tok/s on MI355X); the two
-    GEMMs for longer ones, where they are MFMA-bound (Llama-3-8B 512 / 2048-token
-    buckets: 21.3k / 28.3k tok/s against 20.0k / 26.2k paired).
+    Paired at every length, measured on MI355X: the Qwen2-0.5B 128-token prefill
+    (58.5k -> 69.6k tok/s when introduced) and the Llama-3-8B 512 / 2048-token
+    buckets (37.6k / 41.2k tok/s paired against 36.7k / 40.2k with two GEMMs).
     ``AOTOLITH_PREFILL_GATE_UP=0`` keeps the two GEMMs.
     """
 
     if os.environ.get("AOTOLITH_PREFILL_GATE_UP", "1") == "0":
         return False
-    return tokens <= 256
+    return tokens > 0
 
 
 def prefill_selections(spec: DecoderSpec, bits: int = 4, tokens: int = 128) -> tuple[KernelSelection, ...]:
