@@ -53,6 +53,10 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "aoto_hip_w8_gemm": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
     "aoto_hip_w4_gemm_gate_up": (_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
+    "aoto_hip_w4_gemm_residual_norm": (_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p,
+                                       _c_float, _p, _p),
+    "aoto_hip_w8_gemm_residual_norm": (_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p,
+                                       _c_float, _p, _p),
     "aoto_hip_w8_gemm_gate_up": (_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p),
     "aoto_hip_w4_gemm_gate_up_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int),
     "aoto_hip_rms_norm": (_p, _p, _c_float, _p, _c_int, _c_int, _p),

@@ -505,7 +505,8 @@ namespace {
 int packed_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* bias,
                 const void* residual, const void* gate, void* y, int M, int N, int K, int group, int tile,
                 int splits, void* workspace, void* stream, const int32_t* up_words = nullptr,
-                const void* up_scales = nullptr) {
+                const void* up_scales = nullptr, const void* norm_weight = nullptr, float eps = 0.f,
+                void* norm_out = nullptr) {
   const bool paired = up_words != nullptr;
   const char* what = paired ? (bits == 4 ? "w4_gemm_gate_up" : "w8_gemm_gate_up") : (bits == 4 ? "w4_gemm" : "w8_gemm");
   if (!x || !words || !scales || !y || (paired && !up_scales))
@@ -548,9 +549,31 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   if (int st = launch(name, grid, dim3(256), 0, stream, x, words, scales, bias, residual, gate, y, M, N, K, group,
                       p.kslice, partials))
     return st;
+  if (norm_out != nullptr) {
+    if (!split)
+      return launch("aoto_rms_norm", dim3((M + 3) / 4), dim3(256), 0, stream, y, norm_weight, eps, norm_out, M, N);
+    return launch("aoto_w4_gemm_reduce_norm", dim3(M), dim3(256), 0, stream, (const float*)partials,
+                  p.splits, residual, y, norm_weight, eps, norm_out, M, N);
+  }
   if (!split) return AOTO_OK;
   return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
                 (const float*)partials, p.splits, bias, residual, gate, y, M, N);
+}
+
+// GEMM with a residual epilogue followed by the row RMSNorm of its result.
+int residual_norm_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* residual,
+                       void* y, int M, int N, int K, int group, int tile, int splits, void* workspace,
+                       const void* norm_weight, float eps, void* norm_out, void* stream) {
+  const char* what = bits == 4 ? "w4_gemm_residual_norm" : "w8_gemm_residual_norm";
+  if (!residual || !norm_weight || !norm_out) return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
+  if (N % 8 != 0 || N > 4096)
+    return fail(AOTO_ERR_UNSUPPORTED, "%s: the norm takes rows of N %% 8 == 0 up to 4096 (N=%d)", what, N);
+  if (!aligned16(y) || !aligned16(residual) || !aligned16(norm_weight) || !aligned16(norm_out))
+    return fail(AOTO_ERR_ARGUMENT, "%s: y, residual, norm weight and norm output must be 16-byte aligned", what);
+  if (norm_out == y || norm_out == residual || norm_out == x)
+    return fail(AOTO_ERR_ARGUMENT, "%s: the norm output must not alias x, y or the residual", what);
+  return packed_gemm(bits, x, words, scales, nullptr, residual, nullptr, y, M, N, K, group, tile, splits, workspace,
+                     stream, nullptr, nullptr, norm_weight, eps, norm_out);
 }
 
 }  // namespace
@@ -585,6 +608,20 @@ int aoto_hip_w8_gemm_gate_up(const void* x, const int32_t* gate_words, const voi
   if (!up_words) return fail(AOTO_ERR_ARGUMENT, "w8_gemm_gate_up: null pointer");
   return packed_gemm(8, x, gate_words, gate_scales, nullptr, nullptr, nullptr, y, M, N, K, group, tile, splits,
                      workspace, stream, up_words, up_scales);
+}
+
+int aoto_hip_w4_gemm_residual_norm(const void* x, const int32_t* words, const void* scales, const void* residual,
+                                   void* y, int M, int N, int K, int group, int tile, int splits, void* workspace,
+                                   const void* norm_weight, float eps, void* norm_out, void* stream) {
+  return residual_norm_gemm(4, x, words, scales, residual, y, M, N, K, group, tile, splits, workspace,
+                            norm_weight, eps, norm_out, stream);
+}
+
+int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const void* scales, const void* residual,
+                                   void* y, int M, int N, int K, int group, int tile, int splits, void* workspace,
+                                   const void* norm_weight, float eps, void* norm_out, void* stream) {
+  return residual_norm_gemm(8, x, words, scales, residual, y, M, N, K, group, tile, splits, workspace,
+                            norm_weight, eps, norm_out, stream);
 }
 
 int aoto_hip_w8_quantize(const void* weight, int weight_is_f32, int rows, int inner, int group,

@@ -347,6 +347,33 @@ AOTO_DEVICE void sum_partials(const float* __restrict__ partials, int splits, si
   }
 }
 
+// v[0..8) += partials[s][e .. e+8) in split order (per element the same adds as
+// sum_partials on each half), four splits' loads in flight at a time.
+AOTO_DEVICE void sum_partials8(const float* __restrict__ partials, int splits, size_t stride, size_t e,
+                               float (&v)[8]) {
+  for (int s = 0; s < splits; s += 4) {
+    float4 p[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (s + u < splits) {
+        const float4* src = reinterpret_cast<const float4*>(partials + (size_t)(s + u) * stride + e);
+        p[u][0] = src[0];
+        p[u][1] = src[1];
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (s + u < splits) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          v[4 * h] += p[u][h].x;
+          v[4 * h + 1] += p[u][h].y;
+          v[4 * h + 2] += p[u][h].z;
+          v[4 * h + 3] += p[u][h].w;
+        }
+      }
+  }
+}
+
 // Sum the split-K partial tiles and apply the epilogue: one thread per 4 outputs.
 // (The f32 sum of the slices replaces the single-block accumulation; each slice
 // is itself an f32 MFMA accumulation, so only the summation order differs.)
@@ -387,6 +414,65 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce(
   *reinterpret_cast<uint2*>(Y + e) = o;
 }
 
+
+// The split-K sum with a residual epilogue followed by the row RMSNorm of its
+// result (the decoder layer's o and down projections, each followed by the next
+// block's norm): one block per row, one 8-wide vector of the row per thread
+// (two for rows over 2048), its partial loads issued together:
+//   y[m]    = bf16(residual[m] + sum of partials[..][m])      (aoto_w4_gemm_reduce)
+//   norm[m] = bf16((ns * y[m][e]) * w[e]),  ns = 1 / sqrt(mean(y[m]^2) + eps)
+// y equals the reduce launch's bit for bit; the sum of squares is a block sum,
+// so ns may differ from aoto_rms_norm's wave-serial sum in the last f32 bits.
+// y may alias residual.
+extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_norm(
+    const float* __restrict__ partials, int splits, const uint16_t* residual, uint16_t* Y,
+    const uint16_t* __restrict__ norm_w, float eps, uint16_t* __restrict__ norm_out, int M, int N) {
+  __shared__ float scratch[4];
+  const int row = blockIdx.x;
+  const int vecs = N >> 3;
+  uint32_t yv[2][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c >= vecs) continue;
+    const size_t e = (size_t)row * N + (size_t)c * 8;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    sum_partials8(partials, splits, (size_t)M * N, e, v);
+    if (residual != nullptr) {
+      const uint4 rr = *reinterpret_cast<const uint4*>(residual + e);
+      const uint32_t r[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] += bf16_lo(r[j]);
+        v[2 * j + 1] += bf16_hi(r[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      yv[i][j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+      const float a = bf16_lo(yv[i][j]), b = bf16_hi(yv[i][j]);
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+    *reinterpret_cast<uint4*>(Y + e) = make_uint4(yv[i][0], yv[i][1], yv[i][2], yv[i][3]);
+  }
+  ss = block_sum<256>(ss, scratch);
+  const float ns = 1.0f / sqrtf(ss / (float)N + eps);
+  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c >= vecs) continue;
+    const uint4 q = wv[c];
+    const uint32_t wr[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = cvt_pk_bf16((ns * bf16_lo(yv[i][j])) * bf16_lo(wr[j]), (ns * bf16_hi(yv[i][j])) * bf16_hi(wr[j]));
+    *reinterpret_cast<uint4*>(norm_out + (size_t)row * N + (size_t)c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
 
 // The paired form's split-K sum: gate = sum of partials[0 .. splits), up = sum
 // of partials[splits .. 2 * splits), y = bf16(up * silu(bf16(gate))), one thread

@@ -499,13 +499,33 @@ def _prefill_pairs_gate_up(tokens: int, spec: DecoderSpec) -> bool:
     return tokens > 0
 
 
+def _prefill_fuses_norms(spec: DecoderSpec) -> bool:
+    """Whether the prefill runs each RMSNorm after a residual projection (o, and
+    the previous layer's down) through :func:`ops.matmul_residual_norm`: rows up
+    to 4096 wide, a multiple of 8."""
+
+    return spec.hidden % 8 == 0 and spec.hidden <= 4096
+
+
+def _norm_selection(index, node, tokens, spec, after, bits):
+    """The norm node after the residual projection ``after`` (its [N, K]): one
+    launch with the projection's split-K sum when its plan splits."""
+
+    if after is not None and _prefill_fuses_norms(spec) and ops.gemm_workspace_bytes(tokens, *after) > 0:
+        return _sel(index, "rms_norm", node, "rms_norm",
+                    "row RMSNorm fused with the preceding projection's split-K sum and residual",
+                    "aoto_w4_gemm_reduce_norm")
+    return _sel(index, "rms_norm", node, "rms_norm", "row RMSNorm", "aoto_rms_norm")
+
+
 def prefill_selections(spec: DecoderSpec, bits: int = 4, tokens: int = 128) -> tuple[KernelSelection, ...]:
     w, kind, gemm = f"W{bits}", f"w{bits}_gemm", f"aoto_w{bits}_gemm"
     out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather", "aoto_embedding")]
     for layer in range(spec.layers):
         base = len(out)
         out += [
-            _sel(base, "rms_norm", f"norm_{layer}a", "rms_norm", "row RMSNorm", "aoto_rms_norm"),
+            _norm_selection(base, f"norm_{layer}a", tokens, spec,
+                            (spec.hidden, spec.intermediate) if layer else None, bits),
             _sel(base + 1, "addmm" if spec.qkv_bias else "matmul", f"qkv_{layer}", kind,
                  f"fused-dequant {w} GEMM on bf16 MFMA" + (" with q/k/v bias epilogue" if spec.qkv_bias else ""),
                  gemm),
@@ -515,7 +535,7 @@ def prefill_selections(spec: DecoderSpec, bits: int = 4, tokens: int = 128) -> t
                  "causal + left-pad masked GQA flash attention on MFMA",
                  f"aoto_flash_attention_d{spec.head_dim}"),
             _sel(base + 4, "addmm", f"hidden_{layer}a", kind, f"{w} GEMM with residual epilogue", gemm),
-            _sel(base + 5, "rms_norm", f"norm_{layer}b", "rms_norm", "row RMSNorm", "aoto_rms_norm"),
+            _norm_selection(base + 5, f"norm_{layer}b", tokens, spec, (spec.hidden, spec.attention_width), bits),
         ]
         if _prefill_pairs_gate_up(tokens, spec):
             out.append(_sel(base + 6, "matmul", f"mlp_{layer}", kind,
@@ -857,8 +877,11 @@ class _Engine:
         paired = _prefill_pairs_gate_up(m, s)
         gate = None if paired else torch.empty_like(act)
         ops.embedding(self.state.embed, ids.reshape(-1), out=x)
-        for index, layer in enumerate(self.state.layers):
-            ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
+        layers = self.state.layers
+        fuse = _prefill_fuses_norms(s)
+        for index, layer in enumerate(layers):
+            if index == 0 or not fuse:
+                ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
             self._matmul(xn, layer.qkv, bias=layer.qkv_bias, out=qkv.view(m, -1))
             pair = pair_of(index)
             ops.rope_qkv_prefill(qkv, positions.reshape(1, -1), self.cos, self.sin, pair, query_heads=s.heads,
@@ -869,8 +892,12 @@ class _Engine:
                 ops.prefill_attention(q, keys, values, mask=mask, scale=self.scale, out=attn)
             else:
                 ops.prefill_attention(q, keys, values, causal=True, key_start=key_start, scale=self.scale, out=attn)
-            self._matmul(attn.view(m, -1), layer.o, residual=x, out=x)
-            ops.rms_norm(x, layer.post_norm, s.eps, out=xn)
+            if fuse:
+                ops.matmul_residual_norm(attn.view(m, -1), layer.o.packed, layer.o.scales, layer.o.group, x,
+                                         layer.post_norm, s.eps, bits=layer.o.bits, out=x, norm_out=xn)
+            else:
+                self._matmul(attn.view(m, -1), layer.o, residual=x, out=x)
+                ops.rms_norm(x, layer.post_norm, s.eps, out=xn)
             if paired:
                 gate_up = ops.w4_matmul_gate_up if layer.gate.bits == 4 else ops.w8_matmul_gate_up
                 gate_up(xn, layer.gate.packed, layer.gate.scales, layer.up.packed, layer.up.scales,
@@ -878,7 +905,13 @@ class _Engine:
             else:
                 self._matmul(xn, layer.gate, out=gate)
                 self._matmul(xn, layer.up, gate=gate, out=act)
-            self._matmul(act, layer.down, residual=x, out=x)
+            if fuse and index + 1 < len(layers):
+                # the next layer's input norm with this projection's split-K sum
+                ops.matmul_residual_norm(act, layer.down.packed, layer.down.scales, layer.down.group, x,
+                                         layers[index + 1].input_norm, s.eps, bits=layer.down.bits, out=x,
+                                         norm_out=xn)
+            else:
+                self._matmul(act, layer.down, residual=x, out=x)
         logits = torch.empty((1, 1, s.vocab), dtype=BF16, device=dev)
         self._gemv(x[m - 1], self.state.lm_head, logits.view(-1), norm_weight=self.state.final_norm, eps=s.eps)
         return logits

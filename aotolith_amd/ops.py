@@ -398,6 +398,56 @@ def w8_matmul_gate_up(x, gate_packed, gate_scales, up_packed, up_scales, group_s
                            workspace)
 
 
+def matmul_residual_norm(x, packed, scales, group_size, residual, norm_weight, eps, *, bits=4, out=None,
+                         norm_out=None, tile=0, splits=0, workspace=None):
+    """``y = bf16(x @ W^T + residual)`` then ``norm_out = rms_norm(y, norm_weight, eps)``.
+
+    A decoder layer's o / down projection and the next block's RMSNorm: the same
+    values as :func:`w4_matmul` (``residual=``) followed by :func:`rms_norm`, with the
+    split-K sum and the norm in one launch. ``out`` may be ``residual`` (in place).
+    Returns ``(y, norm_out)``.
+    """
+
+    per_word = CODES_PER_WORD[bits]
+    _expect(packed, "packed", torch.int32)
+    if packed.dim() != 2:
+        raise ValueError(f"packed must be 2-D [N, K/{per_word}]")
+    n, words = packed.shape
+    k = words * per_word
+    _expect(x, "x", BF16)
+    if x.shape[-1] != k:
+        raise ValueError(f"x has last dimension {x.shape[-1]}, the weight reduces over {k}")
+    m = x.numel() // k
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"group size {group_size} does not divide K={k}")
+    _expect(scales, "scales", BF16, (n, k // group_size))
+    _expect(residual, "residual", BF16)
+    _expect(norm_weight, "norm_weight", BF16, (n,))
+    if residual.numel() != m * n:
+        raise ValueError(f"residual has {residual.numel()} elements, expected {m * n}")
+    shape = tuple(x.shape[:-1]) + (n,)
+    out = torch.empty(shape, dtype=BF16, device=x.device) if out is None else out
+    norm_out = torch.empty(shape, dtype=BF16, device=x.device) if norm_out is None else norm_out
+    for name, t in (("out", out), ("norm_out", norm_out)):
+        _expect(t, name, BF16)
+        if t.numel() != m * n:
+            raise ValueError(f"{name} has {t.numel()} elements, expected {m * n}")
+    _ready(x)
+    need = gemm_workspace_bytes(m, n, k, tile, splits)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
+    lib = _lib.library()
+    entry = lib.aoto_hip_w4_gemm_residual_norm if bits == 4 else lib.aoto_hip_w8_gemm_residual_norm
+    _lib.check(
+        entry(
+            _ptr(x), _ptr(packed), _ptr(scales), _ptr(residual), _ptr(out), m, n, k, group_size, int(tile),
+            int(splits), _ptr(workspace if need else None), _ptr(norm_weight), float(eps), _ptr(norm_out),
+            _stream(),
+        )
+    )
+    return out, norm_out
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """Row RMSNorm over the last dimension, ``bf16((x * rsqrt(mean(x^2) + eps)) * w)``."""
 

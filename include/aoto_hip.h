@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 11
+#define AOTO_HIP_ABI_VERSION 12
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -155,6 +155,22 @@ int aoto_hip_w4_gemm_gate_up(const void* x, const int32_t* gate_words, const voi
 int aoto_hip_w8_gemm_gate_up(const void* x, const int32_t* gate_words, const void* gate_scales,
                              const int32_t* up_words, const void* up_scales, void* y, int M, int N, int K,
                              int group, int tile, int splits, void* workspace, void* stream);
+
+/* A decoder layer's o or down projection followed by the next block's RMSNorm
+ * (models/decoder.py:150-204 layer order; codegen/matmul.py:1721-1742 residual
+ * epilogue; the norm as aoto_hip_rms_norm): y[M, N] = bf16(x . W^T + residual),
+ * then norm_out = bf16((y * rsqrt(mean(y^2) + eps)) * norm_weight) per row.
+ * y equals aoto_hip_w4_gemm with the residual epilogue bit for bit; a split
+ * plan sums the partials and normalizes in one launch, its sum of squares a
+ * block sum (norm_out within one bf16 rounding of aoto_hip_rms_norm's). y may alias the residual; norm_out may alias neither. Limits,
+ * tile, splits and workspace as aoto_hip_w4_gemm, plus N % 8 == 0, N <= 4096
+ * and 16-byte aligned y, residual, norm_weight and norm_out. */
+int aoto_hip_w4_gemm_residual_norm(const void* x, const int32_t* words, const void* scales, const void* residual,
+                                   void* y, int M, int N, int K, int group, int tile, int splits, void* workspace,
+                                   const void* norm_weight, float eps, void* norm_out, void* stream);
+int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const void* scales, const void* residual,
+                                   void* y, int M, int N, int K, int group, int tile, int splits, void* workspace,
+                                   const void* norm_weight, float eps, void* norm_out, void* stream);
 
 /* Bytes of split-K workspace the gate/up entry points need (0 when unsplit). */
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits);

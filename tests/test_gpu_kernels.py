@@ -502,3 +502,51 @@ def test_gemm_gate_up_rejects_mismatched_weights():
     gs = torch.zeros((64, 4), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ValueError):
         ops.w4_matmul_gate_up(x, gp, gs, torch.zeros((32, 32), dtype=torch.int32, device="cuda"), gs, 64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k,splits", [
+    (128, 896, 896, 0),     # Qwen o projection at the prefill length (auto plan: split-K)
+    (128, 896, 4864, 0),    # Qwen down projection (split)
+    (96, 896, 896, 1),      # forced single pass: GEMM then the row norm
+    (40, 4096, 512, 3),     # 4096-wide rows, forced split
+])
+def test_matmul_residual_norm_equals_matmul_then_norm(m, n, k, splits):
+    """The fused o/down projection + RMSNorm gives the two-launch path's y bit for bit, in
+    place over the residual, and its norm within one bf16 rounding of the two-launch norm
+    and of the oracle's (the fused sum of squares is a block sum)."""
+
+    rng = np.random.default_rng(70 + m + k)
+    packed, scales = _packed(rng, n, k)
+    x = bf16_normal(rng, (m, k))
+    residual = bf16_normal(rng, (m, n), 2.0)
+    weight = bf16_normal(rng, (n,), 0.5)
+    ops = _ops()
+    gp, gs = _gpu_packed(packed, scales)
+    gx, gw = to_gpu_bf16(x), to_gpu_bf16(weight)
+    y_ref = ops.w4_matmul(gx, gp, gs, 64, residual=to_gpu_bf16(residual), splits=splits)
+    norm_ref = ops.rms_norm(y_ref, gw, 1e-6)
+    y = to_gpu_bf16(residual)  # in place: out aliases the residual
+    y_out, norm = ops.matmul_residual_norm(gx, gp, gs, 64, y, gw, 1e-6, out=y, splits=splits)
+    assert y_out.data_ptr() == y.data_ptr()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert_bf16_parity(from_gpu_bf16(norm), from_gpu_bf16(norm_ref), max_ulp=1.0)
+    expected_norm = oracle.rms_norm(from_gpu_bf16(y_ref), weight, 1e-6)
+    assert_bf16_parity(from_gpu_bf16(norm), expected_norm, max_ulp=1.0)
+
+
+@pytest.mark.gpu
+def test_matmul_residual_norm_rejects_wide_rows_and_aliasing():
+    rng = np.random.default_rng(77)
+    packed, scales = _packed(rng, 4104, 64)
+    ops = _ops()
+    gp, gs = _gpu_packed(packed, scales)
+    x = to_gpu_bf16(bf16_normal(rng, (4, 64)))
+    res = to_gpu_bf16(bf16_normal(rng, (4, 4104)))
+    with pytest.raises(Exception, match="4096"):
+        ops.matmul_residual_norm(x, gp, gs, 64, res, to_gpu_bf16(bf16_normal(rng, (4104,))), 1e-6)
+    packed, scales = _packed(rng, 512, 64)
+    gp, gs = _gpu_packed(packed, scales)
+    res = to_gpu_bf16(bf16_normal(rng, (4, 512)))
+    with pytest.raises(Exception, match="alias"):
+        ops.matmul_residual_norm(x, gp, gs, 64, res, to_gpu_bf16(bf16_normal(rng, (512,))), 1e-6, norm_out=res)
