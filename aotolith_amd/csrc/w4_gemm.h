@@ -65,10 +65,12 @@ template <> struct GemmWord<8> { using type = uint2; };
 constexpr int kGemmBK = 128;                 // k per step: 16 packed words of a weight row
 constexpr int kGemmLdsStride = kGemmBK + 8;  // bf16 per staged X row
 
-// k-steps whose loads are in flight. The 64-row tiles serve the prefills of up
-// to 256 rows, whose blocks do little MFMA work per k-step; the 128-row tiles
-// have the MFMA work to cover one step of prefetch and the registers for little more.
-constexpr int gemm_depth(int tm) { return tm <= 4 ? 3 : 2; }
+// k-steps whose loads are in flight: one step ahead for every tile. Measured on
+// MI355X for the 64-row tiles at M = 128 (Qwen2-0.5B q/k/v, o, gate/up, down):
+// 8.17 / 7.54 / 11.78 / 11.47 us with 2 slots, 8.41 / 7.78 / 12.19 / 11.75 with
+// 3, 8.63 / 7.98 / 13.33 / 12.69 with 4 - a 128-k step's loads are enough to
+// cover, and more slots only cost registers.
+constexpr int gemm_depth(int) { return 2; }
 
 // f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order: the
 // step index is a constant in each call, so register arrays indexed by it stay
