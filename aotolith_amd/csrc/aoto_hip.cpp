@@ -866,9 +866,12 @@ int aoto_hip_prefill_attention(const void* q, const void* keys, const void* valu
     return fail(AOTO_ERR_ARGUMENT, "prefill_attention: q/keys/values 16-byte, out 8-byte aligned");
   char name[64];
   snprintf(name, sizeof(name), "aoto_flash_attention_d%d", head_dim);
-  return launch(name, dim3((tokens + 63) / 64, batch * query_heads), dim3(256), 0, stream, q, keys, values,
-                (long long)kv_batch_stride, (long long)kv_head_stride, mask, (long long)mask_batch_stride, causal,
-                key_start, tokens, key_tokens, query_heads, kv_heads, scale, out);
+  // one block per (128-query tile, batch, query head), the query tile slowest
+  const long long blocks = (long long)((tokens + 127) / 128) * batch * query_heads;
+  if (blocks > 0x7FFFFFFFLL) return fail(AOTO_ERR_UNSUPPORTED, "prefill_attention: grid too large");
+  return launch(name, dim3((unsigned)blocks), dim3(256), 0, stream, q, keys, values, (long long)kv_batch_stride,
+                (long long)kv_head_stride, mask, (long long)mask_batch_stride, causal, key_start, tokens,
+                key_tokens, batch, query_heads, kv_heads, scale, out);
 }
 
 int aoto_hip_embedding(const void* weight, const int64_t* ids, int count, int hidden, int64_t vocab, void* out,

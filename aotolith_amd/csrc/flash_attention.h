@@ -3,8 +3,9 @@
 // Semantics (runtime/mlx_ops/attention.py:73-122, legalize/attention.py:105-170,
 // mask from models/decoder.py:226-247):
 //   O[b][i][h*D:(h+1)*D] = sum_j softmax_j(scale * q_i . k_j | keep(i, j)) v_j
-// with key/value head h / (Hq/Hkv), f32 scores and softmax, and a query row
-// whose keys are all masked giving 0 (safe_softmax).
+// with key/value head h / (Hq/Hkv), f32 scores and softmax, P rounded to bf16
+// before P.V (codegen/attention.py:367-371), and a query row whose keys are all
+// masked giving 0 (safe_softmax).
 // keep(i, j): with `mask` non-null, mask[b*mask_batch_stride + i*Mk + j] != 0;
 // otherwise j >= key_start and, when `causal`, j <= i + (Mk - M) - the
 // reference's prefill mask "causal and not a left pad" at key_start = M - length.
@@ -13,12 +14,20 @@
 // values at k/v + b*kv_batch_stride + kvh*kv_head_stride + j*D; output
 // [B][M][Hq*D] (the o projection's input rows).
 //
-// Block: 4 waves x 16 queries = 64 queries of one head; key tiles of 64 staged
-// in LDS (K row-major, V transposed). Per wave and key tile:
-//   S^T (16 keys x 16 queries) = K . Q^T   v_mfma_f32_16x16x32_bf16, Q in registers
-//   O^T (16 d x 16 queries)  += V^T . P^T  v_mfma_f32_16x16x16_bf16, P from S^T's registers
-// In both products lane l owns query l%16 of its accumulators, so the running
-// max/sum of that query live in the lane that rescales its O^T columns.
+// Block: 4 waves, 128 queries of one head (wave w: queries q0 + 32w .. q0 + 32w + 31).
+// Key tiles of 64 rows are staged in LDS row-major, K and V alike (row stride
+// D + 16 bf16: the row reads below hit distinct banks), double-buffered: the next
+// tile's global loads are in flight while the current tile is computed, one
+// barrier per tile. Per wave and key tile, with v_mfma_f32_32x32x16_bf16:
+//   S^T (2 x [32 keys x 32 queries]) = K . Q^T   A: K rows from LDS, B: Q in registers
+//   O^T (D/32 x [32 d x 32 queries]) += V^T . P^T  A: V^T by LDS transpose reads
+//                                                 (ds_read_b64_tr_b16), B: P from S^T
+// Lane l owns query l % 32 in both products (C column), so the softmax state of a
+// query lives in lanes l and l ^ 32, which hold the other half of its keys.
+// The MFMA's k slots are a permutation of the tile's keys, the same for both
+// operands: k-step t, slot (h = l / 32, j) holds key 16t + 8(j / 4) + 4h + j % 4,
+// which is where S^T's C layout leaves that key in lane l.
+// The softmax runs in base 2 with log2(e) folded into the scale.
 #pragma once
 
 #include "common.h"
@@ -26,143 +35,233 @@
 namespace aoto {
 
 typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 fa_bf16x4 __attribute__((ext_vector_type(4)));
-typedef float fa_f32x4 __attribute__((ext_vector_type(4)));
+typedef float fa_f32x16 __attribute__((ext_vector_type(16)));
+typedef short fa_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) fa_s16x4 fa_lds_s16x4;
+
+constexpr int kFlashQueries = 128;  // queries per block
+constexpr int kFlashKeys = 64;      // keys per staged tile
+
+// Two LDS transpose reads give lane l the A operand of O^T's k-step `t` for the
+// 32 d rows starting at `d_base`: V[key][d] for d = d_base + l % 32 and the keys of
+// slots (l / 32, j). In each 16-lane group lane r addresses the 8 bytes at
+// V[kb + r / 4][d0 + 4 (r % 4)]; the transpose hands lane i element i % 4 of the
+// chunks of lanes i / 4 + 4m (m = 0..3), i.e. V[kb + m][d0 + i].
+template <int STR>
+AOTO_DEVICE fa_bf16x8 flash_v_operand(const uint16_t* vs, int t, int d_base, int lane) {
+  const int group = lane >> 4, r = lane & 15, half = lane >> 5;
+  const int d0 = d_base + 16 * (group & 1) + 4 * (r & 3);
+  const int row = 16 * t + 4 * half + (r >> 2);
+  const uint16_t* p0 = vs + row * STR + d0;
+  const fa_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_s16x4*)(p0));
+  const fa_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_s16x4*)(p0 + 8 * STR));
+  const short v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(fa_bf16x8, v);
+}
 
 template <int D>
 __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                      const uint16_t* __restrict__ v, long long kv_batch_stride,
                                      long long kv_head_stride, const uint8_t* __restrict__ mask,
                                      long long mask_batch_stride, int causal, int key_start, int M, int Mk,
-                                     int query_heads, int kv_heads, float scale, uint16_t* __restrict__ out) {
-  constexpr int BKV = 64;
-  constexpr int KSTR = D + 8;       // bf16 per K row in LDS
-  constexpr int VSTR = BKV + 8;     // bf16 per V^T row in LDS
-  constexpr int DT = D / 16;        // d tiles of O^T
-  constexpr int DK = D / 32;        // k-steps of S^T
-  __shared__ __attribute__((aligned(16))) uint16_t ks[BKV * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[D * VSTR];
+                                     int batch, int query_heads, int kv_heads, float scale,
+                                     uint16_t* __restrict__ out) {
+  constexpr int BQ = kFlashQueries, BK = kFlashKeys;
+  constexpr int STR = D + 16;              // bf16 per staged row
+  constexpr int DS = D / 16;               // k-steps of S^T (16 d each)
+  constexpr int DT = D / 32;               // 32-row d tiles of O^T
+  constexpr int CHUNKS = BK * D / 8;       // 16-byte chunks of one K (or V) tile
+  constexpr int PER = 2 * CHUNKS / 256;    // chunks per thread per tile, K then V
+  constexpr int ROW_CHUNKS = D / 8;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BK * STR];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = lane & 15, quad = lane >> 4;
-  const int bh = blockIdx.y;
-  const int b = bh / query_heads, h = bh % query_heads;
+  const int col = lane & 31, half = lane >> 5;
+  // Heaviest (last) query tiles first; with a multiple of 8 query heads the heads
+  // of one kv group go to one XCD (blocks are dealt to the 8 XCDs round robin), so
+  // their K/V stays in that XCD's L2.
+  const int bh_count = batch * query_heads;
+  const int tiles_q = (M + BQ - 1) / BQ;
+  const int qt = tiles_q - 1 - (int)blockIdx.x / bh_count;
+  const int slot = (int)blockIdx.x % bh_count;
+  const int b = slot / query_heads;
+  const int hs = slot % query_heads;
+  const int h = (query_heads % 8 == 0) ? (hs % 8) * (query_heads / 8) + hs / 8 : hs;
   const int kvh = h / (query_heads / kv_heads);
-  const int q_block = blockIdx.x * 64;
-  const int q_wave = q_block + wave * 16;
-  const int qi = q_wave + col;           // this lane's query (column of S^T / O^T)
+  const int q0 = qt * BQ;
+  const int qa = q0 + wave * 32;           // this wave's first query
+  const int qi = qa + col;                 // this lane's query
+  const int qrow = min(qi, M - 1);
   const int shift = Mk - M;
 
   const uint16_t* kh = k + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
   const uint16_t* vh = v + (size_t)b * kv_batch_stride + (size_t)kvh * kv_head_stride;
 
-  // Q fragments (B operand of S^T): query qi, d = kk*32 + quad*8 + j.
-  fa_bf16x8 qf[DK];
+  // Q^T operand: query qi, d = 16 s + 8 half + j.
+  fa_bf16x8 qf[DS];
   {
-    const int qrow = min(qi, M - 1);
-    const uint16_t* qp = q + (((size_t)b * query_heads + h) * M + qrow) * D;
+    const uint16_t* qp = q + (((size_t)b * query_heads + h) * M + qrow) * D + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < DK; ++kk) qf[kk] = *reinterpret_cast<const fa_bf16x8*>(qp + kk * 32 + quad * 8);
+    for (int s = 0; s < DS; ++s) qf[s] = *reinterpret_cast<const fa_bf16x8*>(qp + 16 * s);
   }
 
-  fa_f32x4 o[DT];
+  // Keys this block can see, and this wave.
+  const int j_lo = mask ? 0 : max(0, key_start);
+  int j_hi = Mk;
+  if (!mask && causal) j_hi = min(Mk, q0 + BQ + shift);
+  int w_hi = j_hi;
+  if (!mask && causal) w_hi = min(j_hi, qa + 32 + shift);
+  const int tile_begin = (j_lo / BK) * BK;
+  const int n_tiles = j_hi > tile_begin ? (j_hi - tile_begin + BK - 1) / BK : 0;
+
+  // Rows outside [key_start, Mk) (without an explicit mask) are staged as zeros, so
+  // a masked key's value never meets P (0 * NaN would poison the row). The load
+  // address is clamped into the head and the zero is selected when the tile is
+  // written to LDS (no branch or wait around the loads themselves).
+  auto load_tile = [&](int j0, uint4 (&reg)[PER]) {
 #pragma unroll
-  for (int t = 0; t < DT; ++t) o[t] = fa_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < PER; ++i) {
+      const int c = (int)threadIdx.x + (i % (PER / 2)) * 256;
+      const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
+      const uint16_t* base = i < PER / 2 ? kh : vh;
+      reg[i] = *reinterpret_cast<const uint4*>(base + (size_t)min(j0 + row, Mk - 1) * D + cc * 8);
+    }
+  };
+  auto store_tile = [&](int buffer, int j0, const uint4 (&reg)[PER]) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = (int)threadIdx.x + (i % (PER / 2)) * 256;
+      const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
+      const int j = j0 + row;
+      const bool valid = j < Mk && (mask != nullptr || j >= key_start);
+      *reinterpret_cast<uint4*>(&lds[buffer][i < PER / 2 ? 0 : 1][row * STR + cc * 8]) =
+          valid ? reg[i] : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  const float c2 = scale * 1.4426950408889634f;  // scores in log2 units
+  fa_f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = fa_f32x16{};
   float run_max = -INFINITY, run_sum = 0.f;
 
-  // Key range this block can see.
-  int j_begin = mask ? 0 : key_start;
-  int j_end = Mk;
-  if (!mask && causal) j_end = min(Mk, q_block + 64 + shift);
-  j_begin = max(0, j_begin);
-  const int tile_begin = (j_begin / BKV) * BKV;
+  uint4 stage[PER];
+  if (n_tiles > 0) {
+    load_tile(tile_begin, stage);
+    store_tile(0, tile_begin, stage);
+  }
+  // Nothing may be pending when the loop starts: the compiler's wait counting
+  // merges this point from both branches above, and a Q load it believed still in
+  // flight would make every S^T product below wait for the next tile's prefetch
+  // (loads retire in issue order).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
 
-  for (int j0 = tile_begin; j0 < j_end; j0 += BKV) {
-    __syncthreads();
-    // Stage K (row-major) and V (transposed) for keys j0 .. j0+63.
-    constexpr int VEC = BKV * D / 8;
-    for (int idx = threadIdx.x; idx < VEC; idx += 256) {
-      const int key = idx / (D / 8), c = idx % (D / 8);
-      const int j = j0 + key;
-      uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
-      if (j < Mk) {
-        kr = reinterpret_cast<const uint4*>(kh + (size_t)j * D)[c];
-        vr = reinterpret_cast<const uint4*>(vh + (size_t)j * D)[c];
-      }
-      *reinterpret_cast<uint4*>(ks + key * KSTR + c * 8) = kr;
-      const uint32_t raw[4] = {vr.x, vr.y, vr.z, vr.w};
+  for (int t = 0; t < n_tiles; ++t) {
+    const int j0 = tile_begin + t * BK;
+    const int cur = t & 1;
+    const bool more = t + 1 < n_tiles;
+    if (more) load_tile(j0 + BK, stage);  // lands while this tile is computed
+    if (j0 < w_hi) {
+      const uint16_t* ks = lds[cur][0];
+      const uint16_t* vs = lds[cur][1];
+      fa_f32x16 sacc[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[(c * 8 + 2 * e) * VSTR + key] = (uint16_t)(raw[e] & 0xFFFFu);
-        vt[(c * 8 + 2 * e + 1) * VSTR + key] = (uint16_t)(raw[e] >> 16);
-      }
-    }
-    __syncthreads();
-
-    // S^T for 4 sub-tiles of 16 keys.
-    float s[4][4];
-    float tile_max = -INFINITY;
+      for (int sub = 0; sub < 2; ++sub) {
+        sacc[sub] = fa_f32x16{};
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      fa_f32x4 c4 = fa_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < DK; ++kk) {
-        const fa_bf16x8 a = *reinterpret_cast<const fa_bf16x8*>(ks + (st * 16 + col) * KSTR + kk * 32 + quad * 8);
-        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[kk], c4, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = j0 + st * 16 + quad * 4 + i;
-        bool keep = j < Mk && qi < M;
-        if (keep) {
-          if (mask) {
-            keep = mask[(size_t)b * mask_batch_stride + (size_t)qi * Mk + j] != 0;
-          } else {
-            keep = j >= key_start && (!causal || j <= qi + shift);
-          }
+        for (int s = 0; s < DS; ++s) {
+          const fa_bf16x8 a = *reinterpret_cast<const fa_bf16x8*>(ks + (sub * 32 + col) * STR + 16 * s + 8 * half);
+          sacc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[sub], 0, 0, 0);
         }
-        const float sc = keep ? c4[i] * scale : -INFINITY;
-        s[st][i] = sc;
-        tile_max = fmaxf(tile_max, sc);
+      }
+      // Scores of key j0 + 32 sub + 8 (e / 4) + 4 half + e % 4 for query qi; only
+      // tiles that straddle the causal diagonal, the left pad or the end of the keys
+      // (or any tile, with an explicit mask) test each key.
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[sub][e] *= c2;
+      const bool whole = !mask && j0 >= key_start && j0 + BK <= Mk && (!causal || j0 + BK - 1 <= qa + shift);
+      if (!whole) {
+        const int key0 = j0 + 4 * half;
+        if (mask) {
+          const uint8_t* mrow = mask + (size_t)b * mask_batch_stride + (size_t)qrow * Mk;
+          uint32_t keep[2][16];
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int j = key0 + 32 * sub + 8 * (e >> 2) + (e & 3);
+              keep[sub][e] = mrow[min(j, Mk - 1)];
+              if (j >= Mk) keep[sub][e] = 0;
+            }
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              if (!keep[sub][e]) sacc[sub][e] = -INFINITY;
+        } else {
+          const int last = causal ? min(Mk - 1, qi + shift) : Mk - 1;
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int j = key0 + 32 * sub + 8 * (e >> 2) + (e & 3);
+              if (j < key_start || j > last) sacc[sub][e] = -INFINITY;
+            }
+        }
+      }
+      float tile_max = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tile_max = fmaxf(tile_max, sacc[sub][e]);
+      tile_max = xor32_max(tile_max);
+      const float new_max = fmaxf(run_max, tile_max);
+      const float ref = new_max == -INFINITY ? 0.f : new_max;
+      const float correction = __builtin_amdgcn_exp2f(run_max - ref);
+      run_max = new_max;
+      if (__any(correction != 1.f)) {
+        run_sum *= correction;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d] *= correction;
+      }
+      // P (bf16) as the B operand of k-step kt: elements 8 (kt % 2) .. +7 of sacc[kt / 2].
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          p[j] = __builtin_amdgcn_exp2f(sacc[kt >> 1][8 * (kt & 1) + j] - ref);
+          run_sum += p[j];
+        }
+        const uint32_t packed[4] = {cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
+                                    cvt_pk_bf16(p[6], p[7])};
+        const fa_bf16x8 pb = __builtin_bit_cast(fa_bf16x8, packed);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(flash_v_operand<STR>(vs, kt, 32 * d, lane), pb, o[d], 0,
+                                                          0, 0);
       }
     }
-    tile_max = xor32_max(xor16_max(tile_max));
-    const float new_max = fmaxf(run_max, tile_max);
-    const float correction = (new_max == -INFINITY) ? 1.f : expf(run_max - new_max);
-    float tile_sum = 0.f;
-    fa_bf16x4 p[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = (s[st][i] == -INFINITY) ? 0.f : expf(s[st][i] - new_max);
-        tile_sum += e;
-        p[st][i] = (__bf16)e;
-      }
-    tile_sum = xor32_sum(xor16_sum(tile_sum));
-    run_sum = run_sum * correction + tile_sum;
-    run_max = new_max;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      o[t] *= correction;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const fa_bf16x4 a = *reinterpret_cast<const fa_bf16x4*>(vt + (t * 16 + col) * VSTR + st * 16 + quad * 4);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, p[st], o[t], 0, 0, 0);
-      }
-    }
+    if (more) store_tile(cur ^ 1, j0 + BK, stage);
+    __syncthreads();
   }
 
+  const float total = xor32_sum(run_sum);
   if (qi >= M) return;
-  const float inv = run_sum > 0.f ? 1.0f / run_sum : 0.f;
-  uint16_t* orow = out + ((size_t)b * M + qi) * ((size_t)query_heads * D) + (size_t)h * D;
+  const float inv = total > 0.f ? 1.0f / total : 0.f;
+  uint16_t* orow = out + ((size_t)b * M + qi) * ((size_t)query_heads * D) + (size_t)h * D + 4 * half;
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    uint2 w;
-    w.x = pack_bf16x2(o[t][0] * inv, o[t][1] * inv);
-    w.y = pack_bf16x2(o[t][2] * inv, o[t][3] * inv);
-    *reinterpret_cast<uint2*>(orow + t * 16 + quad * 4) = w;
-  }
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = pack_bf16x2(o[d][4 * g] * inv, o[d][4 * g + 1] * inv);
+      w.y = pack_bf16x2(o[d][4 * g + 2] * inv, o[d][4 * g + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + 32 * d + 8 * g) = w;
+    }
 }
 
 }  // namespace aoto
@@ -171,7 +270,8 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   extern "C" __global__ __launch_bounds__(256) void aoto_flash_attention_d##D(                         \
       const uint16_t* q, const uint16_t* k, const uint16_t* v, long long kv_batch_stride,               \
       long long kv_head_stride, const uint8_t* mask, long long mask_batch_stride, int causal,           \
-      int key_start, int M, int Mk, int query_heads, int kv_heads, float scale, uint16_t* out) {        \
+      int key_start, int M, int Mk, int batch, int query_heads, int kv_heads, float scale,              \
+      uint16_t* out) {                                                                                  \
     aoto::flash_attention_body<D>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride,    \
-                                  causal, key_start, M, Mk, query_heads, kv_heads, scale, out);         \
+                                  causal, key_start, M, Mk, batch, query_heads, kv_heads, scale, out);  \
   }

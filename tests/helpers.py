@@ -178,3 +178,50 @@ def state_to_oracle(state) -> dict:
             for l in state.layers
         ],
     }
+
+
+def near_tie(divergence: dict, logits_history) -> bool:
+    """Whether a token flip sits on a near-tie of the oracle's logits.
+
+    The oracle's top two logits must be within two bf16 ulps of their magnitude
+    (floored at 1/16 of the step's largest logit): there the order in which the
+    GPU's f32 accumulators sum decides which of the two rounds higher.
+    """
+
+    scale = float(np.abs(np.asarray(logits_history[divergence["step"]], dtype=np.float64)).max())
+    return divergence["margin"] <= 2 * 2.0 ** -7 * max(abs(divergence["want_logit"]), scale * 2.0 ** -4)
+
+
+def teacher_forced_logits(runtime, prompt_ids, forced_tokens) -> tuple[list[np.ndarray], list[int]]:
+    """GPU logits of every greedy step when the loop is fed ``forced_tokens`` instead of its own picks.
+
+    The ring prefill, then the ring loop's step kernels launched eagerly one step
+    at a time (the same kernels the captured graph replays); after each step the
+    loop's next input token (and, with the fused argmax tail, the embedding row it
+    gathered) is overwritten with the forced one. Returns the per-step logits and
+    the GPU's own argmax at each step (the pattern of the reference's agreement
+    check, ``examples/qwen_quantized_agreement.py``: teacher-forced after a flip).
+    """
+
+    from aotolith_amd import ops
+
+    engine = runtime.engine
+    ids = torch.as_tensor(np.asarray(prompt_ids, dtype=np.int64)).reshape(1, -1).cuda()
+    length = int(ids.shape[1])
+    assert length == runtime.prompt_length, "teacher forcing runs unpadded prompts"
+    logits = runtime._prefill_ring(ids, use_graph=False)
+    out = [from_gpu_bf16(logits).reshape(-1)]
+    picks = [int(engine.token.item())]
+    device = engine.token.device
+    engine.token.fill_(int(forced_tokens[0]))
+    engine.step_state.copy_(torch.tensor([length, length + 1, 1 % engine.capacity, 0], dtype=torch.int32))
+    engine._enter_loop(length)
+    for step in range(1, len(forced_tokens)):
+        engine._ring_step()
+        out.append(from_gpu_bf16(engine.logits).reshape(-1))
+        picks.append(int(engine.token.item()))
+        engine.token.copy_(torch.tensor([int(forced_tokens[step])], dtype=torch.int64, device=device))
+        if engine.keys is not None:
+            ops.embedding(engine.state.embed, engine.token, out=engine.hidden.view(1, -1))
+    torch.cuda.synchronize()
+    return out, picks

@@ -505,31 +505,38 @@ def test_gemm_gate_up_rejects_mismatched_weights():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("m,n,k,splits", [
     (128, 896, 896, 0),     # Qwen o projection at the prefill length (auto plan: split-K)
     (128, 896, 4864, 0),    # Qwen down projection (split)
     (96, 896, 896, 1),      # forced single pass: GEMM then the row norm
     (40, 4096, 512, 3),     # 4096-wide rows, forced split
 ])
-def test_matmul_residual_norm_equals_matmul_then_norm(m, n, k, splits):
+def test_matmul_residual_norm_equals_matmul_then_norm(m, n, k, splits, bits):
     """The fused o/down projection + RMSNorm gives the two-launch path's y bit for bit, in
     place over the residual, and its norm within one bf16 rounding of the two-launch norm
-    and of the oracle's (the fused sum of squares is a block sum)."""
+    and of the oracle's (the fused sum of squares is a block sum). The y half is also
+    checked against the oracle's matmul, for either code width."""
 
-    rng = np.random.default_rng(70 + m + k)
-    packed, scales = _packed(rng, n, k)
+    from oracle.quant import pack_weight_bits_bf16
+
+    rng = np.random.default_rng(70 + m + k + bits)
+    packed, scales = pack_weight_bits_bf16(bf16_normal(rng, (n, k), 0.02), 64, bits)
     x = bf16_normal(rng, (m, k))
     residual = bf16_normal(rng, (m, n), 2.0)
     weight = bf16_normal(rng, (n,), 0.5)
     ops = _ops()
+    matmul = ops.w4_matmul if bits == 4 else ops.w8_matmul
     gp, gs = _gpu_packed(packed, scales)
     gx, gw = to_gpu_bf16(x), to_gpu_bf16(weight)
-    y_ref = ops.w4_matmul(gx, gp, gs, 64, residual=to_gpu_bf16(residual), splits=splits)
+    y_ref = matmul(gx, gp, gs, 64, residual=to_gpu_bf16(residual), splits=splits)
     norm_ref = ops.rms_norm(y_ref, gw, 1e-6)
     y = to_gpu_bf16(residual)  # in place: out aliases the residual
-    y_out, norm = ops.matmul_residual_norm(gx, gp, gs, 64, y, gw, 1e-6, out=y, splits=splits)
+    y_out, norm = ops.matmul_residual_norm(gx, gp, gs, 64, y, gw, 1e-6, bits=bits, out=y, splits=splits)
     assert y_out.data_ptr() == y.data_ptr()
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert_bf16_parity(from_gpu_bf16(y), oracle.w4_matmul(x, packed, scales, 64, residual=residual, bits=bits),
+                       max_ulp=1.0)
     assert_bf16_parity(from_gpu_bf16(norm), from_gpu_bf16(norm_ref), max_ulp=1.0)
     expected_norm = oracle.rms_norm(from_gpu_bf16(y_ref), weight, 1e-6)
     assert_bf16_parity(from_gpu_bf16(norm), expected_norm, max_ulp=1.0)

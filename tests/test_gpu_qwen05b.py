@@ -1,0 +1,130 @@
+"""Config 4 end to end: the Qwen2.5-0.5B-shape W4g64 model, 128-token prompt, 64 greedy tokens.
+
+24 layers, hidden 896, intermediate 4864, 14/2 heads, head_dim 64, vocab 151936, q/k/v bias,
+tied embeddings, rope_theta 1e6, bf16, batch 1 (reference ``compile_qwen2_static_cache``,
+``models/qwen2.py:70-98``). The state is random-init on the GPU with non-trivial norms
+(1 + N(0, 0.1)), seeded q/k/v biases and weights N(0, 0.03): at this width the stream of
+greedy tokens then moves (with N(0, 0.02) weights a random model falls onto one repeated
+token within a few steps, which would leave the check without power).
+
+Agreement criterion (reference ``examples/qwen_quantized_agreement.py:1-24, 150-165`` and
+``tests/test_quantized_qwen2.py:107-123``):
+
+* the captured-graph greedy loop gives the oracle's 64 tokens, or the first divergence is
+  reported with its top-2 margin;
+* teacher-forced on the oracle's stream, the GPU's logits stay within the bar at every one of
+  the 64 steps (per-step max|logit difference|, cosine and top-2 gap are printed), and every
+  step where the two argmaxes differ is reported.
+
+The bar on the logits is set by the model's own sensitivity to rounding: 24 layers amplify a
+one-ulp difference in any intermediate (the per-layer cache deviation grows geometrically with
+depth). The oracle evaluated twice - its GEMMs accumulated in f32 BLAS and in f64, nothing
+else changed - differs by a measured ``1 - cos``; the GPU may differ by at most ten times
+that. To show the bar has power, the same check is applied to the oracle with one planted
+mistake (the final RMSNorm weight dropped), which must fail it.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle.bf16 import round_bf16
+from oracle.decoder import DecoderShape, OracleDecoder
+from tests.helpers import (
+    first_divergence,
+    from_gpu_bf16,
+    parity,
+    state_to_oracle,
+    teacher_forced_logits,
+)
+
+pytestmark = pytest.mark.gpu
+
+PROMPT, NEW = 128, 64
+
+
+def qwen05b_spec():
+    from aotolith_amd.decoder import DecoderSpec
+
+    return DecoderSpec(family="qwen2", vocab=151936, hidden=896, intermediate=4864, layers=24, heads=14,
+                       kv_heads=2, head_dim=64, eps=1e-6, theta=1e6, qkv_bias=True, tied=True,
+                       max_position=32768)
+
+
+class _F64Oracle(OracleDecoder):
+    """The oracle with its prefill GEMMs accumulated in f64 instead of f32 BLAS: the same
+    rounding points, a different summation order (the measure of the model's sensitivity)."""
+
+    def _matmul(self, x, pair, *, bias=None, residual=None, gate=None):
+        acc = np.asarray(x, dtype=np.float64) @ self._w_rounded(pair).T.astype(np.float64)
+        if bias is not None:
+            acc = acc + bias[None, :]
+        if residual is not None:
+            acc = acc + residual
+        if gate is not None:
+            g = gate.astype(np.float64)
+            acc = acc.astype(np.float32).astype(np.float64) * (g / (1.0 + np.exp(-g)))
+        return round_bf16(acc)
+
+
+@pytest.mark.timeout(900)
+def test_qwen05b_64_greedy_tokens_match_the_oracle():
+    from aotolith_amd.decoder import compile_decoder_state, random_state
+
+    spec = qwen05b_spec()
+    state = random_state(spec, 64, seed=11, std=0.03, norm_std=0.1)
+    runtime = compile_decoder_state(spec, state, prompt_length=PROMPT, max_new_tokens=NEW)
+    shape = DecoderShape(vocab=spec.vocab, hidden=spec.hidden, intermediate=spec.intermediate, layers=spec.layers,
+                         heads=spec.heads, kv_heads=spec.kv_heads, head_dim=spec.head_dim, eps=spec.eps,
+                         theta=spec.theta)
+    ostate = state_to_oracle(state)
+    oracle = OracleDecoder(shape, ostate, PROMPT + NEW)
+    ids = np.random.default_rng(12).integers(0, spec.vocab, PROMPT)
+
+    want, history = oracle.greedy_generate(ids, NEW, record_logits=True)
+    distinct = len(set(want.tolist()))
+    print(f"oracle stream: {distinct} distinct of {NEW}: {want.tolist()}")
+    assert distinct >= 16, "the oracle's stream must move for the check to have power"
+
+    # The bar: ten times the oracle's own rounding sensitivity at the prefill logits.
+    ref0 = np.asarray(history[0], dtype=np.float64).reshape(-1)
+    noise = 1.0 - parity(_F64Oracle(shape, ostate, PROMPT + NEW).prefill(ids)[0], ref0)["cosine"]
+    bar = max(10.0 * noise, 1e-5)
+    planted = OracleDecoder(shape, {**ostate, "final_norm": np.ones_like(ostate["final_norm"])}, PROMPT + NEW)
+    planted_gap = 1.0 - parity(planted.prefill(ids)[0], ref0)["cosine"]
+    print(f"oracle f32-vs-f64 noise 1-cos {noise:.3g}; bar {bar:.3g}; dropped final norm 1-cos {planted_gap:.3g}")
+    assert planted_gap > bar, "the bar must reject a dropped norm weight"
+
+    _, ref_cache = oracle.prefill(ids)
+    _, cache = runtime.prefill_ids(ids)
+    got_cache = from_gpu_bf16(cache)
+    for layer in range(spec.layers):
+        stats = parity(got_cache[layer], ref_cache[layer])
+        print(f"prefill cache layer {layer:2d}: max|d| {stats['max_abs']:.4f} 1-cos {1 - stats['cosine']:.3g}")
+
+    tokens = runtime.greedy_generate(ids).cpu().numpy().reshape(-1)
+    assert runtime.engine.graph_error is None, runtime.engine.graph_error
+    divergence = first_divergence(tokens, want, history)
+    agree = NEW if divergence is None else divergence["step"]
+    print(f"graph loop: identical prefix {agree}/{NEW}; first divergence {divergence}")
+
+    forced, picks = teacher_forced_logits(runtime, ids, want)
+    if divergence is not None:
+        # Up to the divergence the loop saw the oracle's tokens, so its logits there are the
+        # teacher-forced ones: its pick must be the forced run's pick.
+        assert picks[divergence["step"]] == divergence["got"], (picks[divergence["step"]], divergence)
+    flips = []
+    worst = 0.0
+    for step, (got, ref) in enumerate(zip(forced, history)):
+        ref = np.asarray(ref, dtype=np.float64).reshape(-1)
+        stats = parity(got, ref)
+        top = np.sort(ref)[-2:]
+        print(f"step {step:2d}: max|dlogit| {stats['max_abs']:.4f} 1-cos {1 - stats['cosine']:.3g} "
+              f"top-2 gap {top[1] - top[0]:.4f} max|logit| {np.abs(ref).max():.2f}")
+        worst = max(worst, 1.0 - stats["cosine"])
+        if picks[step] != int(want[step]):
+            flips.append({"step": step, "got": picks[step], "want": int(want[step]),
+                          "margin": float(top[1] - top[0])})
+    print(f"teacher-forced: worst 1-cos {worst:.3g} (bar {bar:.3g}); argmax flips {flips}")
+    assert worst <= bar
