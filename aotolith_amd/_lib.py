@@ -78,9 +78,6 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _p, _p, _p, _p, _p,
     ),
     "aoto_hip_step_advance": (_p, _c_int, _p),
-    "aoto_hip_decode_attention_o": (
-        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _p,
-    ),
     "aoto_hip_prefill_attention": (
         _p, _p, _p, _i64, _i64, _p, _i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
         _c_float, _p, _p,

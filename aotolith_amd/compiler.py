@@ -126,51 +126,64 @@ class CompiledModulePlan:
         return self.plan(*values, verify_index_bounds=verify_index_bounds, memory=memory)
 
 
-def _select_output(output: Any, output_key: str | None):
-    """The reference's output selection (``compiler.py:843-889``): tensor, ``.logits`` or flattened leaves."""
+def _tensor_leaves(value) -> list[torch.Tensor] | None:
+    """Depth-first tensor leaves of nested tuples/lists (``None`` entries dropped); ``None``
+    when some leaf is neither a tensor nor ``None``."""
 
-    selected = output
+    if value is None:
+        return []
+    if isinstance(value, torch.Tensor):
+        return [value]
+    if not isinstance(value, (tuple, list)):
+        return None
+    out: list[torch.Tensor] = []
+    for item in value:
+        found = _tensor_leaves(item)
+        if found is None:
+            return None
+        out += found
+    return out
+
+
+def _pick_by_key(output: Any, key: str):
+    """``output[key]`` for a mapping (``KeyError`` when absent), else the attribute ``key``
+    (``ValueError`` when absent)."""
+
+    if isinstance(output, Mapping):
+        if key in output:
+            return output[key]
+        raise KeyError(f"output_key {key!r} is not among the module's outputs {sorted(map(str, output))}")
+    if hasattr(output, key):
+        return getattr(output, key)
+    raise ValueError(f"output_key {key!r}: the module's {type(output).__name__} output has no such attribute")
+
+
+def _select_output(output: Any, output_key: str | None):
+    """Which part of a module's return value a plan returns (reference ``compiler.py:843-889``).
+
+    An explicit ``output_key`` wins. Otherwise a tensor is returned as is; a model
+    output object gives its ``logits``; a one-entry mapping gives its value; a tuple or
+    list gives its tensor leaves, flattened in order. Anything else is refused.
+    """
+
+    chosen = output
     if output_key is not None:
-        if isinstance(output, Mapping):
-            if output_key not in output:
-                raise KeyError(f"module output has no key {output_key!r}")
-            selected = output[output_key]
-        else:
-            try:
-                selected = getattr(output, output_key)
-            except AttributeError as exc:
-                raise ValueError(f"module output has no attribute {output_key!r}") from exc
+        chosen = _pick_by_key(output, output_key)
     elif not isinstance(output, torch.Tensor):
         if hasattr(output, "logits"):
-            selected = output.logits
+            chosen = output.logits
         elif isinstance(output, Mapping) and len(output) == 1:
-            selected = next(iter(output.values()))
-        elif isinstance(output, (tuple, list)):
-            selected = tuple(output)
-
-    def leaves(value):
-        if value is None:
-            return []
-        if isinstance(value, torch.Tensor):
-            return [value]
-        if isinstance(value, (tuple, list)):
-            found = []
-            for item in value:
-                sub = leaves(item)
-                if sub is None:
-                    return None
-                found.extend(sub)
-            return found
-        return None
-
-    if isinstance(selected, (tuple, list)):
-        flat = leaves(selected)
-        if not flat:
-            raise ValueError("module sequence outputs must be a non-empty tuple or list of tensor leaves")
-        return tuple(flat)
-    if not isinstance(selected, torch.Tensor):
-        raise ValueError("module output must be a tensor, a tuple/list of tensors, or expose one via output_key")
-    return selected
+            (chosen,) = output.values()
+    if isinstance(chosen, torch.Tensor):
+        return chosen
+    if isinstance(chosen, (tuple, list)):
+        leaves = _tensor_leaves(chosen)
+        if leaves:
+            return tuple(leaves)
+        raise ValueError(f"cannot compile a {type(chosen).__name__} output holding no tensors or a non-tensor leaf; "
+                         "return tensors (possibly nested in tuples/lists)")
+    raise ValueError(f"cannot compile a module returning {type(chosen).__name__}: return a tensor or tensors, "
+                     "or pass output_key to select one")
 
 
 class _ModuleCall(torch.nn.Module):

@@ -19,23 +19,6 @@
 #include "aoto_hip.h"
 #include "generic_args.h"
 
-namespace aoto {
-// Must match the kernel-argument record of aoto_decode_attention_o_d64 (attn_o.h).
-struct AttnOArgs {
-  const uint16_t* row;
-  const uint16_t* cos_table;
-  const uint16_t* sin_table;
-  const uint16_t* rope_rows;
-  uint16_t* keys;
-  uint16_t* values;
-  const int* step;
-  const void* words;
-  const uint16_t* scales;
-  uint16_t* hidden;
-  int query_heads, kv_heads, cap, n_out;
-  float scale;
-};
-}  // namespace aoto
 
 namespace {
 
@@ -1365,41 +1348,4 @@ int aoto_hip_generic_attention(const aoto_tensor* out, const aoto_tensor* q, con
   return launch("aoto_generic_attention", dim3((unsigned)Lq, (unsigned)(B * H)), dim3(256), 0, stream, args);
 }
 
-int aoto_hip_decode_attention_o(const void* row, const void* cos_table, const void* sin_table, const void* rope_rows,
-                                void* keys, void* values, const int32_t* step_state, const int32_t* o_words,
-                                const void* o_scales, void* hidden, int query_heads, int kv_heads, int capacity,
-                                int head_dim, int n_out, int group, float scale, void* stream) {
-  const char* what = "decode_attention_o";
-  if (!row || !keys || !values || !step_state || !o_words || !o_scales || !hidden)
-    return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
-  if (!rope_rows && (!cos_table || !sin_table))
-    return fail(AOTO_ERR_ARGUMENT, "%s: needs rope_rows or the cos/sin tables", what);
-  if (head_dim != 64 || (kv_heads != 1 && kv_heads != 2) || query_heads <= 0 || query_heads % kv_heads != 0 ||
-      query_heads / kv_heads > 8 || capacity <= 0 || capacity > 64 * (8 / kv_heads) || n_out <= 0 || group != 64 ||
-      ((query_heads * 64) / 64) % 2 != 0)
-    return fail(AOTO_ERR_UNSUPPORTED, "%s: needs head_dim 64, 1-2 kv heads of at most 8 query heads, capacity <= %d, "
-                "group 64 and an even number of o-projection groups (Hq=%d Hkv=%d cap=%d D=%d group=%d)", what,
-                kv_heads == 2 ? 256 : 512, query_heads, kv_heads, capacity, head_dim, group);
-  if (!aligned16(row) || !aligned16(keys) || !aligned16(values) || !aligned16(o_words) || !aligned4(o_scales) ||
-      (rope_rows && !aligned4(rope_rows)) || (cos_table && !aligned4(cos_table)) || (sin_table && !aligned4(sin_table)))
-    return fail(AOTO_ERR_ARGUMENT, "%s: row/keys/values/words 16-byte, scales and tables 4-byte aligned", what);
-  aoto::AttnOArgs args;
-  memset(&args, 0, sizeof(args));
-  args.row = static_cast<const uint16_t*>(row);
-  args.cos_table = static_cast<const uint16_t*>(cos_table);
-  args.sin_table = static_cast<const uint16_t*>(sin_table);
-  args.rope_rows = static_cast<const uint16_t*>(rope_rows);
-  args.keys = static_cast<uint16_t*>(keys);
-  args.values = static_cast<uint16_t*>(values);
-  args.step = step_state;
-  args.words = o_words;
-  args.scales = static_cast<const uint16_t*>(o_scales);
-  args.hidden = static_cast<uint16_t*>(hidden);
-  args.query_heads = query_heads;
-  args.kv_heads = kv_heads;
-  args.cap = capacity;
-  args.n_out = n_out;
-  args.scale = scale;
-  return launch("aoto_decode_attention_o_d64", dim3((unsigned)((n_out + 15) / 16)), dim3(512), 0, stream, args);
-}
 }  // extern "C"

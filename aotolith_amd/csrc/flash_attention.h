@@ -27,7 +27,9 @@
 // The MFMA's k slots are a permutation of the tile's keys, the same for both
 // operands: k-step t, slot (h = l / 32, j) holds key 16t + 8(j / 4) + 4h + j % 4,
 // which is where S^T's C layout leaves that key in lane l.
-// The softmax runs in base 2 with log2(e) folded into the scale.
+// The softmax runs in base 2 with log2(e) folded into the scale. Two blocks share a
+// CU (256 VGPRs a lane at most, two 4-wave blocks of LDS), so one block's softmax
+// overlaps the other's products.
 #pragma once
 
 #include "common.h"
@@ -77,12 +79,16 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 31, half = lane >> 5;
-  // Heaviest (last) query tiles first; with a multiple of 8 query heads the heads
-  // of one kv group go to one XCD (blocks are dealt to the 8 XCDs round robin), so
-  // their K/V stays in that XCD's L2.
+  // Query tiles in the order T-1, T-2, ..., T/2 (heaviest first), then 0, 1, ...:
+  // blocks are dealt to the 8 XCDs round robin and to each XCD's CUs in turn, so the
+  // block that takes a CU's second slot comes from the second half of the order and
+  // each CU gets a heavy and a light tile of the causal triangle. With a multiple of
+  // 8 query heads the heads of one kv group go to one XCD, so their K/V stays in
+  // that XCD's L2.
   const int bh_count = batch * query_heads;
   const int tiles_q = (M + BQ - 1) / BQ;
-  const int qt = tiles_q - 1 - (int)blockIdx.x / bh_count;
+  const int rank = (int)blockIdx.x / bh_count;
+  const int qt = rank < tiles_q / 2 ? tiles_q - 1 - rank : rank - tiles_q / 2;
   const int slot = (int)blockIdx.x % bh_count;
   const int b = slot / query_heads;
   const int hs = slot % query_heads;
@@ -178,10 +184,6 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
       // Scores of key j0 + 32 sub + 8 (e / 4) + 4 half + e % 4 for query qi; only
       // tiles that straddle the causal diagonal, the left pad or the end of the keys
       // (or any tile, with an explicit mask) test each key.
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[sub][e] *= c2;
       const bool whole = !mask && j0 >= key_start && j0 + BK <= Mk && (!causal || j0 + BK - 1 <= qa + shift);
       if (!whole) {
         const int key0 = j0 + 4 * half;
@@ -212,16 +214,21 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
             }
         }
       }
+      // Raw scores; the scale (> 0) is applied to the maximum and inside the exponent's FMA.
       float tile_max = -INFINITY;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int e = 0; e < 16; ++e) tile_max = fmaxf(tile_max, sacc[sub][e]);
+      tile_max *= c2;
+      // The exponentials' reference point moves only when a score passes it by more
+      // than 8 (in log2 units), so p stays below 2^8 and O (D/2 accumulators a lane)
+      // is rescaled on few tiles; the final division by the sum is unchanged.
       tile_max = xor32_max(tile_max);
-      const float new_max = fmaxf(run_max, tile_max);
-      const float ref = new_max == -INFINITY ? 0.f : new_max;
-      const float correction = __builtin_amdgcn_exp2f(run_max - ref);
-      run_max = new_max;
+      const float moved = tile_max > run_max + 8.f ? tile_max : run_max;
+      const float correction = moved == run_max ? 1.f : __builtin_amdgcn_exp2f(run_max - moved);
+      run_max = moved;
+      const float ref = moved == -INFINITY ? 0.f : moved;
       if (__any(correction != 1.f)) {
         run_sum *= correction;
 #pragma unroll
@@ -233,7 +240,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
         float p[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(sacc[kt >> 1][8 * (kt & 1) + j] - ref);
+          p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt >> 1][8 * (kt & 1) + j], c2, -ref));
           run_sum += p[j];
         }
         const uint32_t packed[4] = {cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
@@ -267,7 +274,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
 }  // namespace aoto
 
 #define AOTO_FLASH_INSTANCE(D)                                                                          \
-  extern "C" __global__ __launch_bounds__(256) void aoto_flash_attention_d##D(                         \
+  extern "C" __global__ __launch_bounds__(256, 2) void aoto_flash_attention_d##D(                      \
       const uint16_t* q, const uint16_t* k, const uint16_t* v, long long kv_batch_stride,               \
       long long kv_head_stride, const uint8_t* mask, long long mask_batch_stride, int causal,           \
       int key_start, int M, int Mk, int batch, int query_heads, int kv_heads, float scale,              \

@@ -8,7 +8,6 @@
 #include "w4_gemm.h"
 #include "w8.h"
 #include "generic.h"
-#include "attn_o.h"
 #include "decode.h"
 #include "prefill.h"
 #include "flash_attention.h"

@@ -629,17 +629,6 @@ class _Engine:
         self._graph = None
         self._graphs: dict[int, object] = {}
         self.graph_error: str | None = None
-        # Ring-loop attention fused with the o projection (one launch per layer
-        # instead of two), opt-in with AOTOLITH_FUSED_ATTN_O=1 where the kernel's
-        # limits hold. Off by default: on MI355X the fused launch takes ~17 us per
-        # Qwen2-0.5B layer against ~9 us for attention plus the o GEMV.
-        o = self.state.layers[0].o if self.state.layers else None
-        self.fused_attention_o = (
-            os.environ.get("AOTOLITH_FUSED_ATTN_O", "0") == "1"
-            and o is not None and o.bits == 4 and o.group == 64
-            and s.head_dim == 64 and s.kv_heads in (1, 2) and s.heads // s.kv_heads <= 8
-            and self.capacity <= 64 * (8 // s.kv_heads) and (s.attention_width // 64) % 2 == 0
-        )
 
     #: longest run of decode steps captured in one graph (AOTOLITH_GRAPH_STEPS
     #: overrides). Measured on MI355X, one-step graphs replayed back to back beat
@@ -665,11 +654,7 @@ class _Engine:
             self._gemv(self.hidden, layer.qkv, self.qkv, norm_weight=layer.input_norm, eps=s.eps,
                        bias=layer.qkv_bias)
             pair_out = cache_out[index]
-            if ring and self.fused_attention_o:
-                ops.decode_attention_o(self.qkv, self.cos, self.sin, pair_out, self.step_state, layer.o.packed,
-                                       layer.o.scales, layer.o.group, self.hidden, query_heads=s.heads,
-                                       scale=self.scale, rope_rows=self.rope_rows if self.keys is not None else None)
-            elif ring:
+            if ring:
                 ops.decode_rope_attention(self.qkv.view(1, -1), self.cos, self.sin, pair_out, query_heads=s.heads,
                                           query_start=0, key_start=qd, value_start=qd + kd,
                                           step_state=self.step_state, scale=self.scale, workspace=self.workspace,
@@ -683,8 +668,7 @@ class _Engine:
                                          key_start=qd, value_start=qd + kd, q_out=self.q)
                 ops.decode_attention(self.q, pair_out[0], pair_out[1], valid=valid, scale=self.scale,
                                      workspace=self.workspace, splits=self.attention_splits, out=self.attn)
-            if not (ring and self.fused_attention_o):
-                self._gemv(self.attn.view(-1), layer.o, self.hidden, bias=self.hidden)
+            self._gemv(self.attn.view(-1), layer.o, self.hidden, bias=self.hidden)
             self._gemv(self.hidden, layer.gate, self.act, norm_weight=layer.post_norm, eps=s.eps,
                        up=(layer.up.packed, layer.up.scales))
             self._gemv(self.act, layer.down, self.hidden, bias=self.hidden)

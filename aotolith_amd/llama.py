@@ -22,7 +22,8 @@ __all__ = ["check_llama_model", "compile_llama_bucketed", "compile_llama_static_
 
 
 def check_llama_model(model: torch.nn.Module) -> None:
-    """Raise unless ``model`` is a Llama checkpoint this adapter covers."""
+    """Check the family of ``model`` before any packing: a config whose ``model_type`` is not
+    ``llama`` is refused with ``UnsupportedModelError`` naming the entry point to use instead."""
 
     family_for(model, require=FAMILY)
 
@@ -40,7 +41,8 @@ def compile_llama_static_cache(
     target: str = TARGET,
     memory: str = "latency",
 ) -> DecoderStaticCacheRuntime:
-    """Compile a Llama causal LM for greedy single-request generation."""
+    """Pack a Llama model's projections on the GPU and build its prefill / decode plan pair
+    for one prompt length (cache capacity ``prompt_length + max_new_tokens``), batch 1."""
 
     check_llama_model(model)
     return compile_decoder_static_cache(
@@ -62,7 +64,8 @@ def compile_llama_bucketed(
     quantize_bits: int = 4,
     target: str = TARGET,
 ) -> DecoderBucketedRuntime:
-    """Compile one Llama plan pair per prompt-length bucket."""
+    """Pack the Llama weights once and build a prefill / decode plan pair for every width in
+    ``prompt_lengths`` over that one device state; a prompt runs in the narrowest bucket it fits."""
 
     check_llama_model(model)
     return compile_decoder_bucketed(

@@ -687,60 +687,6 @@ def decode_rope_attention(
     return out
 
 
-def decode_attention_o(
-    row: torch.Tensor,
-    cos_table: torch.Tensor,
-    sin_table: torch.Tensor,
-    pair: torch.Tensor,
-    step_state: torch.Tensor,
-    o_packed: torch.Tensor,
-    o_scales: torch.Tensor,
-    group_size: int,
-    hidden: torch.Tensor,
-    *,
-    query_heads: int,
-    scale: float | None = None,
-    rope_rows: torch.Tensor | None = None,
-) -> torch.Tensor:
-    """One ring decode step's attention fused with the W4 o projection and its residual (in place on ``hidden``).
-
-    ``row``: the packed q/k/v projection row ``[(Hq + 2 Hkv) * 64]``; ``pair``: the layer's ring window
-    ``[2, 1, Hkv, cap, 64]`` (the step's key/value are written at the step's slot); ``step_state``:
-    int32 ``{position, valid, ring_offset, slot}``. Raises :class:`~aotolith_amd._lib.UnsupportedShape`
-    outside the kernel's limits (head dim 64, 1-2 kv heads of <= 8 query heads, small windows).
-    """
-
-    _expect(row, "row", BF16)
-    _expect(pair, "pair", BF16)
-    _expect(hidden, "hidden", BF16)
-    _expect(o_packed, "o_packed", torch.int32)
-    _expect(step_state, "step_state", torch.int32, (4,))
-    two, batch, kv_heads, capacity, head_dim = pair.shape
-    if two != 2 or batch != 1:
-        raise ValueError("pair must be [2, 1, Hkv, cap, D]")
-    n_out, words = o_packed.shape
-    if words * 8 != query_heads * head_dim:
-        raise ValueError(f"o projection reduces over {words * 8}, attention gives {query_heads * head_dim}")
-    _expect(o_scales, "o_scales", BF16, (n_out, query_heads * head_dim // group_size))
-    if hidden.numel() != n_out:
-        raise ValueError(f"hidden has {hidden.numel()} elements, the o projection gives {n_out}")
-    if row.numel() != (query_heads + 2 * kv_heads) * head_dim:
-        raise ValueError("row must be the packed q/k/v projection of one token")
-    if rope_rows is not None:
-        _expect(rope_rows, "rope_rows", BF16, (2, head_dim))
-    if scale is None:
-        scale = float(torch.tensor(head_dim ** -0.5, dtype=torch.float32))
-    _ready(row)
-    _lib.check(
-        _lib.library().aoto_hip_decode_attention_o(
-            _ptr(row), _ptr(cos_table), _ptr(sin_table), _ptr(rope_rows), _ptr(pair[0]), _ptr(pair[1]),
-            _ptr(step_state), _ptr(o_packed), _ptr(o_scales), _ptr(hidden), query_heads, kv_heads, capacity,
-            head_dim, n_out, group_size, float(scale), _stream(),
-        )
-    )
-    return hidden
-
-
 def prefill_attention(
     q: torch.Tensor,
     keys: torch.Tensor,

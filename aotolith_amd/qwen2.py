@@ -22,7 +22,8 @@ __all__ = ["check_qwen2_model", "compile_qwen2_bucketed", "compile_qwen2_static_
 
 
 def check_qwen2_model(model: torch.nn.Module) -> None:
-    """Raise unless ``model`` is a Qwen2 checkpoint this adapter covers."""
+    """Check the family of ``model`` before any packing: a config whose ``model_type`` is not
+    ``qwen2`` is refused with ``UnsupportedModelError`` naming the entry point to use instead."""
 
     family_for(model, require=FAMILY)
 
@@ -40,7 +41,8 @@ def compile_qwen2_static_cache(
     target: str = TARGET,
     memory: str = "latency",
 ) -> DecoderStaticCacheRuntime:
-    """Compile a Qwen2/Qwen2.5 causal LM for greedy single-request generation."""
+    """Pack a Qwen2 / Qwen2.5 model's projections on the GPU and build its prefill / decode plan pair
+    for one prompt length (cache capacity ``prompt_length + max_new_tokens``), batch 1."""
 
     check_qwen2_model(model)
     return compile_decoder_static_cache(
@@ -62,7 +64,8 @@ def compile_qwen2_bucketed(
     quantize_bits: int = 4,
     target: str = TARGET,
 ) -> DecoderBucketedRuntime:
-    """Compile one Qwen2 plan pair per prompt-length bucket."""
+    """Pack the Qwen2 / Qwen2.5 weights once and build a prefill / decode plan pair for every width in
+    ``prompt_lengths`` over that one device state; a prompt runs in the narrowest bucket it fits."""
 
     check_qwen2_model(model)
     return compile_decoder_bucketed(

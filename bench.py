@@ -9,13 +9,17 @@ Printed JSON line (rank 0):
   value            decode tok/s = 63 decode tokens per generation / their device time
   prefill_tok_s    128 / (prefill + cache fill + argmax), device time
   decode_tok_s_sync decode tok/s with a host sync after every token
-  roofline         the LM-head W4 GEMV (151936 x 896, RMSNorm prologue): algorithmic
-                   bytes per launch / average launch duration (HIP events on its
-                   stream, rotating weight copies > 1 GiB so HBM, not the 256 MB
-                   Infinity Cache, feeds it) against 8 TB/s
+  roofline         the LM-head W4 GEMV the greedy loop runs (151936 x 896, RMSNorm
+                   prologue, fused argmax keys): algorithmic bytes per launch / average
+                   launch duration (HIP events on its stream, rotating weight copies
+                   > 1 GiB so HBM, not the 256 MB Infinity Cache, feeds it) against 8 TB/s
+  kernels          per-kernel table of the decode step and the prefill: each kernel
+                   launched once per layer over the model's own 24 layer copies inside
+                   a HIP graph, HIP events around the replays; GB/s against 8 TB/s for
+                   the decode kernels, TFLOP/s against 2.5 PFLOP/s for the prefill ones
   cpu_baseline     the CPU oracle (restated reference semantics, NumPy) on the host
-                   cores: prefill of the same prompt plus a bounded number of decode steps
-  parity           greedy tokens of the GPU run vs the CPU oracle over the sampled steps
+                   cores: prefill of the same prompt plus 63 decode steps
+  parity           greedy tokens of the GPU run vs the CPU oracle over the 64 tokens
 
 ``--gpus N`` with N > 1 exits: every GPU box here has one GPU.
 """
@@ -34,6 +38,11 @@ if ROOT not in sys.path:
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0
+# Random-init state of the Qwen workload: weights N(0, 0.03) and norms 1 + N(0, 0.1), the
+# recipe of the config-4 parity test (a random model at N(0, 0.02) falls onto one
+# repeated greedy token within a few steps, which leaves a token comparison no power).
+STATE_STD = 0.03
+STATE_NORM_STD = 0.1
 
 
 def qwen_spec():
@@ -82,17 +91,19 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 24, rounds: int = 
                          bits: int = 4) -> dict:
     """Average duration of the LM-head GEMV over a rotating pool of weight copies.
 
-    Each round queues ``launches`` back-to-back launches behind a spin kernel
-    (so they run without host gaps) between two HIP events on the launching
-    stream; the result is the median round's per-launch time. Long rounds
-    (hundreds of launches) measured ~1-2 us per launch slower than short ones
-    on the same box, so rounds are kept short.
+    For four-bit weights this is the greedy loop's own LM-head kernel: the GEMV
+    with the RMSNorm prologue that also writes the per-wave argmax keys
+    (``ops.w4_gemv_argmax``); the plain GEMV otherwise. Each round queues
+    ``launches`` back-to-back launches behind a spin kernel (so they run without
+    host gaps) between two HIP events on the launching stream; the result is the
+    median round's per-launch time. Long rounds (hundreds of launches) measured
+    ~1-2 us per launch slower than short ones on the same box, so rounds are kept
+    short.
     """
 
     n, k, group = spec.vocab, spec.hidden, 64
     per = gemv_bytes(n, k, group, norm=True, bits=bits)
     copies = max(2, int(pool_bytes // per) + 1)
-    gemv = ops.w4_gemv if bits == 4 else ops.w8_gemv
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1)
     words = [torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k * bits // 32), generator=gen, dtype=torch.int32,
@@ -103,9 +114,23 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 24, rounds: int = 
     x = torch.randn(k, generator=gen, device="cuda").to(torch.bfloat16)
     norm = torch.ones(k, dtype=torch.bfloat16, device="cuda")
     out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    key_count = ops.argmax_key_count(k, n, group) if bits == 4 else 0
+    keys = torch.empty((max(key_count, 1),), dtype=torch.int64, device="cuda")
+    if key_count:
+        kernel = "aoto_w4_gemv_s*_n1_argmax (the greedy loop's LM head: RMSNorm prologue + argmax keys)"
+
+        def launch(i):
+            ops.w4_gemv_argmax(x, words[i], scales[i], group, keys, norm_weight=norm, eps=spec.eps, out=out)
+    else:
+        kernel = f"aoto_w{bits}_gemv (RMSNorm prologue)"
+        gemv = ops.w4_gemv if bits == 4 else ops.w8_gemv
+
+        def launch(i):
+            gemv(x, words[i], scales[i], group, norm_weight=norm, eps=spec.eps, out=out)
+
     stream = torch.cuda.current_stream()
     for i in range(copies):
-        gemv(x, words[i], scales[i], group, norm_weight=norm, eps=spec.eps, out=out)
+        launch(i)
     torch.cuda.synchronize()
     per_round = []
     index = 0
@@ -117,7 +142,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 24, rounds: int = 
         torch.cuda._sleep(5_000_000)
         start.record(stream)
         for _ in range(launches):
-            gemv(x, words[index % copies], scales[index % copies], group, norm_weight=norm, eps=spec.eps, out=out)
+            launch(index % copies)
             index += 1
         end.record(stream)
         torch.cuda.synchronize()
@@ -128,7 +153,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 24, rounds: int = 
     del words, scales
     torch.cuda.empty_cache()
     return {
-        "kernel": f"aoto_w{bits}_gemv (LM head {n}x{k}, g64, RMSNorm prologue)",
+        "kernel": f"{kernel}, LM head {n}x{k}, g64",
         "bytes_per_launch": per,
         "avg_us": avg_us,
         "round_us": [round(v, 3) for v in per_round],
@@ -136,6 +161,201 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 24, rounds: int = 
         "copies": copies,
         "launches": launches * rounds,
     }
+
+
+def _graph_us(torch, body, count: int, rounds: int = 5) -> float:
+    """Per-launch microseconds of ``body`` (``count`` launches) replayed as one HIP graph."""
+
+    body()  # kernel lookup and any workspace allocation happen outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(rounds):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) * 1000.0 / count)
+    del graph
+    return sorted(times)[rounds // 2]
+
+
+def _row(name: str, kernel: str, us: float, *, nbytes: int | None = None, flops: float | None = None) -> dict:
+    row = {"name": name, "kernel": kernel, "avg_us": round(us, 3)}
+    if nbytes is not None:
+        gbs = nbytes / (us * 1e-6) / 1e9
+        row.update({"bytes": int(nbytes), "achieved": round(gbs, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS,
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    if flops is not None:
+        tf = flops / (us * 1e-6) / 1e12
+        row.update({"flops": float(flops), "achieved": round(tf, 1), "unit": "TFLOP/s", "peak": MFMA_BF16_PEAK_TFLOPS,
+                    "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
+    return row
+
+
+def decode_kernel_table(runtime, torch, ops, valid: int | None = None) -> list[dict]:
+    """Per-kernel times of the greedy loop's decode step, one row per kernel kind.
+
+    Each kernel is launched once per layer with that layer's weights (so, as in the
+    loop, no launch finds its weights in the Infinity Cache from the previous
+    launch of the same kind) inside one HIP graph; the time is the median replay /
+    layer count. Bytes are the algorithmic bytes of one launch (weights, scales, x,
+    y, bias or residual, norm weight; the attention's K/V window of ``valid``
+    keys). The loop's state is left as a fresh loop would find it.
+    """
+
+    eng = runtime.engine
+    spec = runtime.spec
+    layers = eng.state.layers
+    n = len(layers)
+    bits = eng.state.bits
+    h, i = spec.hidden, spec.intermediate
+    qd, kd = spec.heads * spec.head_dim, spec.kv_heads * spec.head_dim
+    valid = valid or (runtime.prompt_length + runtime.max_new_tokens // 2)
+    eng.step_state.copy_(torch.tensor([valid - 1, valid, 1 % eng.capacity, 0], dtype=torch.int32))
+    eng.rope_rows[0].copy_(eng.cos[valid - 1])
+    eng.rope_rows[1].copy_(eng.sin[valid - 1])
+    eng.hidden.copy_(eng.state.embed[1])
+    eng.attn.zero_()
+    eng.act.zero_()
+    rows = []
+
+    def qkv():
+        for layer in layers:
+            eng._gemv(eng.hidden, layer.qkv, eng.qkv, norm_weight=layer.input_norm, eps=spec.eps,
+                      bias=layer.qkv_bias)
+
+    def attention():
+        for index in range(n):
+            ops.decode_rope_attention(eng.qkv.view(1, -1), eng.cos, eng.sin, eng.ring[index],
+                                      query_heads=spec.heads, query_start=0, key_start=qd, value_start=qd + kd,
+                                      step_state=eng.step_state, scale=eng.scale, workspace=eng.workspace,
+                                      splits=eng.attention_splits,
+                                      rope_rows=eng.rope_rows if eng.keys is not None else None, out=eng.attn)
+
+    def o_proj():
+        for layer in layers:
+            eng._gemv(eng.attn.view(-1), layer.o, eng.hidden, bias=eng.hidden)
+
+    def gate_up():
+        for layer in layers:
+            eng._gemv(eng.hidden, layer.gate, eng.act, norm_weight=layer.post_norm, eps=spec.eps,
+                      up=(layer.up.packed, layer.up.scales))
+
+    def down():
+        for layer in layers:
+            eng._gemv(eng.act, layer.down, eng.hidden, bias=eng.hidden)
+
+    w = f"w{bits}"
+    rows.append(_row("qkv", f"aoto_{w}_gemv (RMSNorm prologue, bias)", _graph_us(torch, qkv, n),
+                     nbytes=gemv_bytes(spec.qkv_width, h, norm=True, bias=spec.qkv_bias, bits=bits)))
+    rows.append(_row("attention", f"aoto_decode_rope_attention_d{spec.head_dim} (RoPE, KV write, {valid} keys)",
+                     _graph_us(torch, attention, n), nbytes=2 * spec.kv_heads * valid * spec.head_dim * 2))
+    rows.append(_row("o", f"aoto_{w}_gemv (residual)", _graph_us(torch, o_proj, n),
+                     nbytes=gemv_bytes(h, spec.attention_width, bias=True, bits=bits)))
+    rows.append(_row("gate_up", f"aoto_{w}_gemv paired (RMSNorm prologue, silu_mul)", _graph_us(torch, gate_up, n),
+                     nbytes=gemv_bytes(i, h, norm=True, paired=True, bits=bits)))
+    rows.append(_row("down", f"aoto_{w}_gemv (residual)", _graph_us(torch, down, n),
+                     nbytes=gemv_bytes(h, i, bias=True, bits=bits)))
+    if eng.keys is not None:
+        head = eng.state.lm_head
+
+        def finish():
+            for _ in range(n):
+                ops.argmax_finish(eng.keys, eng.key_count, out=eng.token, history=None, history_len=None)
+
+        ops.w4_gemv_argmax(eng.hidden, head.packed, head.scales, head.group, eng.keys,
+                           norm_weight=eng.state.final_norm, eps=spec.eps, out=eng.logits.view(-1))
+        rows.append(_row("argmax_finish", "aoto_argmax_finish (token from the per-wave keys)",
+                         _graph_us(torch, finish, n)))
+    torch.cuda.synchronize()
+    return rows
+
+
+def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
+    """Per-kernel times of the prefill at the bucket length, one row per launch kind.
+
+    Each op is launched once per layer with that layer's weights inside one HIP
+    graph (median replay / layer count); a GEMM row includes its split-K reduce (or
+    the fused reduce + residual + next RMSNorm) when the plan splits. FLOPs are
+    ``2 M N K`` for a projection and ``4 M^2 D Hq / 2`` for the causal attention.
+    """
+
+    eng = runtime.engine
+    spec = runtime.spec
+    layers = eng.state.layers
+    n = len(layers)
+    m = runtime.prompt_length
+    h, i = spec.hidden, spec.intermediate
+    dev = eng.device
+    bf16 = torch.bfloat16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    x = torch.randn((m, h), generator=gen, device=dev).to(bf16)
+    xn = torch.randn((m, h), generator=gen, device=dev).to(bf16)
+    qkv = torch.empty((1, m, spec.qkv_width), dtype=bf16, device=dev)
+    q = torch.randn((1, spec.heads, m, spec.head_dim), generator=gen, device=dev).to(bf16)
+    attn = torch.randn((1, m, spec.attention_width), generator=gen, device=dev).to(bf16)
+    act = torch.randn((m, i), generator=gen, device=dev).to(bf16)
+    positions = torch.arange(m, dtype=torch.int64, device=dev)[None, :]
+    slot0 = eng.capacity - m
+    matmul = ops.w4_matmul if eng.state.bits == 4 else ops.w8_matmul
+    gate_up = ops.w4_matmul_gate_up if eng.state.bits == 4 else ops.w8_matmul_gate_up
+
+    def qkv_proj():
+        for layer in layers:
+            matmul(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, bias=layer.qkv_bias,
+                   out=qkv.view(m, -1))
+
+    def rope():
+        for index in range(n):
+            ops.rope_qkv_prefill(qkv, positions, eng.cos, eng.sin, eng.ring[index], query_heads=spec.heads,
+                                 kv_heads=spec.kv_heads, head_dim=spec.head_dim, slot0=slot0, zero_prefix=True,
+                                 q_out=q)
+
+    def attention():
+        for index in range(n):
+            pair = eng.ring[index]
+            ops.prefill_attention(q, pair[0][:, :, slot0:slot0 + m], pair[1][:, :, slot0:slot0 + m], causal=True,
+                                  key_start=0, scale=eng.scale, out=attn)
+
+    def o_norm():
+        for layer in layers:
+            ops.matmul_residual_norm(attn.view(m, -1), layer.o.packed, layer.o.scales, layer.o.group, x,
+                                     layer.post_norm, spec.eps, bits=layer.o.bits, out=x, norm_out=xn)
+
+    def mlp():
+        for layer in layers:
+            gate_up(xn, layer.gate.packed, layer.gate.scales, layer.up.packed, layer.up.scales, layer.gate.group,
+                    out=act)
+
+    def down_norm():
+        for layer in layers:
+            ops.matmul_residual_norm(act, layer.down.packed, layer.down.scales, layer.down.group, x,
+                                     layer.input_norm, spec.eps, bits=layer.down.bits, out=x, norm_out=xn)
+
+    gemm = f"aoto_w{eng.state.bits}_gemm"
+    rows = [
+        _row("qkv", f"{gemm} + bias (with its split-K reduce when split)", _graph_us(torch, qkv_proj, n),
+             flops=2.0 * m * spec.qkv_width * h),
+        _row("rope", "aoto_rope_qkv_prefill (RoPE of q/k, q head-major, cache fill)", _graph_us(torch, rope, n),
+             nbytes=m * spec.qkv_width * 2 + m * (spec.qkv_width) * 2),
+        _row("attention", f"aoto_flash_attention_d{spec.head_dim} (causal)", _graph_us(torch, attention, n),
+             flops=4.0 * m * m * spec.head_dim * spec.heads / 2),
+        _row("o_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, o_norm, n),
+             flops=2.0 * m * h * spec.attention_width),
+        _row("gate_up", f"aoto_w{eng.state.bits}_gemm paired gate/up + silu_mul", _graph_us(torch, mlp, n),
+             flops=2.0 * m * 2 * i * h),
+        _row("down_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, down_norm, n),
+             flops=2.0 * m * h * i),
+    ]
+    torch.cuda.synchronize()
+    return rows
 
 
 def counter_traffic() -> int | None:
@@ -250,7 +470,7 @@ def run_llama8b(args, torch, ops) -> dict:
 
     spec = llama8b_spec()
     print("[bench] building the random-init Llama-3-8B-shape W4 state", file=sys.stderr, flush=True)
-    state = random_state(spec, 64, seed=0)
+    state = random_state(spec, 64, seed=0, norm_std=STATE_NORM_STD)
     new = 256
     runtime = compile_decoder_bucketed_state(spec, state, prompt_lengths=[512, 2048], max_new_tokens=new)
     gen = torch.Generator().manual_seed(0)
@@ -277,6 +497,14 @@ def run_llama8b(args, torch, ops) -> dict:
             "generations": len(records),
         }
         print(f"[bench] llama8b bucket {bucket}: {out[f'bucket_{bucket}']}", file=sys.stderr, flush=True)
+        if not args.no_kernels:
+            b = runtime.bucket_for(bucket)
+            out[f"bucket_{bucket}"]["kernels"] = {"decode": decode_kernel_table(b, torch, ops),
+                                                  "prefill": prefill_kernel_table(b, torch, ops)}
+            for name, table in out[f"bucket_{bucket}"]["kernels"].items():
+                for row in table:
+                    print(f"[bench] llama8b {bucket} {name} {row['name']}: {row['avg_us']} us {row.get('frac', '')}",
+                          file=sys.stderr, flush=True)
     if not args.no_roofline:
         lm = measure_lm_head_gemv(spec, torch, ops, launches=12, rounds=5, pool_bytes=1.5e9)
         out["lm_head_gemv"] = {"avg_us": round(lm["avg_us"], 2), "achieved_gbs": round(lm["achieved"], 1),
@@ -367,9 +595,11 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--prompt", type=int, default=128)
     parser.add_argument("--new", type=int, default=64)
-    parser.add_argument("--cpu-decode-steps", type=int, default=8)
+    parser.add_argument("--cpu-decode-steps", type=int, default=63,
+                        help="oracle decode steps timed and compared (63: the whole 64-token generation)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-roofline", action="store_true")
+    parser.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     parser.add_argument("--workload", choices=("qwen0.5b", "llama8b"), default="qwen0.5b")
     parser.add_argument("--bits", type=int, choices=(4, 8), default=4,
                         help="weight code width of the qwen0.5b workload (8: the quantize_bits=8 variant)")
@@ -414,7 +644,7 @@ def main() -> int:
     bits = args.bits
     print(f"[bench] building the random-init W{bits} state on {torch.cuda.get_device_name(0)}", file=sys.stderr,
           flush=True)
-    state = random_state(spec, 64, seed=0, bits=bits)
+    state = random_state(spec, 64, seed=0, std=STATE_STD, norm_std=STATE_NORM_STD, bits=bits)
     runtime = compile_decoder_state(spec, state, prompt_length=args.prompt, max_new_tokens=args.new)
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, spec.vocab, (1, args.prompt), generator=gen)
@@ -463,12 +693,23 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(lm["achieved"] / HBM_PEAK_GBS, 4),
             "traffic": counter_traffic() if bits == 4 else None,
+            "traffic_source": ("recorded: profiles/lm_head_gemv_qwen05b_traffic.md (rocprofv3 --pmc FETCH_SIZE, "
+                               "WRITE_SIZE of bench.py --roofline-only, calibrated on a copy)") if bits == 4 else None,
             "kernel": lm["kernel"],
             "avg_us": round(lm["avg_us"], 3),
             "round_us": lm["round_us"],
             "bytes_per_launch": lm["bytes_per_launch"],
         }
         print(f"[bench] LM-head GEMV {lm['avg_us']:.2f} us, {lm['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+
+    kernels = None
+    if not args.no_kernels:
+        kernels = {"decode": decode_kernel_table(runtime, torch, ops),
+                   "prefill": prefill_kernel_table(runtime, torch, ops)}
+        for name, table in kernels.items():
+            for row in table:
+                print(f"[bench] {name} {row['name']}: {row['avg_us']} us "
+                      f"{row.get('frac', '')}", file=sys.stderr, flush=True)
 
     baseline = None
     parity = None
@@ -492,8 +733,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": f"synthetic (random-init weights N(0,0.02) packed W{bits} g64 on the GPU, seeded q/k/v bias, "
-                "uniform-random prompt ids)",
+        "data": f"synthetic (random-init weights N(0,{STATE_STD}) packed W{bits} g64 on the GPU, seeded q/k/v bias, "
+                f"norms 1+N(0,{STATE_NORM_STD}), uniform-random prompt ids)",
         "config": {
             "workload": f"qwen2.5-0.5b-shape W{bits}g64 static-cache greedy: prompt 128, 64 new tokens, bs1 "
                         "(one step = one generation: prefill + 63 graph-replayed decode steps)",
@@ -510,6 +751,7 @@ def main() -> int:
         "decode_graph": runtime.engine.graph_error or "captured",
         "prefill_graph": runtime.engine.prefill_graph_error or "captured",
         "roofline": roofline,
+        "kernels": kernels,
         "cpu_baseline": baseline,
         "parity": parity,
     }

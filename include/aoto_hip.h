@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 12
+#define AOTO_HIP_ABI_VERSION 13
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -260,23 +260,6 @@ int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_sta
                                    int slot, int valid, int ring_offset, int batch, int query_heads, int kv_heads,
                                    int capacity, int head_dim, float scale, int splits, void* workspace,
                                    const int32_t* step_state, const void* rope_rows, void* out, void* stream);
-
-/* Ring decode step of one layer's attention fused with its o projection (no
- * counterpart node in the reference: its decode graph runs the decode attention,
- * codegen/attention.py:447-656, then the packed o GEMV with the residual
- * epilogue, codegen/matmul.py:542-739; this launch computes both): RoPE of the
- * step's q and k from the packed q/k/v row (q at 0, k at Hq*64, v at
- * (Hq+Hkv)*64) with rope_rows [2][64] (or the tables at the step's position),
- * GQA attention over the layer's ring window keys/values [Hkv][cap][64] with the
- * new (k_rot, v) at the step's slot (and written there), then
- * hidden[n] = bf16(hidden[n] + Wo[n] . attn) for the W4 o projection o_words
- * [n_out, Hq*64/8], o_scales [n_out, Hq*64/64]. step_state = {position, valid,
- * ring_offset, slot}. Limits: head_dim 64, 1-2 kv heads of <= 8 query heads,
- * capacity <= 64 * 8 / kv_heads, group 64. */
-int aoto_hip_decode_attention_o(const void* row, const void* cos_table, const void* sin_table, const void* rope_rows,
-                                void* keys, void* values, const int32_t* step_state, const int32_t* o_words,
-                                const void* o_scales, void* hidden, int query_heads, int kv_heads, int capacity,
-                                int head_dim, int n_out, int group, float scale, void* stream);
 
 /* Advance a decode loop's device step state {position, valid, ring_offset,
  * slot} by one token (ring offset and slot wrap at capacity). The greedy loop

@@ -96,25 +96,6 @@ def test_greedy_tokens_match_the_oracle(use_graph):
         assert runtime.engine.graph_error is None, runtime.engine.graph_error
 
 
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_fused_attention_o_loop_matches_the_oracle(monkeypatch, use_graph):
-    """The opt-in fused attention + o projection launch (AOTOLITH_FUSED_ATTN_O=1)."""
-
-    monkeypatch.setenv("AOTOLITH_FUSED_ATTN_O", "1")
-    runtime, oracle = _pair(seed=17)
-    assert runtime.engine.fused_attention_o
-    ids = np.random.default_rng(18).integers(0, TINY.vocab, PROMPT)
-    tokens = runtime.greedy_generate(ids, use_graph=use_graph).cpu().numpy()
-    want, history = oracle.greedy_generate(ids, NEW, record_logits=True)
-    divergence = first_divergence(tokens, want, history)
-    if divergence is not None:
-        scale = float(np.abs(history[divergence["step"]]).max())
-        assert _margin_ok(divergence, scale), divergence
-    monkeypatch.delenv("AOTOLITH_FUSED_ATTN_O")
-    plain, _ = _pair(seed=17)
-    assert not plain.engine.fused_attention_o
-
-
 def test_graph_and_eager_loops_agree_and_repeat():
     runtime, _ = _pair(seed=9)
     ids = np.random.default_rng(10).integers(0, TINY.vocab, PROMPT)

@@ -393,66 +393,6 @@ def test_w4_matmul_in_place_residual_with_split_k():
     assert_bf16_parity(from_gpu_bf16(buf), oracle.w4_matmul(x, packed, scales, 64, residual=residual), max_ulp=1.0)
 
 
-@pytest.mark.parametrize("hq,hkv,cap,valid,offset,slot,n_out", [
-    (14, 2, 192, 140, 61, 60, 896),    # Qwen2.5-0.5B shape at the bench's window
-    (14, 2, 256, 256, 0, 255, 896),    # largest window for two kv heads, rolled layout
-    (4, 2, 26, 17, 0, 16, 256),        # the small decoder tests' shape
-    (8, 1, 512, 300, 123, 122, 200),   # one kv head of 8 queries, 512 keys, ragged row count
-    (14, 2, 192, 1, 5, 4, 896),        # only the step's own key is kept
-])
-@pytest.mark.parametrize("rows", [False, True])
-def test_decode_attention_o_matches_attention_then_o_projection(hq, hkv, cap, valid, offset, slot, n_out, rows):
-    """The fused ring step (RoPE + KV write + attention + W4 o GEMV + residual) against the oracle."""
-
-    dim = 64
-    rng = np.random.default_rng(cap + slot + hq)
-    cos, sin, gcos, gsin = _tables(cap, dim, 1e6)
-    pair = bf16_normal(rng, (2, 1, hkv, cap, dim))
-    row = bf16_normal(rng, (1, (hq + 2 * hkv) * dim))
-    position = valid - 1
-    ref_q, ref_pair = oracle.rope_kv_cache_append(
-        pair[None], row, cos[position], sin[position], layer=0, query_heads=hq,
-        query_start=0, key_start=hq * dim, value_start=(hq + hkv) * dim,
-    )
-    ring = pair.copy()
-    ring[:, :, :, slot] = ref_pair[:, :, :, cap - 1]
-    logical = (np.arange(cap) - offset) % cap
-    keep = (logical >= cap - valid)[None, None, None, :]
-    attn = oracle.attention(ref_q, ring[0], ring[1], keep).reshape(-1)
-    packed, scales = _packed(rng, n_out, hq * dim)
-    hidden = bf16_normal(rng, (n_out,), 2.0)
-    expected = oracle.w4_gemv(attn, packed, scales, 64, bias=hidden)
-    ops = _ops()
-    gpair = to_gpu_bf16(pair)
-    ghidden = to_gpu_bf16(hidden)
-    step = torch.tensor([(position + 7) % cap if rows else position, valid, offset, slot], dtype=torch.int32,
-                        device="cuda")
-    rope_rows = torch.stack([gcos[position], gsin[position]]).contiguous() if rows else None
-    ops.decode_attention_o(to_gpu_bf16(row).view(-1), gcos, gsin, gpair, step, *_gpu_packed(packed, scales), 64,
-                           ghidden, query_heads=hq, rope_rows=rope_rows)
-    assert_bf16_parity(from_gpu_bf16(ghidden), expected, max_ulp=2.0)
-    got = from_gpu_bf16(gpair)
-    others = np.ones(cap, dtype=bool)
-    others[slot] = False
-    np.testing.assert_array_equal(got[:, :, :, others], pair[:, :, :, others])
-    np.testing.assert_array_equal(got[1, :, :, slot], ref_pair[1, :, :, cap - 1])
-    assert_bf16_parity(got[0, :, :, slot], ref_pair[0, :, :, cap - 1], max_ulp=1.0)
-
-
-def test_decode_attention_o_refuses_large_windows():
-    from aotolith_amd._lib import UnsupportedShape
-
-    rng = np.random.default_rng(3)
-    ops = _ops()
-    pair = torch.zeros((2, 1, 2, 320, 64), dtype=torch.bfloat16, device="cuda")
-    packed, scales = _packed(rng, 64, 14 * 64)
-    step = torch.tensor([0, 1, 0, 0], dtype=torch.int32, device="cuda")
-    with pytest.raises(UnsupportedShape):
-        ops.decode_attention_o(torch.zeros(18 * 64, dtype=torch.bfloat16, device="cuda"), pair[0, 0, 0],
-                               pair[0, 0, 0], pair, step, *_gpu_packed(packed, scales), 64,
-                               torch.zeros(64, dtype=torch.bfloat16, device="cuda"), query_heads=14)
-
-
 GATE_UP_CASES = [
     (128, 4864, 896, 64, 0),    # Qwen prefill MLP (auto plan: split-K)
     (16, 4864, 896, 64, 0),     # config 2, M = 16

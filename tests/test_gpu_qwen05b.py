@@ -19,7 +19,7 @@ Agreement criterion (reference ``examples/qwen_quantized_agreement.py:1-24, 150-
 The bar on the logits is set by the model's own sensitivity to rounding: 24 layers amplify a
 one-ulp difference in any intermediate (the per-layer cache deviation grows geometrically with
 depth). The oracle evaluated twice - its GEMMs accumulated in f32 BLAS and in f64, nothing
-else changed - differs by a measured ``1 - cos``; the GPU may differ by at most ten times
+else changed - differs by a measured ``1 - cos``; the GPU may differ by at most five times
 that. To show the bar has power, the same check is applied to the oracle with one planted
 mistake (the final RMSNorm weight dropped), which must fail it.
 """
@@ -87,10 +87,10 @@ def test_qwen05b_64_greedy_tokens_match_the_oracle():
     print(f"oracle stream: {distinct} distinct of {NEW}: {want.tolist()}")
     assert distinct >= 16, "the oracle's stream must move for the check to have power"
 
-    # The bar: ten times the oracle's own rounding sensitivity at the prefill logits.
+    # The bar: five times the oracle's own rounding sensitivity at the prefill logits.
     ref0 = np.asarray(history[0], dtype=np.float64).reshape(-1)
     noise = 1.0 - parity(_F64Oracle(shape, ostate, PROMPT + NEW).prefill(ids)[0], ref0)["cosine"]
-    bar = max(10.0 * noise, 1e-5)
+    bar = max(5.0 * noise, 1e-5)
     planted = OracleDecoder(shape, {**ostate, "final_norm": np.ones_like(ostate["final_norm"])}, PROMPT + NEW)
     planted_gap = 1.0 - parity(planted.prefill(ids)[0], ref0)["cosine"]
     print(f"oracle f32-vs-f64 noise 1-cos {noise:.3g}; bar {bar:.3g}; dropped final norm 1-cos {planted_gap:.3g}")
