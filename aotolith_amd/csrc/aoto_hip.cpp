@@ -18,6 +18,7 @@
 
 #include "aoto_hip.h"
 #include "generic_args.h"
+#include "internal.h"
 
 
 namespace {
@@ -33,6 +34,20 @@ int fail(int code, const char* fmt, ...) {
   g_error = buf;
   return code;
 }
+
+}  // namespace
+
+int aoto::set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, args);
+  va_end(args);
+  g_error = buf;
+  return code;
+}
+
+namespace {
 
 struct DeviceModule {
   hipModule_t module = nullptr;
@@ -297,6 +312,7 @@ int aoto_hip_load_code_object(const void* image, size_t size) {
   if (slot.module != nullptr) hipModuleUnload(slot.module);
   slot.module = module;
   slot.functions.clear();
+  aoto::noalloc_prepare_device(device);
   return AOTO_OK;
 }
 

@@ -55,6 +55,8 @@ def build(verbose: bool = False) -> tuple[str, str]:
     _run([HIPCC, *DEVICE_FLAGS, "--genco", "--no-gpu-bundle-output", os.path.join(CSRC, "kernels.hip"), "-o", tmp_obj], verbose)
     os.replace(tmp_obj, CODE_OBJECT)
     tmp_lib = LIBRARY + ".tmp"
+    # The host library: the C-ABI launchers, plus noalloc.hip, whose device part is
+    # only the static scratch buffer of the allocation-free GEMM entry point.
     _run(
         [
             HIPCC,
@@ -62,9 +64,15 @@ def build(verbose: bool = False) -> tuple[str, str]:
             "-std=c++17",
             "-fPIC",
             "-shared",
+            "--offload-arch=gfx950",
+            "-Xclang",
+            "-target-feature",
+            "-Xclang",
+            "-packed-fp32-ops",
             "-I" + INCLUDE,
             "-I" + CSRC,
             os.path.join(CSRC, "aoto_hip.cpp"),
+            os.path.join(CSRC, "noalloc.hip"),
             "-o",
             tmp_lib,
         ],

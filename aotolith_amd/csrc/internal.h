@@ -1,0 +1,14 @@
+// Host-side helpers shared by the C-ABI sources of libaoto_hip.so (not part of the ABI).
+#pragma once
+
+namespace aoto {
+
+// Record a printf-style message for aoto_hip_last_error() and return `code`.
+int set_error(int code, const char* fmt, ...);
+
+// Resolve, once per device and with that device current, the address of the
+// allocation-free GEMM's static scratch buffer (noalloc.hip). Called when a code
+// object is installed on the device.
+void noalloc_prepare_device(int device);
+
+}  // namespace aoto

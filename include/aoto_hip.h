@@ -110,6 +110,20 @@ int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, co
  * it does not split). */
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits);
 
+/* No counterpart in the reference. aoto_hip_w4_gemm for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same arguments and results without the
+ * workspace. A split-K plan keeps its f32 partials in a static device buffer of
+ * AOTO_HIP_NOALLOC_SCRATCH_BYTES that the library holds on each GPU until the
+ * process ends; a plan that needs more (aoto_hip_w4_gemm_workspace() bytes) is
+ * refused with AOTO_ERR_UNSUPPORTED (pass splits = 1, or use aoto_hip_w4_gemm).
+ * Nothing is allocated or freed. All calls on one GPU share its buffer: calls that
+ * overlap in time on one device (different streams) race. */
+#define AOTO_HIP_NOALLOC_SCRATCH_BYTES (16u << 20)
+int aoto_hip_w4_gemm_noalloc(const void* x, const int32_t* words, const void* scales, const void* bias,
+                             const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                             int tile, int splits, void* stream);
+
 /* Symmetric int8 group quantizer + packer, bit-exact with quantize.py:155-172
  * (quantize_int8: scale = max|w| / 127, an all-zero group 1/127, codes
  * clip(rint(w / scale), -128, 127)) and the bf16 scale cast of
