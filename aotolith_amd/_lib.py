@@ -68,6 +68,14 @@ SIGNATURES: dict[str, tuple] = {
         _p, _c_int, _p, _p, _c_int, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_int, _p, _p,
     ),
+    "aoto_hip_w4_gemm_qkv_rope": (
+        _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _p,
+    ),
+    "aoto_hip_w8_gemm_qkv_rope": (
+        _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _p,
+    ),
     "aoto_hip_w4_gemm_noalloc": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p),
     "aoto_hip_decode_attention_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int, _c_int),
     "aoto_hip_decode_attention": (

@@ -497,6 +497,16 @@ size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int spl
 
 namespace {
 
+// The q/k/v projection's RoPE and cache fill (aoto_rope_qkv_prefill's arguments, batch 1).
+struct RopeFill {
+  const int64_t* positions;
+  const void* cos_table;
+  const void* sin_table;
+  void* q_out;
+  void* pair;
+  int query_heads, kv_heads, head_dim, capacity, slot0, zero_prefix;
+};
+
 // The prefill GEMM of either code width (the kernels differ only in how many
 // packed words make one lane's 8-code operand).
 // With up_words / up_scales (the gate/up entry points) the launch is the paired
@@ -505,7 +515,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
                 const void* residual, const void* gate, void* y, int M, int N, int K, int group, int tile,
                 int splits, void* workspace, void* stream, const int32_t* up_words = nullptr,
                 const void* up_scales = nullptr, const void* norm_weight = nullptr, float eps = 0.f,
-                void* norm_out = nullptr) {
+                void* norm_out = nullptr, const struct RopeFill* rope = nullptr) {
   const bool paired = up_words != nullptr;
   const char* what = paired ? (bits == 4 ? "w4_gemm_gate_up" : "w8_gemm_gate_up") : (bits == 4 ? "w4_gemm" : "w8_gemm");
   if (!x || !words || !scales || !y || (paired && !up_scales))
@@ -554,9 +564,46 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
     return launch("aoto_w4_gemm_reduce_norm", dim3(M), dim3(256), 0, stream, (const float*)partials,
                   p.splits, residual, y, norm_weight, eps, norm_out, M, N);
   }
+  if (rope != nullptr) {
+    // q/k/v: the split sum, bias, RoPE and cache fill in one launch; unsplit, the
+    // GEMM stored y with its bias and the RoPE / cache fill kernel follows
+    const int D = rope->head_dim;
+    long long items = split ? (long long)M * (N / D) * (D / 8) : (long long)M * N;
+    if (rope->zero_prefix) items += split ? 2LL * rope->kv_heads * rope->slot0 * D / 4
+                                          : 2LL * rope->kv_heads * rope->slot0 * D;
+    if (split)
+      return launch("aoto_w4_gemm_reduce_rope", dim3(blocks_for(items, 256)), dim3(256), 0, stream,
+                    (const float*)partials, p.splits, bias, y, M, (const long long*)rope->positions,
+                    rope->cos_table, rope->sin_table, rope->q_out, rope->pair, rope->query_heads, rope->kv_heads, D,
+                    rope->capacity, rope->slot0, rope->zero_prefix);
+    return launch("aoto_rope_qkv_prefill", dim3(blocks_for(items, 256)), dim3(256), 0, stream, (const void*)y,
+                  (const long long*)rope->positions, rope->cos_table, rope->sin_table, rope->q_out, rope->pair, 1, M,
+                  rope->query_heads, rope->kv_heads, D, rope->capacity, rope->slot0, rope->zero_prefix);
+  }
   if (!split) return AOTO_OK;
   return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
                 (const float*)partials, p.splits, bias, residual, gate, y, M, N);
+}
+
+// The packed q/k/v projection (+ bias) with its RoPE and the layer's cache fill.
+int qkv_rope_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
+                  int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
+                  const void* cos_table, const void* sin_table, void* q_out, void* pair, int query_heads,
+                  int kv_heads, int head_dim, int capacity, int slot0, int zero_prefix, void* stream) {
+  const char* what = bits == 4 ? "w4_gemm_qkv_rope" : "w8_gemm_qkv_rope";
+  if (!positions || !cos_table || !sin_table || !q_out || !pair) return fail(AOTO_ERR_ARGUMENT, "%s: null pointer", what);
+  if (query_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0)
+    return fail(AOTO_ERR_ARGUMENT, "%s: bad heads (Hq=%d Hkv=%d D=%d)", what, query_heads, kv_heads, head_dim);
+  if (M <= 0 || slot0 < 0 || slot0 + M > capacity)
+    return fail(AOTO_ERR_ARGUMENT, "%s: slots [%d, %d) exceed capacity %d", what, slot0, slot0 + M, capacity);
+  if (!aligned8(q_out) || !aligned8(pair) || !aligned8(cos_table) || !aligned8(sin_table) || (bias && !aligned8(bias)))
+    return fail(AOTO_ERR_ARGUMENT, "%s: q_out, pair, tables and bias must be 8-byte aligned", what);
+  if (y == q_out || y == pair || y == x) return fail(AOTO_ERR_ARGUMENT, "%s: y must not alias x, q_out or pair", what);
+  const RopeFill rope{positions, cos_table, sin_table, q_out, pair, query_heads, kv_heads, head_dim, capacity, slot0,
+                      zero_prefix};
+  const int N = (query_heads + 2 * kv_heads) * head_dim;
+  return packed_gemm(bits, x, words, scales, bias, nullptr, nullptr, y, M, N, K, group, tile, splits, workspace,
+                     stream, nullptr, nullptr, nullptr, 0.f, nullptr, &rope);
 }
 
 // GEMM with a residual epilogue followed by the row RMSNorm of its result.
@@ -621,6 +668,22 @@ int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const vo
                                    const void* norm_weight, float eps, void* norm_out, void* stream) {
   return residual_norm_gemm(8, x, words, scales, residual, y, M, N, K, group, tile, splits, workspace,
                             norm_weight, eps, norm_out, stream);
+}
+
+int aoto_hip_w4_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
+                              int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
+                              const void* cos_table, const void* sin_table, void* q_out, void* pair, int query_heads,
+                              int kv_heads, int head_dim, int capacity, int slot0, int zero_prefix, void* stream) {
+  return qkv_rope_gemm(4, x, words, scales, bias, y, M, K, group, tile, splits, workspace, positions, cos_table,
+                       sin_table, q_out, pair, query_heads, kv_heads, head_dim, capacity, slot0, zero_prefix, stream);
+}
+
+int aoto_hip_w8_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
+                              int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
+                              const void* cos_table, const void* sin_table, void* q_out, void* pair, int query_heads,
+                              int kv_heads, int head_dim, int capacity, int slot0, int zero_prefix, void* stream) {
+  return qkv_rope_gemm(8, x, words, scales, bias, y, M, K, group, tile, splits, workspace, positions, cos_table,
+                       sin_table, q_out, pair, query_heads, kv_heads, head_dim, capacity, slot0, zero_prefix, stream);
 }
 
 int aoto_hip_w8_quantize(const void* weight, int weight_is_f32, int rows, int inner, int group,

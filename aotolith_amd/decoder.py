@@ -866,10 +866,12 @@ class _Engine:
         for index, layer in enumerate(layers):
             if index == 0 or not fuse:
                 ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
-            self._matmul(xn, layer.qkv, bias=layer.qkv_bias, out=qkv.view(m, -1))
             pair = pair_of(index)
-            ops.rope_qkv_prefill(qkv, positions.reshape(1, -1), self.cos, self.sin, pair, query_heads=s.heads,
-                                 kv_heads=s.kv_heads, head_dim=s.head_dim, slot0=slot0, zero_prefix=True, q_out=q)
+            # q/k/v projection, RoPE and the cache fill (one launch fewer when the plan splits K)
+            ops.matmul_qkv_rope(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, positions.reshape(-1),
+                                self.cos, self.sin, pair, query_heads=s.heads, kv_heads=s.kv_heads,
+                                head_dim=s.head_dim, slot0=slot0, bias=layer.qkv_bias, bits=layer.qkv.bits,
+                                out=qkv.view(m, -1), q_out=q)
             keys = pair[0][:, :, slot0:slot0 + m]
             values = pair[1][:, :, slot0:slot0 + m]
             if mask is not None:

@@ -534,6 +534,83 @@ def rope_qkv_prefill(
     return q_out
 
 
+def matmul_qkv_rope(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    positions: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    pair: torch.Tensor,
+    *,
+    query_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    slot0: int,
+    bias: torch.Tensor | None = None,
+    zero_prefix: bool = True,
+    bits: int = 4,
+    out: torch.Tensor | None = None,
+    q_out: torch.Tensor | None = None,
+    tile: int = 0,
+    splits: int = 0,
+    workspace: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The packed q/k/v projection ``out = bf16(x @ W^T + bias)`` ``[M, W]`` with RoPE of q into
+    ``q_out [1, Hq, M, D]`` and the rotated keys / values into ``pair [2, 1, Hkv, cap, D]`` at
+    ``slot0``: :func:`w4_matmul` then :func:`rope_qkv_prefill` (batch 1), one launch fewer when
+    the plan splits K. Returns ``(out, q_out)``."""
+
+    per_word = CODES_PER_WORD[bits]
+    _expect(packed, "packed", torch.int32)
+    if packed.dim() != 2:
+        raise ValueError(f"packed must be 2-D [N, K/{per_word}]")
+    n, words = packed.shape
+    k = words * per_word
+    if n != (query_heads + 2 * kv_heads) * head_dim:
+        raise ValueError("the projection's rows do not match the head counts")
+    _expect(x, "x", BF16)
+    if x.shape[-1] != k:
+        raise ValueError(f"x has last dimension {x.shape[-1]}, the weight reduces over {k}")
+    m = x.numel() // k
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"group size {group_size} does not divide K={k}")
+    _expect(scales, "scales", BF16, (n, k // group_size))
+    if bias is not None:
+        _expect(bias, "bias", BF16, (n,))
+    _i64(positions, "positions")
+    if positions.numel() != m:
+        raise ValueError("positions must hold one entry per row of x")
+    _expect(pair, "pair", BF16)
+    if pair.dim() != 5 or tuple(pair.shape[:3]) != (2, 1, kv_heads) or pair.shape[4] != head_dim \
+            or not pair.is_contiguous():
+        raise ValueError(f"pair must be a contiguous [2, 1, {kv_heads}, cap, {head_dim}], got {tuple(pair.shape)}")
+    capacity = pair.shape[3]
+    if out is None:
+        out = torch.empty((m, n), dtype=BF16, device=x.device)
+    elif out.numel() != m * n:
+        raise ValueError(f"out has {out.numel()} elements, expected {m * n}")
+    if q_out is None:
+        q_out = torch.empty((1, query_heads, m, head_dim), dtype=BF16, device=x.device)
+    else:
+        _expect(q_out, "q_out", BF16, (1, query_heads, m, head_dim))
+    _ready(x)
+    need = gemm_workspace_bytes(m, n, k, tile, splits)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
+    lib = _lib.library()
+    entry = lib.aoto_hip_w4_gemm_qkv_rope if bits == 4 else lib.aoto_hip_w8_gemm_qkv_rope
+    _lib.check(
+        entry(
+            _ptr(x), _ptr(packed), _ptr(scales), _ptr(bias), _ptr(out), m, k, group_size, int(tile), int(splits),
+            _ptr(workspace if need else None), _ptr(positions), _ptr(cos_table), _ptr(sin_table), _ptr(q_out),
+            _ptr(pair), query_heads, kv_heads, head_dim, capacity, int(slot0), int(bool(zero_prefix)), _stream(),
+        )
+    )
+    return out, q_out
+
+
 def rope_kv_cache_append(
     row: torch.Tensor,
     cos_table: torch.Tensor,

@@ -304,19 +304,14 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
     act = torch.randn((m, i), generator=gen, device=dev).to(bf16)
     positions = torch.arange(m, dtype=torch.int64, device=dev)[None, :]
     slot0 = eng.capacity - m
-    matmul = ops.w4_matmul if eng.state.bits == 4 else ops.w8_matmul
     gate_up = ops.w4_matmul_gate_up if eng.state.bits == 4 else ops.w8_matmul_gate_up
 
-    def qkv_proj():
-        for layer in layers:
-            matmul(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, bias=layer.qkv_bias,
-                   out=qkv.view(m, -1))
-
-    def rope():
-        for index in range(n):
-            ops.rope_qkv_prefill(qkv, positions, eng.cos, eng.sin, eng.ring[index], query_heads=spec.heads,
-                                 kv_heads=spec.kv_heads, head_dim=spec.head_dim, slot0=slot0, zero_prefix=True,
-                                 q_out=q)
+    def qkv_rope():
+        for index, layer in enumerate(layers):
+            ops.matmul_qkv_rope(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, positions.reshape(-1),
+                                eng.cos, eng.sin, eng.ring[index], query_heads=spec.heads, kv_heads=spec.kv_heads,
+                                head_dim=spec.head_dim, slot0=slot0, bias=layer.qkv_bias, bits=layer.qkv.bits,
+                                out=qkv.view(m, -1), q_out=q)
 
     def attention():
         for index in range(n):
@@ -341,10 +336,9 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
 
     gemm = f"aoto_w{eng.state.bits}_gemm"
     rows = [
-        _row("qkv", f"{gemm} + bias (with its split-K reduce when split)", _graph_us(torch, qkv_proj, n),
+        _row("qkv_rope", f"{gemm} + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: "
+             "aoto_rope_qkv_prefill after the GEMM)", _graph_us(torch, qkv_rope, n),
              flops=2.0 * m * spec.qkv_width * h),
-        _row("rope", "aoto_rope_qkv_prefill (RoPE of q/k, q head-major, cache fill)", _graph_us(torch, rope, n),
-             nbytes=m * spec.qkv_width * 2 + m * (spec.qkv_width) * 2),
         _row("attention", f"aoto_flash_attention_d{spec.head_dim} (causal)", _graph_us(torch, attention, n),
              flops=4.0 * m * m * spec.head_dim * spec.heads / 2),
         _row("o_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, o_norm, n),

@@ -497,3 +497,54 @@ def test_matmul_residual_norm_rejects_wide_rows_and_aliasing():
     res = to_gpu_bf16(bf16_normal(rng, (4, 512)))
     with pytest.raises(Exception, match="alias"):
         ops.matmul_residual_norm(x, gp, gs, 64, res, to_gpu_bf16(bf16_normal(rng, (512,))), 1e-6, norm_out=res)
+
+
+# ---------------------------------------------------------------- q/k/v projection + RoPE + cache fill
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m,hq,hkv,dim,k,splits,bias,slot0", [
+    (128, 14, 2, 64, 896, 0, True, 64),    # Qwen prefill: the auto plan splits K 7 ways
+    (128, 14, 2, 64, 896, 1, True, 0),     # the same unsplit (GEMM, then the RoPE kernel)
+    (40, 8, 2, 128, 512, 3, False, 9),     # head_dim 128, no bias, ragged M, forced split
+])
+def test_matmul_qkv_rope_equals_matmul_then_rope(m, hq, hkv, dim, k, splits, bias, slot0, bits):
+    """The fused q/k/v projection + RoPE + cache fill gives the projection of w4_matmul bit for bit,
+    and q / keys / values within one bf16 rounding of rope_qkv_prefill over it (and of the oracle)."""
+
+    from oracle.quant import pack_weight_bits_bf16
+
+    ops = _ops()
+    rng = np.random.default_rng(m + dim + splits + bits)
+    n = (hq + 2 * hkv) * dim
+    packed, scales = pack_weight_bits_bf16(bf16_normal(rng, (n, k), 0.02), 64, bits)
+    gp, gs = _gpu_packed(packed, scales)
+    x = bf16_normal(rng, (m, k))
+    b = bf16_normal(rng, (n,), 0.02) if bias else None
+    cap = slot0 + m + 5
+    cos, sin = oracle.rope_tables(cap, dim, 1e6)
+    positions = rng.integers(0, cap, m)
+    gx, gb = to_gpu_bf16(x), (to_gpu_bf16(b) if bias else None)
+    gcos, gsin = to_gpu_bf16(cos), to_gpu_bf16(sin)
+    gpos = torch.from_numpy(positions).cuda()
+    matmul = ops.w4_matmul if bits == 4 else ops.w8_matmul
+    y_ref = matmul(gx, gp, gs, 64, bias=gb, splits=splits)
+    pair_ref = torch.full((2, 1, hkv, cap, dim), 7.0, dtype=torch.bfloat16, device="cuda")
+    q_ref = ops.rope_qkv_prefill(y_ref.view(1, m, n), gpos.view(1, m), gcos, gsin, pair_ref, query_heads=hq,
+                                 kv_heads=hkv, head_dim=dim, slot0=slot0, zero_prefix=True)
+    pair = torch.full((2, 1, hkv, cap, dim), 7.0, dtype=torch.bfloat16, device="cuda")
+    y, q = ops.matmul_qkv_rope(gx, gp, gs, 64, gpos, gcos, gsin, pair, query_heads=hq, kv_heads=hkv, head_dim=dim,
+                               slot0=slot0, bias=gb, bits=bits, splits=splits)
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert_bf16_parity(from_gpu_bf16(q), from_gpu_bf16(q_ref), max_ulp=1.0)
+    assert_bf16_parity(from_gpu_bf16(pair), from_gpu_bf16(pair_ref), max_ulp=1.0)
+    got_pair = from_gpu_bf16(pair)
+    assert np.all(got_pair[:, :, :, :slot0] == 0.0), "slots below slot0 are zeroed"
+    assert np.all(got_pair[:, :, :, slot0 + m:] == 7.0), "slots past the prompt are untouched"
+    # against the oracle: the projection within one rounding of the oracle's, and RoPE of the
+    # projection the GPU stored within one rounding of the oracle's RoPE of it
+    assert_bf16_parity(from_gpu_bf16(y), oracle.w4_matmul(x, packed, scales, 64, bias=b, bits=bits), max_ulp=1.0)
+    heads = from_gpu_bf16(y).reshape(m, hq + 2 * hkv, dim).transpose(1, 0, 2)[None]
+    c, s_ = cos[positions][None, None], sin[positions][None, None]
+    assert_bf16_parity(from_gpu_bf16(q), oracle.rope(heads[:, :hq], c, s_), max_ulp=1.0)
+    assert_bf16_parity(got_pair[0, :, :, slot0:slot0 + m], oracle.rope(heads[:, hq:hq + hkv], c, s_), max_ulp=1.0)
+    np.testing.assert_array_equal(got_pair[1, :, :, slot0:slot0 + m], from_gpu_bf16(y).reshape(
+        m, hq + 2 * hkv, dim).transpose(1, 0, 2)[None, hq + hkv:])
