@@ -33,6 +33,8 @@ _p = ctypes.c_void_p
 #: Every exported entry point with its argument types, in header order.
 SIGNATURES: dict[str, tuple] = {
     "aoto_hip_abi_version": (),
+    "aoto_hip_trace_launches": (_c_int,),
+    "aoto_hip_take_launches": (ctypes.c_char_p, _c_size),
     "aoto_hip_last_error": (ctypes.c_char_p, _c_size),
     "aoto_hip_load_code_object": (_p, _c_size),
     "aoto_hip_unload_code_object": (),
@@ -109,8 +111,8 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 #: Entry points returning a size rather than a status.
-SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_decode_attention_workspace", "aoto_hip_w4_gemm_workspace",
-                  "aoto_hip_w4_gemm_gate_up_workspace", "aoto_hip_w4_gemv_argmax_keys"}
+SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_take_launches", "aoto_hip_decode_attention_workspace",
+                  "aoto_hip_w4_gemm_workspace", "aoto_hip_w4_gemm_gate_up_workspace", "aoto_hip_w4_gemv_argmax_keys"}
 
 
 class HipBackendUnavailable(RuntimeError):

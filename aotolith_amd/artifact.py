@@ -19,7 +19,8 @@ Counterpart of the reference's ``artifact.py`` (``save_compiled`` /
   Metal kernels from the stored graph, artifact.py:367-384), the profile records
   ``architecture = "gfx950"`` and the loader refuses any other architecture, the
   ABI is the C ABI of ``include/aoto_hip.h`` the code object's kernels were
-  built against, and ``FORMAT_VERSION`` is 6 (the reference's is 5).
+  built against, and ``FORMAT_VERSION`` is 7 (the reference's is 5; 7: selections name the
+  exact kernel symbols each node launches).
 
 A static-cache runtime saves as the reference's does (models/decoder.py:953-958):
 ``prefix.prefill.aoto`` and ``prefix.decode.aoto``, each a complete artifact of
@@ -52,8 +53,8 @@ from .plan import ARCHITECTURE, TARGET
 from .selection import KernelBenchmark, KernelSelection
 
 ARTIFACT_FORMAT = "aotolith"
-FORMAT_VERSION = 6
-_SUPPORTED_FORMAT_VERSIONS = (6,)
+FORMAT_VERSION = 7
+_SUPPORTED_FORMAT_VERSIONS = (7,)
 KINDS = ("prefill", "decode", "graph")
 CODE_OBJECT_ENTRY = "code/gfx950.hsaco"
 _ZIP_TIMESTAMP = (1980, 1, 1, 0, 0, 0)

@@ -86,6 +86,11 @@ int lookup(const char* name, hipFunction_t* fn) {
   return AOTO_OK;
 }
 
+// Kernel symbols launched by this thread while recording is on (aoto_hip_trace_launches),
+// newline-separated, for plans that name the kernels they run.
+thread_local bool g_trace = false;
+thread_local std::string g_trace_names;
+
 template <typename... Args>
 int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* stream, Args... args) {
   hipFunction_t fn = nullptr;
@@ -94,6 +99,10 @@ int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* strea
   hipError_t err = hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z, shared,
                                          static_cast<hipStream_t>(stream), params, nullptr);
   if (err != hipSuccess) return fail(AOTO_ERR_HIP, "launch %s: %s", name, hipGetErrorString(err));
+  if (g_trace) {
+    g_trace_names += name;
+    g_trace_names += '\n';
+  }
   return AOTO_OK;
 }
 
@@ -289,6 +298,24 @@ void decode_split(int head_dim, int capacity, int requested, long long rows, int
 extern "C" {
 
 int aoto_hip_abi_version(void) { return AOTO_HIP_ABI_VERSION; }
+
+int aoto_hip_trace_launches(int enable) {
+  const int previous = g_trace ? 1 : 0;
+  g_trace = enable != 0;
+  if (g_trace && !previous) g_trace_names.clear();
+  return previous;
+}
+
+size_t aoto_hip_take_launches(char* buf, size_t size) {
+  const size_t n = g_trace_names.size();
+  if (buf != nullptr && size > 0) {
+    const size_t copied = n < size - 1 ? n : size - 1;
+    memcpy(buf, g_trace_names.data(), copied);
+    buf[copied] = '\0';
+    if (copied == n) g_trace_names.clear();
+  }
+  return n;
+}
 
 size_t aoto_hip_last_error(char* buf, size_t size) {
   if (buf != nullptr && size > 0) {

@@ -426,10 +426,6 @@ def _sel(index: int, op: str, output: str, kind: str, reason: str, artifact: str
     )
 
 
-def _gemv_symbol(norm: bool, paired: bool, bias: bool, bits: int = 4) -> str:
-    return f"aoto_w{bits}_gemv_n{int(norm)}_p{int(paired)}_b{int(bias)}"
-
-
 def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
     problems = []
     if spec.head_dim not in (64, 128):
@@ -450,38 +446,6 @@ def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
             f"{TARGET} cannot compile this decoder: " + "; ".join(problems),
             hint="every node must run as a gfx950 kernel; there is no fallback",
         )
-
-
-def decode_selections(spec: DecoderSpec, bits: int = 4) -> tuple[KernelSelection, ...]:
-    """The decode plan's nodes after the reference's fusions (passes/fusion.py, passes/cache.py)."""
-
-    w, kind = f"W{bits}", f"w{bits}_gemv"
-    out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather by device token", "aoto_embedding")]
-    g = spec.heads // spec.kv_heads
-    for layer in range(spec.layers):
-        base = len(out)
-        out += [
-            _sel(base, "addmm", f"qkv_{layer}", kind,
-                 f"packed {w} GEMV (M=1) with RMSNorm prologue"
-                 + (" and q/k/v bias epilogue" if spec.qkv_bias else ""),
-                 _gemv_symbol(True, False, spec.qkv_bias, bits)),
-            _sel(base + 1, "rope_kv_cache_append", f"query_{layer}", "rope_kv_append",
-                 "rotates q/k and appends (k, v) to the layer's cache window", "aoto_rope_kv_append"),
-            _sel(base + 2, "attention", f"attention_{layer}", "decode_attention",
-                 f"single-query GQA ({g} query heads per kv head), one block per query head, split-K merge "
-                 "for long windows", f"aoto_decode_attention_d{spec.head_dim}"),
-            _sel(base + 3, "addmm", f"hidden_{layer}a", kind, f"packed {w} GEMV with residual epilogue",
-                 _gemv_symbol(False, False, True, bits)),
-            _sel(base + 4, "matmul", f"mlp_{layer}", kind,
-                 f"paired gate/up {w} GEMV with RMSNorm prologue and silu_mul_paired epilogue",
-                 _gemv_symbol(True, True, False, bits)),
-            _sel(base + 5, "addmm", f"hidden_{layer}b", kind, f"packed {w} GEMV with residual epilogue",
-                 _gemv_symbol(False, False, True, bits)),
-        ]
-    n = len(out)
-    out.append(_sel(n, "matmul", "logits", kind, f"LM-head {w} GEMV with final RMSNorm prologue",
-                    _gemv_symbol(True, False, False, bits)))
-    return tuple(out)
 
 
 def _prefill_pairs_gate_up(tokens: int, spec: DecoderSpec) -> bool:
@@ -507,49 +471,49 @@ def _prefill_fuses_norms(spec: DecoderSpec) -> bool:
     return spec.hidden % 8 == 0 and spec.hidden <= 4096
 
 
-def _norm_selection(index, node, tokens, spec, after, bits):
-    """The norm node after the residual projection ``after`` (its [N, K]): one
-    launch with the projection's split-K sum when its plan splits."""
+class _LaunchRecorder:
+    """Node-by-node record of the kernels one pass of a sequence launches.
 
-    if after is not None and _prefill_fuses_norms(spec) and ops.gemm_workspace_bytes(tokens, *after) > 0:
-        return _sel(index, "rms_norm", node, "rms_norm",
-                    "row RMSNorm fused with the preceding projection's split-K sum and residual",
-                    "aoto_w4_gemm_reduce_norm")
-    return _sel(index, "rms_norm", node, "rms_norm", "row RMSNorm", "aoto_rms_norm")
+    ``node(...)`` opens a node; the kernel symbols the C ABI reports launched
+    until the next node (``ops.take_launches``) are that node's. Each launched
+    kernel becomes one ``KernelSelection`` whose ``artifact_name`` is the exact
+    symbol (the reference's selection names the kernel the node emitted,
+    ``selection.py:19-34``); a node that launches two kernels (a split-K GEMM and
+    its sum) gives two records, the second with output id ``<node>.1``.
+    """
+
+    def __init__(self, take) -> None:
+        self._take = take
+        self._open: tuple[str, str, str, str] | None = None
+        self.nodes: list[tuple[str, str, str, str, list[str]]] = []
+        take()  # drop anything recorded before the first node
+
+    def node(self, op: str, output: str, kind: str, reason: str) -> None:
+        self._close()
+        self._open = (op, output, kind, reason)
+
+    def _close(self) -> None:
+        names = self._take()
+        if self._open is not None:
+            self.nodes.append((*self._open, names))
+        elif names:
+            raise CompilationError(f"kernels launched outside a plan node: {names}")
+        self._open = None
+
+    def selections(self) -> tuple[KernelSelection, ...]:
+        self._close()
+        out: list[KernelSelection] = []
+        for op, output, kind, reason, names in self.nodes:
+            if not names:
+                raise CompilationError(f"plan node {output} ({op}) launched no kernel")
+            for index, name in enumerate(names):
+                out.append(_sel(len(out), op, output if index == 0 else f"{output}.{index}", kind, reason, name))
+        return tuple(out)
 
 
-def prefill_selections(spec: DecoderSpec, bits: int = 4, tokens: int = 128) -> tuple[KernelSelection, ...]:
-    w, kind, gemm = f"W{bits}", f"w{bits}_gemm", f"aoto_w{bits}_gemm"
-    out = [_sel(0, "embedding", "hidden_0", "gather", "bf16 embedding row gather", "aoto_embedding")]
-    for layer in range(spec.layers):
-        base = len(out)
-        out += [
-            _norm_selection(base, f"norm_{layer}a", tokens, spec,
-                            (spec.hidden, spec.intermediate) if layer else None, bits),
-            _sel(base + 1, "addmm" if spec.qkv_bias else "matmul", f"qkv_{layer}", kind,
-                 f"fused-dequant {w} GEMM on bf16 MFMA" + (" with q/k/v bias epilogue" if spec.qkv_bias else ""),
-                 gemm),
-            _sel(base + 2, "rope", f"rope_{layer}", "rope_qkv_prefill",
-                 "RoPE of q and k fused with the layer's cache fill", "aoto_rope_qkv_prefill"),
-            _sel(base + 3, "attention", f"attention_{layer}", "flash_attention",
-                 "causal + left-pad masked GQA flash attention on MFMA",
-                 f"aoto_flash_attention_d{spec.head_dim}"),
-            _sel(base + 4, "addmm", f"hidden_{layer}a", kind, f"{w} GEMM with residual epilogue", gemm),
-            _norm_selection(base + 5, f"norm_{layer}b", tokens, spec, (spec.hidden, spec.attention_width), bits),
-        ]
-        if _prefill_pairs_gate_up(tokens, spec):
-            out.append(_sel(base + 6, "matmul", f"mlp_{layer}", kind,
-                            f"paired gate/up {w} GEMM (one pass over x) with silu_mul epilogue",
-                            f"aoto_w{bits}_gemm_gate_up"))
-        else:
-            out += [_sel(base + 6, "matmul", f"gate_{layer}", kind, f"{w} GEMM", gemm),
-                    _sel(base + 7, "matmul", f"up_{layer}", kind, f"{w} GEMM with silu_mul epilogue", gemm)]
-        out.append(_sel(len(out), "addmm", f"hidden_{layer}b", kind, f"{w} GEMM with residual epilogue", gemm))
-    n = len(out)
-    out.append(_sel(n, "matmul", "logits", f"w{bits}_gemv",
-                    f"LM-head {w} GEMV on the last row with final RMSNorm prologue",
-                    _gemv_symbol(True, False, False, bits)))
-    return tuple(out)
+def _mark(rec: _LaunchRecorder | None, op: str, output: str, kind: str, reason: str) -> None:
+    if rec is not None:
+        rec.node(op, output, kind, reason)
 
 
 # ----------------------------------------------------------------------------- engine
@@ -645,16 +609,23 @@ class _Engine:
         matmul = ops.w4_matmul if w.bits == 4 else ops.w8_matmul
         return matmul(x, w.packed, w.scales, w.group, **kwargs)
 
-    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool, lm_head: bool = True):
+    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool, lm_head: bool = True, rec=None):
         """Run the per-layer decode kernels (and the LM head); ``hidden`` holds the embedded token."""
 
         s = self.spec
         qd, kd = s.heads * s.head_dim, s.kv_heads * s.head_dim
+        bits = self.state.bits
+        gemv = f"w{bits}_gemv"
         for index, layer in enumerate(self.state.layers):
+            _mark(rec, "addmm", f"qkv_{index}", gemv,
+                  f"packed W{bits} GEMV (M=1) with RMSNorm prologue" + (" and q/k/v bias epilogue" if s.qkv_bias else ""))
             self._gemv(self.hidden, layer.qkv, self.qkv, norm_weight=layer.input_norm, eps=s.eps,
                        bias=layer.qkv_bias)
             pair_out = cache_out[index]
             if ring:
+                _mark(rec, "attention", f"attention_{index}", "decode_attention",
+                      "ring step: RoPE of q/k, in-place KV write at the step's slot and single-query GQA attention "
+                      "(long windows split, then merged)")
                 ops.decode_rope_attention(self.qkv.view(1, -1), self.cos, self.sin, pair_out, query_heads=s.heads,
                                           query_start=0, key_start=qd, value_start=qd + kd,
                                           step_state=self.step_state, scale=self.scale, workspace=self.workspace,
@@ -663,28 +634,39 @@ class _Engine:
                                           out=self.attn)
             else:
                 position = valid - 1
+                _mark(rec, "rope_kv_cache_append", f"query_{index}", "rope_kv_append",
+                      "rotates q/k and appends (k, v) to the rolled cache window")
                 ops.rope_kv_cache_append(self.qkv.view(1, -1), self.cos, self.sin, position, pair_out,
                                          pair_in=cache_in[index], query_heads=s.heads, query_start=0,
                                          key_start=qd, value_start=qd + kd, q_out=self.q)
+                _mark(rec, "attention", f"attention_{index}", "decode_attention",
+                      f"single-query GQA ({s.heads // s.kv_heads} query heads per kv head) over the last "
+                      f"{valid} slots (long windows split, then merged)")
                 ops.decode_attention(self.q, pair_out[0], pair_out[1], valid=valid, scale=self.scale,
                                      workspace=self.workspace, splits=self.attention_splits, out=self.attn)
+            _mark(rec, "addmm", f"hidden_{index}a", gemv, f"packed W{bits} GEMV with residual epilogue")
             self._gemv(self.attn.view(-1), layer.o, self.hidden, bias=self.hidden)
+            _mark(rec, "matmul", f"mlp_{index}", gemv,
+                  f"paired gate/up W{bits} GEMV with RMSNorm prologue and silu_mul_paired epilogue")
             self._gemv(self.hidden, layer.gate, self.act, norm_weight=layer.post_norm, eps=s.eps,
                        up=(layer.up.packed, layer.up.scales))
+            _mark(rec, "addmm", f"hidden_{index}b", gemv, f"packed W{bits} GEMV with residual epilogue")
             self._gemv(self.act, layer.down, self.hidden, bias=self.hidden)
         if lm_head:
+            _mark(rec, "matmul", "logits", gemv, f"LM-head W{bits} GEMV with final RMSNorm prologue")
             self._gemv(self.hidden, self.state.lm_head, self.logits.view(-1), norm_weight=self.state.final_norm,
                        eps=s.eps)
 
-    def decode_functional(self, token: torch.Tensor, cache: torch.Tensor, valid: int):
+    def decode_functional(self, token: torch.Tensor, cache: torch.Tensor, valid: int, rec=None):
         """The reference decode plan: fresh logits and the rolled next cache."""
 
+        _mark(rec, "embedding", "hidden_0", "gather", "bf16 embedding row gather by device token")
         ops.embedding(self.state.embed, token.reshape(-1)[:1], out=self.hidden.view(1, -1))
         next_cache = torch.empty_like(cache)
-        self._decode_layers(cache, next_cache, valid=valid, ring=False)
+        self._decode_layers(cache, next_cache, valid=valid, ring=False, rec=rec)
         return self.logits.clone(), next_cache
 
-    def _ring_step(self) -> None:
+    def _ring_step(self, rec=None) -> None:
         """One captured-loop step: token -> logits -> token, cache/step state advanced on device.
 
         With the fused tail ``hidden`` must hold the token's embedding on entry
@@ -692,16 +674,24 @@ class _Engine:
         """
 
         if self.keys is None:
+            _mark(rec, "embedding", "hidden_0", "gather", "bf16 embedding row gather by device token")
             ops.embedding(self.state.embed, self.token, out=self.hidden.view(1, -1))
-            self._decode_layers(None, self.ring, ring=True)
+            self._decode_layers(None, self.ring, ring=True, rec=rec)
+            _mark(rec, "argmax", "token", "argmax", "first-index greedy argmax, appended to the token history")
             ops.argmax(self.logits.view(1, -1), out=self.token, history=self.history,
                        history_len=self.history_len)
+            _mark(rec, "step_advance", "step_state", "step_state", "advances {position, valid, ring offset, slot}")
             ops.step_advance(self.step_state, self.capacity)
             return
         head = self.state.lm_head
-        self._decode_layers(None, self.ring, ring=True, lm_head=False)
+        self._decode_layers(None, self.ring, ring=True, lm_head=False, rec=rec)
+        _mark(rec, "matmul", "logits", "w4_gemv",
+              "LM-head W4 GEMV with final RMSNorm prologue, writing per-wave greedy-argmax keys")
         ops.w4_gemv_argmax(self.hidden, head.packed, head.scales, head.group, self.keys,
                            norm_weight=self.state.final_norm, eps=self.spec.eps, out=self.logits.view(-1))
+        _mark(rec, "argmax", "token", "argmax",
+              "reduces the argmax keys to the token; appends it to the history, advances the step state, "
+              "copies the next position's RoPE rows and gathers the next token's embedding")
         ops.argmax_finish(self.keys, self.key_count, out=self.token, history=self.history,
                           history_len=self.history_len, step_state=self.step_state, capacity=self.capacity,
                           embedding=self.state.embed, hidden_out=self.hidden, rope_tables=(self.cos, self.sin),
@@ -843,7 +833,7 @@ class _Engine:
         return logits
 
     def prefill_into(self, ids: torch.Tensor, positions: torch.Tensor, pair_of, slot0: int, window: int, *,
-                     key_start: int, mask: torch.Tensor | None = None) -> torch.Tensor:
+                     key_start: int, mask: torch.Tensor | None = None, rec=None) -> torch.Tensor:
         """Run the prefill kernels; layer ``i``'s keys/values go to ``pair_of(i)`` at ``slot0``.
 
         Returns logits ``[1, 1, V]`` of the last token.
@@ -852,6 +842,8 @@ class _Engine:
         s = self.spec
         m = ids.numel()
         dev = self.device
+        bits = self.state.bits
+        gemm = f"w{bits}_gemm"
         x = torch.empty((m, s.hidden), dtype=BF16, device=dev)
         xn = torch.empty_like(x)
         qkv = torch.empty((1, m, s.qkv_width), dtype=BF16, device=dev)
@@ -860,13 +852,18 @@ class _Engine:
         act = torch.empty((m, s.intermediate), dtype=BF16, device=dev)
         paired = _prefill_pairs_gate_up(m, s)
         gate = None if paired else torch.empty_like(act)
+        _mark(rec, "embedding", "hidden_0", "gather", "bf16 embedding row gather")
         ops.embedding(self.state.embed, ids.reshape(-1), out=x)
         layers = self.state.layers
         fuse = _prefill_fuses_norms(s)
         for index, layer in enumerate(layers):
             if index == 0 or not fuse:
+                _mark(rec, "rms_norm", f"norm_{index}a", "rms_norm", "row RMSNorm")
                 ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
             pair = pair_of(index)
+            _mark(rec, "addmm" if s.qkv_bias else "matmul", f"qkv_{index}", gemm,
+                  f"fused-dequant W{bits} GEMM on bf16 MFMA" + (" with q/k/v bias" if s.qkv_bias else "")
+                  + ", RoPE of q/k and the layer's cache fill (with the split-K sum when the plan splits)")
             # q/k/v projection, RoPE and the cache fill (one launch fewer when the plan splits K)
             ops.matmul_qkv_rope(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, positions.reshape(-1),
                                 self.cos, self.sin, pair, query_heads=s.heads, kv_heads=s.kv_heads,
@@ -874,33 +871,98 @@ class _Engine:
                                 out=qkv.view(m, -1), q_out=q)
             keys = pair[0][:, :, slot0:slot0 + m]
             values = pair[1][:, :, slot0:slot0 + m]
+            _mark(rec, "attention", f"attention_{index}", "flash_attention",
+                  "masked GQA flash attention on MFMA" if mask is not None
+                  else "causal + left-pad masked GQA flash attention on MFMA")
             if mask is not None:
                 ops.prefill_attention(q, keys, values, mask=mask, scale=self.scale, out=attn)
             else:
                 ops.prefill_attention(q, keys, values, causal=True, key_start=key_start, scale=self.scale, out=attn)
             if fuse:
+                _mark(rec, "addmm", f"hidden_{index}a", gemm,
+                      f"W{bits} GEMM with residual epilogue, then the next RMSNorm (one launch with the split-K sum "
+                      "when the plan splits)")
                 ops.matmul_residual_norm(attn.view(m, -1), layer.o.packed, layer.o.scales, layer.o.group, x,
                                          layer.post_norm, s.eps, bits=layer.o.bits, out=x, norm_out=xn)
             else:
+                _mark(rec, "addmm", f"hidden_{index}a", gemm, f"W{bits} GEMM with residual epilogue")
                 self._matmul(attn.view(m, -1), layer.o, residual=x, out=x)
+                _mark(rec, "rms_norm", f"norm_{index}b", "rms_norm", "row RMSNorm")
                 ops.rms_norm(x, layer.post_norm, s.eps, out=xn)
             if paired:
+                _mark(rec, "matmul", f"mlp_{index}", gemm,
+                      f"paired gate/up W{bits} GEMM (one pass over x) with silu_mul epilogue")
                 gate_up = ops.w4_matmul_gate_up if layer.gate.bits == 4 else ops.w8_matmul_gate_up
                 gate_up(xn, layer.gate.packed, layer.gate.scales, layer.up.packed, layer.up.scales,
                         layer.gate.group, out=act)
             else:
+                _mark(rec, "matmul", f"gate_{index}", gemm, f"W{bits} GEMM")
                 self._matmul(xn, layer.gate, out=gate)
+                _mark(rec, "matmul", f"up_{index}", gemm, f"W{bits} GEMM with silu_mul epilogue")
                 self._matmul(xn, layer.up, gate=gate, out=act)
             if fuse and index + 1 < len(layers):
+                _mark(rec, "addmm", f"hidden_{index}b", gemm,
+                      f"W{bits} GEMM with residual epilogue, then the next layer's input RMSNorm (one launch with "
+                      "the split-K sum when the plan splits)")
                 # the next layer's input norm with this projection's split-K sum
                 ops.matmul_residual_norm(act, layer.down.packed, layer.down.scales, layer.down.group, x,
                                          layers[index + 1].input_norm, s.eps, bits=layer.down.bits, out=x,
                                          norm_out=xn)
             else:
+                _mark(rec, "addmm", f"hidden_{index}b", gemm, f"W{bits} GEMM with residual epilogue")
                 self._matmul(act, layer.down, residual=x, out=x)
         logits = torch.empty((1, 1, s.vocab), dtype=BF16, device=dev)
+        _mark(rec, "matmul", "logits", f"w{bits}_gemv",
+              f"LM-head W{bits} GEMV on the last row with final RMSNorm prologue")
         self._gemv(x[m - 1], self.state.lm_head, logits.view(-1), norm_weight=self.state.final_norm, eps=s.eps)
         return logits
+
+    # -- selections ---------------------------------------------------------------
+    def record_selections(self) -> dict[str, tuple[KernelSelection, ...]]:
+        """The kernels each plan launches, node by node, from one real pass of each sequence.
+
+        Run at compile time on placeholder inputs (the reference's selections are
+        likewise made when the plan is built): the functional prefill of a zero
+        prompt, one functional decode step, and the greedy loop's first-token
+        argmax and one ring step. The loop's buffers are left for the first
+        ``greedy_generate`` to initialize, as a warm-up pass does.
+        """
+
+        s = self.spec
+        dev = self.device
+        out = {}
+        with ops.recording_launches() as take:
+            ids = torch.zeros((1, self.prompt_length), dtype=torch.int64, device=dev)
+            positions = torch.arange(self.prompt_length, dtype=torch.int64, device=dev)[None, :]
+            compact = torch.empty((s.layers, 2, 1, s.kv_heads, self.prompt_length, s.head_dim), dtype=BF16,
+                                  device=dev)
+            rec = _LaunchRecorder(take)
+            logits = self.prefill_into(ids, positions, lambda i: compact[i], 0, self.prompt_length, key_start=0,
+                                       rec=rec)
+            out["prefill"] = rec.selections()
+            del compact
+            rec = _LaunchRecorder(take)
+            cache = torch.zeros((s.layers, 2, 1, s.kv_heads, self.capacity, s.head_dim), dtype=BF16, device=dev)
+            valid = min(self.prompt_length + 1, self.capacity)
+            self.decode_functional(torch.zeros((1,), dtype=torch.int64, device=dev), cache, valid, rec=rec)
+            out["decode"] = rec.selections()
+            del cache
+            rec = _LaunchRecorder(take)
+            self.history_len.zero_()
+            _mark(rec, "argmax", "first_token", "argmax",
+                  "first-index greedy argmax of the prefill logits, the first entry of the token history")
+            ops.argmax(logits.view(1, -1), out=self.token, history=self.history, history_len=self.history_len)
+            self.token.zero_()
+            self.step_state.copy_(torch.tensor([0, 1, 1 % self.capacity, 0], dtype=torch.int32))
+            if self.keys is not None:
+                _mark(rec, "embedding", "hidden_0", "gather",
+                      "the first token's embedding row, gathered once when the loop starts (each step's finish "
+                      "gathers the next one)")
+            self._enter_loop(0)
+            self._ring_step(rec=rec)
+            out["decode_loop"] = rec.selections()
+        torch.cuda.synchronize()
+        return out
 
 
 # ----------------------------------------------------------------------------- runtime
@@ -950,6 +1012,8 @@ class DecoderStaticCacheRuntime:
     engine: _Engine
     group_size: int
     quantize_bits: int = 4
+    #: the greedy loop's plan (first-token argmax + one ring step), set at compile time
+    decode_loop: CompiledPlan | None = None
 
     # -- reference API -----------------------------------------------------------
     def prefill_ids(self, input_ids):
@@ -1124,17 +1188,15 @@ def _build_plans(spec: DecoderSpec, engine: _Engine, prompt_length: int):
             raise PlanInputError(f"expected a bf16 device cache of shape {expected}, got {tuple(cache.shape)}")
         return engine.decode_functional(token, cache.contiguous(), int(valid_length))
 
-    bits = engine.state.bits
-    p_sel = prefill_selections(spec, bits, prompt_length)
-    d_sel = decode_selections(spec, bits)
-    require_native(p_sel, "prefill plan")
-    require_native(d_sel, "decode plan")
-    prefill = CompiledPlan("prefill", tuple(PlanNode(s) for s in p_sel), run_prefill,
+    recorded = engine.record_selections()
+    for name, selections in recorded.items():
+        require_native(selections, f"{name} plan")
+    prefill = CompiledPlan("prefill", tuple(PlanNode(s) for s in recorded["prefill"]), run_prefill,
                            input_names=("input_ids", "positions", "attention_mask"),
                            output_names=("logits", "cache"))
-    decode = CompiledPlan("decode", tuple(PlanNode(s) for s in d_sel), run_decode,
+    decode = CompiledPlan("decode", tuple(PlanNode(s) for s in recorded["decode"]), run_decode,
                           input_names=("input_ids", "cache", "valid_length"), output_names=("logits", "cache"))
-    return prefill, decode
+    return prefill, decode, recorded["decode_loop"]
 
 
 def _check_target(target: str) -> None:
@@ -1172,15 +1234,21 @@ def compile_decoder_state(
     if any(w.group != group_size for w in state.weights):
         raise CompilationError(f"the state's packed weights are not all grouped by {group_size}")
     engine = _Engine(spec, state, prompt_length, capacity, _device(), attention_splits)
-    prefill, decode = _build_plans(spec, engine, prompt_length)
+    prefill, decode, loop_selections = _build_plans(spec, engine, prompt_length)
     runtime = DecoderStaticCacheRuntime(
         prefill=prefill, decode=decode, prompt_length=prompt_length, max_new_tokens=max_new_tokens,
         cache_capacity=capacity, num_layers=spec.layers, num_key_value_heads=spec.kv_heads,
         head_dim=spec.head_dim, family=spec.family, memory=memory, spec=spec, engine=engine,
         group_size=group_size, quantize_bits=bits,
     )
+    # The greedy loop's own plan: the first token's argmax over the prefill logits and
+    # one device-driven ring step (replayed per token); its run is greedy_generate.
+    loop = CompiledPlan("decode_loop", tuple(PlanNode(s) for s in loop_selections), runtime.greedy_generate,
+                        input_names=("input_ids",), output_names=("tokens",))
+    object.__setattr__(runtime, "decode_loop", loop)
     prefill.runtime = runtime
     decode.runtime = runtime
+    loop.runtime = runtime
     return runtime
 
 

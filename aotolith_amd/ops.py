@@ -8,6 +8,7 @@ current stream. No function here computes anything on the CPU.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -44,6 +45,33 @@ def _ready(tensor: torch.Tensor) -> None:
 
 #: codes per packed int32 word of each width
 CODES_PER_WORD = {4: 8, 8: 4}
+
+
+def take_launches() -> list[str]:
+    """Kernel symbols this thread launched since the last call, while :func:`recording_launches`
+    is active (``aoto_hip_take_launches``)."""
+
+    lib = _lib.library()
+    size = int(lib.aoto_hip_take_launches(None, 0))
+    if size == 0:
+        return []
+    buf = ctypes.create_string_buffer(size + 1)
+    lib.aoto_hip_take_launches(buf, size + 1)
+    return buf.value.decode().split()
+
+
+@contextlib.contextmanager
+def recording_launches():
+    """Record the kernel symbols this thread launches (read them with :func:`take_launches`)."""
+
+    lib = _lib.library()
+    previous = int(lib.aoto_hip_trace_launches(1))
+    try:
+        yield take_launches
+    finally:
+        if not previous:
+            take_launches()
+        lib.aoto_hip_trace_launches(previous)
 
 
 def _quantize(weight: torch.Tensor, group_size: int, bits: int) -> tuple[torch.Tensor, torch.Tensor]:

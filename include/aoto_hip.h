@@ -35,10 +35,21 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 14
+#define AOTO_HIP_ABI_VERSION 15
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
+
+/* Record the kernel symbols this host thread launches (the counterpart of the
+ * reference's KernelSelection.artifact_name, selection.py:19-34, which names the
+ * kernel each node emitted): enable != 0 starts recording (clearing the record),
+ * 0 stops. Returns the previous state. */
+int aoto_hip_trace_launches(int enable);
+
+/* Copy the recorded symbols, newline-separated, into buf (NUL-terminated) and
+ * clear the record when they fit; returns the record's length in bytes (call with
+ * size 0 to size the buffer). */
+size_t aoto_hip_take_launches(char* buf, size_t size);
 
 /* Copy the calling thread's last error message into buf (NUL-terminated,
  * truncated to size). Returns the full message length. */

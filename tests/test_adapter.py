@@ -81,18 +81,6 @@ def test_kernel_limits_are_checked_at_compile_time():
         _check_kernel_limits(good, 48)
 
 
-def test_selections_cover_every_node_natively():
-    from aotolith_amd.decoder import DecoderSpec, decode_selections, prefill_selections
-
-    spec = DecoderSpec("llama", 128256, 4096, 14336, 2, 32, 8, 128, 1e-5, 5e5, False)
-    dec = decode_selections(spec)
-    pre = prefill_selections(spec)
-    assert all(s.is_native for s in dec + pre)
-    assert [s.op_index for s in dec] == list(range(len(dec)))
-    assert sum(s.kind == "decode_attention" for s in dec) == 2
-    assert "aoto_decode_attention_d128" in {s.artifact_name for s in dec}
-
-
 def test_no_gpu_means_a_device_error():
     from aotolith_amd.decoder import DecoderSpec, random_state
     from aotolith_amd.errors import DeviceError

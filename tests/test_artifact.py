@@ -18,8 +18,9 @@ import pytest
 import torch
 
 from aotolith_amd import artifact
-from aotolith_amd.decoder import DecoderSpec, DecoderState, LayerState, PackedWeight, decode_selections
+from aotolith_amd.decoder import DecoderSpec, DecoderState, LayerState, PackedWeight
 from aotolith_amd.errors import ArtifactCompatibilityError
+from aotolith_amd.selection import KernelSelection
 
 SPEC = DecoderSpec(family="qwen2", vocab=96, hidden=64, intermediate=128, layers=2, heads=4, kv_heads=2,
                    head_dim=16, eps=1e-6, theta=1e6, qkv_bias=True)
@@ -27,6 +28,16 @@ GROUP = 32
 PROFILE = {"device_name": "AMD Instinct MI355X", "architecture": "gfx950", "arch_features": "gfx950:sramecc+:xnack-"}
 CONFIG = {"prompt_length": 8, "max_new_tokens": 4, "cache_capacity": 12, "group_size": GROUP, "memory": "latency",
           "attention_splits": 0}
+
+#: A decode plan's selections as an artifact stores them (the GPU tests record real ones).
+SELECTIONS = (
+    KernelSelection(0, "embedding", "hidden_0", "hip_kernel", "gather", "bf16 embedding row gather", "aoto_embedding",
+                    device_name="AMD Instinct MI355X", device_architecture="gfx950"),
+    KernelSelection(1, "addmm", "qkv_0", "hip_kernel", "w4_gemv", "packed W4 GEMV with RMSNorm prologue",
+                    "aoto_w4_gemv_r32x1x2_n1_b1", device_name="AMD Instinct MI355X", device_architecture="gfx950"),
+    KernelSelection(2, "attention", "attention_0", "hip_kernel", "decode_attention", "single-query GQA",
+                    "aoto_decode_attention_d64_w4j2", device_name="AMD Instinct MI355X", device_architecture="gfx950"),
+)
 
 
 def _fake_state(seed: int = 0) -> DecoderState:
@@ -50,7 +61,7 @@ def _fake_state(seed: int = 0) -> DecoderState:
 def _write(path: Path, state: DecoderState | None = None, **overrides) -> Path:
     state = _fake_state() if state is None else state
     kwargs = dict(kind="decode", spec=SPEC, config=CONFIG, state=artifact.state_items(state),
-                  selections=decode_selections(SPEC), code_object=b"\x7fELF-gfx950-code-object" * 8,
+                  selections=SELECTIONS, code_object=b"\x7fELF-gfx950-code-object" * 8,
                   profile=PROFILE)
     kwargs.update(overrides)
     return artifact.write_artifact(path, **kwargs)
@@ -90,7 +101,7 @@ def test_round_trip_and_manifest(tmp_path):
     assert manifest["payloads"]["code_object"] == "code/gfx950.hsaco"
 
     contents = artifact.read_artifact(path)
-    assert contents.selections == decode_selections(SPEC)
+    assert contents.selections == SELECTIONS
     assert contents.code_object == b"\x7fELF-gfx950-code-object" * 8
     items = artifact.state_items(state)
     assert list(contents.state) == [name for name, _ in items]

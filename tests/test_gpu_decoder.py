@@ -196,20 +196,37 @@ def test_bucketed_runtime_dispatches_by_length():
     assert runtime.buckets[0].engine.state is runtime.buckets[1].engine.state
 
 
-def test_selections_are_all_native():
+def test_selections_name_the_kernels_each_plan_launches():
+    """Each plan's selections are one record per kernel it launches, named by the exact symbol,
+    and the greedy loop launches exactly the kernels its plans name."""
+
+    from aotolith_amd import ops
     from aotolith_amd.decoder import _prefill_pairs_gate_up
 
     runtime, _ = _pair(seed=17)
-    paired = _prefill_pairs_gate_up(PROMPT, TINY)
-    for plan, per_layer in ((runtime.decode, 6), (runtime.prefill, 8 if paired else 9)):
+    for plan in (runtime.prefill, runtime.decode, runtime.decode_loop):
         selections = plan.selections
+        assert selections, plan.name
         assert all(s.is_native and s.implementation == "hip_kernel" for s in selections)
-        assert len(selections) == 2 + per_layer * TINY.layers
-        assert all(s.device_architecture == "gfx950" for s in selections)
-    kinds = [s.kind for s in runtime.decode.selections]
-    assert kinds.count("decode_attention") == TINY.layers
-    assert "aoto_decode_attention_d64" in runtime.decode.kernel_names()
-    assert ("aoto_w4_gemm_gate_up" in runtime.prefill.kernel_names()) == paired
+        assert all(s.device_architecture == "gfx950" and s.artifact_name.startswith("aoto_") for s in selections)
+        assert [s.op_index for s in selections] == list(range(len(selections)))
+    for plan in (runtime.decode, runtime.decode_loop):
+        heads = [s for s in plan.selections if s.kind == "decode_attention" and "." not in s.output_id]
+        assert len(heads) == TINY.layers
+    paired = _prefill_pairs_gate_up(PROMPT, TINY)
+    assert any(name.endswith("_paired") for name in runtime.prefill.kernel_names()) == paired
+    ids = np.random.default_rng(19).integers(0, TINY.vocab, PROMPT)
+    with ops.recording_launches() as take:
+        take()
+        runtime.greedy_generate(ids, use_graph=False)
+        greedy = take()
+        logits, compact = runtime.prefill_ids(ids)
+        cache = runtime.pad_cache(compact)
+        take()
+        runtime.decode_token(torch.tensor([[3]]), cache, PROMPT + 1)
+        decode = take()
+    assert set(greedy) == set(runtime.prefill.kernel_names()) | set(runtime.decode_loop.kernel_names())
+    assert set(decode) == set(runtime.decode.kernel_names())
 
 
 def test_runtime_rejects_bad_inputs():
