@@ -18,23 +18,12 @@ from typing import Any
 
 import torch
 
+from .backends import backend_for
 from .errors import CompilationError, PlanInputError
 from .graph import LoweredGraph, capture
 from .plan import TARGET, CompiledPlan
 
 MEMORY_POLICIES = ("latency", "balanced", "minimal")
-
-
-def _check_target(target: str, codegen_matmul: bool, codegen_attention: bool, autotune: bool) -> None:
-    if target != TARGET:
-        raise CompilationError(
-            f"unsupported target: {target}",
-            hint=f"this package implements {TARGET!r}; 'apple-metal' and 'mlx-reference' run on Apple silicon",
-        )
-    if autotune:
-        raise CompilationError(f"target {TARGET!r} has one kernel per node family and nothing to autotune",
-                               hint="drop autotune=True")
-    del codegen_matmul, codegen_attention  # every node is a generated kernel on this target
 
 
 @dataclass(frozen=True)
@@ -215,12 +204,10 @@ def compile_callable(
 ) -> CompilationResult:
     """Capture ``fn`` on ``example_inputs`` and lower it to gfx950 kernels (``compiler.py:301-321``)."""
 
-    _check_target(target, codegen_matmul, codegen_attention, autotune)
-    from .graph_ops import build_graph_plan
-
+    backend = backend_for(target, codegen_matmul=codegen_matmul, codegen_attention=codegen_attention,
+                          autotune=autotune)
     graph = capture(fn, tuple(example_inputs))
-    plan, runner = build_graph_plan(graph, name=getattr(fn, "__name__", "callable"))
-    plan._keepalive = runner
+    plan = backend.compile(graph, plan_name=getattr(fn, "__name__", "callable"))
     return CompilationResult(plan=plan, input_graph=graph, lowered_graph=graph)
 
 
@@ -237,7 +224,8 @@ def compile_module(
 ) -> CompiledModulePlan:
     """Compile an ``nn.Module`` with its parameters and buffers bound as plan state (``compiler.py:324-405``)."""
 
-    _check_target(target, codegen_matmul, codegen_attention, autotune)
+    backend = backend_for(target, codegen_matmul=codegen_matmul, codegen_attention=codegen_attention,
+                          autotune=autotune)
     if not isinstance(module, torch.nn.Module):
         raise TypeError(f"expected torch.nn.Module, got {type(module).__name__}")
     if getattr(module, "training", False):
@@ -259,12 +247,10 @@ def compile_module(
     clashes = sorted({"verify_index_bounds", "memory"} & set(tensor_names))
     if clashes:
         raise CompilationError(f"a tensor keyword input cannot be named {clashes[0]!r}: the plan uses that name")
-    from .graph_ops import build_graph_plan
-
     wrapper = _ModuleCall(module, len(example_inputs), static_kwargs, tensor_names, output_key).eval()
     graph = capture(wrapper, tuple(example_inputs) + tuple(tensor_values))
-    plan, runner = build_graph_plan(graph, name=type(module).__name__)
-    plan._keepalive = runner
+    plan = backend.compile(graph, plan_name=type(module).__name__)
+    runner = plan._keepalive
     result = CompilationResult(plan=plan, input_graph=graph, lowered_graph=graph)
     labels = tuple(graph.state_labels.get(n, n).removeprefix("module.") for n in graph.state_names)
     return CompiledModulePlan(compilation=result, input_count=len(example_inputs), state_names=labels,

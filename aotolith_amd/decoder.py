@@ -426,26 +426,64 @@ def _sel(index: int, op: str, output: str, kind: str, reason: str, artifact: str
     )
 
 
-def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
-    problems = []
+def kernel_refusals(spec: DecoderSpec, group: int) -> tuple[KernelSelection, ...]:
+    """Per-node refusals of a decoder shape outside the kernels' limits.
+
+    The reference refuses an unsupported shape per node at candidate time and
+    records the reason in that node's selection (``backends/apple.py:719-740``).
+    This target has no fallback to send such a node to, so each refused node gets a
+    ``KernelSelection`` with implementation ``"unsupported"`` and the reason; a
+    non-empty result stops the compile (:func:`_check_kernel_limits`).
+    """
+
+    out: list[KernelSelection] = []
+
+    def refuse(op: str, output: str, kind: str, reason: str) -> None:
+        out.append(KernelSelection(op_index=len(out), op=op, output_id=output, implementation="unsupported",
+                                   kind=kind, reason=reason, device_architecture=ARCHITECTURE))
+
+    layers = range(spec.layers)
+    attention = []
     if spec.head_dim not in (64, 128):
-        problems.append(f"head_dim {spec.head_dim} (attention kernels take 64 or 128)")
+        attention.append(f"head_dim {spec.head_dim}: the decode and flash attention kernels take 64 or 128")
     if spec.heads % spec.kv_heads:
-        problems.append(f"{spec.heads} query heads are not a multiple of {spec.kv_heads} kv heads")
-    for name, k in (("hidden", spec.hidden), ("intermediate", spec.intermediate),
-                    ("attention width", spec.attention_width)):
+        attention.append(f"{spec.heads} query heads are not a multiple of {spec.kv_heads} kv heads")
+    for reason in attention:
+        for layer in layers:
+            refuse("attention", f"attention_{layer}", "attention", reason)
+
+    # (node, output features N, reduction K) of every packed projection
+    projections = [("qkv", spec.qkv_width, spec.hidden), ("hidden_{}a", spec.hidden, spec.attention_width),
+                   ("mlp", spec.intermediate, spec.hidden), ("hidden_{}b", spec.hidden, spec.intermediate)]
+    for node, n, k in projections:
+        reasons = []
         if k % 64:
-            problems.append(f"{name} {k} is not a multiple of 64")
-    for name, n in (("hidden", spec.hidden), ("intermediate", spec.intermediate), ("qkv width", spec.qkv_width)):
+            reasons.append(f"reduction length {k} is not a multiple of 64")
         if n % 16:
-            problems.append(f"{name} {n} is not a multiple of 16")
-    if group % 32 or spec.hidden % group or spec.intermediate % group:
-        problems.append(f"group size {group} must be a multiple of 32 dividing hidden and intermediate")
-    if problems:
-        raise CompilationError(
-            f"{TARGET} cannot compile this decoder: " + "; ".join(problems),
-            hint="every node must run as a gfx950 kernel; there is no fallback",
+            reasons.append(f"{n} output features are not a multiple of 16")
+        if group % 32 or k % group:
+            reasons.append(f"group size {group} is not a multiple of 32 dividing the reduction length {k}")
+        for reason in reasons:
+            for layer in layers:
+                output = node.format(layer) if "{}" in node else f"{node}_{layer}"
+                refuse("matmul", output, "packed_matmul", reason)
+    if group % 32 or spec.hidden % group:
+        refuse("matmul", "logits", "packed_matmul",
+               f"group size {group} is not a multiple of 32 dividing the hidden size {spec.hidden}")
+    return tuple(out)
+
+
+def _check_kernel_limits(spec: DecoderSpec, group: int) -> None:
+    refused = kernel_refusals(spec, group)
+    if refused:
+        reasons = sorted({s.reason for s in refused})
+        error = CompilationError(
+            f"{TARGET} cannot compile this decoder: {len(refused)} node(s) refused: " + "; ".join(reasons),
+            hint="every node must run as a gfx950 kernel; there is no fallback (the error's `refused` "
+                 "attribute holds each node's selection record)",
         )
+        error.refused = refused
+        raise error
 
 
 def _prefill_pairs_gate_up(tokens: int, spec: DecoderSpec) -> bool:

@@ -89,3 +89,39 @@ def test_no_gpu_means_a_device_error():
         pytest.skip("a GPU is visible")
     with pytest.raises(DeviceError):
         random_state(DecoderSpec("qwen2", 64, 128, 256, 1, 2, 1, 64, 1e-6, 1e6, True))
+
+
+def test_kernel_limits_refuse_per_node_with_reasons():
+    """A shape outside the kernels' limits is refused node by node (reference backends/apple.py:719-740);
+    the compile error carries each refused node's selection record."""
+
+    from aotolith_amd.decoder import DecoderSpec, _check_kernel_limits, kernel_refusals
+    from aotolith_amd.errors import CompilationError
+
+    assert kernel_refusals(DecoderSpec("qwen2", 64, 896, 4864, 2, 14, 2, 64, 1e-6, 1e6, True), 64) == ()
+    bad = DecoderSpec("llama", 64, 896, 4864, 2, 14, 2, 96, 1e-6, 1e6, False)   # head_dim 96
+    refused = kernel_refusals(bad, 64)
+    assert [s.output_id for s in refused] == ["attention_0", "attention_1"]
+    assert all(s.implementation == "unsupported" and not s.is_native and "head_dim 96" in s.reason for s in refused)
+    with pytest.raises(CompilationError) as info:
+        _check_kernel_limits(bad, 64)
+    assert info.value.refused == refused
+    odd = DecoderSpec("qwen2", 64, 896, 4864, 1, 14, 2, 64, 1e-6, 1e6, True)
+    by_node = {s.output_id: s.reason for s in kernel_refusals(odd, 48)}
+    assert set(by_node) == {"qkv_0", "hidden_0a", "mlp_0", "hidden_0b", "logits"}
+    assert all("group size 48" in reason for reason in by_node.values())
+
+
+def test_backend_seam_registry():
+    """The target registry and backend object of the reference's seam (backends/__init__.py:38-55)."""
+
+    from aotolith_amd.backends import TARGETS, HipGfx950Backend, backend_for
+    from aotolith_amd.errors import CompilationError
+
+    assert TARGETS == ("hip-gfx950",)
+    assert isinstance(backend_for("hip-gfx950"), HipGfx950Backend)
+    assert backend_for("hip-gfx950").name == "hip-gfx950"
+    with pytest.raises(CompilationError, match="unsupported target"):
+        backend_for("apple-metal")
+    with pytest.raises(CompilationError, match="autotune"):
+        backend_for("hip-gfx950", autotune=True)
