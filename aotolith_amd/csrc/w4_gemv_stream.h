@@ -88,90 +88,73 @@ AOTO_DEVICE float sum_squares8(const uint4 raw, float ss) {
   return dot2_bf16(raw.w, raw.w, ss);
 }
 
-// x (optionally RMS-normalized and rounded to bf16) staged by one wave into its
-// own LDS region, in dot2 pair order, plus per-chunk offsets (136 x the chunk's
-// sum, pack_x8). All of x (and the
-// norm weight) is loaded up front - XV 16-byte vectors per lane, XV >= K/512 -
-// so staging costs one round trip. No block barrier: the wave's LDS accesses
-// are ordered among themselves.
-template <bool NORM, int XV>
-AOTO_DEVICE void stage_activation_wave(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
-                                       float eps, int K, uint4* __restrict__ xp, float* __restrict__ csum) {
-  const int lane = threadIdx.x & 63;
-  const int vecs = K >> 3;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
-  uint4 xr[XV], wr[NORM ? XV : 1];
-#pragma unroll
-  for (int i = 0; i < XV; ++i) xr[i] = xv[min(lane + 64 * i, vecs - 1)];
-  if (NORM) {
-#pragma unroll
-    for (int i = 0; i < XV; ++i) wr[i] = wv[min(lane + 64 * i, vecs - 1)];
-  }
-  float ns = 1.f;
-  if (NORM) {
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < XV; ++i)
-      if (lane + 64 * i < vecs) ss = sum_squares8(xr[i], ss);
-    ss = wave_sum(ss);
-    ns = 1.0f / sqrtf(ss / (float)K + eps);
-  }
-#pragma unroll
-  for (int i = 0; i < XV; ++i) {
-    const int v = lane + 64 * i;
-    uint4 packed;
-    float sum = pack_x8<NORM>(xr[i], wr[NORM ? i : 0], ns, packed);
-    if (v < vecs) xp[v] = packed;
-    // A chunk (32 codes) is four consecutive vectors: lanes 4c .. 4c+3.
-    sum = group_sum<4>(sum);
-    if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+// x (optionally RMS-normalized and rounded to bf16) staged into LDS, in dot2 pair
+// order, plus per-chunk offsets (136 x the chunk's sum, pack_x8). Split in two like
+// DirectActivation: issue() loads all of x (and the norm weight) - XV 16-byte
+// vectors per thread - and finish() packs and stores it. The caller issues x
+// first and the first tile's weights right after, so the wait for x is a wait for
+// x alone (loads return in issue order) while the weights are already in flight.
+// WAVE: each wave stages its own copy with wave-level reductions only (no block
+// barrier; XV >= K/512). Otherwise one copy per block of kGemvThreads threads,
+// whose RMS statistic is a block sum (a barrier; XV >= K/2048): for long
+// reductions (K = 4096, 14336) a per-wave copy would cost as many LDS writes and
+// cache reads as the wave's share of the weights.
+template <bool NORM, int XV, bool WAVE>
+struct StagedActivation {
+  uint4 xr[XV];
+  uint4 wr[NORM ? XV : 1];
 
-// x staged once per block (kGemvThreads threads) into one shared LDS region, in
-// the same layout as stage_activation_wave, with the RMS statistic reduced over
-// the block: for long reductions (K = 4096, 14336) a per-wave copy would cost
-// as many LDS writes and cache reads as the wave's share of the weights.
-// Contains barriers: every thread of the block calls it. XV >= K / (8 * 256).
-template <bool NORM, int XV>
-AOTO_DEVICE void stage_activation_block(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
-                                        float eps, int K, uint4* __restrict__ xp, float* __restrict__ csum) {
-  __shared__ float scratch[kGemvThreads / 64];
-  const int vecs = K >> 3;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-  const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
-  uint4 xr[XV], wr[NORM ? XV : 1];
+  AOTO_DEVICE static int index(int i) { return WAVE ? (int)(threadIdx.x & 63) + 64 * i
+                                                     : (int)threadIdx.x + kGemvThreads * i; }
+
+  AOTO_DEVICE void issue(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w, int K) {
+    const int vecs = K >> 3;
+    const uint4* xv = reinterpret_cast<const uint4*>(x);
+    const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
 #pragma unroll
-  for (int i = 0; i < XV; ++i) xr[i] = xv[min((int)threadIdx.x + kGemvThreads * i, vecs - 1)];
-  if (NORM) {
+    for (int i = 0; i < XV; ++i) xr[i] = xv[min(index(i), vecs - 1)];
+    if (NORM) {
 #pragma unroll
-    for (int i = 0; i < XV; ++i) wr[i] = wv[min((int)threadIdx.x + kGemvThreads * i, vecs - 1)];
+      for (int i = 0; i < XV; ++i) wr[i] = wv[min(index(i), vecs - 1)];
+    }
   }
-  float ns = 1.f;
-  if (NORM) {
-    float ss = 0.f;
+
+  AOTO_DEVICE void finish(float eps, int K, uint4* __restrict__ xp, float* __restrict__ csum) const {
+    const int vecs = K >> 3;
+    float ns = 1.f;
+    if (NORM) {
+      float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < XV; ++i)
-      if ((int)threadIdx.x + kGemvThreads * i < vecs) ss = sum_squares8(xr[i], ss);
-    ss = block_sum<kGemvThreads>(ss, scratch);
-    ns = 1.0f / sqrtf(ss / (float)K + eps);
-  }
+      for (int i = 0; i < XV; ++i)
+        if (index(i) < vecs) ss = sum_squares8(xr[i], ss);
+      if (WAVE) {
+        ss = wave_sum(ss);
+      } else {
+        __shared__ float scratch[kGemvThreads / 64];
+        ss = block_sum<kGemvThreads>(ss, scratch);
+      }
+      ns = 1.0f / sqrtf(ss / (float)K + eps);
+    }
 #pragma unroll
-  for (int i = 0; i < XV; ++i) {
-    const int v = threadIdx.x + kGemvThreads * i;
-    uint4 packed;
-    float sum = pack_x8<NORM>(xr[i], wr[NORM ? i : 0], ns, packed);
-    if (v < vecs) xp[v] = packed;
-    // A chunk (32 codes) is four consecutive vectors: threads 4c .. 4c+3.
-    sum = group_sum<4>(sum);
-    if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
+    for (int i = 0; i < XV; ++i) {
+      const int v = index(i);
+      uint4 packed;
+      float sum = pack_x8<NORM>(xr[i], wr[NORM ? i : 0], ns, packed);
+      if (v < vecs) xp[v] = packed;
+      // A chunk (32 codes) is four consecutive vectors: threads 4c .. 4c+3.
+      sum = group_sum<4>(sum);
+      if (v < vecs && (v & 3) == 0) csum[v >> 2] = sum;
+    }
+    if (WAVE) {
+      // no block barrier: the wave's LDS accesses are ordered among themselves
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+      __syncthreads();
+    }
   }
-  __syncthreads();
-}
+};
 
 // Direct staging for the latency-bound shapes: the LPR lanes of a row group hold,
 // between them, every chunk of x (chunk li + LPR*j), so each lane loads just its
@@ -236,7 +219,7 @@ struct DirectActivation {
 // ARGMAX: also reduce the wave's rows to one greedy-argmax key (argmax_key of
 // the stored bf16 value and its row) and store it at keys[global wave index],
 // 0 for a wave without rows; aoto_argmax_finish reduces the keys.
-// BLOCKX: x staged once per block (stage_activation_block; XV >= K/2048) into
+// BLOCKX: x staged once per block (StagedActivation; XV >= K/2048) into
 // one LDS region the block's waves share; needs 4-wave blocks.
 template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX, bool BLOCKX = false>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
@@ -372,9 +355,11 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   int tile = blockIdx.x * waves_per_block + wave;
   if constexpr (BLOCKX) {
     // every wave takes part in the block's staging barrier, tile or not
+    StagedActivation<NORM, (XV > 0 ? XV : 1), false> act;
+    act.issue(x, norm_w, K);
     load(tile, ra);
-    __builtin_amdgcn_sched_barrier(0);  // the first tile's loads ahead of the staging
-    stage_activation_block<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
+    __builtin_amdgcn_sched_barrier(0);  // x, then the first tile's loads, then the staging
+    act.finish(eps, K, xp, csum);
   }
   if (tile >= tiles) {
     if (ARGMAX && lane == 0) keys[tile] = 0;
@@ -389,13 +374,15 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     __builtin_amdgcn_sched_barrier(0);  // x, then every load of the first tile, then the math
     act.finish(eps, K, li, xr, cr);
   } else {
+    StagedActivation<NORM, (XV > 0 ? XV : 1), true> act;
+    act.issue(x, norm_w, K);
     load(tile, ra);
     // Keep every load of the first tile ahead of the staging code: the
     // scheduler otherwise sinks some of them behind the wait for x, which costs
     // a memory round trip per wave and leaves the loop's entry waits
     // conservative.
     __builtin_amdgcn_sched_barrier(0);
-    stage_activation_wave<NORM, (XV > 0 ? XV : 1)>(x, norm_w, eps, K, xp, csum);
+    act.finish(eps, K, xp, csum);
     if (XREG) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
@@ -436,6 +423,9 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     // The scheduling barriers keep each prefetch ahead of the math on the
     // other set (the scheduler would otherwise start the math first, and the
     // prefetch would wait behind the current set's loads).
+    // (Measured and not kept: both register sets loaded before the x staging,
+    // reloads clamped to the wave's own last tile - 0.7-1.4 us slower on every
+    // Llama-8B layer projection and the Qwen LM head.)
     const int mine = (tiles - tile + total_waves - 1) / total_waves;
     for (int i = 0; i + 2 <= mine; i += 2) {
       load(tile + total_waves, rb);
