@@ -78,6 +78,7 @@ SIGNATURES: dict[str, tuple] = {
         _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_int, _p,
     ),
+    "aoto_hip_w4_gemm_qkv_rope_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int),
     "aoto_hip_w4_gemm_noalloc": (_p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _p),
     "aoto_hip_decode_attention_workspace": (_c_int, _c_int, _c_int, _c_int, _c_int, _c_int),
     "aoto_hip_decode_attention": (
@@ -112,7 +113,8 @@ SIGNATURES: dict[str, tuple] = {
 
 #: Entry points returning a size rather than a status.
 SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_take_launches", "aoto_hip_decode_attention_workspace",
-                  "aoto_hip_w4_gemm_workspace", "aoto_hip_w4_gemm_gate_up_workspace", "aoto_hip_w4_gemv_argmax_keys"}
+                  "aoto_hip_w4_gemm_workspace", "aoto_hip_w4_gemm_gate_up_workspace", "aoto_hip_w4_gemm_qkv_rope_workspace",
+                  "aoto_hip_w4_gemv_argmax_keys"}
 
 
 class HipBackendUnavailable(RuntimeError):

@@ -69,6 +69,23 @@ AOTO_GEMM_PAIRED_INSTANCE(8, 1, 4)
 AOTO_GEMM_PAIRED_INSTANCE(8, 1, 8)
 AOTO_GEMM_PAIRED_INSTANCE(8, 2, 4)
 AOTO_GEMM_PAIRED_INSTANCE(8, 2, 8)
+// The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
+AOTO_GEMM_ROPE_INSTANCE(4, 1, 4, 0)
+AOTO_GEMM_ROPE_INSTANCE(4, 1, 4, 1)
+AOTO_GEMM_ROPE_INSTANCE(4, 1, 8, 0)
+AOTO_GEMM_ROPE_INSTANCE(4, 1, 8, 1)
+AOTO_GEMM_ROPE_INSTANCE(4, 2, 4, 0)
+AOTO_GEMM_ROPE_INSTANCE(4, 2, 4, 1)
+AOTO_GEMM_ROPE_INSTANCE(4, 2, 8, 0)
+AOTO_GEMM_ROPE_INSTANCE(4, 2, 8, 1)
+AOTO_GEMM_ROPE_INSTANCE(8, 1, 4, 0)
+AOTO_GEMM_ROPE_INSTANCE(8, 1, 4, 1)
+AOTO_GEMM_ROPE_INSTANCE(8, 1, 8, 0)
+AOTO_GEMM_ROPE_INSTANCE(8, 1, 8, 1)
+AOTO_GEMM_ROPE_INSTANCE(8, 2, 4, 0)
+AOTO_GEMM_ROPE_INSTANCE(8, 2, 4, 1)
+AOTO_GEMM_ROPE_INSTANCE(8, 2, 8, 0)
+AOTO_GEMM_ROPE_INSTANCE(8, 2, 8, 1)
 
 // Eight-bit decode GEMV: {rows per wave} x {chunks per lane per pass}, with
 // the decoder's epilogues (rms-norm prologue, paired gate/up, bias/residual).

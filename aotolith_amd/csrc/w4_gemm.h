@@ -29,6 +29,7 @@
 #include <utility>
 
 #include "common.h"
+#include "gemm_args.h"
 
 namespace aoto {
 
@@ -84,6 +85,100 @@ AOTO_DEVICE void static_for(F&& f) {
   static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
+// RoPE and the cache fill of one staged q/k/v block: BM rows of the projection
+// from m0, BN columns - whole heads - from n0, as bf16 in tile[r][c] (row
+// stride TS). Item i = r * BN/8 + c8 of a thread's IPT = BM*BN/2048 items is one
+// (token, head, 4 consecutive d of the head's first half) with its partner
+// columns d + D/2, the same arithmetic as aoto_rope_qkv_prefill: v = x cos +
+// partner sin from the rounded projection, one rounding; values are copied
+// unrotated. The table rows of each item are loaded by RopeRows (early, so the
+// epilogue does not wait for them). Block row 0 also zeroes the prefix slots
+// of the block's key and value heads when asked.
+template <int BM, int BN>
+struct RopeRows {
+  static constexpr int IPT = BM * BN / 2048;
+  long long pos[IPT];
+  uint2 cs[IPT][4];  // cos[d..d+4), cos[d+D/2..), sin[d..), sin[d+D/2..)
+
+  AOTO_DEVICE static int row_of(int j) { return ((int)threadIdx.x + 256 * j) / (BN / 8); }
+  AOTO_DEVICE static int col_of(int j, int D) {  // first-half column of the item within the block
+    const int c8 = ((int)threadIdx.x + 256 * j) % (BN / 8), quads = D / 8;
+    return (c8 / quads) * D + 4 * (c8 % quads);
+  }
+  AOTO_DEVICE void load_positions(const QkvRope& r, int M, int m0) {
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) pos[j] = r.positions[min(m0 + row_of(j), M - 1)];
+  }
+  AOTO_DEVICE void load_tables(const QkvRope& r) {
+    const int D = r.head_dim, half = D >> 1;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+      const int d = col_of(j, D) % D;
+      const uint16_t* cr = r.cos_table + (size_t)pos[j] * D + d;
+      const uint16_t* sr = r.sin_table + (size_t)pos[j] * D + d;
+      cs[j][0] = *reinterpret_cast<const uint2*>(cr);
+      cs[j][1] = *reinterpret_cast<const uint2*>(cr + half);
+      cs[j][2] = *reinterpret_cast<const uint2*>(sr);
+      cs[j][3] = *reinterpret_cast<const uint2*>(sr + half);
+    }
+  }
+};
+
+template <int BM, int BN, int TS>
+AOTO_DEVICE void rope_tile(const uint16_t* tile, const RopeRows<BM, BN>& rows, const QkvRope& r, int M, int m0,
+                           int n0) {
+  const int D = r.head_dim, half = D >> 1;
+  const int h0 = n0 / D;
+  const size_t head_stride = (size_t)r.cap * D;
+  const size_t pair_stride = (size_t)r.kv_heads * head_stride;
+#pragma unroll
+  for (int j = 0; j < RopeRows<BM, BN>::IPT; ++j) {
+    const int row = RopeRows<BM, BN>::row_of(j);
+    const int m = m0 + row;
+    if (m >= M) continue;
+    const int c = RopeRows<BM, BN>::col_of(j, D);
+    const int h = h0 + c / D, d = c % D;
+    const uint2 ya = *reinterpret_cast<const uint2*>(tile + row * TS + c);
+    const uint2 yb = *reinterpret_cast<const uint2*>(tile + row * TS + c + half);
+    uint16_t* dst;
+    if (h < r.query_heads)
+      dst = r.q_out + ((size_t)h * M + m) * D;
+    else if (h < r.query_heads + r.kv_heads)
+      dst = r.pair + (size_t)(h - r.query_heads) * head_stride + (size_t)(r.slot0 + m) * D;
+    else
+      dst = r.pair + pair_stride + (size_t)(h - r.query_heads - r.kv_heads) * head_stride + (size_t)(r.slot0 + m) * D;
+    if (h >= r.query_heads + r.kv_heads) {
+      *reinterpret_cast<uint2*>(dst + d) = ya;
+      *reinterpret_cast<uint2*>(dst + d + half) = yb;
+      continue;
+    }
+    const float xa[4] = {bf16_lo(ya.x), bf16_hi(ya.x), bf16_lo(ya.y), bf16_hi(ya.y)};
+    const float xb[4] = {bf16_lo(yb.x), bf16_hi(yb.x), bf16_lo(yb.y), bf16_hi(yb.y)};
+    const uint2 ca = rows.cs[j][0], cb = rows.cs[j][1], sa = rows.cs[j][2], sb = rows.cs[j][3];
+    const float c0[4] = {bf16_lo(ca.x), bf16_hi(ca.x), bf16_lo(ca.y), bf16_hi(ca.y)};
+    const float c1[4] = {bf16_lo(cb.x), bf16_hi(cb.x), bf16_lo(cb.y), bf16_hi(cb.y)};
+    const float s0[4] = {bf16_lo(sa.x), bf16_hi(sa.x), bf16_lo(sa.y), bf16_hi(sa.y)};
+    const float s1[4] = {bf16_lo(sb.x), bf16_hi(sb.x), bf16_lo(sb.y), bf16_hi(sb.y)};
+    float ra[4], rb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      ra[k] = xa[k] * c0[k] + (-xb[k]) * s0[k];  // first half: x cos - x[d + D/2] sin
+      rb[k] = xb[k] * c1[k] + xa[k] * s1[k];     // second half: x cos + x[d - D/2] sin
+    }
+    *reinterpret_cast<uint2*>(dst + d) = make_uint2(pack_bf16x2(ra[0], ra[1]), pack_bf16x2(ra[2], ra[3]));
+    *reinterpret_cast<uint2*>(dst + d + half) = make_uint2(pack_bf16x2(rb[0], rb[1]), pack_bf16x2(rb[2], rb[3]));
+  }
+  if (!r.zero_prefix || blockIdx.y != 0) return;
+  const int prefix = r.slot0 * D / 4;  // 8-byte stores per head
+  for (int hh = 0; hh < BN / D; ++hh) {
+    const int h = h0 + hh;
+    if (h < r.query_heads) continue;
+    uint16_t* base = r.pair + (size_t)(h - r.query_heads) * head_stride;  // k heads, then v heads
+    for (int z = threadIdx.x; z < prefix; z += blockDim.x)
+      *reinterpret_cast<uint2*>(base + (size_t)z * 4) = make_uint2(0u, 0u);
+  }
+}
+
 // Split-K: blockIdx.z selects the reduction slice [z*kslice, min(K, (z+1)*kslice));
 // with `partials` non-null the block stores its f32 tile to partials[z][m][n]
 // and aoto_w4_gemm_reduce applies the sum and the epilogue.
@@ -101,15 +196,22 @@ AOTO_DEVICE void static_for(F&& f) {
 // of the step takes unit 4q + j from every lane - for both operands, so the
 // sum over k is the same, only its order differs. A step past K (K = 64 mod
 // 128) zeroes the codes of quads 2 and 3.
-template <int BITS, int TN, int TM, int DEPTH, bool BIAS, bool RESIDUAL, bool GATE, bool PAIRED = false>
+//
+// ROPE (unsplit q/k/v, block columns a whole number of heads): the epilogue
+// also stages the block's bf16 tile in LDS and applies RoPE and the cache fill
+// to it (aoto_rope_qkv_prefill on the tile's heads, same values), so the
+// projection, its bias, RoPE and the cache fill are one launch.
+template <int BITS, int TN, int TM, int DEPTH, bool BIAS, bool RESIDUAL, bool GATE, bool PAIRED = false,
+          bool ROPE = false>
 __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename GemmWord<BITS>::type* __restrict__ words,
                              const uint16_t* __restrict__ scales, const uint16_t* __restrict__ bias,
                              const uint16_t* __restrict__ residual, const uint16_t* __restrict__ gate,
                              uint16_t* __restrict__ Y, int M, int N, int K, int group, int kslice,
                              float* __restrict__ partials,
                              const typename GemmWord<BITS>::type* __restrict__ up_words = nullptr,
-                             const uint16_t* __restrict__ up_scales = nullptr) {
+                             const uint16_t* __restrict__ up_scales = nullptr, const QkvRope rope = QkvRope{}) {
   static_assert(!(PAIRED && (BIAS || RESIDUAL || GATE)), "the paired form has its own epilogue");
+  static_assert(!(ROPE && (PAIRED || RESIDUAL || GATE)), "RoPE follows the bias epilogue only");
   constexpr int BM = 16 * TM;
   constexpr int BN = 64 * TN;
   constexpr int XVEC = BM * (kGemmBK / 8);        // 16-byte vectors per X tile
@@ -189,6 +291,21 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
     }
   };
 
+  // ROPE: the block's table rows are loaded early - positions now, the cos/sin
+  // rows after the first step (small blocks) or ahead of the epilogue (blocks
+  // whose rows would not fit the loop's registers) - so the RoPE tail does not
+  // wait on two dependent memory round trips.
+  constexpr bool EARLY_TABLES = BM * BN <= 4096;
+  RopeRows<BM, BN> rope_rows;
+  if constexpr (ROPE) rope_rows.load_positions(rope, M, m_block);
+  // the bias of this lane's columns, loaded before the loop rather than in the epilogue
+  uint2 bias_cols[TN];
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+      bias_cols[t] = *reinterpret_cast<const uint2*>(bias + min(n_wave + t * 16 + quad * 4, N - 4));
+  }
+
   const int kb = blockIdx.z * kslice;
   const int ke = min(K, kb + kslice);
   const int steps = (ke - kb + kGemmBK - 1) / kGemmBK;
@@ -247,6 +364,8 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
               for (int t = 0; t < TN; ++t)
                 acc[p][t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][t], b[u], acc[p][t][u], 0, 0, 0);
         }
+        if constexpr (ROPE && EARLY_TABLES)
+          if (s == 0) rope_rows.load_tables(rope);
       }
     });
   }
@@ -271,6 +390,12 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
     return;
   }
   // Epilogue: lane holds Y[m0 + col][n0 + quad*4 + i].
+  constexpr int YS = BN + 8;  // ROPE: bf16 per staged tile row
+  static_assert(!ROPE || BM * YS <= 2 * BM * kGemmLdsStride, "the staged tile fits the X tiles");
+  if constexpr (ROPE) {
+    if constexpr (!EARLY_TABLES) rope_rows.load_tables(rope);
+    __syncthreads();  // every wave is past its last read of the X tiles
+  }
 #pragma unroll
   for (int u = 0; u < TM; ++u) {
     const int m = m_block + u * 16 + col;
@@ -289,7 +414,7 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
         }
       }
       if (BIAS) {
-        const uint2 bb = *reinterpret_cast<const uint2*>(bias + n);
+        const uint2 bb = bias_cols[t];
         v[0] += bf16_lo(bb.x);
         v[1] += bf16_hi(bb.x);
         v[2] += bf16_lo(bb.y);
@@ -312,7 +437,12 @@ __device__ void w4_gemm_body(const uint16_t* __restrict__ X, const typename Gemm
       o.x = pack_bf16x2(v[0], v[1]);
       o.y = pack_bf16x2(v[2], v[3]);
       *reinterpret_cast<uint2*>(Y + (size_t)m * N + n) = o;
+      if (ROPE) *reinterpret_cast<uint2*>(xs + (u * 16 + col) * YS + (n - n_block)) = o;
     }
+  }
+  if constexpr (ROPE) {
+    __syncthreads();
+    rope_tile<BM, BN, YS>(xs, rope_rows, rope, M, m_block, n_block);
   }
 }
 
@@ -618,4 +748,13 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_paired(con
     aoto::w4_gemm_body<BITS, TN, TM, aoto::gemm_depth(TM), false, false, false, true>(X, words, scales, nullptr, nullptr,       \
                                                                 nullptr, Y, M, N, K, group, kslice,       \
                                                                 partials, up_words, up_scales);           \
+  }
+// aoto_w{BITS}_gemm_n{TN}_m{TM}_rope_b{BIAS}: the unsplit q/k/v projection with
+// its bias, RoPE and cache fill (block columns a whole number of heads).
+#define AOTO_GEMM_ROPE_INSTANCE(BITS, TN, TM, BIAS)                                                         \
+  extern "C" __global__ __launch_bounds__(256) void aoto_w##BITS##_gemm_n##TN##_m##TM##_rope_b##BIAS(        \
+      const uint16_t* X, const aoto::GemmWord<BITS>::type* words, const uint16_t* scales,                    \
+      const uint16_t* bias, uint16_t* Y, int M, int N, int K, int group, aoto::QkvRope rope) {               \
+    aoto::w4_gemm_body<BITS, TN, TM, aoto::gemm_depth(TM), BIAS, false, false, false, true>(                 \
+        X, words, scales, bias, nullptr, nullptr, Y, M, N, K, group, K, nullptr, nullptr, nullptr, rope);    \
   }

@@ -587,8 +587,9 @@ def matmul_qkv_rope(
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The packed q/k/v projection ``out = bf16(x @ W^T + bias)`` ``[M, W]`` with RoPE of q into
     ``q_out [1, Hq, M, D]`` and the rotated keys / values into ``pair [2, 1, Hkv, cap, D]`` at
-    ``slot0``: :func:`w4_matmul` then :func:`rope_qkv_prefill` (batch 1), one launch fewer when
-    the plan splits K. Returns ``(out, q_out)``."""
+    ``slot0``: :func:`w4_matmul` then :func:`rope_qkv_prefill` (batch 1) in one launch - RoPE in
+    the GEMM's epilogue when unsplit (``splits=0`` prefers it whenever a block's columns are
+    whole heads), in the split-K sum's launch when split. Returns ``(out, q_out)``."""
 
     per_word = CODES_PER_WORD[bits]
     _expect(packed, "packed", torch.int32)
@@ -624,10 +625,10 @@ def matmul_qkv_rope(
     else:
         _expect(q_out, "q_out", BF16, (1, query_heads, m, head_dim))
     _ready(x)
-    need = gemm_workspace_bytes(m, n, k, tile, splits)
+    lib = _lib.library()
+    need = int(lib.aoto_hip_w4_gemm_qkv_rope_workspace(m, k, int(tile), int(splits), query_heads, kv_heads, head_dim))
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty((need // 4,), dtype=torch.float32, device=x.device)
-    lib = _lib.library()
     entry = lib.aoto_hip_w4_gemm_qkv_rope if bits == 4 else lib.aoto_hip_w8_gemm_qkv_rope
     _lib.check(
         entry(

@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 15
+#define AOTO_HIP_ABI_VERSION 16
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -202,13 +202,15 @@ int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const vo
  * 1443-1471) followed by RoPE of q and k (codegen/index.py:22-126, tables of
  * models/decoder.py:323-334) and the prefill module's returned key/value window
  * (models/decoder.py:524-561, 870-887) - the values of aoto_hip_w4_gemm (bias) then
- * aoto_hip_rope_qkv_prefill (batch 1), in one pass over the projection when the
- * plan splits K (the split sum, bias, RoPE and cache fill share one launch).
+ * aoto_hip_rope_qkv_prefill (batch 1), in one launch: unsplit, when a block's
+ * columns are whole heads, RoPE and the cache fill run in the GEMM's epilogue;
+ * split, the split sum, bias, RoPE and cache fill share the second launch.
  * x [M, K]; the weight packs N = (Hq + 2 Hkv) * head_dim rows; y [M, N] receives
  * the projection; q_out [Hq, M, head_dim]; pair [2, Hkv, capacity, head_dim] gets
  * rotated keys / values at slots slot0 .. slot0 + M - 1 (slots below slot0 zeroed
- * when zero_prefix != 0); positions[M] int64. tile / splits / workspace as
- * aoto_hip_w4_gemm (workspace: aoto_hip_w4_gemm_workspace(M, N, K, ...) bytes). */
+ * when zero_prefix != 0); positions[M] int64. tile as aoto_hip_w4_gemm; splits 0
+ * chooses (unsplit whenever the epilogue form applies), else as aoto_hip_w4_gemm;
+ * workspace: aoto_hip_w4_gemm_qkv_rope_workspace() bytes. */
 int aoto_hip_w4_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
                               int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
                               const void* cos_table, const void* sin_table, void* q_out, void* pair, int query_heads,
@@ -217,6 +219,10 @@ int aoto_hip_w8_gemm_qkv_rope(const void* x, const int32_t* words, const void* s
                               int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
                               const void* cos_table, const void* sin_table, void* q_out, void* pair, int query_heads,
                               int kv_heads, int head_dim, int capacity, int slot0, int zero_prefix, void* stream);
+/* Workspace bytes of aoto_hip_w{4,8}_gemm_qkv_rope with these arguments (0: the
+ * plan does not split K). */
+size_t aoto_hip_w4_gemm_qkv_rope_workspace(int M, int K, int tile, int splits, int query_heads, int kv_heads,
+                                           int head_dim);
 
 /* Bytes of split-K workspace the gate/up entry points need (0 when unsplit). */
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits);

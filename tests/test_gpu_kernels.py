@@ -501,19 +501,25 @@ def test_matmul_residual_norm_rejects_wide_rows_and_aliasing():
 
 # ---------------------------------------------------------------- q/k/v projection + RoPE + cache fill
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("m,hq,hkv,dim,k,splits,bias,slot0", [
-    (128, 14, 2, 64, 896, 0, True, 64),    # Qwen prefill: the auto plan splits K 7 ways
-    (128, 14, 2, 64, 896, 1, True, 0),     # the same unsplit (GEMM, then the RoPE kernel)
-    (40, 8, 2, 128, 512, 3, False, 9),     # head_dim 128, no bias, ragged M, forced split
+@pytest.mark.parametrize("m,hq,hkv,dim,k,splits,bias,slot0,tile", [
+    (128, 14, 2, 64, 896, 0, True, 64, 0),   # Qwen prefill, auto plan
+    (128, 14, 2, 64, 896, 7, True, 64, 0),   # split 7 ways: the split-K sum with RoPE and the fill
+    (128, 14, 2, 64, 896, 1, True, 0, 0),    # unsplit 64-column blocks: RoPE in the GEMM epilogue
+    (128, 14, 2, 64, 896, 1, True, 64, 0),   # the same with a zeroed prefix
+    (40, 8, 2, 128, 512, 3, False, 9, 0),    # head_dim 128, no bias, ragged M, forced split
+    (40, 8, 2, 128, 512, 1, False, 9, 24),   # 128-column blocks hold one 128-wide head: epilogue
+    (40, 8, 2, 128, 512, 1, True, 9, 14),    # 64-column blocks split a head: GEMM, then the RoPE kernel
+    (40, 8, 2, 64, 512, 1, True, 3, 24),     # two 64-wide heads per block
+    (200, 8, 2, 128, 512, 1, True, 5, 28),   # 128x128 blocks, ragged M
 ])
-def test_matmul_qkv_rope_equals_matmul_then_rope(m, hq, hkv, dim, k, splits, bias, slot0, bits):
+def test_matmul_qkv_rope_equals_matmul_then_rope(m, hq, hkv, dim, k, splits, bias, slot0, tile, bits):
     """The fused q/k/v projection + RoPE + cache fill gives the projection of w4_matmul bit for bit,
     and q / keys / values within one bf16 rounding of rope_qkv_prefill over it (and of the oracle)."""
 
     from oracle.quant import pack_weight_bits_bf16
 
     ops = _ops()
-    rng = np.random.default_rng(m + dim + splits + bits)
+    rng = np.random.default_rng(m + dim + splits + bits + tile)
     n = (hq + 2 * hkv) * dim
     packed, scales = pack_weight_bits_bf16(bf16_normal(rng, (n, k), 0.02), 64, bits)
     gp, gs = _gpu_packed(packed, scales)
@@ -526,13 +532,17 @@ def test_matmul_qkv_rope_equals_matmul_then_rope(m, hq, hkv, dim, k, splits, bia
     gcos, gsin = to_gpu_bf16(cos), to_gpu_bf16(sin)
     gpos = torch.from_numpy(positions).cuda()
     matmul = ops.w4_matmul if bits == 4 else ops.w8_matmul
-    y_ref = matmul(gx, gp, gs, 64, bias=gb, splits=splits)
+    # the projection of the same plan: with splits=0 the q/k/v form prefers the unsplit
+    # epilogue, whose plan needs no workspace
+    from aotolith_amd import _lib
+    auto_unsplit = _lib.library().aoto_hip_w4_gemm_qkv_rope_workspace(m, k, tile, 0, hq, hkv, dim) == 0
+    y_ref = matmul(gx, gp, gs, 64, bias=gb, tile=tile, splits=splits or (1 if auto_unsplit else 0))
     pair_ref = torch.full((2, 1, hkv, cap, dim), 7.0, dtype=torch.bfloat16, device="cuda")
     q_ref = ops.rope_qkv_prefill(y_ref.view(1, m, n), gpos.view(1, m), gcos, gsin, pair_ref, query_heads=hq,
                                  kv_heads=hkv, head_dim=dim, slot0=slot0, zero_prefix=True)
     pair = torch.full((2, 1, hkv, cap, dim), 7.0, dtype=torch.bfloat16, device="cuda")
     y, q = ops.matmul_qkv_rope(gx, gp, gs, 64, gpos, gcos, gsin, pair, query_heads=hq, kv_heads=hkv, head_dim=dim,
-                               slot0=slot0, bias=gb, bits=bits, splits=splits)
+                               slot0=slot0, bias=gb, bits=bits, tile=tile, splits=splits)
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
     assert_bf16_parity(from_gpu_bf16(q), from_gpu_bf16(q_ref), max_ulp=1.0)
     assert_bf16_parity(from_gpu_bf16(pair), from_gpu_bf16(pair_ref), max_ulp=1.0)
