@@ -970,12 +970,16 @@ int aoto_hip_prefill_attention(const void* q, const void* keys, const void* valu
   if (!aligned16(q) || !aligned16(keys) || !aligned16(values) || !aligned8(out) || (kv_head_stride % 8) ||
       (kv_batch_stride % 8))
     return fail(AOTO_ERR_ARGUMENT, "prefill_attention: q/keys/values 16-byte, out 8-byte aligned");
-  char name[64];
-  snprintf(name, sizeof(name), "aoto_flash_attention_d%d", head_dim);
-  // one block per (128-query tile, batch, query head), the query tile slowest
+  // one block per (128-query tile, batch, query head), the query tile slowest.
+  // Grids that do not fill two 4-wave blocks per CU use 8-wave blocks whose two
+  // wave groups split the keys (every CU then runs two waves per SIMD throughout).
   const long long blocks = (long long)((tokens + 127) / 128) * batch * query_heads;
   if (blocks > 0x7FFFFFFFLL) return fail(AOTO_ERR_UNSUPPORTED, "prefill_attention: grid too large");
-  return launch(name, dim3((unsigned)blocks), dim3(256), 0, stream, q, keys, values, (long long)kv_batch_stride,
+  const bool split_keys = blocks <= 2LL * cu_count();
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_flash_attention_d%d%s", head_dim, split_keys ? "_k2" : "");
+  return launch(name, dim3((unsigned)blocks), dim3(split_keys ? 512 : 256), 0, stream, q, keys, values,
+                (long long)kv_batch_stride,
                 (long long)kv_head_stride, mask, (long long)mask_batch_stride, causal, key_start, tokens,
                 key_tokens, batch, query_heads, kv_heads, scale, out);
 }

@@ -39,6 +39,7 @@ namespace aoto {
 typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float fa_f32x16 __attribute__((ext_vector_type(16)));
 typedef short fa_s16x4 __attribute__((ext_vector_type(4)));
+typedef short fa_s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) fa_s16x4 fa_lds_s16x4;
 
 constexpr int kFlashQueries = 128;  // queries per block
@@ -57,11 +58,20 @@ AOTO_DEVICE fa_bf16x8 flash_v_operand(const uint16_t* vs, int t, int d_base, int
   const uint16_t* p0 = vs + row * STR + d0;
   const fa_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_s16x4*)(p0));
   const fa_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((fa_lds_s16x4*)(p0 + 8 * STR));
-  const short v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(fa_bf16x8, v);
+  // concatenated as vectors: through a short[8] the compiler merges halves with a
+  // v_bfi per read, and each merge waits for its read (the reads then retire one by one)
+  const fa_s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(fa_bf16x8, both);
 }
 
-template <int D>
+// KG key groups: with KG = 2 the block has 8 waves, two groups of 4 over the same
+// 128 queries; group g takes the g-th half of the block's key tiles, with its own
+// double-buffered K/V stages, and after the loop group 1 hands its softmax state
+// (reference max, sum, O) to group 0 through LDS, which combines the two as the
+// split merge of decode attention does. A CU then always holds two waves per SIMD
+// - one block of 8, where two 4-wave blocks would leave the heavy causal tile alone
+// once its light partner ends - and a q-tile's keys take half the time.
+template <int D, int KG>
 __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                      const uint16_t* __restrict__ v, long long kv_batch_stride,
                                      long long kv_head_stride, const uint8_t* __restrict__ mask,
@@ -75,9 +85,12 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   constexpr int CHUNKS = BK * D / 8;       // 16-byte chunks of one K (or V) tile
   constexpr int PER = 2 * CHUNKS / 256;    // chunks per thread per tile, K then V
   constexpr int ROW_CHUNKS = D / 8;
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BK * STR];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_all[KG][2][2][BK * STR];
+  const int group = KG == 1 ? 0 : (int)(threadIdx.x >> 8);
+  const int lt = (int)threadIdx.x & 255;  // thread index within the group
+  auto& lds = lds_all[group];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3;
   const int col = lane & 31, half = lane >> 5;
   // Query tiles in the order T-1, T-2, ..., T/2 (heaviest first), then 0, 1, ...:
   // blocks are dealt to the 8 XCDs round robin and to each XCD's CUs in turn, so the
@@ -88,7 +101,9 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   const int bh_count = batch * query_heads;
   const int tiles_q = (M + BQ - 1) / BQ;
   const int rank = (int)blockIdx.x / bh_count;
-  const int qt = rank < tiles_q / 2 ? tiles_q - 1 - rank : rank - tiles_q / 2;
+  // (KG = 2: one block per CU, so the second round of blocks goes to the CUs that
+  // finish first - heaviest first throughout pairs each heavy tile with a light one.)
+  const int qt = KG == 2 ? tiles_q - 1 - rank : (rank < tiles_q / 2 ? tiles_q - 1 - rank : rank - tiles_q / 2);
   const int slot = (int)blockIdx.x % bh_count;
   const int b = slot / query_heads;
   const int hs = slot % query_heads;
@@ -117,8 +132,14 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   if (!mask && causal) j_hi = min(Mk, q0 + BQ + shift);
   int w_hi = j_hi;
   if (!mask && causal) w_hi = min(j_hi, qa + 32 + shift);
-  const int tile_begin = (j_lo / BK) * BK;
-  const int n_tiles = j_hi > tile_begin ? (j_hi - tile_begin + BK - 1) / BK : 0;
+  const int tile_begin0 = (j_lo / BK) * BK;
+  const int n_all = j_hi > tile_begin0 ? (j_hi - tile_begin0 + BK - 1) / BK : 0;
+  // this group's contiguous share of the key tiles; both groups run the longer
+  // share's trip count (every thread meets every barrier)
+  const int share = (n_all + KG - 1) / KG;
+  const int tile_begin = tile_begin0 + group * share * BK;
+  const int n_tiles = max(0, min(share, n_all - group * share));
+  const int trips = share;
 
   // Rows outside [key_start, Mk) (without an explicit mask) are staged as zeros, so
   // a masked key's value never meets P (0 * NaN would poison the row). The load
@@ -127,7 +148,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   auto load_tile = [&](int j0, uint4 (&reg)[PER]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int c = (int)threadIdx.x + (i % (PER / 2)) * 256;
+      const int c = lt + (i % (PER / 2)) * 256;
       const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
       const uint16_t* base = i < PER / 2 ? kh : vh;
       reg[i] = *reinterpret_cast<const uint4*>(base + (size_t)min(j0 + row, Mk - 1) * D + cc * 8);
@@ -136,7 +157,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   auto store_tile = [&](int buffer, int j0, const uint4 (&reg)[PER]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int c = (int)threadIdx.x + (i % (PER / 2)) * 256;
+      const int c = lt + (i % (PER / 2)) * 256;
       const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
       const int j = j0 + row;
       const bool valid = j < Mk && (mask != nullptr || j >= key_start);
@@ -163,12 +184,12 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
+  for (int t = 0; t < trips; ++t) {
     const int j0 = tile_begin + t * BK;
     const int cur = t & 1;
     const bool more = t + 1 < n_tiles;
     if (more) load_tile(j0 + BK, stage);  // lands while this tile is computed
-    if (j0 < w_hi) {
+    if (t < n_tiles && j0 < w_hi) {
       const uint16_t* ks = lds[cur][0];
       const uint16_t* vs = lds[cur][1];
       fa_f32x16 sacc[2];
@@ -256,6 +277,32 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
     __syncthreads();
   }
 
+  if constexpr (KG == 2) {
+    // group 1's state to LDS (the tiles are dead: the loop ended on a barrier),
+    // then group 0 combines it with its own, lane by lane (same query, same d)
+    constexpr int REC = 2 + 16 * DT;
+    static_assert(4 * 64 * REC * 4 <= (int)sizeof(lds_all), "the handover fits the K/V stages");
+    float* hand = reinterpret_cast<float*>(&lds_all[0][0][0][0]) + (size_t)(wave * 64 + lane) * REC;
+    if (group == 1) {
+      hand[0] = run_max;
+      hand[1] = run_sum;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) hand[2 + 16 * d + e] = o[d][e];
+    }
+    __syncthreads();
+    if (group == 1) return;
+    const float m1 = hand[0], s1 = hand[1];
+    const float big = fmaxf(run_max, m1);
+    const float a0 = (big == -INFINITY || run_max == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(run_max - big);
+    const float a1 = (big == -INFINITY || m1 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m1 - big);
+    run_sum = run_sum * a0 + s1 * a1;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[d][e] = o[d][e] * a0 + hand[2 + 16 * d + e] * a1;
+  }
   const float total = xor32_sum(run_sum);
   if (qi >= M) return;
   const float inv = total > 0.f ? 1.0f / total : 0.f;
@@ -273,12 +320,17 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
 
 }  // namespace aoto
 
-#define AOTO_FLASH_INSTANCE(D)                                                                          \
-  extern "C" __global__ __launch_bounds__(256, 2) void aoto_flash_attention_d##D(                      \
+// aoto_flash_attention_d{D} (4-wave blocks, two per CU) and aoto_flash_attention_d{D}_k2
+// (8-wave blocks whose two wave groups split the keys).
+#define AOTO_FLASH_INSTANCE_KG(D, KG, SUFFIX, MINB)                                                     \
+  extern "C" __global__ __launch_bounds__(256 * KG, MINB) void aoto_flash_attention_d##D##SUFFIX(      \
       const uint16_t* q, const uint16_t* k, const uint16_t* v, long long kv_batch_stride,               \
       long long kv_head_stride, const uint8_t* mask, long long mask_batch_stride, int causal,           \
       int key_start, int M, int Mk, int batch, int query_heads, int kv_heads, float scale,              \
       uint16_t* out) {                                                                                  \
-    aoto::flash_attention_body<D>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride,    \
-                                  causal, key_start, M, Mk, batch, query_heads, kv_heads, scale, out);  \
+    aoto::flash_attention_body<D, KG>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
+                                      causal, key_start, M, Mk, batch, query_heads, kv_heads, scale, out); \
   }
+#define AOTO_FLASH_INSTANCE(D)           \
+  AOTO_FLASH_INSTANCE_KG(D, 1, , 2)      \
+  AOTO_FLASH_INSTANCE_KG(D, 2, _k2, 1)
