@@ -185,9 +185,12 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) 
       return true;
     case 4096:
       // Up to 16384 outputs (q/k/v, o, gate/up of an 8B model) a wave holds too
-      // few row tiles to amortize its own copy of x: one copy per block.
+      // few row tiles to amortize its own copy of x: one copy per block, and one
+      // block per CU - every block stages all of x, so fewer blocks move fewer
+      // bytes (Llama-8B, 1 / 2 / 3 / 4 blocks per CU: gate/up 14.8 / 16.3 / 17.1 /
+      // 16.8 us, q/k/v 5.39 / 5.46 / 5.84 / 5.80, o 4.14-4.18).
       if (N <= 16384)
-        *s = {32, 4, false, 2, true};
+        *s = {32, 4, false, 1, true};
       else
         *s = {32, 4, false};
       return true;
@@ -196,8 +199,10 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) 
       *s = {64, 3, true};
       return true;
     case 14336:
+      // 28 KB of x per block: one block per CU (down projection 10.28 against
+      // 10.75 us at two).
       if (paired) return false;
-      *s = {64, 7, false, 2, true};
+      *s = {64, 7, false, 1, true};
       return true;
     default:
       // Other reductions use the block-staged kernel.
