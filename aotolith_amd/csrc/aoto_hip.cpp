@@ -512,15 +512,21 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   return p;
 }
 
-// The q/k/v projection's split count: the requested one, or with 0 the unsplit
-// plan when its blocks' columns are whole heads (the RoPE epilogue: one launch,
-// measured on MI355X at M = 128 / 512 / 2048: 9.9 / 61.5 / 142.6 us against
-// 9.8 / 63.6 / 148.7 for the auto split and its RoPE reduce), else the auto split.
-int qkv_rope_splits(int M, int N, int K, int tile, int splits, int head_dim) {
-  if (splits != 0 || head_dim <= 0) return splits;
-  const GemmPlan p = gemm_plan(M, N, K, tile, 1, false);
+// The q/k/v projection's plan: the requested tile and split count, or with 0 the
+// unsplit plan when its blocks' columns are whole heads (the RoPE epilogue: one
+// launch, measured on MI355X at M = 128 / 512 / 2048: 9.9 / 61.5 / 142.6 us against
+// 9.8 / 63.6 / 148.7 for the auto split and its RoPE reduce), on 32-row blocks up to
+// 128 rows (twice the blocks; each wave's dequant per step is the same: 7.5 against
+// 9.3 us on 64-row blocks for Qwen2-0.5B at 128 rows), else the auto split.
+void qkv_rope_plan(int M, int N, int K, int head_dim, int* tile, int* splits) {
+  if (*splits != 0 || head_dim <= 0) return;
+  const int t = *tile == 0 && M <= 128 && 64 % head_dim == 0 ? 12 : *tile;
+  const GemmPlan p = gemm_plan(M, N, K, t, 1, false);
   const int bn = 64 * p.tn;
-  return bn % head_dim == 0 && N % bn == 0 ? 1 : 0;
+  if (bn % head_dim == 0 && N % bn == 0) {
+    *tile = t;
+    *splits = 1;
+  }
 }
 
 }  // namespace
@@ -541,7 +547,8 @@ size_t aoto_hip_w4_gemm_qkv_rope_workspace(int M, int K, int tile, int splits, i
                                            int head_dim) {
   if (query_heads <= 0 || kv_heads <= 0 || head_dim <= 0) return 0;
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  return aoto_hip_w4_gemm_workspace(M, N, K, tile, qkv_rope_splits(M, N, K, tile, splits, head_dim));
+  qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  return aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
 }
 
 }  // extern "C"
@@ -573,8 +580,8 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       (gate && !aligned8(gate)) || !aligned16(words) || (paired && !aligned16(up_words)))
     return fail(AOTO_ERR_ARGUMENT, "%s: x and words must be 16-byte aligned, y/bias/residual/gate 8-byte aligned",
                 what);
-  if (tile != 0 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
-    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 14, 18, 24, 28", what, tile);
+  if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
+    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28", what, tile);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
   if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
     return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
@@ -650,9 +657,9 @@ int qkv_rope_gemm(int bits, const void* x, const int32_t* words, const void* sca
                            (uint16_t*)q_out, (uint16_t*)pair, query_heads, kv_heads, head_dim, capacity, slot0,
                            zero_prefix};
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  return packed_gemm(bits, x, words, scales, bias, nullptr, nullptr, y, M, N, K, group, tile,
-                     qkv_rope_splits(M, N, K, tile, splits, head_dim), workspace, stream, nullptr, nullptr, nullptr,
-                     0.f, nullptr, &rope);
+  qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  return packed_gemm(bits, x, words, scales, bias, nullptr, nullptr, y, M, N, K, group, tile, splits, workspace,
+                     stream, nullptr, nullptr, nullptr, 0.f, nullptr, &rope);
 }
 
 // GEMM with a residual epilogue followed by the row RMSNorm of its result.

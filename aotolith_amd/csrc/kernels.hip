@@ -52,24 +52,30 @@ AOTO_GEMV_STREAM_ARGMAX(64, 1, 0, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 3, 0, true)
 
 // Prefill GEMM: {code width} x {n tiles per wave} x {m tiles per wave} x epilogue.
+AOTO_GEMM_EPILOGUES(4, 1, 2)
 AOTO_GEMM_EPILOGUES(4, 1, 4)
 AOTO_GEMM_EPILOGUES(4, 1, 8)
 AOTO_GEMM_EPILOGUES(4, 2, 4)
 AOTO_GEMM_EPILOGUES(4, 2, 8)
+AOTO_GEMM_EPILOGUES(8, 1, 2)
 AOTO_GEMM_EPILOGUES(8, 1, 4)
 AOTO_GEMM_EPILOGUES(8, 1, 8)
 AOTO_GEMM_EPILOGUES(8, 2, 4)
 AOTO_GEMM_EPILOGUES(8, 2, 8)
 // The MLP's gate/up pair in one pass: {code width} x {n tiles} x {m tiles}.
+AOTO_GEMM_PAIRED_INSTANCE(4, 1, 2)
 AOTO_GEMM_PAIRED_INSTANCE(4, 1, 4)
 AOTO_GEMM_PAIRED_INSTANCE(4, 1, 8)
 AOTO_GEMM_PAIRED_INSTANCE(4, 2, 4)
 AOTO_GEMM_PAIRED_INSTANCE(4, 2, 8)
+AOTO_GEMM_PAIRED_INSTANCE(8, 1, 2)
 AOTO_GEMM_PAIRED_INSTANCE(8, 1, 4)
 AOTO_GEMM_PAIRED_INSTANCE(8, 1, 8)
 AOTO_GEMM_PAIRED_INSTANCE(8, 2, 4)
 AOTO_GEMM_PAIRED_INSTANCE(8, 2, 8)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
+AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)
+AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 1)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 4, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 4, 1)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 8, 0)
@@ -78,6 +84,8 @@ AOTO_GEMM_ROPE_INSTANCE(4, 2, 4, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 2, 4, 1)
 AOTO_GEMM_ROPE_INSTANCE(4, 2, 8, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 2, 8, 1)
+AOTO_GEMM_ROPE_INSTANCE(8, 1, 2, 0)
+AOTO_GEMM_ROPE_INSTANCE(8, 1, 2, 1)
 AOTO_GEMM_ROPE_INSTANCE(8, 1, 4, 0)
 AOTO_GEMM_ROPE_INSTANCE(8, 1, 4, 1)
 AOTO_GEMM_ROPE_INSTANCE(8, 1, 8, 0)

@@ -109,7 +109,7 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales,
  *   gate     bf16 [M, N]  -> bf16(acc * silu(gate[m][n]))
  * Limits: K % 64 == 0, N % 16 == 0, group % 32 == 0 dividing K. x 16-byte and
  * y/bias/residual/gate 8-byte aligned. tile: 0 chooses, else 14/18/24/28 (n
- * tiles x m tiles of 16 per wave). splits: 0 chooses (small grids split the
+ * tiles x m tiles of 16 per wave) or 12 (32-row blocks). splits: 0 chooses (small grids split the
  * reduction), else the split-K count; a split launch stores f32 partial tiles
  * in `workspace` (aoto_hip_w4_gemm_workspace() bytes, 16-byte aligned) and a
  * second launch sums them and applies the epilogue. y must not alias x. */
@@ -208,8 +208,9 @@ int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const vo
  * x [M, K]; the weight packs N = (Hq + 2 Hkv) * head_dim rows; y [M, N] receives
  * the projection; q_out [Hq, M, head_dim]; pair [2, Hkv, capacity, head_dim] gets
  * rotated keys / values at slots slot0 .. slot0 + M - 1 (slots below slot0 zeroed
- * when zero_prefix != 0); positions[M] int64. tile as aoto_hip_w4_gemm; splits 0
- * chooses (unsplit whenever the epilogue form applies), else as aoto_hip_w4_gemm;
+ * when zero_prefix != 0); positions[M] int64. tile and splits as aoto_hip_w4_gemm,
+ * with 0 / 0 choosing the unsplit epilogue form whenever it applies (32-row blocks
+ * up to 128 rows);
  * workspace: aoto_hip_w4_gemm_qkv_rope_workspace() bytes. */
 int aoto_hip_w4_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
                               int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,

@@ -51,7 +51,7 @@ GEMM_CASES = [
 
 
 @pytest.mark.parametrize("m,n,k,group", GEMM_CASES)
-@pytest.mark.parametrize("tile", [0, 14, 28])
+@pytest.mark.parametrize("tile", [0, 12, 14, 28])
 def test_w4_matmul_plain(m, n, k, group, tile):
     rng = np.random.default_rng(m + n + k + tile)
     packed, scales = _packed(rng, n, k, group)
@@ -506,6 +506,8 @@ def test_matmul_residual_norm_rejects_wide_rows_and_aliasing():
     (128, 14, 2, 64, 896, 7, True, 64, 0),   # split 7 ways: the split-K sum with RoPE and the fill
     (128, 14, 2, 64, 896, 1, True, 0, 0),    # unsplit 64-column blocks: RoPE in the GEMM epilogue
     (128, 14, 2, 64, 896, 1, True, 64, 0),   # the same with a zeroed prefix
+    (128, 14, 2, 64, 896, 1, True, 9, 14),   # 64-row blocks (the auto plan takes 32-row ones)
+    (72, 14, 2, 64, 896, 1, False, 5, 12),   # 32-row blocks, ragged M
     (40, 8, 2, 128, 512, 3, False, 9, 0),    # head_dim 128, no bias, ragged M, forced split
     (40, 8, 2, 128, 512, 1, False, 9, 24),   # 128-column blocks hold one 128-wide head: epilogue
     (40, 8, 2, 128, 512, 1, True, 9, 14),    # 64-column blocks split a head: GEMM, then the RoPE kernel

@@ -160,7 +160,7 @@ GEMM_CASES = [
 
 
 @pytest.mark.parametrize("m,n,k,group", GEMM_CASES)
-@pytest.mark.parametrize("tile", [0, 28])
+@pytest.mark.parametrize("tile", [0, 12, 28])
 def test_w8_matmul_plain(m, n, k, group, tile):
     rng = np.random.default_rng(m + n + k + tile + 8)
     packed, scales = _packed(rng, n, k, group)
