@@ -476,10 +476,14 @@ struct GemmPlan {
 GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
   if (tile == 0) {
-    // 64-row blocks up to M = 128 (the latency-bound prefill of a small model
-    // wants the blocks), 128-row blocks beyond: measured on MI355X with the
+    // Up to M = 128 (the latency-bound prefill of a small model wants blocks)
+    // 32-row blocks - a wave's dequant per k-step does not depend on the rows,
+    // so halving them halves its MFMA time and doubles the blocks (Qwen2-0.5B at
+    // 128 rows: o + reduce/norm 8.6 -> 7.9 us, down 13.1 -> 12.4, prefill 104.0k
+    // -> 106.1k tok/s) - except the paired gate/up, faster on 64-row blocks
+    // (11.3 against 12.3 us); 128-row blocks beyond: measured on MI355X with the
     // 128-k step kernel, M = 256: gate/up 114 -> 83 us, down 84 -> 58 us.
-    p.tm = M <= 128 ? 4 : 8;
+    p.tm = M <= 128 ? (paired ? 4 : 2) : 8;
     const long long mb = (M + 16 * p.tm - 1) / (16 * p.tm);
     // 128-column blocks with 128-row blocks, except for the paired gate/up,
     // whose two accumulator sets fit one wave's registers only at 64 columns
