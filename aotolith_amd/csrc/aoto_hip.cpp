@@ -993,7 +993,7 @@ int aoto_hip_prefill_attention(const void* q, const void* keys, const void* valu
   if (blocks > 0x7FFFFFFFLL) return fail(AOTO_ERR_UNSUPPORTED, "prefill_attention: grid too large");
   const bool split_keys = blocks <= 2LL * cu_count();
   char name[64];
-  snprintf(name, sizeof(name), "aoto_flash_attention_d%d%s", head_dim, split_keys ? "_k2" : "");
+  snprintf(name, sizeof(name), "aoto_flash_attention_d%d%s%s", head_dim, split_keys ? "_k2" : "", mask ? "_m" : "");
   return launch(name, dim3((unsigned)blocks), dim3(split_keys ? 512 : 256), 0, stream, q, keys, values,
                 (long long)kv_batch_stride,
                 (long long)kv_head_stride, mask, (long long)mask_batch_stride, causal, key_start, tokens,

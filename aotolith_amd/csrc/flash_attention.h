@@ -15,8 +15,12 @@
 // [B][M][Hq*D] (the o projection's input rows).
 //
 // Block: 4 waves, 128 queries of one head (wave w: queries q0 + 32w .. q0 + 32w + 31).
-// Key tiles of 64 rows are staged in LDS row-major, K and V alike (row stride
-// D + 16 bf16: the row reads below hit distinct banks), double-buffered: the next
+// Key tiles of 64 rows are staged in LDS row-major, each with its own row stride
+// so that its reads touch all 64 four-byte banks once per phase: K rows D + 8 bf16
+// apart (a 16-byte read per lane, 16 lanes a phase: rows 4 banks apart), V rows
+// D + 32 apart (the transpose reads' 4 rows of 16 banks start 16 banks apart).
+// One stride D + 16 for both left every K and V read 2-way conflicted (rocprof
+// SQ_LDS_BANK_CONFLICT = 128 cycles per wave and tile). Double-buffered: the next
 // tile's global loads are in flight while the current tile is computed, one
 // barrier per tile. Per wave and key tile, with v_mfma_f32_32x32x16_bf16:
 //   S^T (2 x [32 keys x 32 queries]) = K . Q^T   A: K rows from LDS, B: Q in registers
@@ -64,6 +68,8 @@ AOTO_DEVICE fa_bf16x8 flash_v_operand(const uint16_t* vs, int t, int d_base, int
   return __builtin_bit_cast(fa_bf16x8, both);
 }
 
+// MASKED: the explicit-mask form (a separate instance, so the causal form carries
+// no mask registers).
 // KG key groups: with KG = 2 the block has 8 waves, two groups of 4 over the same
 // 128 queries; group g takes the g-th half of the block's key tiles, with its own
 // double-buffered K/V stages, and after the loop group 1 hands its softmax state
@@ -71,7 +77,7 @@ AOTO_DEVICE fa_bf16x8 flash_v_operand(const uint16_t* vs, int t, int d_base, int
 // split merge of decode attention does. A CU then always holds two waves per SIMD
 // - one block of 8, where two 4-wave blocks would leave the heavy causal tile alone
 // once its light partner ends - and a q-tile's keys take half the time.
-template <int D, int KG>
+template <int D, int KG, bool MASKED>
 __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                      const uint16_t* __restrict__ v, long long kv_batch_stride,
                                      long long kv_head_stride, const uint8_t* __restrict__ mask,
@@ -79,18 +85,23 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
                                      int batch, int query_heads, int kv_heads, float scale,
                                      uint16_t* __restrict__ out) {
   constexpr int BQ = kFlashQueries, BK = kFlashKeys;
-  constexpr int STR = D + 16;              // bf16 per staged row
+  constexpr int STRK = D + 8;              // bf16 per staged K row
+  constexpr int STRV = D + 32;             // bf16 per staged V row
+  constexpr int VOFF = BK * STRK;          // V tile after the K tile in a stage
   constexpr int DS = D / 16;               // k-steps of S^T (16 d each)
   constexpr int DT = D / 32;               // 32-row d tiles of O^T
   constexpr int CHUNKS = BK * D / 8;       // 16-byte chunks of one K (or V) tile
   constexpr int PER = 2 * CHUNKS / 256;    // chunks per thread per tile, K then V
   constexpr int ROW_CHUNKS = D / 8;
-  __shared__ __attribute__((aligned(16))) uint16_t lds_all[KG][2][2][BK * STR];
-  const int group = KG == 1 ? 0 : (int)(threadIdx.x >> 8);
+  __shared__ __attribute__((aligned(16))) uint16_t lds_all[KG][2][BK * (STRK + STRV)];
+  // wave and group are uniform per wave; saying so (readfirstlane) keeps the tile
+  // loop's branches scalar - as exec-masked branches their paths merged, and the
+  // loads of one path made the other wait for them
+  const int group = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
   const int lt = (int)threadIdx.x & 255;  // thread index within the group
   auto& lds = lds_all[group];
 
-  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) & 3);
   const int col = lane & 31, half = lane >> 5;
   // Query tiles in the order T-1, T-2, ..., T/2 (heaviest first), then 0, 1, ...:
   // blocks are dealt to the 8 XCDs round robin and to each XCD's CUs in turn, so the
@@ -126,12 +137,10 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
     for (int s = 0; s < DS; ++s) qf[s] = *reinterpret_cast<const fa_bf16x8*>(qp + 16 * s);
   }
 
-  // Keys this block can see, and this wave.
-  const int j_lo = mask ? 0 : max(0, key_start);
+  // Keys this block can see.
+  const int j_lo = MASKED ? 0 : max(0, key_start);
   int j_hi = Mk;
-  if (!mask && causal) j_hi = min(Mk, q0 + BQ + shift);
-  int w_hi = j_hi;
-  if (!mask && causal) w_hi = min(j_hi, qa + 32 + shift);
+  if (!MASKED && causal) j_hi = min(Mk, q0 + BQ + shift);
   const int tile_begin0 = (j_lo / BK) * BK;
   const int n_all = j_hi > tile_begin0 ? (j_hi - tile_begin0 + BK - 1) / BK : 0;
   // this group's contiguous share of the key tiles; both groups run the longer
@@ -142,27 +151,36 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   const int trips = share;
 
   // Rows outside [key_start, Mk) (without an explicit mask) are staged as zeros, so
-  // a masked key's value never meets P (0 * NaN would poison the row). The load
-  // address is clamped into the head and the zero is selected when the tile is
-  // written to LDS (no branch or wait around the loads themselves).
+  // a masked key's value never meets P (0 * NaN would poison the row); tiles wholly
+  // inside are stored without that test. The load address is clamped into the
+  // head (no branch or wait around the loads themselves).
+  auto load_one = [&](int i, int j0, uint4 (&reg)[PER]) {
+    const int c = lt + (i % (PER / 2)) * 256;
+    const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
+    const uint16_t* base = i < PER / 2 ? kh : vh;
+    reg[i] = *reinterpret_cast<const uint4*>(base + (size_t)min(j0 + row, Mk - 1) * D + cc * 8);
+  };
   auto load_tile = [&](int j0, uint4 (&reg)[PER]) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = lt + (i % (PER / 2)) * 256;
-      const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
-      const uint16_t* base = i < PER / 2 ? kh : vh;
-      reg[i] = *reinterpret_cast<const uint4*>(base + (size_t)min(j0 + row, Mk - 1) * D + cc * 8);
-    }
+    for (int i = 0; i < PER; ++i) load_one(i, j0, reg);
   };
   auto store_tile = [&](int buffer, int j0, const uint4 (&reg)[PER]) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
+    auto slot = [&](int i) {
       const int c = lt + (i % (PER / 2)) * 256;
       const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
-      const int j = j0 + row;
-      const bool valid = j < Mk && (mask != nullptr || j >= key_start);
-      *reinterpret_cast<uint4*>(&lds[buffer][i < PER / 2 ? 0 : 1][row * STR + cc * 8]) =
-          valid ? reg[i] : make_uint4(0, 0, 0, 0);
+      return reinterpret_cast<uint4*>(&lds[buffer][i < PER / 2 ? row * STRK : VOFF + row * STRV] + cc * 8);
+    };
+    if (j0 + BK <= Mk && (MASKED || j0 >= key_start)) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) *slot(i) = reg[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int j = j0 + (lt + (i % (PER / 2)) * 256) / ROW_CHUNKS;
+        // zeroed by a mask, not a select: a select became a branch around register copies
+        const uint32_t keep = (j < Mk && (MASKED || j >= key_start)) ? 0xFFFFFFFFu : 0u;
+        *slot(i) = make_uint4(reg[i].x & keep, reg[i].y & keep, reg[i].z & keep, reg[i].w & keep);
+      }
     }
   };
 
@@ -172,66 +190,63 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   for (int t = 0; t < DT; ++t) o[t] = fa_f32x16{};
   float run_max = -INFINITY, run_sum = 0.f;
 
-  uint4 stage[PER];
-  if (n_tiles > 0) {
-    load_tile(tile_begin, stage);
-    store_tile(0, tile_begin, stage);
-  }
-  // Nothing may be pending when the loop starts: the compiler's wait counting
-  // merges this point from both branches above, and a Q load it believed still in
-  // flight would make every S^T product below wait for the next tile's prefetch
-  // (loads retire in issue order).
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  for (int t = 0; t < trips; ++t) {
+  // Tile t from stage `cur`, and the loads of the tile at `jn` into `stage`: one
+  // load after every second S^T product (2·DS products, PER = DS loads), so the
+  // CU's address path works through the next tile's 32 KB per group while the
+  // products run - issued all at once after the barrier, the eight waves' loads
+  // queued there for ~0.5 us (a fifth of the interval) before the first product.
+  // Every wave computes every trip: a tile past the group's share (t >= n_tiles,
+  // the stage then holds a clamped copy) or past the wave's causal edge is fully
+  // masked (p = 0). Skipping it put the next tile's loads on two paths, and the
+  // compiler's wait counting, merging them, made the computing path wait for them.
+  auto compute_tile = [&](int t, int cur, int jn, uint4 (&stage)[PER]) {
     const int j0 = tile_begin + t * BK;
-    const int cur = t & 1;
-    const bool more = t + 1 < n_tiles;
-    if (more) load_tile(j0 + BK, stage);  // lands while this tile is computed
-    if (t < n_tiles && j0 < w_hi) {
-      const uint16_t* ks = lds[cur][0];
-      const uint16_t* vs = lds[cur][1];
+    const bool real = t < n_tiles;
+    {
+      const uint16_t* ks = lds[cur];
+      const uint16_t* vs = lds[cur] + VOFF;
       fa_f32x16 sacc[2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         sacc[sub] = fa_f32x16{};
 #pragma unroll
         for (int s = 0; s < DS; ++s) {
-          const fa_bf16x8 a = *reinterpret_cast<const fa_bf16x8*>(ks + (sub * 32 + col) * STR + 16 * s + 8 * half);
+          const fa_bf16x8 a = *reinterpret_cast<const fa_bf16x8*>(ks + (sub * 32 + col) * STRK + 16 * s + 8 * half);
           sacc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[sub], 0, 0, 0);
+          if ((sub * DS + s) & 1) load_one((sub * DS + s) >> 1, jn, stage);
         }
       }
       // Scores of key j0 + 32 sub + 8 (e / 4) + 4 half + e % 4 for query qi; only
       // tiles that straddle the causal diagonal, the left pad or the end of the keys
       // (or any tile, with an explicit mask) test each key.
-      const bool whole = !mask && j0 >= key_start && j0 + BK <= Mk && (!causal || j0 + BK - 1 <= qa + shift);
+      const bool whole = !MASKED && real && j0 >= key_start && j0 + BK <= Mk && (!causal || j0 + BK - 1 <= qa + shift);
       if (!whole) {
         const int key0 = j0 + 4 * half;
-        if (mask) {
+        if constexpr (MASKED) {
           const uint8_t* mrow = mask + (size_t)b * mask_batch_stride + (size_t)qrow * Mk;
-          uint32_t keep[2][16];
 #pragma unroll
-          for (int sub = 0; sub < 2; ++sub)
+          for (int sub = 0; sub < 2; ++sub) {
+            uint32_t keep[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
               const int j = key0 + 32 * sub + 8 * (e >> 2) + (e & 3);
-              keep[sub][e] = mrow[min(j, Mk - 1)];
-              if (j >= Mk) keep[sub][e] = 0;
+              keep[e] = (real && j < Mk) ? mrow[min(j, Mk - 1)] : 0u;
             }
 #pragma unroll
-          for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
             for (int e = 0; e < 16; ++e)
-              if (!keep[sub][e]) sacc[sub][e] = -INFINITY;
+              if (!keep[e]) sacc[sub][e] = -INFINITY;
+          }
         } else {
-          const int last = causal ? min(Mk - 1, qi + shift) : Mk - 1;
+          // key key0 + c is kept for lo <= c <= hi; c is a constant per element, so
+          // the tests compare against two registers instead of 32 key indices
+          const int lo = key_start - key0;
+          const int hi = real ? (causal ? min(Mk - 1, qi + shift) : Mk - 1) - key0 : -1;
 #pragma unroll
           for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-              const int j = key0 + 32 * sub + 8 * (e >> 2) + (e & 3);
-              if (j < key_start || j > last) sacc[sub][e] = -INFINITY;
+              const int c = 32 * sub + 8 * (e >> 2) + (e & 3);
+              if (c < lo || c > hi) sacc[sub][e] = -INFINITY;
             }
         }
       }
@@ -269,20 +284,43 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
         const fa_bf16x8 pb = __builtin_bit_cast(fa_bf16x8, packed);
 #pragma unroll
         for (int d = 0; d < DT; ++d)
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(flash_v_operand<STR>(vs, kt, 32 * d, lane), pb, o[d], 0,
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(flash_v_operand<STRV>(vs, kt, 32 * d, lane), pb, o[d], 0,
                                                           0, 0);
       }
     }
-    if (more) store_tile(cur ^ 1, j0 + BK, stage);
+  };
+
+  // The first stage is written even for a group without tiles: every trip computes
+  // (fully masked past the share), and P = 0 meeting uninitialized LDS in V could
+  // meet a NaN bit pattern; clamped rows hold keys, rows outside them zeros.
+  uint4 stage[PER];
+  load_tile(tile_begin, stage);
+  store_tile(0, tile_begin, stage);
+  // Nothing may be pending when the loop starts: a Q load the compiler's wait
+  // counting believed still in flight would make every S^T product below wait for
+  // the next tile's prefetch (loads retire in issue order).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // The next tile's loads and stores are unconditional - past the group's share a
+  // clamped tile goes into the stage no product reads again (its last reads ended
+  // before the previous barrier) - so the compiler's wait counting sees the same
+  // loads on every path: with a conditional store it assumed loads still in
+  // flight at the loop head and waited for them before reusing their registers.
+  const int last_tile = max(n_tiles - 1, 0);
+  for (int t = 0; t < trips; ++t) {
+    const int jn = tile_begin + min(t + 1, last_tile) * BK;
+    compute_tile(t, t & 1, jn, stage);
+    store_tile((t + 1) & 1, jn, stage);
     __syncthreads();
   }
 
   if constexpr (KG == 2) {
-    // group 1's state to LDS (the tiles are dead: the loop ended on a barrier),
-    // then group 0 combines it with its own, lane by lane (same query, same d)
+    // group 1's state into its own stages (dead: the loop ended on a barrier), then
+    // group 0 combines it with its own, lane by lane (same query, same d)
     constexpr int REC = 2 + 16 * DT;
-    static_assert(4 * 64 * REC * 4 <= (int)sizeof(lds_all), "the handover fits the K/V stages");
-    float* hand = reinterpret_cast<float*>(&lds_all[0][0][0][0]) + (size_t)(wave * 64 + lane) * REC;
+    static_assert(4 * 64 * REC * 4 <= (int)sizeof(lds_all[1]), "the handover fits group 1's stages");
+    float* hand = reinterpret_cast<float*>(&lds_all[1][0][0]) + (size_t)(wave * 64 + lane) * REC;
     if (group == 1) {
       hand[0] = run_max;
       hand[1] = run_sum;
@@ -321,16 +359,18 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
 }  // namespace aoto
 
 // aoto_flash_attention_d{D} (4-wave blocks, two per CU) and aoto_flash_attention_d{D}_k2
-// (8-wave blocks whose two wave groups split the keys).
-#define AOTO_FLASH_INSTANCE_KG(D, KG, SUFFIX, MINB)                                                     \
+// (8-wave blocks whose two wave groups split the keys); the _m forms take an explicit mask.
+#define AOTO_FLASH_INSTANCE_KG(D, KG, MASKED, SUFFIX, MINB)                                             \
   extern "C" __global__ __launch_bounds__(256 * KG, MINB) void aoto_flash_attention_d##D##SUFFIX(      \
       const uint16_t* q, const uint16_t* k, const uint16_t* v, long long kv_batch_stride,               \
       long long kv_head_stride, const uint8_t* mask, long long mask_batch_stride, int causal,           \
       int key_start, int M, int Mk, int batch, int query_heads, int kv_heads, float scale,              \
       uint16_t* out) {                                                                                  \
-    aoto::flash_attention_body<D, KG>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
+    aoto::flash_attention_body<D, KG, MASKED>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
                                       causal, key_start, M, Mk, batch, query_heads, kv_heads, scale, out); \
   }
-#define AOTO_FLASH_INSTANCE(D)           \
-  AOTO_FLASH_INSTANCE_KG(D, 1, , 2)      \
-  AOTO_FLASH_INSTANCE_KG(D, 2, _k2, 1)
+#define AOTO_FLASH_INSTANCE(D)                 \
+  AOTO_FLASH_INSTANCE_KG(D, 1, false, , 2)     \
+  AOTO_FLASH_INSTANCE_KG(D, 2, false, _k2, 1)  \
+  AOTO_FLASH_INSTANCE_KG(D, 1, true, _m, 2)    \
+  AOTO_FLASH_INSTANCE_KG(D, 2, true, _k2_m, 1)

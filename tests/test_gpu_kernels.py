@@ -238,6 +238,9 @@ PREFILL_CASES = [
     (14, 2, 64, 128, 77),    # left-padded bucket
     (32, 8, 128, 200, 200),  # Llama heads, ragged length
     (4, 4, 64, 64, 64),      # MHA
+    (4, 2, 64, 16, 16),      # one key tile: the block's second key group has none
+    (4, 2, 64, 16, 11),      # ... left-padded
+    (32, 8, 128, 40, 40),    # ... at D = 128
 ]
 
 
@@ -257,6 +260,30 @@ def test_prefill_attention_causal_left_pad(hq, hkv, dim, m, length):
     assert_bf16_parity(got, expected, max_ulp=None, atol=2.0 ** -6)
     if length < m:
         assert np.all(got[:, :, : m - length] == 0.0), "fully masked pad rows must be zero"
+
+
+def test_prefill_attention_single_tile_ignores_stale_lds():
+    """A block with one key tile leaves its second key group without tiles; that
+    group's masked trip must compute on a staged tile, not on LDS an earlier launch
+    left behind - here NaN values, which P = 0 would turn into a NaN output."""
+    rng = np.random.default_rng(12)
+    ops = _ops()
+    # an earlier launch of the same kernel (8-wave blocks on every CU) with NaN values
+    hq, hkv, dim, m = 32, 8, 64, 1024
+    q = bf16_normal(rng, (1, hq, m, dim))
+    k = bf16_normal(rng, (1, hkv, m, dim))
+    v = np.full((1, hkv, m, dim), np.nan, dtype=np.float32)
+    ops.prefill_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(v), causal=True)
+    torch.cuda.synchronize()
+    hq, hkv, m = 4, 2, 16
+    q = bf16_normal(rng, (1, hq, m, dim))
+    k = bf16_normal(rng, (1, hkv, m, dim))
+    v = bf16_normal(rng, (1, hkv, m, dim))
+    expected = oracle.attention(q, k, v, oracle.prefill_mask(m, m))
+    out = ops.prefill_attention(to_gpu_bf16(q), to_gpu_bf16(k), to_gpu_bf16(v), causal=True)
+    got = from_gpu_bf16(out).reshape(1, m, hq, dim).transpose(0, 2, 1, 3)
+    assert not np.isnan(got).any()
+    assert_bf16_parity(got, expected, max_ulp=None, atol=2.0 ** -6)
 
 
 def test_prefill_attention_explicit_mask_matches_the_implicit_one():
