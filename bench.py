@@ -506,6 +506,35 @@ def run_llama8b(args, torch, ops) -> dict:
     return out
 
 
+def measure_prefill_attention(spec, torch, ops, tokens: int, launches: int = 20, std: float = 1.0) -> dict:
+    """The causal prefill attention of one layer at ``tokens`` queries, timed alone.
+
+    q [1, Hq, tokens, D], keys and values [1, Hkv, tokens, D] of N(0, std^2) bf16,
+    the model's GQA heads and 1/sqrt(D) scale; the median of 5 replays of a HIP
+    graph of ``launches`` launches between HIP events. FLOP = 2 * tokens^2 * D * Hq
+    (the causal half of 4 * M * Mk * D * Hq), against the bf16 MFMA peak. The time
+    depends on the data (MI355X lowers its clock under MFMA work on busier bit
+    patterns: ~10-20% between std 1 and 0.02 at 2048 tokens), hence ``std``.
+    """
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    hq, hkv, d = spec.heads, spec.kv_heads, spec.head_dim
+    q = (torch.randn(1, hq, tokens, d, generator=gen, device="cuda") * std).to(torch.bfloat16)
+    k = (torch.randn(1, hkv, tokens, d, generator=gen, device="cuda") * std).to(torch.bfloat16)
+    v = (torch.randn(1, hkv, tokens, d, generator=gen, device="cuda") * std).to(torch.bfloat16)
+    out = torch.empty(1, tokens, hq * d, device="cuda", dtype=torch.bfloat16)
+
+    def body():
+        for _ in range(launches):
+            ops.prefill_attention(q, k, v, causal=True, scale=d ** -0.5, out=out)
+
+    us = _graph_us(torch, body, launches)
+    flops = 2.0 * tokens * tokens * d * hq
+    return {"kernel": f"aoto_flash_attention_d{d}* (causal)", "avg_us": round(us, 3), "flops": flops,
+            "tflops": round(flops / us / 1e6, 1), "frac": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> dict:
     """One decoder layer's prefill projections at ``tokens`` rows, timed alone.
 
@@ -599,6 +628,10 @@ def main() -> int:
                         help="weight code width of the qwen0.5b workload (8: the quantize_bits=8 variant)")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the LM-head GEMV loop, after a calibration copy of 256 MiB (for counter runs)")
+    parser.add_argument("--prefill-attention-only", type=int, default=0, metavar="TOKENS",
+                        help="only the causal prefill attention of one layer at TOKENS queries (timing, counter runs)")
+    parser.add_argument("--input-std", type=float, default=1.0,
+                        help="standard deviation of the --prefill-attention-only inputs")
     parser.add_argument("--prefill-gemm-only", type=int, default=0, metavar="TOKENS",
                         help="only one layer's prefill GEMMs at TOKENS rows (for MFMA counter runs)")
     args = parser.parse_args()
@@ -622,6 +655,12 @@ def main() -> int:
         torch.cuda.synchronize()
         lm = measure_lm_head_gemv(spec, torch, ops, bits=args.bits)
         print(json.dumps({"calibration_copy_bytes": src.numel() * 4, **lm}), flush=True)
+        return 0
+    if args.prefill_attention_only:
+        spec = qwen_spec() if args.workload == "qwen0.5b" else llama8b_spec()
+        result = measure_prefill_attention(spec, torch, ops, args.prefill_attention_only, std=args.input_std)
+        print(json.dumps({"workload": f"{args.workload} prefill attention", "tokens": args.prefill_attention_only,
+                          "input_std": args.input_std, "peak_tflops": MFMA_BF16_PEAK_TFLOPS, **result}), flush=True)
         return 0
     if args.prefill_gemm_only:
         spec = qwen_spec() if args.workload == "qwen0.5b" else llama8b_spec()
