@@ -171,8 +171,10 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) 
     case 896:
       // Long outputs: 8 lanes x 4 chunks (32 slots for the 28 chunks of a row;
       // the 4 spare slots repeat the last chunk), x read from LDS so the two
-      // weight register sets fit; 4 blocks per CU (measured in one process
-      // against 3 and 5: 14.3 vs 15.6 / 14.6 us for the 151936-row LM head).
+      // weight register sets fit; 2 blocks per CU - each wave then takes ~9 row
+      // tiles, over which its x staging and pipeline fill and drain amortize
+      // (greedy loop's LM-head kernel, 151936 rows, 1 / 2 / 3 / 4 / 5 / 6 / 8
+      // blocks per CU: 16.7 / 14.9 / 15.5 / 16.0 / 16.8 / 17.0 / 17.5 us).
       // Short outputs: the multi-row direct form where one normalized copy of x
       // serves several rows (paired gate/up: 4 rows per lane, 3.9 vs 4.3 us for
       // Qwen's 2 x 4864 rows; normed q/k/v: 2, 2.45 vs 2.6 us); without a norm
@@ -181,7 +183,7 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) 
         *s = {32, 1, true};
         s->rows = gemv_rows(32, paired ? 4 : (norm ? 2 : 0));
       } else
-        *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 4};
+        *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 2};
       return true;
     case 4096:
       // Up to 16384 outputs (q/k/v, o, gate/up of an 8B model) a wave holds too
