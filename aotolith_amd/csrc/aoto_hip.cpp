@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "aoto_hip.h"
 #include "gemm_args.h"
@@ -53,6 +54,11 @@ namespace {
 struct DeviceModule {
   hipModule_t module = nullptr;
   std::unordered_map<std::string, hipFunction_t> functions;
+  // Modules replaced by a later load. They stay loaded: a HIP graph captured
+  // earlier holds their kernel handles, and replaying it after an unload would
+  // execute freed code (a GPU memory fault). Released by
+  // aoto_hip_unload_code_object only.
+  std::vector<hipModule_t> retired;
 };
 
 std::mutex g_mutex;
@@ -344,7 +350,7 @@ int aoto_hip_load_code_object(const void* image, size_t size) {
     return fail(AOTO_ERR_HIP, "hipModuleLoadData (%zu bytes): %s", size, hipGetErrorString(err));
   std::lock_guard<std::mutex> lock(g_mutex);
   auto& slot = g_modules[device];
-  if (slot.module != nullptr) hipModuleUnload(slot.module);
+  if (slot.module != nullptr) slot.retired.push_back(slot.module);
   slot.module = module;
   slot.functions.clear();
   aoto::noalloc_prepare_device(device);
@@ -358,6 +364,7 @@ int aoto_hip_unload_code_object(void) {
   auto it = g_modules.find(device);
   if (it != g_modules.end()) {
     if (it->second.module != nullptr) hipModuleUnload(it->second.module);
+    for (hipModule_t old : it->second.retired) hipModuleUnload(old);
     g_modules.erase(it);
   }
   return AOTO_OK;

@@ -56,13 +56,16 @@ size_t aoto_hip_take_launches(char* buf, size_t size);
 size_t aoto_hip_last_error(char* buf, size_t size);
 
 /* Install a gfx950 code object (the bytes of an .hsaco) as the kernel module of
- * the current device, replacing any previous one. Replaces the reference's
- * kernel shell and cache (codegen/msl.py:625-646) and, on artifact reload, its
- * re-emission of MSL (artifact.py:367-384): the stored code object is loaded
- * as-is instead of regenerating source. */
+ * the current device: later launches use its kernels. The module it replaces
+ * stays loaded, because HIP graphs captured earlier launch its kernels by handle.
+ * Replaces the reference's kernel shell and cache (codegen/msl.py:625-646) and,
+ * on artifact reload, its re-emission of MSL (artifact.py:367-384): the stored
+ * code object is loaded as-is instead of regenerating source. */
 int aoto_hip_load_code_object(const void* image, size_t size);
 
-/* Unload the current device's module. */
+/* Unload the current device's module and every module it replaced. The caller
+ * must first drop every graph captured over them: replaying one afterwards
+ * executes unloaded code. */
 int aoto_hip_unload_code_object(void);
 
 /* 1 when a module is installed on the current device, else 0. */

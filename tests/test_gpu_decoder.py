@@ -110,6 +110,21 @@ def test_graph_and_eager_loops_agree_and_repeat():
     np.testing.assert_array_equal(short[0], first[0, :3])
 
 
+def test_graphs_captured_before_a_code_object_install_still_replay():
+    """Installing a code object (an artifact load does) keeps the replaced module
+    loaded: a runtime whose decode loop was captured over it replays its graph and
+    gets the same tokens (an unload there would run freed kernel code)."""
+    from aotolith_amd import _lib
+
+    runtime, _ = _pair(seed=11)
+    ids = np.random.default_rng(12).integers(0, TINY.vocab, PROMPT)
+    first = runtime.greedy_generate(ids).cpu().numpy()
+    _lib.install_code_object(_lib.default_code_object())
+    again = runtime.greedy_generate(ids).cpu().numpy()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(first, again)
+
+
 def test_prefill_graph_replays_match_eager():
     """Captured ring prefills (one graph per left-pad width) replay with new ids and match eager runs."""
 
