@@ -98,6 +98,13 @@ int lookup(const char* name, hipFunction_t* fn) {
 thread_local bool g_trace = false;
 thread_local std::string g_trace_names;
 
+void trace_launch(const char* name) {
+  if (g_trace) {
+    g_trace_names += name;
+    g_trace_names += '\n';
+  }
+}
+
 template <typename... Args>
 int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* stream, Args... args) {
   hipFunction_t fn = nullptr;
@@ -106,10 +113,7 @@ int launch(const char* name, dim3 grid, dim3 block, unsigned shared, void* strea
   hipError_t err = hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z, shared,
                                          static_cast<hipStream_t>(stream), params, nullptr);
   if (err != hipSuccess) return fail(AOTO_ERR_HIP, "launch %s: %s", name, hipGetErrorString(err));
-  if (g_trace) {
-    g_trace_names += name;
-    g_trace_names += '\n';
-  }
+  trace_launch(name);
   return AOTO_OK;
 }
 
@@ -354,6 +358,9 @@ int aoto_hip_load_code_object(const void* image, size_t size) {
   slot.module = module;
   slot.functions.clear();
   aoto::noalloc_prepare_device(device);
+  // the hipBLASLt handle of long prefills, created here (never inside a graph
+  // capture); a failure is reported by the first long prefill that needs it
+  aoto::library_prepare(device);
   return AOTO_OK;
 }
 
@@ -482,6 +489,9 @@ struct GemmPlan {
   int tn, tm, splits, kslice;
 };
 
+// The first row count of the long-prefill library path (see library_rows).
+constexpr int kLibraryRows = 1024;
+
 GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
   if (tile == 0) {
@@ -525,6 +535,40 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   return p;
 }
 
+}  // namespace
+
+// Where automatic codes would take the long-prefill library path, the fused
+// kernel's own plan as explicit tile / split codes (128-row blocks there, so the
+// code is 18 or 28); other codes are left as they are.
+extern "C++" void aoto::fused_gemm_codes(int M, int N, int K, int* tile, int* splits) {
+  if (M < kLibraryRows || *tile != 0 || *splits != 0) return;
+  const GemmPlan p = gemm_plan(M, N, K, *tile, *splits, false);
+  *tile = 10 * p.tn + p.tm;
+  *splits = p.splits;
+}
+
+namespace {
+
+// Long prefills: from kLibraryRows rows on, with the automatic plan (tile = splits
+// = 0), the packed weight is unpacked to bf16 into the workspace (the bit-exact
+// aoto_w{4,8}_dequantize) and the product runs on hipBLASLt (blaslt.cpp), the
+// reference's own prefill form. The fused-dequant kernels are bound by their
+// dequant VALU there (MFMA ~33% busy); measured on MI355X at 2048 rows for the
+// Llama-8B projections, hipBLASLt alone takes 68 / 67 / 2 x 140 / 201 us for
+// q/k/v, o, gate + up and down against 146-166 / 98 / 582-590 / 287-296 for the
+// fused kernels, the unpack ~100 us per layer. At 512 rows the unpack would
+// cost as much as the library saves.
+bool library_rows(int M, int tile, int splits) { return M >= kLibraryRows && tile == 0 && splits == 0; }
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// The library path's workspace: the unpacked weight (two for the paired form),
+// then the f32 product that the gate epilogue reads, then (paired) the bf16 gate.
+size_t library_workspace(int M, int N, int K, bool paired) {
+  const size_t weights = align256((paired ? 2 : 1) * (size_t)N * K * 2);
+  return weights + (size_t)M * N * sizeof(float) + (paired ? (size_t)M * N * 2 : 0);
+}
+
 // The q/k/v projection's plan: the requested tile and split count, or with 0 the
 // unsplit plan when its blocks' columns are whole heads (the RoPE epilogue: one
 // launch, measured on MI355X at M = 128 / 512 / 2048: 9.9 / 61.5 / 142.6 us against
@@ -546,12 +590,14 @@ void qkv_rope_plan(int M, int N, int K, int head_dim, int* tile, int* splits) {
 
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  if (library_rows(M, tile, splits)) return library_workspace(M, N, K, false);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, false);
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  if (library_rows(M, tile, splits)) return library_workspace(M, N, K, true);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, true);
   return p.splits > 1 ? 2 * (size_t)p.splits * M * N * sizeof(float) : 0;
 }
@@ -560,13 +606,84 @@ size_t aoto_hip_w4_gemm_qkv_rope_workspace(int M, int K, int tile, int splits, i
                                            int head_dim) {
   if (query_heads <= 0 || kv_heads <= 0 || head_dim <= 0) return 0;
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  if (!library_rows(M, tile, splits)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
   return aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
 }
 
 }  // extern "C"
 
 namespace {
+
+// The unsplit GEMM's tail for the q/k/v projection: RoPE of q/k, q head-major and
+// the K/V cache fill from y (the GEMM's output with its bias).
+// (aoto_rope_qkv_rows: one thread per 4 + 4 partner columns, 8-byte accesses)
+int rope_after_gemm(const void* y, int M, const aoto::QkvRope& rope, void* stream) {
+  const int D = rope.head_dim;
+  long long items = (long long)M * (rope.query_heads + 2 * rope.kv_heads) * (D / 8);
+  if (rope.zero_prefix) items += 2LL * rope.kv_heads * rope.slot0 * D / 4;
+  return launch("aoto_rope_qkv_rows", dim3(blocks_for(items, 256)), dim3(256), 0, stream, y, M, rope.positions,
+                rope.cos_table, rope.sin_table, rope.q_out, rope.pair, rope.query_heads, rope.kv_heads, D, rope.cap,
+                rope.slot0, rope.zero_prefix);
+}
+
+// Unpack N rows of K codes to bf16 [N][K] (aoto_w4_dequantize / aoto_w8_dequantize).
+int unpack_weight(int bits, const int32_t* words, const void* scales, int N, int K, int group, void* out,
+                  void* stream) {
+  const long long units = (long long)N * (K / (bits == 4 ? 8 : 4));
+  return launch(bits == 4 ? "aoto_w4_dequantize" : "aoto_w8_dequantize", dim3(blocks_for(units, 256)), dim3(256), 0,
+                stream, words, scales, N, K, group, out);
+}
+
+// One hipBLASLt GEMM of the long-prefill path, traced as hipblaslt_matmul_{bf16,f32}
+// (the output type) for plans that name the kernels they run.
+int library_launch(int M, int N, int K, const void* x, const void* w, const void* bias, const void* c, void* d,
+                   bool d_f32, void* stream) {
+  if (int st = aoto::library_gemm(M, N, K, x, w, bias, c, d, d_f32, stream)) return st;
+  trace_launch(d_f32 ? "hipblaslt_matmul_f32" : "hipblaslt_matmul_bf16");
+  return AOTO_OK;
+}
+
+// The long-prefill form of packed_gemm (see kLibraryRows): unpack, then hipBLASLt
+// with the bias or the residual in its epilogue (one rounding of the f32 sum, as
+// the fused epilogue), the row norm or the RoPE after it as for an unsplit plan;
+// the gate epilogue reads the f32 product through the split-K reduce kernel with
+// one split, so every rounding point is the fused kernels'. The paired form is
+// the gate GEMM with bf16 output (the paired epilogue's bf16(gate)), then the up
+// GEMM with the gate epilogue: the two-step values of the fused paired kernel.
+int library_packed_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* bias,
+                        const void* residual, const void* gate, void* y, int M, int N, int K, int group,
+                        void* workspace, void* stream, const int32_t* up_words, const void* up_scales,
+                        const void* norm_weight, float eps, void* norm_out, const aoto::QkvRope* rope,
+                        const char* what) {
+  const bool paired = up_words != nullptr;
+  if (workspace == nullptr || ((uintptr_t)workspace & 255))
+    return fail(AOTO_ERR_ARGUMENT, "%s: %d rows unpack the weight: a 256-byte aligned workspace of "
+                "aoto_hip_w4_gemm%s_workspace() bytes is needed", what, M, paired ? "_gate_up" : "");
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* wbuf = reinterpret_cast<uint16_t*>(ws);
+  float* dbuf = reinterpret_cast<float*>(ws + align256((size_t)(paired ? 2 : 1) * N * K * 2));
+  const long long quads = (long long)M * N / 4;
+  if (int st = unpack_weight(bits, words, scales, N, K, group, wbuf, stream)) return st;
+  if (paired) {
+    uint16_t* ubuf = wbuf + (size_t)N * K;
+    uint16_t* gbuf = reinterpret_cast<uint16_t*>(dbuf + (size_t)M * N);
+    if (int st = unpack_weight(bits, up_words, up_scales, N, K, group, ubuf, stream)) return st;
+    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, gbuf, false, stream)) return st;
+    gate = gbuf;
+    wbuf = ubuf;
+  }
+  if (gate != nullptr) {
+    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, dbuf, true, stream)) return st;
+    const void* none = nullptr;
+    return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream, (const float*)dbuf,
+                  1, none, none, gate, y, M, N);
+  }
+  if (int st = library_launch(M, N, K, x, wbuf, bias, residual, y, false, stream)) return st;
+  if (norm_out != nullptr)
+    return launch("aoto_rms_norm", dim3((M + 3) / 4), dim3(256), 0, stream, y, norm_weight, eps, norm_out, M, N);
+  if (rope != nullptr) return rope_after_gemm(y, M, *rope, stream);
+  return AOTO_OK;
+}
 
 // The prefill GEMM of either code width (the kernels differ only in how many
 // packed words make one lane's 8-code operand).
@@ -595,6 +712,9 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
                 what);
   if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28", what, tile);
+  if (library_rows(M, tile, splits))
+    return library_packed_gemm(bits, x, words, scales, bias, residual, gate, y, M, N, K, group, workspace, stream,
+                               up_words, up_scales, norm_weight, eps, norm_out, rope, what);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
   if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
     return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
@@ -631,20 +751,16 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
                   p.splits, residual, y, norm_weight, eps, norm_out, M, N);
   }
   if (rope != nullptr) {
-    // q/k/v: the split sum, bias, RoPE and cache fill in one launch; unsplit, the
-    // GEMM stored y with its bias and the RoPE / cache fill kernel follows
+    // q/k/v: unsplit, the GEMM stored y with its bias and the RoPE / cache fill
+    // kernel follows; split, the sum, bias, RoPE and cache fill are one launch
+    if (!split) return rope_after_gemm(y, M, *rope, stream);
     const int D = rope->head_dim;
-    long long items = split ? (long long)M * (N / D) * (D / 8) : (long long)M * N;
-    if (rope->zero_prefix) items += split ? 2LL * rope->kv_heads * rope->slot0 * D / 4
-                                          : 2LL * rope->kv_heads * rope->slot0 * D;
-    if (split)
-      return launch("aoto_w4_gemm_reduce_rope", dim3(blocks_for(items, 256)), dim3(256), 0, stream,
-                    (const float*)partials, p.splits, bias, y, M, rope->positions, rope->cos_table,
-                    rope->sin_table, rope->q_out, rope->pair, rope->query_heads, rope->kv_heads, D, rope->cap,
-                    rope->slot0, rope->zero_prefix);
-    return launch("aoto_rope_qkv_prefill", dim3(blocks_for(items, 256)), dim3(256), 0, stream, (const void*)y,
-                  rope->positions, rope->cos_table, rope->sin_table, rope->q_out, rope->pair, 1, M, rope->query_heads,
-                  rope->kv_heads, D, rope->cap, rope->slot0, rope->zero_prefix);
+    long long items = (long long)M * (N / D) * (D / 8);
+    if (rope->zero_prefix) items += 2LL * rope->kv_heads * rope->slot0 * D / 4;
+    return launch("aoto_w4_gemm_reduce_rope", dim3(blocks_for(items, 256)), dim3(256), 0, stream,
+                  (const float*)partials, p.splits, bias, y, M, rope->positions, rope->cos_table, rope->sin_table,
+                  rope->q_out, rope->pair, rope->query_heads, rope->kv_heads, D, rope->cap, rope->slot0,
+                  rope->zero_prefix);
   }
   if (!split) return AOTO_OK;
   return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
@@ -670,7 +786,7 @@ int qkv_rope_gemm(int bits, const void* x, const int32_t* words, const void* sca
                            (uint16_t*)q_out, (uint16_t*)pair, query_heads, kv_heads, head_dim, capacity, slot0,
                            zero_prefix};
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  if (!library_rows(M, tile, splits)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
   return packed_gemm(bits, x, words, scales, bias, nullptr, nullptr, y, M, N, K, group, tile, splits, workspace,
                      stream, nullptr, nullptr, nullptr, 0.f, nullptr, &rope);
 }

@@ -20,6 +20,7 @@ PACKAGE = os.path.dirname(CSRC)
 ROOT = os.path.dirname(PACKAGE)
 INCLUDE = os.path.join(ROOT, "include")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = os.path.dirname(os.path.dirname(HIPCC))
 
 CODE_OBJECT = os.path.join(PACKAGE, "aoto_gfx950.hsaco")
 LIBRARY = os.path.join(PACKAGE, "libaoto_hip.so")
@@ -55,8 +56,9 @@ def build(verbose: bool = False) -> tuple[str, str]:
     _run([HIPCC, *DEVICE_FLAGS, "--genco", "--no-gpu-bundle-output", os.path.join(CSRC, "kernels.hip"), "-o", tmp_obj], verbose)
     os.replace(tmp_obj, CODE_OBJECT)
     tmp_lib = LIBRARY + ".tmp"
-    # The host library: the C-ABI launchers, plus noalloc.hip, whose device part is
-    # only the static scratch buffer of the allocation-free GEMM entry point.
+    # The host library: the C-ABI launchers, the hipBLASLt calls of long prefills
+    # (blaslt.cpp), plus noalloc.hip, whose device part is only the static scratch
+    # buffer of the allocation-free GEMM entry point.
     _run(
         [
             HIPCC,
@@ -72,7 +74,11 @@ def build(verbose: bool = False) -> tuple[str, str]:
             "-I" + INCLUDE,
             "-I" + CSRC,
             os.path.join(CSRC, "aoto_hip.cpp"),
+            os.path.join(CSRC, "blaslt.cpp"),
             os.path.join(CSRC, "noalloc.hip"),
+            "-L" + os.path.join(ROCM, "lib"),
+            "-lhipblaslt",
+            "-Wl,-rpath," + os.path.join(ROCM, "lib"),
             "-o",
             tmp_lib,
         ],

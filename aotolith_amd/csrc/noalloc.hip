@@ -66,6 +66,9 @@ extern "C" int aoto_hip_w4_gemm_noalloc(const void* x, const int32_t* words, con
     return aoto::set_error(AOTO_ERR_HIP, "w4_gemm_noalloc: scratch address on device %d: %s", device,
                            hipGetErrorString(slot.status));
   }
+  // automatic codes resolve to the fused kernel's plan: from 1024 rows on,
+  // aoto_hip_w4_gemm would otherwise unpack the weight into its workspace
+  if (M > 0 && N > 0 && K > 0 && K % 64 == 0) aoto::fused_gemm_codes(M, N, K, &tile, &splits);
   const size_t need = aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
   if (need > AOTO_HIP_NOALLOC_SCRATCH_BYTES)
     return aoto::set_error(AOTO_ERR_UNSUPPORTED,

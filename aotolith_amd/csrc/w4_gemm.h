@@ -606,6 +606,60 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_norm(
   }
 }
 
+// The RoPE / cache-fill tail of aoto_w4_gemm_reduce_rope and aoto_rope_qkv_rows for
+// one thread's quad: the bf16 projection values ya (d .. d+3 of head h, token m) and
+// yb (the partner columns d + D/2 ..); RoPE in f32 from the rounded pair, one rounding.
+AOTO_DEVICE void rope_quad_store(uint2 ya, uint2 yb, int m, int h, int d, int M,
+                                 const long long* __restrict__ positions, const uint16_t* __restrict__ cos_table,
+                                 const uint16_t* __restrict__ sin_table, uint16_t* __restrict__ q_out,
+                                 uint16_t* __restrict__ pair, int query_heads, int kv_heads, int D, int cap,
+                                 int slot0) {
+  const int half = D >> 1;
+  const size_t head_stride = (size_t)cap * D;
+  const size_t pair_stride = (size_t)kv_heads * head_stride;
+  uint16_t* dst;
+  if (h < query_heads)
+    dst = q_out + ((size_t)h * M + m) * D;
+  else if (h < query_heads + kv_heads)
+    dst = pair + (size_t)(h - query_heads) * head_stride + (size_t)(slot0 + m) * D;
+  else
+    dst = pair + pair_stride + (size_t)(h - query_heads - kv_heads) * head_stride + (size_t)(slot0 + m) * D;
+  if (h >= query_heads + kv_heads) {  // values: the stored projection, unrotated
+    *reinterpret_cast<uint2*>(dst + d) = ya;
+    *reinterpret_cast<uint2*>(dst + d + half) = yb;
+    return;
+  }
+  const float xa[4] = {bf16_lo(ya.x), bf16_hi(ya.x), bf16_lo(ya.y), bf16_hi(ya.y)};
+  const float xb[4] = {bf16_lo(yb.x), bf16_hi(yb.x), bf16_lo(yb.y), bf16_hi(yb.y)};
+  const long long p = positions[m];
+  const uint16_t* cr = cos_table + (size_t)p * D;
+  const uint16_t* sr = sin_table + (size_t)p * D;
+  const uint2 ca = *reinterpret_cast<const uint2*>(cr + d), cb = *reinterpret_cast<const uint2*>(cr + d + half);
+  const uint2 sa = *reinterpret_cast<const uint2*>(sr + d), sb = *reinterpret_cast<const uint2*>(sr + d + half);
+  const float c0[4] = {bf16_lo(ca.x), bf16_hi(ca.x), bf16_lo(ca.y), bf16_hi(ca.y)};
+  const float c1[4] = {bf16_lo(cb.x), bf16_hi(cb.x), bf16_lo(cb.y), bf16_hi(cb.y)};
+  const float s0[4] = {bf16_lo(sa.x), bf16_hi(sa.x), bf16_lo(sa.y), bf16_hi(sa.y)};
+  const float s1[4] = {bf16_lo(sb.x), bf16_hi(sb.x), bf16_lo(sb.y), bf16_hi(sb.y)};
+  float ra[4], rb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ra[i] = xa[i] * c0[i] + (-xb[i]) * s0[i];  // first half: x cos - x[d + D/2] sin
+    rb[i] = xb[i] * c1[i] + xa[i] * s1[i];     // second half: x cos + x[d - D/2] sin
+  }
+  *reinterpret_cast<uint2*>(dst + d) = make_uint2(pack_bf16x2(ra[0], ra[1]), pack_bf16x2(ra[2], ra[3]));
+  *reinterpret_cast<uint2*>(dst + d + half) = make_uint2(pack_bf16x2(rb[0], rb[1]), pack_bf16x2(rb[2], rb[3]));
+}
+
+// Zero-fill of the cache window's slots [0, slot0) for zero_prefix: thread z of
+// 2 Hkv slot0 D / 4 stores one 8-byte zero (threads past the range do nothing).
+AOTO_DEVICE void rope_zero_prefix(long long z, uint16_t* __restrict__ pair, int kv_heads, int D, int cap,
+                                  int slot0) {
+  const long long prefix = (long long)slot0 * D / 4;
+  if (z >= 2LL * kv_heads * prefix) return;
+  const long long hh = z / prefix;
+  *reinterpret_cast<uint2*>(pair + (size_t)hh * cap * D + (size_t)(z % prefix) * 4) = make_uint2(0u, 0u);
+}
+
 // The packed q/k/v projection's split-K sum fused with its bias, the bf16 value
 // the projection stores, RoPE and the layer's cache fill: aoto_w4_gemm_reduce (bias
 // epilogue) followed by aoto_rope_qkv_prefill in one launch, with the same values
@@ -630,8 +684,6 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_rope(
   const int half = D >> 1;
   const int quads = half >> 2;
   const long long items = (long long)M * heads * quads;
-  const size_t head_stride = (size_t)cap * D;
-  const size_t pair_stride = (size_t)kv_heads * head_stride;
   if (t < items) {
     const int dq = (int)(t % quads);
     const int h = (int)((t / quads) % heads);
@@ -657,45 +709,40 @@ extern "C" __global__ __launch_bounds__(256) void aoto_w4_gemm_reduce_rope(
     const uint2 yb = make_uint2(pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3]));
     *reinterpret_cast<uint2*>(Y + e) = ya;
     *reinterpret_cast<uint2*>(Y + e + half) = yb;
-    uint16_t* dst;
-    if (h < query_heads)
-      dst = q_out + ((size_t)h * M + m) * D;
-    else if (h < query_heads + kv_heads)
-      dst = pair + (size_t)(h - query_heads) * head_stride + (size_t)(slot0 + m) * D;
-    else
-      dst = pair + pair_stride + (size_t)(h - query_heads - kv_heads) * head_stride + (size_t)(slot0 + m) * D;
-    if (h >= query_heads + kv_heads) {  // values: the stored projection, unrotated
-      *reinterpret_cast<uint2*>(dst + d) = ya;
-      *reinterpret_cast<uint2*>(dst + d + half) = yb;
-      return;
-    }
-    const float xa[4] = {bf16_lo(ya.x), bf16_hi(ya.x), bf16_lo(ya.y), bf16_hi(ya.y)};
-    const float xb[4] = {bf16_lo(yb.x), bf16_hi(yb.x), bf16_lo(yb.y), bf16_hi(yb.y)};
-    const long long p = positions[m];
-    const uint16_t* cr = cos_table + (size_t)p * D;
-    const uint16_t* sr = sin_table + (size_t)p * D;
-    const uint2 ca = *reinterpret_cast<const uint2*>(cr + d), cb = *reinterpret_cast<const uint2*>(cr + d + half);
-    const uint2 sa = *reinterpret_cast<const uint2*>(sr + d), sb = *reinterpret_cast<const uint2*>(sr + d + half);
-    const float c0[4] = {bf16_lo(ca.x), bf16_hi(ca.x), bf16_lo(ca.y), bf16_hi(ca.y)};
-    const float c1[4] = {bf16_lo(cb.x), bf16_hi(cb.x), bf16_lo(cb.y), bf16_hi(cb.y)};
-    const float s0[4] = {bf16_lo(sa.x), bf16_hi(sa.x), bf16_lo(sa.y), bf16_hi(sa.y)};
-    const float s1[4] = {bf16_lo(sb.x), bf16_hi(sb.x), bf16_lo(sb.y), bf16_hi(sb.y)};
-    float ra[4], rb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ra[i] = xa[i] * c0[i] + (-xb[i]) * s0[i];  // first half: x cos - x[d + D/2] sin
-      rb[i] = xb[i] * c1[i] + xa[i] * s1[i];     // second half: x cos + x[d - D/2] sin
-    }
-    *reinterpret_cast<uint2*>(dst + d) = make_uint2(pack_bf16x2(ra[0], ra[1]), pack_bf16x2(ra[2], ra[3]));
-    *reinterpret_cast<uint2*>(dst + d + half) = make_uint2(pack_bf16x2(rb[0], rb[1]), pack_bf16x2(rb[2], rb[3]));
+    rope_quad_store(ya, yb, m, h, d, M, positions, cos_table, sin_table, q_out, pair, query_heads, kv_heads, D, cap,
+                    slot0);
     return;
   }
-  if (!zero_prefix) return;
-  const long long z = t - items;  // one 8-byte zero store per thread
-  const long long prefix = (long long)slot0 * D / 4;
-  if (z >= 2LL * kv_heads * prefix) return;
-  const long long hh = z / prefix;
-  *reinterpret_cast<uint2*>(pair + (size_t)hh * head_stride + (size_t)(z % prefix) * 4) = make_uint2(0u, 0u);
+  if (zero_prefix) rope_zero_prefix(t - items, pair, kv_heads, D, cap, slot0);
+}
+
+// RoPE and the cache fill from a stored projection y[m][W] (bias included): the
+// values of aoto_rope_qkv_prefill (batch 1) with one thread per quad as in
+// aoto_w4_gemm_reduce_rope, 8-byte loads and stores. Same outputs and limits
+// (D % 8 == 0, y 8-byte aligned).
+extern "C" __global__ __launch_bounds__(256) void aoto_rope_qkv_rows(
+    const uint16_t* __restrict__ Y, int M, const long long* __restrict__ positions,
+    const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ pair, int query_heads, int kv_heads, int D, int cap, int slot0, int zero_prefix) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int heads = query_heads + 2 * kv_heads;
+  const int W = heads * D;
+  const int half = D >> 1;
+  const int quads = half >> 2;
+  const long long items = (long long)M * heads * quads;
+  if (t < items) {
+    const int dq = (int)(t % quads);
+    const int h = (int)((t / quads) % heads);
+    const int m = (int)(t / ((long long)quads * heads));
+    const int d = 4 * dq;
+    const size_t e = (size_t)m * W + (size_t)h * D + d;
+    const uint2 ya = *reinterpret_cast<const uint2*>(Y + e);
+    const uint2 yb = *reinterpret_cast<const uint2*>(Y + e + half);
+    rope_quad_store(ya, yb, m, h, d, M, positions, cos_table, sin_table, q_out, pair, query_heads, kv_heads, D, cap,
+                    slot0);
+    return;
+  }
+  if (zero_prefix) rope_zero_prefix(t - items, pair, kv_heads, D, cap, slot0);
 }
 
 // The paired form's split-K sum: gate = sum of partials[0 .. splits), up = sum

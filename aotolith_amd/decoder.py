@@ -417,7 +417,7 @@ def _sel(index: int, op: str, output: str, kind: str, reason: str, artifact: str
         op_index=index,
         op=op,
         output_id=output,
-        implementation="hip_kernel",
+        implementation="hipblaslt" if artifact.startswith("hipblaslt") else "hip_kernel",
         kind=kind,
         reason=reason,
         artifact_name=artifact,
@@ -900,7 +900,8 @@ class _Engine:
                 ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
             pair = pair_of(index)
             _mark(rec, "addmm" if s.qkv_bias else "matmul", f"qkv_{index}", gemm,
-                  f"fused-dequant W{bits} GEMM on bf16 MFMA" + (" with q/k/v bias" if s.qkv_bias else "")
+                  (f"W{bits} unpack to bf16 and the hipBLASLt GEMM" if m >= ops.LIBRARY_ROWS
+                   else f"fused-dequant W{bits} GEMM on bf16 MFMA") + (" with q/k/v bias" if s.qkv_bias else "")
                   + ", RoPE of q/k and the layer's cache fill (with the split-K sum when the plan splits)")
             # q/k/v projection, RoPE and the cache fill (one launch fewer when the plan splits K)
             ops.matmul_qkv_rope(xn, layer.qkv.packed, layer.qkv.scales, layer.qkv.group, positions.reshape(-1),

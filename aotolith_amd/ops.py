@@ -354,14 +354,22 @@ def w8_matmul(
     return _matmul(8, x, packed, scales, group_size, bias, residual, gate, out, tile, splits, workspace)
 
 
+#: From this many rows on, the prefill GEMMs' automatic plan (tile = splits = 0)
+#: unpacks the weight to bf16 into the workspace and runs the product on
+#: hipBLASLt (the C ABI's kLibraryRows); explicit codes keep the fused kernel.
+LIBRARY_ROWS = 1024
+
+
 def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:
-    """Split-K workspace bytes :func:`w4_matmul` needs for this shape (0: no split)."""
+    """Workspace bytes :func:`w4_matmul` needs for this shape: split-K partials (0: no
+    split), or from :data:`LIBRARY_ROWS` rows the unpacked weight and f32 product."""
 
     return int(_lib.library().aoto_hip_w4_gemm_workspace(int(m), int(n), int(k), int(tile), int(splits)))
 
 
 def gate_up_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:
-    """Split-K workspace bytes :func:`w4_matmul_gate_up` needs (gate and up partials; 0: no split)."""
+    """Workspace bytes :func:`w4_matmul_gate_up` needs (gate and up partials, 0: no split;
+    or from :data:`LIBRARY_ROWS` rows both unpacked weights and f32 products)."""
 
     return int(_lib.library().aoto_hip_w4_gemm_gate_up_workspace(int(m), int(n), int(k), int(tile), int(splits)))
 

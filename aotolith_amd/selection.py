@@ -2,16 +2,18 @@
 
 Same record as the reference's ``selection.py:6-34`` (field names and order),
 so tooling that reads ``plan.selections`` reads ours. ``is_native`` is widened
-from the reference's single ``"metal_kernel"`` to every kernel-generating
-implementation, here ``"hip_kernel"``.
+from the reference's single ``"metal_kernel"`` to every implementation that
+runs a device kernel, here ``"hip_kernel"`` and ``"hipblaslt"``.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 
-#: Implementations that run generated/hand-written device kernels.
-NATIVE_IMPLEMENTATIONS = frozenset({"hip_kernel", "metal_kernel"})
+#: Implementations that run device kernels (no CPU or torch fallback): this
+#: target's gfx950 code object, the hipBLASLt GEMM that long prefills run on the
+#: unpacked weight, and the Metal kernels of the reference's Apple backend.
+NATIVE_IMPLEMENTATIONS = frozenset({"hip_kernel", "hipblaslt", "metal_kernel"})
 
 
 @dataclass(frozen=True, slots=True)

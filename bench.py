@@ -334,16 +334,24 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
             ops.matmul_residual_norm(act, layer.down.packed, layer.down.scales, layer.down.group, x,
                                      layer.input_norm, spec.eps, bits=layer.down.bits, out=x, norm_out=xn)
 
-    gemm = f"aoto_w{eng.state.bits}_gemm"
+    bits = eng.state.bits
+    if m >= ops.LIBRARY_ROWS:  # the automatic plan unpacks the weight for hipBLASLt
+        gemm = f"aoto_w{bits}_dequantize + hipBLASLt bf16 GEMM"
+        qkv_label = f"{gemm} (bias epilogue), then aoto_rope_qkv_rows (RoPE and cache fill)"
+        mlp_label = (f"aoto_w{bits}_dequantize x2, hipBLASLt gate (bf16) and up (f32) GEMMs, "
+                     "aoto_w4_gemm_reduce (silu_mul)")
+    else:
+        gemm = f"aoto_w{bits}_gemm"
+        qkv_label = (f"{gemm} + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: RoPE in the "
+                     "GEMM epilogue, or aoto_rope_qkv_rows after it)")
+        mlp_label = f"{gemm} paired gate/up + silu_mul"
     rows = [
-        _row("qkv_rope", f"{gemm} + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: "
-             "aoto_rope_qkv_prefill after the GEMM)", _graph_us(torch, qkv_rope, n),
-             flops=2.0 * m * spec.qkv_width * h),
+        _row("qkv_rope", qkv_label, _graph_us(torch, qkv_rope, n), flops=2.0 * m * spec.qkv_width * h),
         _row("attention", f"aoto_flash_attention_d{spec.head_dim} (causal)", _graph_us(torch, attention, n),
              flops=4.0 * m * m * spec.head_dim * spec.heads / 2),
         _row("o_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, o_norm, n),
              flops=2.0 * m * h * spec.attention_width),
-        _row("gate_up", f"aoto_w{eng.state.bits}_gemm paired gate/up + silu_mul", _graph_us(torch, mlp, n),
+        _row("gate_up", mlp_label, _graph_us(torch, mlp, n),
              flops=2.0 * m * 2 * i * h),
         _row("down_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, down_norm, n),
              flops=2.0 * m * h * i),

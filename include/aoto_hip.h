@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 16
+#define AOTO_HIP_ABI_VERSION 17
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -115,19 +115,27 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales,
  * tiles x m tiles of 16 per wave) or 12 (32-row blocks). splits: 0 chooses (small grids split the
  * reduction), else the split-K count; a split launch stores f32 partial tiles
  * in `workspace` (aoto_hip_w4_gemm_workspace() bytes, 16-byte aligned) and a
- * second launch sums them and applies the epilogue. y must not alias x. */
+ * second launch sums them and applies the epilogue. Long prefills (M >= 1024
+ * with tile = splits = 0, the reference's own prefill form): the weight is
+ * unpacked to bf16 into `workspace` (aoto_hip_w4_gemm_workspace() bytes, 256-byte
+ * aligned: N * K * 2 rounded up, then M * N * 4 for the gate epilogue's f32
+ * product) and the product runs on hipBLASLt with f32 accumulation and no
+ * library workspace; the epilogues round as above. A nonzero tile or split code
+ * keeps the fused kernel at any M. y must not alias x. */
 int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
                      const void* residual, const void* gate, void* y, int M, int N, int K, int group,
                      int tile, int splits, void* workspace, void* stream);
 
-/* Bytes of split-K workspace aoto_hip_w4_gemm needs for these arguments (0 when
- * it does not split). */
+/* Bytes of workspace aoto_hip_w4_gemm needs for these arguments: the split-K
+ * partials (0 when it does not split), or the long-prefill path's unpacked
+ * weight and f32 product. */
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits);
 
 /* No counterpart in the reference. aoto_hip_w4_gemm for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc): the same arguments and results without the
- * workspace. A split-K plan keeps its f32 partials in a static device buffer of
+ * workspace. Automatic codes at M >= 1024 keep the fused kernel (its own
+ * plan: no unpacked weight). A split-K plan keeps its f32 partials in a static device buffer of
  * AOTO_HIP_NOALLOC_SCRATCH_BYTES that the library holds on each GPU until the
  * process ends; a plan that needs more (aoto_hip_w4_gemm_workspace() bytes) is
  * refused with AOTO_ERR_UNSUPPORTED (pass splits = 1, or use aoto_hip_w4_gemm).
@@ -176,7 +184,9 @@ int aoto_hip_w8_gemm(const void* x, const int32_t* words, const void* scales, co
  * 1721-1742; passes/fusion.py:406-498), with X read once. gate/up words and
  * scales as aoto_hip_w4_gemm (int4) / aoto_hip_w8_gemm (int8), both [N, K].
  * Limits, tile and splits as aoto_hip_w4_gemm; a split launch needs
- * aoto_hip_w4_gemm_gate_up_workspace() bytes (gate and up partials). */
+ * aoto_hip_w4_gemm_gate_up_workspace() bytes (gate and up partials), as does
+ * the long-prefill path (both unpacked weights, the up projection's f32 product
+ * and the bf16 gate). */
 int aoto_hip_w4_gemm_gate_up(const void* x, const int32_t* gate_words, const void* gate_scales,
                              const int32_t* up_words, const void* up_scales, void* y, int M, int N, int K,
                              int group, int tile, int splits, void* workspace, void* stream);
@@ -213,7 +223,8 @@ int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const vo
  * rotated keys / values at slots slot0 .. slot0 + M - 1 (slots below slot0 zeroed
  * when zero_prefix != 0); positions[M] int64. tile and splits as aoto_hip_w4_gemm,
  * with 0 / 0 choosing the unsplit epilogue form whenever it applies (32-row blocks
- * up to 128 rows);
+ * up to 128 rows) and the long-prefill library path from 1024 rows (the RoPE /
+ * cache fill kernel after it);
  * workspace: aoto_hip_w4_gemm_qkv_rope_workspace() bytes. */
 int aoto_hip_w4_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
                               int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
@@ -224,11 +235,12 @@ int aoto_hip_w8_gemm_qkv_rope(const void* x, const int32_t* words, const void* s
                               const void* cos_table, const void* sin_table, void* q_out, void* pair, int query_heads,
                               int kv_heads, int head_dim, int capacity, int slot0, int zero_prefix, void* stream);
 /* Workspace bytes of aoto_hip_w{4,8}_gemm_qkv_rope with these arguments (0: the
- * plan does not split K). */
+ * fused plan does not split K). */
 size_t aoto_hip_w4_gemm_qkv_rope_workspace(int M, int K, int tile, int splits, int query_heads, int kv_heads,
                                            int head_dim);
 
-/* Bytes of split-K workspace the gate/up entry points need (0 when unsplit). */
+/* Bytes of workspace the gate/up entry points need (0 when the fused plan does
+ * not split). */
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits);
 
 /* Row RMSNorm, out = bf16((x * rsqrt(mean(x^2) + eps)) * weight) over [rows, hidden]

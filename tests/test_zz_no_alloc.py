@@ -84,3 +84,28 @@ def test_noalloc_gemm_refuses_plans_beyond_its_scratch():
     assert _noalloc(x, packed, scales, 64, out, splits=1) == 0, _last_error()
     torch.cuda.synchronize()
     assert not torch.any(out.view(torch.int16) != 0)
+
+
+def test_noalloc_gemm_keeps_the_fused_kernel_for_long_prefills():
+    """Automatic codes at 1024+ rows, which send aoto_hip_w4_gemm to the unpacked-weight
+    library path, resolve to the fused kernel's own plan here (no room for the weight):
+    the result is the workspace entry point's under that explicit plan, bit for bit."""
+
+    from aotolith_amd import ops
+
+    m, n, k = ops.LIBRARY_ROWS, 4096, 896  # 256 output tiles: the fused plan does not split
+    rng = np.random.default_rng(90)
+    packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
+    gp, gs = torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
+    x = to_gpu_bf16(bf16_normal(rng, (m, k)))
+    bias = to_gpu_bf16(bf16_normal(rng, (n,), 0.02))
+    want = ops.w4_matmul(x, gp, gs, 64, bias=bias, tile=28)  # 128-row, 128-column blocks
+    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+    with ops.recording_launches() as take:
+        take()
+        status = _noalloc(x, gp, gs, 64, got, bias=bias)
+        names = take()
+    assert status == 0, _last_error()
+    torch.cuda.synchronize()
+    assert not any(name.startswith("hipblaslt") for name in names), names
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
