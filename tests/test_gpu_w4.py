@@ -50,11 +50,12 @@ def test_quantize_is_bit_exact(n, k, group, source):
     np.testing.assert_array_equal(bf16_bits_of(scales), ref_scales)
 
 
-def test_dequantize_is_bit_exact():
-    rng = np.random.default_rng(5)
-    _, packed, scales = _packed_case(rng, 300, 896)
-    out = _ops().w4_dequantize(torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64)
-    np.testing.assert_array_equal(from_gpu_bf16(out), dequantize_i4_bf16(packed, scales, 64))
+@pytest.mark.parametrize("n,k,group", [(300, 896, 64), (37, 96, 16), (5, 40, 8)])
+def test_dequantize_is_bit_exact(n, k, group):
+    rng = np.random.default_rng(5 + group)
+    _, packed, scales = _packed_case(rng, n, k, group)
+    out = _ops().w4_dequantize(torch.from_numpy(packed).cuda(), to_gpu_bits(scales), group)
+    np.testing.assert_array_equal(from_gpu_bf16(out), dequantize_i4_bf16(packed, scales, group))
 
 
 GEMV_SHAPES = [

@@ -58,11 +58,12 @@ def test_w8_quantize_is_bit_exact(n, k, group, source):
     np.testing.assert_array_equal(bf16_bits_of(scales), ref_scales)
 
 
-def test_w8_dequantize_is_bit_exact():
-    rng = np.random.default_rng(6)
-    packed, scales = _packed(rng, 300, 896)
-    out = _ops().w8_dequantize(*_gpu(packed, scales), 64)
-    np.testing.assert_array_equal(from_gpu_bf16(out), dequantize_bits_bf16(packed, scales, 64, 8))
+@pytest.mark.parametrize("n,k,group", [(300, 896, 64), (37, 96, 8), (5, 20, 4)])
+def test_w8_dequantize_is_bit_exact(n, k, group):
+    rng = np.random.default_rng(6 + group)
+    packed, scales = _packed(rng, n, k, group)
+    out = _ops().w8_dequantize(*_gpu(packed, scales), group)
+    np.testing.assert_array_equal(from_gpu_bf16(out), dequantize_bits_bf16(packed, scales, group, 8))
 
 
 def _extreme_case(n, k, group):
