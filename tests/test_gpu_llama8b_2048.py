@@ -60,18 +60,20 @@ def test_prefill_attention_2048_tokens_d128(length):
 
 
 @pytest.mark.timeout(300)
+@pytest.mark.parametrize("plan", ["fused", "library"])
 @pytest.mark.parametrize("n,k,full_n,epilogue", [
     (1024, 4096, 6144, None),        # a slice of the 8B q/k/v projection
     (1024, 4096, 4096, "residual"),  # a slice of the o projection, residual epilogue
     (512, 14336, 4096, "residual"),  # a slice of the down projection
 ])
-def test_w4_matmul_2048_rows_on_the_decoder_plan(n, k, full_n, epilogue):
-    """An N slice run on the plan the decoder picks for the full projection at 2048 rows:
-    128x128 block tiles (tile code 28) and no split-K."""
+def test_w4_matmul_2048_rows_on_the_decoder_plan(n, k, full_n, epilogue, plan):
+    """An N slice at 2048 rows on either plan: the automatic one the decoder takes (the
+    weight unpacked, the product on hipBLASLt) and the fused kernel's own at this length
+    (128x128 block tiles, tile code 28, no split-K)."""
 
     from aotolith_amd import ops
 
-    assert ops.gemm_workspace_bytes(M, full_n, k) == 0, "the full projection runs without split-K"
+    assert ops.gemm_workspace_bytes(M, full_n, k) >= full_n * k * 2, "the automatic plan unpacks the weight"
     assert ops.gemm_workspace_bytes(M, full_n, k, tile=28, splits=1) == 0
     rng = np.random.default_rng(n + k)
     packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
@@ -80,14 +82,19 @@ def test_w4_matmul_2048_rows_on_the_decoder_plan(n, k, full_n, epilogue):
     if epilogue == "residual":
         kwargs["residual"] = bf16_normal(rng, (M, n))
     gpu_kwargs = {key: to_gpu_bf16(value) for key, value in kwargs.items()}
-    y = ops.w4_matmul(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64, tile=28, splits=1,
-                      **gpu_kwargs)
+    codes = {"tile": 28, "splits": 1} if plan == "fused" else {}
+    with ops.recording_launches() as take:
+        take()
+        y = ops.w4_matmul(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64, **codes,
+                          **gpu_kwargs)
+        names = take()
+    assert any(name.startswith("hipblaslt") for name in names) == (plan == "library"), names
     expected = oracle.w4_matmul(x, packed, scales, 64, **kwargs)
     # Outputs reach ~6 with the N(0,1) residual, where one bf16 ulp is 2^-5: the bar is
     # one ulp of each value (and the absolute bar one ulp of the largest).
     top_ulp = 2.0 ** (np.floor(np.log2(np.abs(expected).max())) - 7)
     stats = assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0, atol=max(2e-2, top_ulp))
-    print(f"w4 matmul M={M} N={n} K={k} {epilogue}: {stats}")
+    print(f"w4 matmul {plan} M={M} N={n} K={k} {epilogue}: {stats}")
 
 
 def _spec(layers=2):
