@@ -36,6 +36,8 @@
 // overlaps the other's products.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace aoto {
@@ -199,7 +201,8 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   // the stage then holds a clamped copy) or past the wave's causal edge is fully
   // masked (p = 0). Skipping it put the next tile's loads on two paths, and the
   // compiler's wait counting, merging them, made the computing path wait for them.
-  auto compute_tile = [&](int t, int cur, int jn, uint4 (&stage)[PER]) {
+  // `prefetch` (a compile-time bool) is false for the last trip, which loads nothing.
+  auto compute_tile = [&](int t, int cur, int jn, uint4 (&stage)[PER], auto prefetch) {
     const int j0 = tile_begin + t * BK;
     const bool real = t < n_tiles;
     {
@@ -213,7 +216,8 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
         for (int s = 0; s < DS; ++s) {
           const fa_bf16x8 a = *reinterpret_cast<const fa_bf16x8*>(ks + (sub * 32 + col) * STRK + 16 * s + 8 * half);
           sacc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[sub], 0, 0, 0);
-          if ((sub * DS + s) & 1) load_one((sub * DS + s) >> 1, jn, stage);
+          if constexpr (decltype(prefetch)::value)
+            if ((sub * DS + s) & 1) load_one((sub * DS + s) >> 1, jn, stage);
         }
       }
       // Scores of key j0 + 32 sub + 8 (e / 4) + 4 half + e % 4 for query qi; only
@@ -307,11 +311,18 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   // before the previous barrier) - so the compiler's wait counting sees the same
   // loads on every path: with a conditional store it assumed loads still in
   // flight at the loop head and waited for them before reusing their registers.
+  // The last trip is peeled: it issues no loads and stores no stage, so it does not
+  // wait for a memory round trip before its barrier (a one-trip block - a short
+  // prompt - otherwise fetched its tile twice).
   const int last_tile = max(n_tiles - 1, 0);
-  for (int t = 0; t < trips; ++t) {
+  for (int t = 0; t + 1 < trips; ++t) {
     const int jn = tile_begin + min(t + 1, last_tile) * BK;
-    compute_tile(t, t & 1, jn, stage);
+    compute_tile(t, t & 1, jn, stage, std::true_type{});
     store_tile((t + 1) & 1, jn, stage);
+    __syncthreads();
+  }
+  if (trips > 0) {
+    compute_tile(trips - 1, (trips - 1) & 1, 0, stage, std::false_type{});
     __syncthreads();
   }
 
