@@ -79,31 +79,37 @@ AOTO_DEVICE fa_bf16x8 flash_v_operand(const uint16_t* vs, int t, int d_base, int
 // split merge of decode attention does. A CU then always holds two waves per SIMD
 // - one block of 8, where two 4-wave blocks would leave the heavy causal tile alone
 // once its light partner ends - and a q-tile's keys take half the time.
-template <int D, int KG, bool MASKED>
+// QW waves per key group, 32 queries each (BQ = 32 QW queries per block): 4 in the
+// ordinary instances; 2 in the short-prompt instance, which spreads a short prompt's
+// few blocks over twice the CUs (one wave per SIMD instead of two sharing its MFMA pipe).
+template <int D, int KG, bool MASKED, int QW = 4>
 __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                      const uint16_t* __restrict__ v, long long kv_batch_stride,
                                      long long kv_head_stride, const uint8_t* __restrict__ mask,
                                      long long mask_batch_stride, int causal, int key_start, int M, int Mk,
                                      int batch, int query_heads, int kv_heads, float scale,
                                      uint16_t* __restrict__ out) {
-  constexpr int BQ = kFlashQueries, BK = kFlashKeys;
+  constexpr int BQ = 32 * QW, BK = kFlashKeys;
+  constexpr int GT = 64 * QW;              // threads per key group
+  static_assert(QW != 4 || BQ == kFlashQueries, "the ordinary instances take kFlashQueries queries");
   constexpr int STRK = D + 8;              // bf16 per staged K row
   constexpr int STRV = D + 32;             // bf16 per staged V row
   constexpr int VOFF = BK * STRK;          // V tile after the K tile in a stage
   constexpr int DS = D / 16;               // k-steps of S^T (16 d each)
   constexpr int DT = D / 32;               // 32-row d tiles of O^T
   constexpr int CHUNKS = BK * D / 8;       // 16-byte chunks of one K (or V) tile
-  constexpr int PER = 2 * CHUNKS / 256;    // chunks per thread per tile, K then V
+  constexpr int PER = 2 * CHUNKS / GT;     // chunks per thread per tile, K then V
+  static_assert(PER == DS || PER % (2 * DS) == 0, "tile loads spread evenly over the S^T products");
   constexpr int ROW_CHUNKS = D / 8;
   __shared__ __attribute__((aligned(16))) uint16_t lds_all[KG][2][BK * (STRK + STRV)];
   // wave and group are uniform per wave; saying so (readfirstlane) keeps the tile
   // loop's branches scalar - as exec-masked branches their paths merged, and the
   // loads of one path made the other wait for them
-  const int group = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
-  const int lt = (int)threadIdx.x & 255;  // thread index within the group
+  const int group = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x / GT);
+  const int lt = (int)threadIdx.x % GT;  // thread index within the group
   auto& lds = lds_all[group];
 
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) & 3);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) % QW);
   const int col = lane & 31, half = lane >> 5;
   // Query tiles in the order T-1, T-2, ..., T/2 (heaviest first), then 0, 1, ...:
   // blocks are dealt to the 8 XCDs round robin and to each XCD's CUs in turn, so the
@@ -157,7 +163,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   // inside are stored without that test. The load address is clamped into the
   // head (no branch or wait around the loads themselves).
   auto load_one = [&](int i, int j0, uint4 (&reg)[PER]) {
-    const int c = lt + (i % (PER / 2)) * 256;
+    const int c = lt + (i % (PER / 2)) * GT;
     const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
     const uint16_t* base = i < PER / 2 ? kh : vh;
     reg[i] = *reinterpret_cast<const uint4*>(base + (size_t)min(j0 + row, Mk - 1) * D + cc * 8);
@@ -168,7 +174,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
   };
   auto store_tile = [&](int buffer, int j0, const uint4 (&reg)[PER]) {
     auto slot = [&](int i) {
-      const int c = lt + (i % (PER / 2)) * 256;
+      const int c = lt + (i % (PER / 2)) * GT;
       const int row = c / ROW_CHUNKS, cc = c % ROW_CHUNKS;
       return reinterpret_cast<uint4*>(&lds[buffer][i < PER / 2 ? row * STRK : VOFF + row * STRV] + cc * 8);
     };
@@ -178,7 +184,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        const int j = j0 + (lt + (i % (PER / 2)) * 256) / ROW_CHUNKS;
+        const int j = j0 + (lt + (i % (PER / 2)) * GT) / ROW_CHUNKS;
         // zeroed by a mask, not a select: a select became a branch around register copies
         const uint32_t keep = (j < Mk && (MASKED || j >= key_start)) ? 0xFFFFFFFFu : 0u;
         *slot(i) = make_uint4(reg[i].x & keep, reg[i].y & keep, reg[i].z & keep, reg[i].w & keep);
@@ -216,8 +222,14 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
         for (int s = 0; s < DS; ++s) {
           const fa_bf16x8 a = *reinterpret_cast<const fa_bf16x8*>(ks + (sub * 32 + col) * STRK + 16 * s + 8 * half);
           sacc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[sub], 0, 0, 0);
-          if constexpr (decltype(prefetch)::value)
-            if ((sub * DS + s) & 1) load_one((sub * DS + s) >> 1, jn, stage);
+          if constexpr (decltype(prefetch)::value) {
+            if constexpr (PER >= 2 * DS) {
+#pragma unroll
+              for (int u = 0; u < PER / (2 * DS); ++u) load_one((sub * DS + s) * (PER / (2 * DS)) + u, jn, stage);
+            } else if ((sub * DS + s) & 1) {
+              load_one((sub * DS + s) >> 1, jn, stage);
+            }
+          }
         }
       }
       // Scores of key j0 + 32 sub + 8 (e / 4) + 4 half + e % 4 for query qi; only
@@ -330,7 +342,7 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
     // group 1's state into its own stages (dead: the loop ended on a barrier), then
     // group 0 combines it with its own, lane by lane (same query, same d)
     constexpr int REC = 2 + 16 * DT;
-    static_assert(4 * 64 * REC * 4 <= (int)sizeof(lds_all[1]), "the handover fits group 1's stages");
+    static_assert(QW * 64 * REC * 4 <= (int)sizeof(lds_all[1]), "the handover fits group 1's stages");
     float* hand = reinterpret_cast<float*>(&lds_all[1][0][0]) + (size_t)(wave * 64 + lane) * REC;
     if (group == 1) {
       hand[0] = run_max;
@@ -371,17 +383,17 @@ __device__ void flash_attention_body(const uint16_t* __restrict__ q, const uint1
 
 // aoto_flash_attention_d{D} (4-wave blocks, two per CU) and aoto_flash_attention_d{D}_k2
 // (8-wave blocks whose two wave groups split the keys); the _m forms take an explicit mask.
-#define AOTO_FLASH_INSTANCE_KG(D, KG, MASKED, SUFFIX, MINB)                                             \
-  extern "C" __global__ __launch_bounds__(256 * KG, MINB) void aoto_flash_attention_d##D##SUFFIX(      \
+#define AOTO_FLASH_INSTANCE_KG(D, KG, MASKED, SUFFIX, MINB, QW)                                         \
+  extern "C" __global__ __launch_bounds__(64 * QW * KG, MINB) void aoto_flash_attention_d##D##SUFFIX(   \
       const uint16_t* q, const uint16_t* k, const uint16_t* v, long long kv_batch_stride,               \
       long long kv_head_stride, const uint8_t* mask, long long mask_batch_stride, int causal,           \
       int key_start, int M, int Mk, int batch, int query_heads, int kv_heads, float scale,              \
       uint16_t* out) {                                                                                  \
-    aoto::flash_attention_body<D, KG, MASKED>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
+    aoto::flash_attention_body<D, KG, MASKED, QW>(q, k, v, kv_batch_stride, kv_head_stride, mask, mask_batch_stride, \
                                       causal, key_start, M, Mk, batch, query_heads, kv_heads, scale, out); \
   }
-#define AOTO_FLASH_INSTANCE(D)                 \
-  AOTO_FLASH_INSTANCE_KG(D, 1, false, , 2)     \
-  AOTO_FLASH_INSTANCE_KG(D, 2, false, _k2, 1)  \
-  AOTO_FLASH_INSTANCE_KG(D, 1, true, _m, 2)    \
-  AOTO_FLASH_INSTANCE_KG(D, 2, true, _k2_m, 1)
+#define AOTO_FLASH_INSTANCE(D)                   \
+  AOTO_FLASH_INSTANCE_KG(D, 1, false, , 2, 4)    \
+  AOTO_FLASH_INSTANCE_KG(D, 2, false, _k2, 1, 4) \
+  AOTO_FLASH_INSTANCE_KG(D, 1, true, _m, 2, 4)   \
+  AOTO_FLASH_INSTANCE_KG(D, 2, true, _k2_m, 1, 4)

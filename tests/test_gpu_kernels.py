@@ -241,6 +241,11 @@ PREFILL_CASES = [
     (4, 2, 64, 16, 16),      # one key tile: the block's second key group has none
     (4, 2, 64, 16, 11),      # ... left-padded
     (32, 8, 128, 40, 40),    # ... at D = 128
+    # D = 64 grids of at most a quarter (half) of the CUs take 32-query (64-query) blocks
+    # of two 1-wave (2-wave) key groups:
+    (14, 2, 64, 256, 256),   # 32-query blocks; the last sees four key tiles: prefetched trips, then the last
+    (14, 2, 64, 200, 150),   # 32-query blocks, ragged query tiles with a left pad
+    (14, 2, 64, 1024, 1000), # 64-query blocks, up to 16 key tiles, left pad
 ]
 
 
