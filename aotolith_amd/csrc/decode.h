@@ -361,44 +361,54 @@ __device__ void decode_attention_body(const uint16_t* __restrict__ q, const uint
 
 // Combine the split records of aoto_decode_attention_*: one block per (b, head),
 //   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s; 0 when no key is kept.
-// Every load is independent of the others (split s's record is read by thread
-// s % 128, then each thread reads its column of all records with an unrolled
-// loop), so a merge costs a couple of memory round trips, not one per split.
-// splits <= kMergeMaxSplits (checked on the host).
+// Thread d loads column d of the first kMergeRegSplits records into registers
+// before anything waits, so the columns arrive with the (m, l) pairs in one round
+// trip; the maximum and the denominator are block reductions of one split per
+// thread, the column sums read the weights from LDS. D <= 128 (one column per
+// thread) and splits <= kMergeMaxSplits, both checked on the host.
 constexpr int kMergeMaxSplits = 1024;
+constexpr int kMergeRegSplits = 40;
 extern "C" __global__ __launch_bounds__(128) void aoto_decode_attention_merge(const float* __restrict__ partials,
                                                                              int splits, int D,
                                                                              uint16_t* __restrict__ out) {
   __shared__ float s_w[kMergeMaxSplits];
-  __shared__ float s_red[2];
+  __shared__ float s_red[4];
   const int bh = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float* rec = partials + (size_t)bh * splits * (D + 2);
+  const int d = threadIdx.x;
+  const bool column = d < D;  // uniform per wave (D is 64 or 128)
+  const int dc = column ? d : 0;
+  const size_t stride = (size_t)D + 2;
+  const float* rec = partials + (size_t)bh * splits * stride;
+  float a[kMergeRegSplits];
+#pragma unroll
+  for (int s = 0; s < kMergeRegSplits; ++s) a[s] = s < splits ? rec[(size_t)s * stride + 2 + dc] : 0.f;
   float m = -INFINITY;
-  for (int s = threadIdx.x; s < splits; s += 128) m = fmaxf(m, rec[(size_t)s * (D + 2)]);
+  for (int s = threadIdx.x; s < splits; s += 128) m = fmaxf(m, rec[(size_t)s * stride]);
   m = wave_max(m);
   if (lane == 0) s_red[wave] = m;
   __syncthreads();
   const float M = fmaxf(s_red[0], s_red[1]);
-  __syncthreads();  // s_red is reused for the denominator
   float den = 0.f;
   for (int s = threadIdx.x; s < splits; s += 128) {
-    const float ms = rec[(size_t)s * (D + 2)];
-    const float ls = rec[(size_t)s * (D + 2) + 1];
+    const float ms = rec[(size_t)s * stride];
+    const float ls = rec[(size_t)s * stride + 1];
     const float w = (M == -INFINITY || ms == -INFINITY) ? 0.f : expf(ms - M);
     s_w[s] = w;
     den = fmaf(w, ls, den);
   }
   den = wave_sum(den);
-  if (lane == 0) s_red[wave] = den;
+  if (lane == 0) s_red[2 + wave] = den;
   __syncthreads();
-  den = s_red[0] + s_red[1];
-  for (int d = threadIdx.x; d < D; d += 128) {
-    float num = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < splits; ++s) num = fmaf(s_w[s], rec[(size_t)s * (D + 2) + 2 + d], num);
-    out[(size_t)bh * D + d] = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
+  den = s_red[2] + s_red[3];
+  float num = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMergeRegSplits; ++s) {
+    const float t = fmaf(s_w[s], a[s], num);
+    num = s < splits ? t : num;
   }
+  for (int s = kMergeRegSplits; s < splits; ++s) num = fmaf(s_w[s], rec[(size_t)s * stride + 2 + dc], num);
+  if (column) out[(size_t)bh * D + d] = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
 }
 
 // Embedding gather: out[i][:] = weight[ids[i]][:] for `count` ids (int64 on
