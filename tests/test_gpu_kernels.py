@@ -346,6 +346,8 @@ def test_argmax_records_history():
     (14, 2, 64, 192, 140, 61, 60, 0),      # Qwen shape, one block per kv head
     (14, 2, 64, 192, 191, 0, 191, 3),     # rolled layout, 3 splits + merge
     (32, 8, 128, 2304, 1500, 700, 699, 0),  # Llama-8B window, split-K + merge
+    (32, 8, 128, 768, 640, 0, 639, 0),       # Llama-8B 512 bucket window, slot in the last split
+    (32, 8, 128, 768, 300, 100, 99, 0),      # ... partly filled, wrapped ring
 ])
 @pytest.mark.parametrize("rows", [False, True])
 def test_decode_rope_attention_matches_append_then_attend(hq, hkv, dim, cap, valid, offset, slot, splits, rows):
