@@ -91,6 +91,24 @@ def test_library_gemm_matches_the_oracle_and_the_fused_kernel(epilogue, m, bits)
     assert_bf16_parity(from_gpu_bf16(y), from_gpu_bf16(fused), max_ulp=ulp, atol=_atol(expected))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 128])
+def test_library_gemm_other_group_sizes(group, bits):
+    """The unpack takes any group size the GEMM accepts: groups of 32 and 128 at 1024 rows."""
+
+    ops = _ops()
+    m, n, k = 1024, 640, 1024
+    rng = np.random.default_rng(560 + group + bits)
+    packed, scales, gp, gs = _weights(rng, n, k, bits, group)
+    x = bf16_normal(rng, (m, k))
+    bias = bf16_normal(rng, (n,), 0.5)
+    matmul = ops.w4_matmul if bits == 4 else ops.w8_matmul
+    y, names = _traced(lambda: matmul(to_gpu_bf16(x), gp, gs, group, bias=to_gpu_bf16(bias)))
+    assert "hipblaslt_matmul_bf16" in names, names
+    expected = oracle.w4_matmul(x, packed, scales, group, bias=bias, bits=bits)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0, atol=_atol(expected))
+
+
 def test_library_gemm_in_place_residual():
     ops = _ops()
     m, n, k = 1024, 896, 1024
