@@ -637,8 +637,8 @@ int unpack_weight(int bits, const int32_t* words, const void* scales, int N, int
 // One hipBLASLt GEMM of the long-prefill path, traced as hipblaslt_matmul_{bf16,f32}
 // (the output type) for plans that name the kernels they run.
 int library_launch(int M, int N, int K, const void* x, const void* w, const void* bias, const void* c, void* d,
-                   bool d_f32, void* stream) {
-  if (int st = aoto::library_gemm(M, N, K, x, w, bias, c, d, d_f32, stream)) return st;
+                   bool d_f32, void* scratch, void* stream) {
+  if (int st = aoto::library_gemm(M, N, K, x, w, bias, c, d, d_f32, scratch, stream)) return st;
   trace_launch(d_f32 ? "hipblaslt_matmul_f32" : "hipblaslt_matmul_bf16");
   return AOTO_OK;
 }
@@ -668,17 +668,17 @@ int library_packed_gemm(int bits, const void* x, const int32_t* words, const voi
     uint16_t* ubuf = wbuf + (size_t)N * K;
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(dbuf + (size_t)M * N);
     if (int st = unpack_weight(bits, up_words, up_scales, N, K, group, ubuf, stream)) return st;
-    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, gbuf, false, stream)) return st;
+    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, gbuf, false, dbuf, stream)) return st;
     gate = gbuf;
     wbuf = ubuf;
   }
   if (gate != nullptr) {
-    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, dbuf, true, stream)) return st;
+    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, dbuf, true, dbuf, stream)) return st;
     const void* none = nullptr;
     return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream, (const float*)dbuf,
                   1, none, none, gate, y, M, N);
   }
-  if (int st = library_launch(M, N, K, x, wbuf, bias, residual, y, false, stream)) return st;
+  if (int st = library_launch(M, N, K, x, wbuf, bias, residual, y, false, dbuf, stream)) return st;
   if (norm_out != nullptr)
     return launch("aoto_rms_norm", dim3((M + 3) / 4), dim3(256), 0, stream, y, norm_weight, eps, norm_out, M, N);
   if (rope != nullptr) return rope_after_gemm(y, M, *rope, stream);

@@ -19,7 +19,8 @@
 // at 2048 rows, random data: o 72.5 -> 55.4 us, down 228.6 -> 181.8 us for the
 // best of its first 12 workspace-free candidates), so the first call of a shape
 // outside a graph capture times up to kCandidates of them on the call's own x
-// and w, into a scratch output, and keeps the fastest.
+// and w, into a scratch output the caller provides (a region of its workspace
+// that the call overwrites anyway), and keeps the fastest.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -118,21 +119,21 @@ int lt_plan(hipblasLtHandle_t handle, const LtKey& key, LtPlan** plan) {
 }
 
 // With g_lt_mutex held: time each candidate (one warm-up, then 3 launches between
-// events) on the call's x, w and bias into a zeroed scratch output (also the C
-// input when the plan has one) and keep the fastest. Not inside a graph capture
-// (nothing may synchronize there): the plan stays untuned and the first
-// uncaptured call tunes it. Any failure keeps the heuristic's first pick.
+// events) on the call's x, w and bias into the zeroed scratch output (M * N of the
+// output type, also the C input when the plan has one) and keep the fastest.
+// Nothing is allocated. Not inside a graph capture (nothing may synchronize
+// there): the plan stays untuned and the first uncaptured call tunes it. Any
+// failure keeps the heuristic's first pick.
 void lt_tune(hipblasLtHandle_t handle, const LtKey& key, LtPlan* plan, const void* x, const void* w,
-             const void* bias, hipStream_t stream) {
+             const void* bias, void* scratch, hipStream_t stream) {
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) return;
   plan->tuned = true;
-  if (plan->candidates.size() < 2) return;
+  if (plan->candidates.size() < 2 || scratch == nullptr) return;
   const size_t bytes = (size_t)key.M * key.N * (key.d_f32 ? 4 : 2);
-  void* scratch = nullptr;
   hipEvent_t start = nullptr, stop = nullptr;
-  if (hipMalloc(&scratch, bytes) != hipSuccess || hipEventCreate(&start) != hipSuccess ||
-      hipEventCreate(&stop) != hipSuccess || hipMemsetAsync(scratch, 0, bytes, stream) != hipSuccess) {
+  if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess ||
+      hipMemsetAsync(scratch, 0, bytes, stream) != hipSuccess) {
     (void)hipGetLastError();
   } else {
     if (bias != nullptr)
@@ -158,7 +159,6 @@ void lt_tune(hipblasLtHandle_t handle, const LtKey& key, LtPlan* plan, const voi
   }
   if (start != nullptr) (void)hipEventDestroy(start);
   if (stop != nullptr) (void)hipEventDestroy(stop);
-  if (scratch != nullptr) (void)hipFree(scratch);
 }
 
 }  // namespace
@@ -170,7 +170,7 @@ int library_prepare(int device) {
 }
 
 int library_gemm(int M, int N, int K, const void* x, const void* w, const void* bias, const void* c, void* d,
-                 bool d_f32, void* stream) {
+                 bool d_f32, void* scratch, void* stream) {
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return set_error(AOTO_ERR_HIP, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_lt_mutex);
@@ -179,7 +179,7 @@ int library_gemm(int M, int N, int K, const void* x, const void* w, const void* 
   LtPlan* plan = nullptr;
   const LtKey key{device, M, N, K, d_f32 ? 1 : 0, bias != nullptr, c != nullptr};
   if (int s = lt_plan(handle, key, &plan)) return s;
-  if (!plan->tuned) lt_tune(handle, key, plan, x, w, bias, (hipStream_t)stream);
+  if (!plan->tuned) lt_tune(handle, key, plan, x, w, bias, scratch, (hipStream_t)stream);
   if (bias != nullptr)
     hipblasLtMatmulDescSetAttribute(plan->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
   const float alpha = 1.0f, beta = c != nullptr ? 1.0f : 0.0f;

@@ -19,9 +19,11 @@ void fused_gemm_codes(int M, int N, int K, int* tile, int* splits);
 // Plain bf16 GEMMs on hipBLASLt (blaslt.cpp): D[M][N] = X[M][K] . W[N][K]^T
 // (+ bias[N]) (+ c[M][N]), f32 accumulation, D bf16 or f32. library_prepare
 // creates the device's handle (called when a code object is installed, outside
-// any graph capture); library_gemm enqueues one GEMM on `stream`.
+// any graph capture); library_gemm enqueues one GEMM on `stream`. `scratch`
+// (M * N of the output type, not aliasing the operands) takes the candidate
+// timing of a shape's first uncaptured call; its contents are overwritten.
 int library_prepare(int device);
 int library_gemm(int M, int N, int K, const void* x, const void* w, const void* bias, const void* c, void* d,
-                 bool d_f32, void* stream);
+                 bool d_f32, void* scratch, void* stream);
 
 }  // namespace aoto
