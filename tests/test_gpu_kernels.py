@@ -348,6 +348,7 @@ def test_argmax_records_history():
     (32, 8, 128, 2304, 1500, 700, 699, 0),  # Llama-8B window, split-K + merge
     (32, 8, 128, 768, 640, 0, 639, 0),       # Llama-8B 512 bucket window, slot in the last split
     (32, 8, 128, 768, 300, 100, 99, 0),      # ... partly filled, wrapped ring
+    (32, 8, 128, 2304, 2304, 5, 4, 72),      # 72 splits: the merge's records past its 40 register columns
 ])
 @pytest.mark.parametrize("rows", [False, True])
 def test_decode_rope_attention_matches_append_then_attend(hq, hkv, dim, cap, valid, offset, slot, splits, rows):
