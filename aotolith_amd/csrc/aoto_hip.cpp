@@ -557,8 +557,16 @@ namespace {
 // Llama-8B projections, hipBLASLt alone takes 68 / 67 / 2 x 140 / 201 us for
 // q/k/v, o, gate + up and down against 146-166 / 98 / 582-590 / 287-296 for the
 // fused kernels, the unpack ~100 us per layer. At 512 rows the unpack would
-// cost as much as the library saves.
-bool library_rows(int M, int tile, int splits) { return M >= kLibraryRows && tile == 0 && splits == 0; }
+// cost as much as the library saves - except for the q/k/v projection of an
+// 8B-class model (K >= 2048), whose fused form carries the RoPE epilogue
+// (Llama-3-8B at 512 rows: 52 against 64 us; o 41 / 41, gate/up 231 / 186, down
+// 118 / 94).
+constexpr int kLibraryRowsQkv = 512;
+
+bool library_rows(int M, int tile, int splits, int K = 0, bool qkv = false) {
+  if (tile != 0 || splits != 0) return false;
+  return M >= kLibraryRows || (qkv && K >= 2048 && M >= kLibraryRowsQkv);
+}
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -606,7 +614,8 @@ size_t aoto_hip_w4_gemm_qkv_rope_workspace(int M, int K, int tile, int splits, i
                                            int head_dim) {
   if (query_heads <= 0 || kv_heads <= 0 || head_dim <= 0) return 0;
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  if (!library_rows(M, tile, splits)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  if (library_rows(M, tile, splits, K, true)) return library_workspace(M, N, K, false);
+  qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
   return aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
 }
 
@@ -712,7 +721,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
                 what);
   if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28", what, tile);
-  if (library_rows(M, tile, splits))
+  if (library_rows(M, tile, splits, K, rope != nullptr))
     return library_packed_gemm(bits, x, words, scales, bias, residual, gate, y, M, N, K, group, workspace, stream,
                                up_words, up_scales, norm_weight, eps, norm_out, rope, what);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
@@ -786,7 +795,7 @@ int qkv_rope_gemm(int bits, const void* x, const int32_t* words, const void* sca
                            (uint16_t*)q_out, (uint16_t*)pair, query_heads, kv_heads, head_dim, capacity, slot0,
                            zero_prefix};
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  if (!library_rows(M, tile, splits)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  if (!library_rows(M, tile, splits, K, true)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
   return packed_gemm(bits, x, words, scales, bias, nullptr, nullptr, y, M, N, K, group, tile, splits, workspace,
                      stream, nullptr, nullptr, nullptr, 0.f, nullptr, &rope);
 }

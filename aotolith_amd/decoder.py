@@ -900,7 +900,7 @@ class _Engine:
                 ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
             pair = pair_of(index)
             _mark(rec, "addmm" if s.qkv_bias else "matmul", f"qkv_{index}", gemm,
-                  (f"W{bits} unpack to bf16 and the hipBLASLt GEMM" if m >= ops.LIBRARY_ROWS
+                  (f"W{bits} unpack to bf16 and the hipBLASLt GEMM" if ops.library_plan(m, s.hidden, qkv=True)
                    else f"fused-dequant W{bits} GEMM on bf16 MFMA") + (" with q/k/v bias" if s.qkv_bias else "")
                   + ", RoPE of q/k and the layer's cache fill (with the split-K sum when the plan splits)")
             # q/k/v projection, RoPE and the cache fill (one launch fewer when the plan splits K)

@@ -358,6 +358,17 @@ def w8_matmul(
 #: unpacks the weight to bf16 into the workspace and runs the product on
 #: hipBLASLt (the C ABI's kLibraryRows); explicit codes keep the fused kernel.
 LIBRARY_ROWS = 1024
+#: ... and from this many for the q/k/v RoPE form of a reduction of at least
+#: LIBRARY_QKV_MIN_K (an 8B-class hidden size), whose fused form carries the RoPE.
+LIBRARY_ROWS_QKV = 512
+LIBRARY_QKV_MIN_K = 2048
+
+
+def library_plan(m: int, k: int, *, qkv: bool = False) -> bool:
+    """Whether the automatic prefill GEMM plan for ``m`` rows (reduction ``k``) unpacks the
+    weight for hipBLASLt (the C ABI's rule for tile = splits = 0)."""
+
+    return m >= LIBRARY_ROWS or (qkv and k >= LIBRARY_QKV_MIN_K and m >= LIBRARY_ROWS_QKV)
 
 
 def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:

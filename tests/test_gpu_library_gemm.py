@@ -163,13 +163,33 @@ def test_library_residual_norm_matches_the_oracle(n, bits):
     assert_bf16_parity(from_gpu_bf16(norm), oracle.rms_norm(from_gpu_bf16(y), weight, 1e-6), max_ulp=1.0)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("hq,hkv,dim,bias", [(8, 2, 128, True), (14, 2, 64, False)])
-def test_library_qkv_rope_matches_the_oracle(hq, hkv, dim, bias, bits):
+def test_library_qkv_rule_from_512_rows_at_8b_widths():
+    """The q/k/v RoPE form takes the library path from 512 rows when K >= 2048 (its fused
+    form carries the RoPE epilogue), every other form from 1024."""
+
+    from aotolith_amd import _lib
+
     ops = _ops()
-    m, k, slot0 = 1024, 512, 9
+    lib = _lib.library()
+    n = (32 + 2 * 8) * 128
+    assert lib.aoto_hip_w4_gemm_qkv_rope_workspace(512, 4096, 0, 0, 32, 8, 128) == n * 4096 * 2 + 512 * n * 4
+    assert lib.aoto_hip_w4_gemm_qkv_rope_workspace(511, 4096, 0, 0, 32, 8, 128) < n * 4096 * 2
+    assert lib.aoto_hip_w4_gemm_qkv_rope_workspace(512, 896, 0, 0, 14, 2, 64) < 1152 * 896 * 2
+    assert ops.gemm_workspace_bytes(512, n, 4096) < n * 4096 * 2  # the plain GEMM keeps the fused kernel
+    assert ops.library_plan(512, 4096, qkv=True) and not ops.library_plan(512, 4096)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m,k,hq,hkv,dim,bias", [
+    (1024, 512, 8, 2, 128, True),
+    (1024, 512, 14, 2, 64, False),
+    (512, 2048, 8, 2, 128, True),   # the q/k/v rule's 512-row library plan
+])
+def test_library_qkv_rope_matches_the_oracle(m, k, hq, hkv, dim, bias, bits):
+    ops = _ops()
+    slot0 = 9
     n = (hq + 2 * hkv) * dim
-    rng = np.random.default_rng(540 + dim + bits)
+    rng = np.random.default_rng(540 + dim + bits + m)
     packed, scales, gp, gs = _weights(rng, n, k, bits)
     x = bf16_normal(rng, (m, k))
     b = bf16_normal(rng, (n,), 0.02) if bias else None
