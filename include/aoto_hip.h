@@ -223,8 +223,8 @@ int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const vo
  * rotated keys / values at slots slot0 .. slot0 + M - 1 (slots below slot0 zeroed
  * when zero_prefix != 0); positions[M] int64. tile and splits as aoto_hip_w4_gemm,
  * with 0 / 0 choosing the unsplit epilogue form whenever it applies (32-row blocks
- * up to 128 rows) and the long-prefill library path from 1024 rows (the RoPE /
- * cache fill kernel after it);
+ * up to 128 rows) and the long-prefill library path from 1024 rows, or 512 when
+ * K >= 2048 (the RoPE / cache fill kernel after it);
  * workspace: aoto_hip_w4_gemm_qkv_rope_workspace() bytes. */
 int aoto_hip_w4_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
                               int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,
