@@ -1123,14 +1123,18 @@ int aoto_hip_prefill_attention(const void* q, const void* keys, const void* valu
   // one block per (128-query tile, batch, query head), the query tile slowest.
   // Grids that do not fill two 4-wave blocks per CU use 8-wave blocks whose two
   // wave groups split the keys (every CU then runs two waves per SIMD throughout).
-  // A grid that fills at most a quarter (half) of the CUs at D = 64 - a short
-  // prompt: Qwen2's 128 tokens make 14 blocks - takes 32-query (64-query) blocks of
-  // two 1-wave (2-wave) key groups instead: 4x (2x) the blocks, one wave per SIMD.
+  // A grid that fills at most a quarter (half) of the CUs - a short prompt:
+  // Qwen2's 128 tokens make 14 blocks, Llama-3-8B's 512 make 128 - takes 32-query
+  // (64-query) blocks of two 1-wave (2-wave) key groups instead: 4x (2x) the
+  // blocks, one wave per SIMD (32-query blocks at D = 64 only).
   long long blocks = (long long)((tokens + 127) / 128) * batch * query_heads;
   if (blocks > 0x7FFFFFFFLL) return fail(AOTO_ERR_UNSUPPORTED, "prefill_attention: grid too large");
   const bool split_keys = blocks <= 2LL * cu_count();
   int queries = 128;  // per block
-  if (head_dim == 64 && mask == nullptr) queries = 4 * blocks <= cu_count() ? 32 : 2 * blocks <= cu_count() ? 64 : 128;
+  if (mask == nullptr) {
+    if (head_dim == 64) queries = 4 * blocks <= cu_count() ? 32 : 2 * blocks <= cu_count() ? 64 : 128;
+    else if (2 * blocks <= cu_count()) queries = 64;  // D = 128 has no 32-query instance (registers)
+  }
   if (queries < 128) blocks = (long long)((tokens + queries - 1) / queries) * batch * query_heads;
   char name[64];
   snprintf(name, sizeof(name), "aoto_flash_attention_d%d%s%s%s", head_dim, split_keys ? "_k2" : "", mask ? "_m" : "",

@@ -113,3 +113,4 @@ AOTO_FLASH_INSTANCE(128)
 // short prompts at D = 64: 64 (32) queries per block, two 2-wave (1-wave) key groups
 AOTO_FLASH_INSTANCE_KG(64, 2, false, _k2_q64, 1, 2)
 AOTO_FLASH_INSTANCE_KG(64, 2, false, _k2_q32, 1, 1)
+AOTO_FLASH_INSTANCE_KG(128, 2, false, _k2_q64, 1, 2)

@@ -246,6 +246,7 @@ PREFILL_CASES = [
     (14, 2, 64, 256, 256),   # 32-query blocks; the last sees four key tiles: prefetched trips, then the last
     (14, 2, 64, 200, 150),   # 32-query blocks, ragged query tiles with a left pad
     (14, 2, 64, 1024, 1000), # 64-query blocks, up to 16 key tiles, left pad
+    (32, 8, 128, 512, 500),  # D = 128 64-query blocks (Llama-8B 512 bucket), left pad
 ]
 
 
