@@ -297,10 +297,11 @@ void decode_split(int head_dim, int capacity, int requested, long long rows, int
   const int most = decode_max_chunk(head_dim);
   int s = requested > 0 ? requested : (capacity + most - 1) / most;
   if (requested <= 0 && s > 1) {
-    // A window that needs a merge launch anyway is spread over ~1152 blocks,
-    // chunks of at least 32 keys (Llama-8B, 32 heads: 768-key window 657 ->
-    // 680 tok/s with 24 splits, 2304-key window 614 -> 624 with 36).
-    const long long want = (1152 + rows - 1) / rows;
+    // A window that needs a merge launch anyway is spread over ~768 blocks,
+    // chunks of at least 32 keys (Llama-8B, 32 heads, split + merge per layer:
+    // 768-key window 8.5 us at 12 or 24 splits, 9.3 at 6; 2304-key window 10.8 us
+    // at 24 splits, 11.8 at 36, 13.4 at 48, 13.6 at 18).
+    const long long want = (768 + rows - 1) / rows;
     const int finest = (capacity + 31) / 32;
     if (want > s) s = (int)(want < finest ? want : finest);
   }
