@@ -14,7 +14,8 @@
 // values at k/v + b*kv_batch_stride + kvh*kv_head_stride + j*D; output
 // [B][M][Hq*D] (the o projection's input rows).
 //
-// Block: 4 waves, 128 queries of one head (wave w: queries q0 + 32w .. q0 + 32w + 31).
+// Block: 4 waves, 128 queries of one head (wave w: queries q0 + 32w .. q0 + 32w + 31);
+// the short-prompt instances take 2 or 1 waves (64 or 32 queries) per key group.
 // Key tiles of 64 rows are staged in LDS row-major, each with its own row stride
 // so that its reads touch all 64 four-byte banks once per phase: K rows D + 8 bf16
 // apart (a 16-byte read per lane, 16 lanes a phase: rows 4 banks apart), V rows
