@@ -1179,12 +1179,18 @@ int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* sca
       !aligned8(keys))
     return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: x, words and norm weight must be 16-byte aligned, scales "
                 "4-byte, keys 8-byte");
+  // The K = 896 LM head with its final norm stages the normalized x once per
+  // 4-wave block instead of once per wave (aoto_w4_gemv_x8x4_n1_argmax: Qwen2's
+  // 151936 rows 14.87-14.94 -> 14.82-14.84 us, same-box A/B).
+  const bool blockx = norm_weight != nullptr && ss.lpr == 8 && ss.cpl == 4 && !ss.direct;
+  if (blockx) ss.block_x = true;
   const StreamLaunch l = stream_launch(ss, K, N, group);
   if (key_count < (size_t)(l.grid * l.wpb))
     return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: %zu keys given, %lld needed (aoto_hip_w4_gemv_argmax_keys)",
                 key_count, l.grid * l.wpb);
   char sname[64];
-  snprintf(sname, sizeof(sname), "aoto_w4_gemv_s%dx%d_n%d_argmax", ss.lpr, ss.cpl, norm_weight ? 1 : 0);
+  snprintf(sname, sizeof(sname), "aoto_w4_gemv_%s%dx%d_n%d_argmax", blockx ? "x" : "s", ss.lpr, ss.cpl,
+           norm_weight ? 1 : 0);
   const void* none = nullptr;
   return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, x, words, scales, none, none,
                 norm_weight, eps, none, 1.0f, 0.0f, y, K, N, l.shift, l.wpb, keys);
