@@ -1179,10 +1179,14 @@ int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* sca
       !aligned8(keys))
     return fail(AOTO_ERR_ARGUMENT, "w4_gemv_argmax: x, words and norm weight must be 16-byte aligned, scales "
                 "4-byte, keys 8-byte");
-  // The K = 896 LM head with its final norm stages the normalized x once per
-  // 4-wave block instead of once per wave (aoto_w4_gemv_x8x4_n1_argmax: Qwen2's
-  // 151936 rows 14.87-14.94 -> 14.82-14.84 us, same-box A/B).
-  const bool blockx = norm_weight != nullptr && ss.lpr == 8 && ss.cpl == 4 && !ss.direct;
+  // The K = 896 and K = 4096 LM heads with their final norm stage the
+  // normalized x once per 4-wave block instead of once per wave
+  // (aoto_w4_gemv_x8x4_n1_argmax: Qwen2's 151936 rows 14.87-14.94 -> 14.82-14.84
+  // us; aoto_w4_gemv_x32x4_n1_argmax: Llama-3's 128256 rows 44.1-44.3 -> 43.4-43.5
+  // us; same-box A/Bs). Only where the per-wave form already runs 4-wave blocks,
+  // so the grid, and the key count aoto_hip_w4_gemv_argmax_keys reports, match.
+  const bool blockx = norm_weight != nullptr && !ss.direct && ss.cpl == 4 && (ss.lpr == 8 || ss.lpr == 32) &&
+                      stream_launch(ss, K, N, group).wpb == 4;
   if (blockx) ss.block_x = true;
   const StreamLaunch l = stream_launch(ss, K, N, group);
   if (key_count < (size_t)(l.grid * l.wpb))

@@ -47,8 +47,9 @@ AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 7, 7)
 // LM heads with the fused greedy-argmax keys: K = 896 (8x4), K = 4096 (32x4),
 // and direct 64-lane forms for any other K up to 2048 / 6144.
 AOTO_GEMV_STREAM_ARGMAX(8, 4, 2, false)
-// the K = 896 LM head with its final norm, x staged once per block
+// the K = 896 and K = 4096 LM heads with their final norm, x staged once per block
 AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x8x4_n1_argmax, 8, 4, 1, false, 1, 0, 0, true, true)
+AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x32x4_n1_argmax, 32, 4, 2, false, 1, 0, 0, true, true)
 AOTO_GEMV_STREAM_ARGMAX(32, 4, 8, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 1, 0, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 3, 0, true)

@@ -117,7 +117,7 @@ def measure_lm_head_gemv(spec, torch, ops, *, launches: int = 24, rounds: int = 
     key_count = ops.argmax_key_count(k, n, group) if bits == 4 else 0
     keys = torch.empty((max(key_count, 1),), dtype=torch.int64, device="cuda")
     if key_count:
-        kernel = ("aoto_w4_gemv_x8x4_n1_argmax / _s32x4_n1_argmax (the greedy loop's LM head: RMSNorm prologue + "
+        kernel = ("aoto_w4_gemv_x8x4_n1_argmax / _x32x4_n1_argmax (the greedy loop's LM head: RMSNorm prologue + "
                   "argmax keys)")
 
         def launch(i):
