@@ -359,9 +359,6 @@ int aoto_hip_load_code_object(const void* image, size_t size) {
   slot.module = module;
   slot.functions.clear();
   aoto::noalloc_prepare_device(device);
-  // the hipBLASLt handle of long prefills, created here (never inside a graph
-  // capture); a failure is reported by the first long prefill that needs it
-  aoto::library_prepare(device);
   return AOTO_OK;
 }
 
@@ -488,14 +485,72 @@ namespace {
 // reduction so at least ~256 blocks run; each slice keeps >= 2 k-steps of 64.
 struct GemmPlan {
   int tn, tm, splits, kslice;
+  // the wide-tile family (w4_gemm_wide.h): 32-row / 32-column tiles per wave, waves per block
+  int wide_mt = 0, wide_nt = 0, wide_nw = 0;
+  int bm() const { return wide_mt ? 32 * wide_mt : 16 * tm; }
+  int bn() const { return wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
+  int threads() const { return wide_nw ? 64 * wide_nw : 256; }
 };
 
-// The first row count of the long-prefill library path (see library_rows).
-constexpr int kLibraryRows = 1024;
+// Wide-tile codes: 100 * (waves per block / 2) + 10 * (32-row tiles per wave) +
+// (32-column tiles per wave), the waves side by side along n (w4_gemm_wide.h).
+bool wide_code(int tile) {
+  return tile == 241 || tile == 242 || tile == 243 || tile == 281 || tile == 441 || tile == 442;
+}
+
+// The wide instances in the code object (their staging fits 160 KB of LDS).
+bool wide_instance(int tile, int bits, bool paired) {
+  if (paired) return tile == 241 || (bits == 4 && tile == 441);
+  return bits == 4 || tile == 241 || tile == 242 || tile == 441;
+}
+
+// From this many rows (and K % 256 == 0: every group size up to 128 then gives an
+// even number of groups per row) the automatic plan takes the wide-tile kernels.
+constexpr int kWideRows = 512;
+
+bool wide_auto_rows(int M, int K) { return M >= kWideRows && K % 256 == 0; }
+
+// The automatic wide plan. Tiles: q/k/v-like outputs that fill the chip with
+// 384-column blocks take 128 x 96 waves (243), other grids of >= 224 blocks of 128 x
+// 256 take 8-wave blocks of 128 x 32 waves (441), smaller ones 128 x 32 waves in
+// 4-wave blocks (241), split along k when fewer than 160 blocks would run. The
+// paired gate/up always takes 241 (two accumulator sets). Measured on MI355X for
+// the Llama-3-8B projections at 2048 rows (us, o / down / q/k/v): 242 84.8 / 253.5 /
+// 145.7, 441 83.4 / 253.9 / 139.8, 243 - / - / 114.3; at 512 rows 241 with the split
+// rule: q/k/v 38.7, o 32.9, gate/up 134.6, down 78.6. The choice does not depend on
+// the code width (243 has no 8-bit instance; the launch substitutes 441, whose grid
+// is then unsplit too), so the workspace queries, which do not know it, agree.
+void wide_auto_plan(int M, int N, int K, bool paired, int* tile, int* splits) {
+  const long long mb = (M + 127) / 128;
+  auto blocks = [&](int bn) { return (long long)((N + bn - 1) / bn) * mb; };
+  int t = 241;
+  if (!paired && N % 384 == 0 && blocks(384) >= 224)
+    t = 243;
+  else if (!paired && blocks(256) >= 224)
+    t = 441;
+  const long long b = t == 243 ? blocks(384) : t == 441 ? blocks(256) : blocks(128);
+  int s = 1;
+  if (b < 160) s = (int)((256 + b - 1) / b);
+  const int most = (K / 128) / 2;  // at least two 128-k steps per slice
+  if (s > most) s = most > 1 ? most : 1;
+  *tile = t;
+  *splits = s;
+}
+
+// Automatic codes (tile = splits = 0) resolved to explicit ones for long prompts;
+// other codes pass unchanged (the 16x16 kernel's own plan handles tile = 0 below
+// kWideRows).
+void resolve_auto(int M, int N, int K, bool paired, int* tile, int* splits) {
+  if (*tile == 0 && *splits == 0 && wide_auto_rows(M, K)) wide_auto_plan(M, N, K, paired, tile, splits);
+}
 
 GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
-  if (tile == 0) {
+  if (wide_code(tile)) {
+    p.wide_nw = 2 * (tile / 100);
+    p.wide_mt = (tile / 10) % 10;
+    p.wide_nt = tile % 10;
+  } else if (tile == 0) {
     // Up to M = 128 (the latency-bound prefill of a small model wants blocks)
     // 32-row blocks - a wave's dequant per k-step does not depend on the rows,
     // so halving them halves its MFMA time and doubles the blocks (Qwen2-0.5B at
@@ -514,7 +569,7 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
     p.tn = tile / 10;
     p.tm = tile % 10;
   }
-  const long long tiles = (long long)((N + 64 * p.tn - 1) / (64 * p.tn)) * ((M + 16 * p.tm - 1) / (16 * p.tm));
+  const long long tiles = (long long)((N + p.bn() - 1) / p.bn()) * ((M + p.bm() - 1) / p.bm());
   const int ksteps = (K + 127) / 128;  // the kernel's k-steps (the last may be half)
   int s = splits;
   if (s <= 0) {
@@ -538,45 +593,13 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
 
 }  // namespace
 
-// Where automatic codes would take the long-prefill library path, the fused
-// kernel's own plan as explicit tile / split codes (128-row blocks there, so the
-// code is 18 or 28); other codes are left as they are.
-extern "C++" void aoto::fused_gemm_codes(int M, int N, int K, int* tile, int* splits) {
-  if (M < kLibraryRows || *tile != 0 || *splits != 0) return;
-  const GemmPlan p = gemm_plan(M, N, K, *tile, *splits, false);
-  *tile = 10 * p.tn + p.tm;
-  *splits = p.splits;
+// Automatic codes resolved to the explicit plan aoto_hip_w4_gemm would run (for
+// the allocation-free entry point, which sizes its split against its scratch).
+extern "C++" void aoto::resolve_gemm_codes(int M, int N, int K, int* tile, int* splits) {
+  resolve_auto(M, N, K, false, tile, splits);
 }
 
 namespace {
-
-// Long prefills: from kLibraryRows rows on, with the automatic plan (tile = splits
-// = 0), the packed weight is unpacked to bf16 into the workspace (the bit-exact
-// aoto_w{4,8}_dequantize) and the product runs on hipBLASLt (blaslt.cpp), the
-// reference's own prefill form. The fused-dequant kernels are bound by their
-// dequant VALU there (MFMA ~33% busy); measured on MI355X at 2048 rows for the
-// Llama-8B projections, hipBLASLt alone takes 68 / 67 / 2 x 140 / 201 us for
-// q/k/v, o, gate + up and down against 146-166 / 98 / 582-590 / 287-296 for the
-// fused kernels, the unpack ~100 us per layer. At 512 rows the unpack would
-// cost as much as the library saves - except for the q/k/v projection of an
-// 8B-class model (K >= 2048), whose fused form carries the RoPE epilogue
-// (Llama-3-8B at 512 rows: 52 against 64 us; o 41 / 41, gate/up 231 / 186, down
-// 118 / 94).
-constexpr int kLibraryRowsQkv = 512;
-
-bool library_rows(int M, int tile, int splits, int K = 0, bool qkv = false) {
-  if (tile != 0 || splits != 0) return false;
-  return M >= kLibraryRows || (qkv && K >= 2048 && M >= kLibraryRowsQkv);
-}
-
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-// The library path's workspace: the unpacked weight (two for the paired form),
-// then the f32 product that the gate epilogue reads, then (paired) the bf16 gate.
-size_t library_workspace(int M, int N, int K, bool paired) {
-  const size_t weights = align256((paired ? 2 : 1) * (size_t)N * K * 2);
-  return weights + (size_t)M * N * sizeof(float) + (paired ? (size_t)M * N * 2 : 0);
-}
 
 // The q/k/v projection's plan: the requested tile and split count, or with 0 the
 // unsplit plan when its blocks' columns are whole heads (the RoPE epilogue: one
@@ -585,7 +608,7 @@ size_t library_workspace(int M, int N, int K, bool paired) {
 // 128 rows (twice the blocks; each wave's dequant per step is the same: 7.5 against
 // 9.3 us on 64-row blocks for Qwen2-0.5B at 128 rows), else the auto split.
 void qkv_rope_plan(int M, int N, int K, int head_dim, int* tile, int* splits) {
-  if (*splits != 0 || head_dim <= 0) return;
+  if (*splits != 0 || head_dim <= 0 || wide_code(*tile)) return;
   const int t = *tile == 0 && M <= 128 && 64 % head_dim == 0 ? 12 : *tile;
   const GemmPlan p = gemm_plan(M, N, K, t, 1, false);
   const int bn = 64 * p.tn;
@@ -599,14 +622,14 @@ void qkv_rope_plan(int M, int N, int K, int head_dim, int* tile, int* splits) {
 
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  if (library_rows(M, tile, splits)) return library_workspace(M, N, K, false);
+  resolve_auto(M, N, K, false, &tile, &splits);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, false);
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  if (library_rows(M, tile, splits)) return library_workspace(M, N, K, true);
+  resolve_auto(M, N, K, true, &tile, &splits);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, true);
   return p.splits > 1 ? 2 * (size_t)p.splits * M * N * sizeof(float) : 0;
 }
@@ -615,8 +638,7 @@ size_t aoto_hip_w4_gemm_qkv_rope_workspace(int M, int K, int tile, int splits, i
                                            int head_dim) {
   if (query_heads <= 0 || kv_heads <= 0 || head_dim <= 0) return 0;
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  if (library_rows(M, tile, splits, K, true)) return library_workspace(M, N, K, false);
-  qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  if (!wide_auto_rows(M, K)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
   return aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
 }
 
@@ -634,65 +656,6 @@ int rope_after_gemm(const void* y, int M, const aoto::QkvRope& rope, void* strea
   return launch("aoto_rope_qkv_rows", dim3(blocks_for(items, 256)), dim3(256), 0, stream, y, M, rope.positions,
                 rope.cos_table, rope.sin_table, rope.q_out, rope.pair, rope.query_heads, rope.kv_heads, D, rope.cap,
                 rope.slot0, rope.zero_prefix);
-}
-
-// Unpack N rows of K codes to bf16 [N][K] (aoto_w4_dequantize / aoto_w8_dequantize).
-int unpack_weight(int bits, const int32_t* words, const void* scales, int N, int K, int group, void* out,
-                  void* stream) {
-  const long long units = (long long)N * (K / (bits == 4 ? 8 : 4));
-  return launch(bits == 4 ? "aoto_w4_dequantize" : "aoto_w8_dequantize", dim3(blocks_for(units, 256)), dim3(256), 0,
-                stream, words, scales, N, K, group, out);
-}
-
-// One hipBLASLt GEMM of the long-prefill path, traced as hipblaslt_matmul_{bf16,f32}
-// (the output type) for plans that name the kernels they run.
-int library_launch(int M, int N, int K, const void* x, const void* w, const void* bias, const void* c, void* d,
-                   bool d_f32, void* scratch, void* stream) {
-  if (int st = aoto::library_gemm(M, N, K, x, w, bias, c, d, d_f32, scratch, stream)) return st;
-  trace_launch(d_f32 ? "hipblaslt_matmul_f32" : "hipblaslt_matmul_bf16");
-  return AOTO_OK;
-}
-
-// The long-prefill form of packed_gemm (see kLibraryRows): unpack, then hipBLASLt
-// with the bias or the residual in its epilogue (one rounding of the f32 sum, as
-// the fused epilogue), the row norm or the RoPE after it as for an unsplit plan;
-// the gate epilogue reads the f32 product through the split-K reduce kernel with
-// one split, so every rounding point is the fused kernels'. The paired form is
-// the gate GEMM with bf16 output (the paired epilogue's bf16(gate)), then the up
-// GEMM with the gate epilogue: the two-step values of the fused paired kernel.
-int library_packed_gemm(int bits, const void* x, const int32_t* words, const void* scales, const void* bias,
-                        const void* residual, const void* gate, void* y, int M, int N, int K, int group,
-                        void* workspace, void* stream, const int32_t* up_words, const void* up_scales,
-                        const void* norm_weight, float eps, void* norm_out, const aoto::QkvRope* rope,
-                        const char* what) {
-  const bool paired = up_words != nullptr;
-  if (workspace == nullptr || ((uintptr_t)workspace & 255))
-    return fail(AOTO_ERR_ARGUMENT, "%s: %d rows unpack the weight: a 256-byte aligned workspace of "
-                "aoto_hip_w4_gemm%s_workspace() bytes is needed", what, M, paired ? "_gate_up" : "");
-  char* ws = static_cast<char*>(workspace);
-  uint16_t* wbuf = reinterpret_cast<uint16_t*>(ws);
-  float* dbuf = reinterpret_cast<float*>(ws + align256((size_t)(paired ? 2 : 1) * N * K * 2));
-  const long long quads = (long long)M * N / 4;
-  if (int st = unpack_weight(bits, words, scales, N, K, group, wbuf, stream)) return st;
-  if (paired) {
-    uint16_t* ubuf = wbuf + (size_t)N * K;
-    uint16_t* gbuf = reinterpret_cast<uint16_t*>(dbuf + (size_t)M * N);
-    if (int st = unpack_weight(bits, up_words, up_scales, N, K, group, ubuf, stream)) return st;
-    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, gbuf, false, dbuf, stream)) return st;
-    gate = gbuf;
-    wbuf = ubuf;
-  }
-  if (gate != nullptr) {
-    if (int st = library_launch(M, N, K, x, wbuf, nullptr, nullptr, dbuf, true, dbuf, stream)) return st;
-    const void* none = nullptr;
-    return launch("aoto_w4_gemm_reduce", dim3(blocks_for(quads, 256)), dim3(256), 0, stream, (const float*)dbuf,
-                  1, none, none, gate, y, M, N);
-  }
-  if (int st = library_launch(M, N, K, x, wbuf, bias, residual, y, false, dbuf, stream)) return st;
-  if (norm_out != nullptr)
-    return launch("aoto_rms_norm", dim3((M + 3) / 4), dim3(256), 0, stream, y, norm_weight, eps, norm_out, M, N);
-  if (rope != nullptr) return rope_after_gemm(y, M, *rope, stream);
-  return AOTO_OK;
 }
 
 // The prefill GEMM of either code width (the kernels differ only in how many
@@ -720,38 +683,52 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       (gate && !aligned8(gate)) || !aligned16(words) || (paired && !aligned16(up_words)))
     return fail(AOTO_ERR_ARGUMENT, "%s: x and words must be 16-byte aligned, y/bias/residual/gate 8-byte aligned",
                 what);
-  if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28)
-    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28", what, tile);
-  if (library_rows(M, tile, splits, K, rope != nullptr))
-    return library_packed_gemm(bits, x, words, scales, bias, residual, gate, y, M, N, K, group, workspace, stream,
-                               up_words, up_scales, norm_weight, eps, norm_out, rope, what);
+  if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile))
+    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441, 442", what,
+                tile);
+  if (wide_code(tile)) {
+    if (!wide_instance(tile, bits, paired))
+      return fail(AOTO_ERR_ARGUMENT, "%s: no wide tile %d instance for %d-bit%s codes", what, tile, bits,
+                  paired ? " paired" : "");
+    if ((group & (group - 1)) != 0 || K % 128 != 0 || (K / group) % 2 != 0)
+      return fail(AOTO_ERR_UNSUPPORTED, "%s: wide tile %d needs K %% 128 == 0 and an even number of "
+                  "power-of-two groups per row (K=%d group=%d)", what, tile, K, group);
+  }
+  resolve_auto(M, N, K, paired, &tile, &splits);
+  if (bits == 8 && tile == 243) tile = 441;  // no 8-bit 243 instance; the same (unsplit) grid class
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
   if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
     return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
                 "aoto_hip_w4_gemm%s_workspace() bytes", what, p.splits, paired ? "_gate_up" : "");
-  const int bn = 64 * p.tn, bm = 16 * p.tm;
+  const int bn = p.bn(), bm = p.bm();
   const bool split = p.splits > 1;
+  const bool wide = p.wide_mt != 0;
+  char family[24];
+  if (wide)
+    snprintf(family, sizeof(family), "w%dx%dx%d", p.wide_mt, p.wide_nt, p.wide_nw);
+  else
+    snprintf(family, sizeof(family), "n%d_m%d", p.tn, p.tm);
   const dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, p.splits);
   float* partials = split ? static_cast<float*>(workspace) : nullptr;
   const long long quads = (long long)M * N / 4;
   char name[64];
   if (paired) {
-    snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_paired", bits, p.tn, p.tm);
-    if (int st = launch(name, grid, dim3(256), 0, stream, x, words, scales, up_words, up_scales, y, M, N, K, group,
+    snprintf(name, sizeof(name), "aoto_w%d_gemm_%s_paired", bits, family);
+    if (int st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, up_words, up_scales, y, M, N, K, group,
                         p.kslice, partials))
       return st;
     if (!split) return AOTO_OK;
     return launch("aoto_w4_gemm_reduce_paired", dim3(blocks_for(quads, 256)), dim3(256), 0, stream,
                   (const float*)partials, p.splits, y, M, N);
   }
-  if (rope != nullptr && !split && bn % rope->head_dim == 0 && N % bn == 0) {
+  if (rope != nullptr && !split && !wide && bn % rope->head_dim == 0 && N % bn == 0) {
     // unsplit with whole heads per block: bias, RoPE and the cache fill in the epilogue
     snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_rope_b%d", bits, p.tn, p.tm, bias != nullptr);
     return launch(name, grid, dim3(256), 0, stream, x, words, scales, bias, y, M, N, K, group, *rope);
   }
   const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
-  snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_b%d_r%d_g%d", bits, p.tn, p.tm, b, r, g);
-  if (int st = launch(name, grid, dim3(256), 0, stream, x, words, scales, bias, residual, gate, y, M, N, K, group,
+  snprintf(name, sizeof(name), "aoto_w%d_gemm_%s_b%d_r%d_g%d", bits, family, b, r, g);
+  if (int st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, bias, residual, gate, y, M, N, K, group,
                       p.kslice, partials))
     return st;
   if (norm_out != nullptr) {
@@ -796,7 +773,7 @@ int qkv_rope_gemm(int bits, const void* x, const int32_t* words, const void* sca
                            (uint16_t*)q_out, (uint16_t*)pair, query_heads, kv_heads, head_dim, capacity, slot0,
                            zero_prefix};
   const int N = (query_heads + 2 * kv_heads) * head_dim;
-  if (!library_rows(M, tile, splits, K, true)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
+  if (!wide_auto_rows(M, K)) qkv_rope_plan(M, N, K, head_dim, &tile, &splits);
   return packed_gemm(bits, x, words, scales, bias, nullptr, nullptr, y, M, N, K, group, tile, splits, workspace,
                      stream, nullptr, nullptr, nullptr, 0.f, nullptr, &rope);
 }

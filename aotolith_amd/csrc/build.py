@@ -56,9 +56,8 @@ def build(verbose: bool = False) -> tuple[str, str]:
     _run([HIPCC, *DEVICE_FLAGS, "--genco", "--no-gpu-bundle-output", os.path.join(CSRC, "kernels.hip"), "-o", tmp_obj], verbose)
     os.replace(tmp_obj, CODE_OBJECT)
     tmp_lib = LIBRARY + ".tmp"
-    # The host library: the C-ABI launchers, the hipBLASLt calls of long prefills
-    # (blaslt.cpp), plus noalloc.hip, whose device part is only the static scratch
-    # buffer of the allocation-free GEMM entry point.
+    # The host library: the C-ABI launchers, plus noalloc.hip, whose device part is
+    # only the static scratch buffer of the allocation-free GEMM entry point.
     _run(
         [
             HIPCC,
@@ -74,11 +73,7 @@ def build(verbose: bool = False) -> tuple[str, str]:
             "-I" + INCLUDE,
             "-I" + CSRC,
             os.path.join(CSRC, "aoto_hip.cpp"),
-            os.path.join(CSRC, "blaslt.cpp"),
             os.path.join(CSRC, "noalloc.hip"),
-            "-L" + os.path.join(ROCM, "lib"),
-            "-lhipblaslt",
-            "-Wl,-rpath," + os.path.join(ROCM, "lib"),
             "-o",
             tmp_lib,
         ],

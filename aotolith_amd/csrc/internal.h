@@ -11,19 +11,8 @@ int set_error(int code, const char* fmt, ...);
 // object is installed on the device.
 void noalloc_prepare_device(int device);
 
-// Where automatic (0) tile / split codes of the unpaired prefill GEMM would take
-// the long-prefill library path, resolve them to the fused kernel's own plan
-// (aoto_hip.cpp), for callers without room for the unpacked weight.
-void fused_gemm_codes(int M, int N, int K, int* tile, int* splits);
-
-// Plain bf16 GEMMs on hipBLASLt (blaslt.cpp): D[M][N] = X[M][K] . W[N][K]^T
-// (+ bias[N]) (+ c[M][N]), f32 accumulation, D bf16 or f32. library_prepare
-// creates the device's handle (called when a code object is installed, outside
-// any graph capture); library_gemm enqueues one GEMM on `stream`. `scratch`
-// (M * N of the output type, not aliasing the operands) takes the candidate
-// timing of a shape's first uncaptured call; its contents are overwritten.
-int library_prepare(int device);
-int library_gemm(int M, int N, int K, const void* x, const void* w, const void* bias, const void* c, void* d,
-                 bool d_f32, void* scratch, void* stream);
+// Automatic (0) tile / split codes of the unpaired prefill GEMM resolved to the
+// explicit plan aoto_hip_w4_gemm runs (aoto_hip.cpp); other codes pass unchanged.
+void resolve_gemm_codes(int M, int N, int K, int* tile, int* splits);
 
 }  // namespace aoto

@@ -6,6 +6,7 @@
 #include "w4_gemv_stream.h"
 #include "w4_gemv_rows.h"
 #include "w4_gemm.h"
+#include "w4_gemm_wide.h"
 #include "w8.h"
 #include "generic.h"
 #include "decode.h"
@@ -76,6 +77,21 @@ AOTO_GEMM_PAIRED_INSTANCE(8, 1, 4)
 AOTO_GEMM_PAIRED_INSTANCE(8, 1, 8)
 AOTO_GEMM_PAIRED_INSTANCE(8, 2, 4)
 AOTO_GEMM_PAIRED_INSTANCE(8, 2, 8)
+// Long prefills, wide tiles (v_mfma_f32_32x32x16_bf16, LDS-staged): {code width} x
+// {32-row tiles per wave} x {32-column tiles per wave} x {waves per block} x epilogue
+// (the shapes whose staging buffers fit 160 KB of LDS).
+AOTO_GEMM_WIDE_EPILOGUES(4, 4, 1, 4)
+AOTO_GEMM_WIDE_EPILOGUES(4, 4, 2, 4)
+AOTO_GEMM_WIDE_EPILOGUES(4, 4, 3, 4)
+AOTO_GEMM_WIDE_EPILOGUES(4, 8, 1, 4)
+AOTO_GEMM_WIDE_EPILOGUES(4, 4, 1, 8)
+AOTO_GEMM_WIDE_EPILOGUES(4, 4, 2, 8)
+AOTO_GEMM_WIDE_EPILOGUES(8, 4, 1, 4)
+AOTO_GEMM_WIDE_EPILOGUES(8, 4, 2, 4)
+AOTO_GEMM_WIDE_EPILOGUES(8, 4, 1, 8)
+AOTO_GEMM_WIDE_PAIRED_INSTANCE(4, 4, 1, 4)
+AOTO_GEMM_WIDE_PAIRED_INSTANCE(4, 4, 1, 8)
+AOTO_GEMM_WIDE_PAIRED_INSTANCE(8, 4, 1, 4)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 1)

@@ -66,15 +66,21 @@ extern "C" int aoto_hip_w4_gemm_noalloc(const void* x, const int32_t* words, con
     return aoto::set_error(AOTO_ERR_HIP, "w4_gemm_noalloc: scratch address on device %d: %s", device,
                            hipGetErrorString(slot.status));
   }
-  // automatic codes resolve to the fused kernel's plan: from 1024 rows on,
-  // aoto_hip_w4_gemm would otherwise unpack the weight into its workspace
-  if (M > 0 && N > 0 && K > 0 && K % 64 == 0) aoto::fused_gemm_codes(M, N, K, &tile, &splits);
-  const size_t need = aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
+  // Automatic codes: the workspace entry point's plan, with its split count lowered
+  // (to one at least) until the partials fit the scratch; explicit codes are kept
+  // and refused if they do not fit.
+  const bool automatic = tile == 0 && splits == 0;
+  if (M > 0 && N > 0 && K > 0 && K % 64 == 0) aoto::resolve_gemm_codes(M, N, K, &tile, &splits);
+  size_t need = aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
+  if (automatic && need > AOTO_HIP_NOALLOC_SCRATCH_BYTES) {
+    if (splits == 0) splits = (int)(need / ((size_t)M * N * sizeof(float)));  // the 16x16 plan's own count
+    while (splits > 1 && need > AOTO_HIP_NOALLOC_SCRATCH_BYTES) need = aoto_hip_w4_gemm_workspace(M, N, K, tile, --splits);
+  }
   if (need > AOTO_HIP_NOALLOC_SCRATCH_BYTES)
     return aoto::set_error(AOTO_ERR_UNSUPPORTED,
                            "w4_gemm_noalloc: this plan (M=%d N=%d K=%d tile=%d splits=%d) needs %zu bytes of split-K "
-                           "partials and the static scratch holds %u; pass splits=1, or call aoto_hip_w4_gemm with "
-                           "a workspace", M, N, K, tile, splits, need, (unsigned)AOTO_HIP_NOALLOC_SCRATCH_BYTES);
+                           "partials and the static scratch holds %u; pass fewer splits, or call aoto_hip_w4_gemm "
+                           "with a workspace", M, N, K, tile, splits, need, (unsigned)AOTO_HIP_NOALLOC_SCRATCH_BYTES);
   return aoto_hip_w4_gemm(x, words, scales, bias, residual, gate, y, M, N, K, group, tile, splits,
                           need > 0 ? slot.address : nullptr, stream);
 }

@@ -417,7 +417,7 @@ def _sel(index: int, op: str, output: str, kind: str, reason: str, artifact: str
         op_index=index,
         op=op,
         output_id=output,
-        implementation="hipblaslt" if artifact.startswith("hipblaslt") else "hip_kernel",
+        implementation="hip_kernel",
         kind=kind,
         reason=reason,
         artifact_name=artifact,
@@ -900,7 +900,8 @@ class _Engine:
                 ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
             pair = pair_of(index)
             _mark(rec, "addmm" if s.qkv_bias else "matmul", f"qkv_{index}", gemm,
-                  (f"W{bits} unpack to bf16 and the hipBLASLt GEMM" if ops.library_plan(m, s.hidden, qkv=True)
+                  (f"wide-tile fused-dequant W{bits} GEMM on 32x32x16 bf16 MFMA"
+                   if ops.wide_plan(m, s.qkv_width, s.hidden) is not None
                    else f"fused-dequant W{bits} GEMM on bf16 MFMA") + (" with q/k/v bias" if s.qkv_bias else "")
                   + ", RoPE of q/k and the layer's cache fill (with the split-K sum when the plan splits)")
             # q/k/v projection, RoPE and the cache fill (one launch fewer when the plan splits K)

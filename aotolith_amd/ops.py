@@ -354,33 +354,46 @@ def w8_matmul(
     return _matmul(8, x, packed, scales, group_size, bias, residual, gate, out, tile, splits, workspace)
 
 
-#: From this many rows on, the prefill GEMMs' automatic plan (tile = splits = 0)
-#: unpacks the weight to bf16 into the workspace and runs the product on
-#: hipBLASLt (the C ABI's kLibraryRows); explicit codes keep the fused kernel.
-LIBRARY_ROWS = 1024
-#: ... and from this many for the q/k/v RoPE form of a reduction of at least
-#: LIBRARY_QKV_MIN_K (an 8B-class hidden size), whose fused form carries the RoPE.
-LIBRARY_ROWS_QKV = 512
-LIBRARY_QKV_MIN_K = 2048
+#: From this many rows (with K % 256 == 0) the prefill GEMMs' automatic plan
+#: (tile = splits = 0) takes the wide-tile 32x32x16-MFMA kernel (the C ABI's kWideRows).
+WIDE_ROWS = 512
 
 
-def library_plan(m: int, k: int, *, qkv: bool = False) -> bool:
-    """Whether the automatic prefill GEMM plan for ``m`` rows (reduction ``k``) unpacks the
-    weight for hipBLASLt (the C ABI's rule for tile = splits = 0)."""
+def wide_plan(m: int, n: int, k: int, *, paired: bool = False) -> tuple[int, int] | None:
+    """The automatic plan's ``(tile, splits)`` for ``m`` rows of an ``[n, k]`` weight when
+    it takes the wide kernel, else None: the Python mirror of the C ABI's
+    ``wide_auto_plan`` (``csrc/aoto_hip.cpp``), for labels and host-side checks."""
 
-    return m >= LIBRARY_ROWS or (qkv and k >= LIBRARY_QKV_MIN_K and m >= LIBRARY_ROWS_QKV)
+    if m < WIDE_ROWS or k % 256:
+        return None
+    mb = (m + 127) // 128
+
+    def blocks(bn):
+        return -(-n // bn) * mb
+
+    tile = 241
+    if not paired and n % 384 == 0 and blocks(384) >= 224:
+        tile = 243
+    elif not paired and blocks(256) >= 224:
+        tile = 441
+    count = {243: blocks(384), 441: blocks(256), 241: blocks(128)}[tile]
+    splits = -(-256 // count) if count < 160 else 1
+    most = (k // 128) // 2
+    splits = max(1, min(splits, most))
+    # the launch cuts K into slices of whole 128-k steps: the count it actually runs
+    steps = k // 128
+    per = -(-steps // splits)
+    return tile, -(-steps // per)
 
 
 def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:
-    """Workspace bytes :func:`w4_matmul` needs for this shape: split-K partials (0: no
-    split), or from :data:`LIBRARY_ROWS` rows the unpacked weight and f32 product."""
+    """Workspace bytes :func:`w4_matmul` needs for this shape: split-K partials (0: no split)."""
 
     return int(_lib.library().aoto_hip_w4_gemm_workspace(int(m), int(n), int(k), int(tile), int(splits)))
 
 
 def gate_up_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:
-    """Workspace bytes :func:`w4_matmul_gate_up` needs (gate and up partials, 0: no split;
-    or from :data:`LIBRARY_ROWS` rows both unpacked weights and f32 products)."""
+    """Workspace bytes :func:`w4_matmul_gate_up` needs (gate and up partials, 0: no split)."""
 
     return int(_lib.library().aoto_hip_w4_gemm_gate_up_workspace(int(m), int(n), int(k), int(tile), int(splits)))
 

@@ -3,17 +3,17 @@
 Same record as the reference's ``selection.py:6-34`` (field names and order),
 so tooling that reads ``plan.selections`` reads ours. ``is_native`` is widened
 from the reference's single ``"metal_kernel"`` to every implementation that
-runs a device kernel, here ``"hip_kernel"`` and ``"hipblaslt"``.
+runs a kernel this backend emitted, here ``"hip_kernel"``.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 
-#: Implementations that run device kernels (no CPU or torch fallback): this
-#: target's gfx950 code object, the hipBLASLt GEMM that long prefills run on the
-#: unpacked weight, and the Metal kernels of the reference's Apple backend.
-NATIVE_IMPLEMENTATIONS = frozenset({"hip_kernel", "hipblaslt", "metal_kernel"})
+#: Implementations that run kernels a backend emitted itself (no CPU, torch or
+#: vendor-library fallback): this target's gfx950 code object and the Metal kernels
+#: of the reference's Apple backend.
+NATIVE_IMPLEMENTATIONS = frozenset({"hip_kernel", "metal_kernel"})
 
 
 @dataclass(frozen=True, slots=True)

@@ -336,19 +336,16 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
                                      layer.input_norm, spec.eps, bits=layer.down.bits, out=x, norm_out=xn)
 
     bits = eng.state.bits
-    lib = f"aoto_w{bits}_dequantize + hipBLASLt bf16 GEMM"  # the automatic plan unpacks the weight
-    fused = f"aoto_w{bits}_gemm"
-    gemm = lib if ops.library_plan(m, h) else fused
-    if ops.library_plan(m, h, qkv=True):
-        qkv_label = f"{lib} (bias epilogue), then aoto_rope_qkv_rows (RoPE and cache fill)"
+    plan = ops.wide_plan(m, spec.qkv_width, h)
+    gemm = f"aoto_w{bits}_gemm_w* (wide tiles, 32x32x16 MFMA)" if ops.wide_plan(m, h, h) else f"aoto_w{bits}_gemm_n*"
+    if plan is not None:
+        qkv_label = (f"aoto_w{bits}_gemm_w* tile {plan[0]} + bias, then aoto_rope_qkv_rows (RoPE and cache fill)"
+                     if plan[1] == 1 else f"aoto_w{bits}_gemm_w* tile {plan[0]}, {plan[1]}-way split, then "
+                     "aoto_w4_gemm_reduce_rope (sum, bias, RoPE and cache fill)")
     else:
-        qkv_label = (f"{fused} + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: RoPE in the "
-                     "GEMM epilogue, or aoto_rope_qkv_rows after it)")
-    if ops.library_plan(m, h):
-        mlp_label = (f"aoto_w{bits}_dequantize x2, hipBLASLt gate (bf16) and up (f32) GEMMs, "
-                     "aoto_w4_gemm_reduce (silu_mul)")
-    else:
-        mlp_label = f"{fused} paired gate/up + silu_mul"
+        qkv_label = (f"aoto_w{bits}_gemm + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: RoPE "
+                     "in the GEMM epilogue, or aoto_rope_qkv_rows after it)")
+    mlp_label = (f"{gemm} paired gate/up + silu_mul")
     rows = [
         _row("qkv_rope", qkv_label, _graph_us(torch, qkv_rope, n), flops=2.0 * m * spec.qkv_width * h),
         _row("attention", f"aoto_flash_attention_d{spec.head_dim} (causal)", _graph_us(torch, attention, n),

@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 17
+#define AOTO_HIP_ABI_VERSION 18
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -111,34 +111,35 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales,
  *   residual bf16 [M, N]  -> bf16(residual[m][n] + acc)
  *   gate     bf16 [M, N]  -> bf16(acc * silu(gate[m][n]))
  * Limits: K % 64 == 0, N % 16 == 0, group % 32 == 0 dividing K. x 16-byte and
- * y/bias/residual/gate 8-byte aligned. tile: 0 chooses, else 14/18/24/28 (n
- * tiles x m tiles of 16 per wave) or 12 (32-row blocks). splits: 0 chooses (small grids split the
- * reduction), else the split-K count; a split launch stores f32 partial tiles
- * in `workspace` (aoto_hip_w4_gemm_workspace() bytes, 16-byte aligned) and a
- * second launch sums them and applies the epilogue. Long prefills (M >= 1024
- * with tile = splits = 0, the reference's own prefill form): the weight is
- * unpacked to bf16 into `workspace` (aoto_hip_w4_gemm_workspace() bytes, 256-byte
- * aligned: N * K * 2 rounded up, then M * N * 4 for the gate epilogue's f32
- * product) and the product runs on hipBLASLt with f32 accumulation and no
- * library workspace; the epilogues round as above. A nonzero tile or split code
- * keeps the fused kernel at any M. y must not alias x. */
+ * y/bias/residual/gate 8-byte aligned. tile: 0 chooses; 12/14/18/24/28 the
+ * 16x16x32-MFMA kernel (n tiles x m tiles of 16 per wave; 12: 32-row blocks);
+ * 241/242/243/281/441 the wide-tile 32x32x16 kernel for long prompts (100 *
+ * waves per block / 2 + 10 * 32-row tiles per wave + 32-column tiles per wave;
+ * needs K % 128 == 0 and an even number of power-of-two groups per row; 8-bit
+ * codes: 241, 242, 441). Automatic codes take the wide kernel from M >= 512 when
+ * K % 256 == 0 (group <= 128), else the 16x16 kernel. splits: 0 chooses (small
+ * grids split the reduction), else the split-K count; a split launch stores f32
+ * partial tiles in `workspace` (aoto_hip_w4_gemm_workspace() bytes, 16-byte
+ * aligned) and a second launch sums them and applies the epilogue. Every plan is
+ * a fixed function of the arguments, so results are reproducible across calls and
+ * processes. y must not alias x. */
 int aoto_hip_w4_gemm(const void* x, const int32_t* words, const void* scales, const void* bias,
                      const void* residual, const void* gate, void* y, int M, int N, int K, int group,
                      int tile, int splits, void* workspace, void* stream);
 
 /* Bytes of workspace aoto_hip_w4_gemm needs for these arguments: the split-K
- * partials (0 when it does not split), or the long-prefill path's unpacked
- * weight and f32 product. */
+ * partials (0 when it does not split). */
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits);
 
 /* No counterpart in the reference. aoto_hip_w4_gemm for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc): the same arguments and results without the
- * workspace. Automatic codes at M >= 1024 keep the fused kernel (its own
- * plan: no unpacked weight). A split-K plan keeps its f32 partials in a static device buffer of
+ * workspace. A split-K plan keeps its f32 partials in a static device buffer of
  * AOTO_HIP_NOALLOC_SCRATCH_BYTES that the library holds on each GPU until the
- * process ends; a plan that needs more (aoto_hip_w4_gemm_workspace() bytes) is
- * refused with AOTO_ERR_UNSUPPORTED (pass splits = 1, or use aoto_hip_w4_gemm).
+ * process ends. With automatic codes (tile = splits = 0) the split count of the
+ * automatic plan is lowered, to one at least, until the partials fit; explicit codes
+ * whose plan needs more (aoto_hip_w4_gemm_workspace() bytes) are refused with
+ * AOTO_ERR_UNSUPPORTED.
  * Nothing is allocated or freed. All calls on one GPU share its buffer: calls that
  * overlap in time on one device (different streams) race. */
 #define AOTO_HIP_NOALLOC_SCRATCH_BYTES (16u << 20)
@@ -222,9 +223,9 @@ int aoto_hip_w8_gemm_residual_norm(const void* x, const int32_t* words, const vo
  * the projection; q_out [Hq, M, head_dim]; pair [2, Hkv, capacity, head_dim] gets
  * rotated keys / values at slots slot0 .. slot0 + M - 1 (slots below slot0 zeroed
  * when zero_prefix != 0); positions[M] int64. tile and splits as aoto_hip_w4_gemm,
- * with 0 / 0 choosing the unsplit epilogue form whenever it applies (32-row blocks
- * up to 128 rows) and the long-prefill library path from 1024 rows, or 512 when
- * K >= 2048 (the RoPE / cache fill kernel after it);
+ * with 0 / 0 choosing, below the wide kernel's rows, the unsplit epilogue form
+ * whenever it applies (32-row blocks up to 128 rows), and from them the wide kernel
+ * with the RoPE / cache fill kernel after it;
  * workspace: aoto_hip_w4_gemm_qkv_rope_workspace() bytes. */
 int aoto_hip_w4_gemm_qkv_rope(const void* x, const int32_t* words, const void* scales, const void* bias, void* y,
                               int M, int K, int group, int tile, int splits, void* workspace, const int64_t* positions,

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.aoto_hip_abi_version() == 17
+    assert lib.aoto_hip_abi_version() == 18
 
 
 def test_no_code_object_without_a_gpu():
@@ -58,21 +58,37 @@ def test_launcher_rejects_bad_arguments_on_the_host():
     assert "null pointer" in _lib.last_error()
 
 
-def test_library_plan_matches_the_workspace_queries():
-    """ops.library_plan (the Python mirror of the automatic plan's rule) agrees with what the
-    C ABI's workspace queries size - host logic only, no device call."""
+def test_wide_plan_matches_the_workspace_queries():
+    """ops.wide_plan (the Python mirror of the automatic plan's rule) agrees with what the
+    C ABI's workspace queries size: from ops.WIDE_ROWS rows (K % 256 == 0) a split plan
+    needs splits * M * N f32 partials (twice that for the gate/up pair), an unsplit one
+    none - host logic only, no device call."""
 
     from aotolith_amd import _lib, ops
 
     lib = _lib.library()
-    for m in (1, 128, 511, 512, 1023, 1024, 2048):
-        for n, k in ((896, 896), (4096, 4096), (1152, 896), (6144, 4096), (4096, 14336), (640, 2048)):
-            unpacked = n * k * 2 + m * n * 4
-            assert (ops.gemm_workspace_bytes(m, n, k) == unpacked) == ops.library_plan(m, k), (m, n, k)
-            assert (ops.gate_up_workspace_bytes(m, n, k) == 2 * n * k * 2 + m * n * 6) == ops.library_plan(m, k)
-        for hq, hkv, d, k in ((14, 2, 64, 896), (32, 8, 128, 4096), (8, 2, 128, 2048)):
+    seen = set()
+    for m in (512, 640, 1024, 1100, 2048, 4096):
+        assert ops.wide_plan(m, 896, 896) is None  # K % 256 != 0: the 16x16 kernel's plan
+        for n, k in ((4096, 4096), (1152, 1024), (6144, 4096), (4096, 14336), (14336, 4096), (640, 2048),
+                     (768, 512)):
+            plan = ops.wide_plan(m, n, k)
+            assert plan is not None, (m, n, k)
+            tile, splits = plan
+            seen.add(tile)
+            want = splits * m * n * 4 if splits > 1 else 0
+            assert ops.gemm_workspace_bytes(m, n, k) == want, (m, n, k, plan)
+            ptile, psplits = ops.wide_plan(m, n, k, paired=True)
+            assert ptile == 241
+            assert ops.gate_up_workspace_bytes(m, n, k) == (2 * psplits * m * n * 4 if psplits > 1 else 0), (m, n, k)
+        for hq, hkv, d, k in ((32, 8, 128, 4096), (8, 2, 128, 2048), (28, 4, 128, 3584)):
             n = (hq + 2 * hkv) * d
+            tile, splits = ops.wide_plan(m, n, k)
             got = lib.aoto_hip_w4_gemm_qkv_rope_workspace(m, k, 0, 0, hq, hkv, d)
-            assert (got == n * k * 2 + m * n * 4) == ops.library_plan(m, k, qkv=True), (m, hq, k)
-    # explicit codes always keep the fused kernel
+            assert got == (splits * m * n * 4 if splits > 1 else 0), (m, hq, k)
+    assert seen == {241, 243, 441}, seen
+    # below the wide rows, or K % 256 != 0, the 16x16 kernel's plan (no wide plan)
+    assert ops.wide_plan(511, 4096, 4096) is None and ops.wide_plan(2048, 896, 896) is None
+    # explicit codes are taken as given
     assert ops.gemm_workspace_bytes(2048, 4096, 4096, 28, 1) == 0
+    assert ops.gemm_workspace_bytes(2048, 4096, 4096, 441, 2) == 2 * 2048 * 4096 * 4

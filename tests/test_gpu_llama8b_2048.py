@@ -60,7 +60,7 @@ def test_prefill_attention_2048_tokens_d128(length):
 
 
 @pytest.mark.timeout(300)
-@pytest.mark.parametrize("plan", ["fused", "library"])
+@pytest.mark.parametrize("plan", ["fused", "wide"])
 @pytest.mark.parametrize("n,k,full_n,epilogue", [
     (1024, 4096, 6144, None),        # a slice of the 8B q/k/v projection
     (1024, 4096, 4096, "residual"),  # a slice of the o projection, residual epilogue
@@ -68,12 +68,12 @@ def test_prefill_attention_2048_tokens_d128(length):
 ])
 def test_w4_matmul_2048_rows_on_the_decoder_plan(n, k, full_n, epilogue, plan):
     """An N slice at 2048 rows on either plan: the automatic one the decoder takes (the
-    weight unpacked, the product on hipBLASLt) and the fused kernel's own at this length
-    (128x128 block tiles, tile code 28, no split-K)."""
+    wide-tile 32x32x16 kernel) and the 16x16 kernel's own at this length (128x128 block
+    tiles, tile code 28, no split-K)."""
 
     from aotolith_amd import ops
 
-    assert ops.gemm_workspace_bytes(M, full_n, k) >= full_n * k * 2, "the automatic plan unpacks the weight"
+    assert ops.wide_plan(M, full_n, k) is not None, "the automatic plan takes the wide kernel"
     assert ops.gemm_workspace_bytes(M, full_n, k, tile=28, splits=1) == 0
     rng = np.random.default_rng(n + k)
     packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
@@ -88,7 +88,7 @@ def test_w4_matmul_2048_rows_on_the_decoder_plan(n, k, full_n, epilogue, plan):
         y = ops.w4_matmul(to_gpu_bf16(x), torch.from_numpy(packed).cuda(), to_gpu_bits(scales), 64, **codes,
                           **gpu_kwargs)
         names = take()
-    assert any(name.startswith("hipblaslt") for name in names) == (plan == "library"), names
+    assert any(name.startswith("aoto_w4_gemm_w") for name in names) == (plan == "wide"), names
     expected = oracle.w4_matmul(x, packed, scales, 64, **kwargs)
     # Outputs reach ~6 with the N(0,1) residual, where one bf16 ulp is 2^-5: the bar is
     # one ulp of each value (and the absolute bar one ulp of the largest).

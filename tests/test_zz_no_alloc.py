@@ -68,44 +68,55 @@ def test_noalloc_gemm_matches_the_workspace_entry_point_on_two_calls():
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={m} N={n} K={k}"
 
 
-def test_noalloc_gemm_refuses_plans_beyond_its_scratch():
+def test_noalloc_gemm_refuses_explicit_plans_beyond_its_scratch():
     from aotolith_amd import ops
 
-    m, n, k = 512, 4096, 4096  # the auto plan splits 4 ways: 32 MiB of partials
-    assert ops.gemm_workspace_bytes(m, n, k) > SCRATCH_BYTES
+    m, n, k = 512, 4096, 4096
+    assert ops.gemm_workspace_bytes(m, n, k, 28, 4) > SCRATCH_BYTES  # 4 splits: 32 MiB of partials
     x = torch.zeros((m, k), dtype=torch.bfloat16, device="cuda")
     packed = torch.zeros((n, k // 8), dtype=torch.int32, device="cuda")
     scales = torch.zeros((n, k // 64), dtype=torch.bfloat16, device="cuda")
     out = torch.zeros((m, n), dtype=torch.bfloat16, device="cuda")
-    status = _noalloc(x, packed, scales, 64, out)
+    status = _noalloc(x, packed, scales, 64, out, tile=28, splits=4)
     assert status == 4, status  # AOTO_ERR_UNSUPPORTED, before any launch
     assert "static scratch" in _last_error()
-    # the same shape unsplit needs no scratch and runs
-    assert _noalloc(x, packed, scales, 64, out, splits=1) == 0, _last_error()
     torch.cuda.synchronize()
     assert not torch.any(out.view(torch.int16) != 0)
 
 
-def test_noalloc_gemm_keeps_the_fused_kernel_for_long_prefills():
-    """Automatic codes at 1024+ rows, which send aoto_hip_w4_gemm to the unpacked-weight
-    library path, resolve to the fused kernel's own plan here (no room for the weight):
-    the result is the workspace entry point's under that explicit plan, bit for bit."""
+def test_noalloc_gemm_fits_automatic_plans_to_its_scratch():
+    """Automatic codes whose split would need more than the scratch run with fewer splits:
+    the 16x16 plan at 256 rows (K = 4864 splits 16 ways on its own) and a wide plan at
+    512 rows both match the workspace entry point under the plan the scratch allows, bit
+    for bit; nothing is allocated (the device's free memory is unchanged)."""
 
     from aotolith_amd import ops
 
-    m, n, k = ops.LIBRARY_ROWS, 4096, 896  # 256 output tiles: the fused plan does not split
-    rng = np.random.default_rng(90)
-    packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
-    gp, gs = torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
-    x = to_gpu_bf16(bf16_normal(rng, (m, k)))
-    bias = to_gpu_bf16(bf16_normal(rng, (n,), 0.02))
-    want = ops.w4_matmul(x, gp, gs, 64, bias=bias, tile=28)  # 128-row, 128-column blocks
-    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
-    with ops.recording_launches() as take:
-        take()
-        status = _noalloc(x, gp, gs, 64, got, bias=bias)
-        names = take()
-    assert status == 0, _last_error()
-    torch.cuda.synchronize()
-    assert not any(name.startswith("hipblaslt") for name in names), names
-    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    for m, n, k, tile, splits in [(256, 896, 4864, 0, 0), (1024, 1536, 4096, 241, 0)]:
+        rng = np.random.default_rng(90 + m)
+        packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
+        gp, gs = torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
+        x = to_gpu_bf16(bf16_normal(rng, (m, k)))
+        residual = to_gpu_bf16(bf16_normal(rng, (m, n)))
+        auto = ops.gemm_workspace_bytes(m, n, k)
+        # the largest split count whose partials fit, as the entry point chooses it
+        if tile == 0:
+            count = auto // (m * n * 4)
+            while count > 1 and ops.gemm_workspace_bytes(m, n, k, 0, count) > SCRATCH_BYTES:
+                count -= 1
+            explicit = (0, count)
+        else:
+            plan = ops.wide_plan(m, n, k)
+            count = plan[1]
+            while count > 1 and ops.gemm_workspace_bytes(m, n, k, plan[0], count) > SCRATCH_BYTES:
+                count -= 1
+            explicit = (plan[0], count)
+        want = ops.w4_matmul(x, gp, gs, 64, residual=residual, tile=explicit[0], splits=explicit[1])
+        got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
+        free_before = torch.cuda.mem_get_info()[0]
+        status = _noalloc(x, gp, gs, 64, got, residual=residual)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free_before
+        assert status == 0, _last_error()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (m, n, k, explicit)
