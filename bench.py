@@ -422,16 +422,19 @@ def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
     t_prefill = time.perf_counter() - t0
     cache = oracle.pad_cache(compact)
     tokens = [first]
-    margins = []
+    history = [np.asarray(logits, dtype=np.float32).reshape(-1)]  # the oracle's logits of every token
     valid = ids.shape[0]
     t0 = time.perf_counter()
     for _ in range(decode_steps):
         valid += 1
         logits, cache = oracle.decode(tokens[-1], valid, cache)
-        top = np.sort(np.asarray(logits, dtype=np.float64).reshape(-1))[-2:]
-        margins.append(float(top[1] - top[0]))
+        history.append(np.asarray(logits, dtype=np.float32).reshape(-1))
         tokens.append(int(np.argmax(logits)))
     t_decode = time.perf_counter() - t0
+    margins = []
+    for row in history:
+        top = np.sort(row.astype(np.float64))[-2:]
+        margins.append(float(top[1] - top[0]))
     try:
         from threadpoolctl import threadpool_info
 
@@ -444,6 +447,23 @@ def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
         if a != b:
             break
         agree += 1
+    divergence = None
+    if agree < len(tokens):
+        divergence = {"step": agree, "gpu": gpu[agree], "oracle": tokens[agree], "oracle_top2_margin": margins[agree],
+                      "oracle_logit_max": float(np.abs(history[agree]).max())}
+    # Teacher-forced on the oracle's stream (the GPU's own step kernels, fed the oracle's
+    # tokens): the GPU logits' deviation at every step and the steps whose argmax differs.
+    from tests.helpers import teacher_forced_logits
+
+    forced, picks = teacher_forced_logits(runtime, ids, tokens)
+    worst, flips = 0.0, []
+    for step, (got, ref) in enumerate(zip(forced, history)):
+        got, ref = np.asarray(got, dtype=np.float64), ref.astype(np.float64)
+        cos = float(got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref)))
+        worst = max(worst, 1.0 - cos)
+        if picks[step] != tokens[step]:
+            flips.append({"step": step, "oracle_top2_margin": margins[step],
+                          "max_abs_logit_diff": float(np.abs(got - ref).max())})
     return {
         "baseline": {
             "value": decode_steps / t_decode,
@@ -462,6 +482,9 @@ def cpu_baseline(spec, runtime, prompt, gpu_tokens, decode_steps: int) -> dict:
             "gpu_tokens": gpu,
             "oracle_tokens": tokens,
             "oracle_top2_margins": margins,
+            "first_divergence": divergence,
+            "teacher_forced_worst_1_minus_cos": worst,
+            "teacher_forced_flips": flips,
         },
     }
 

@@ -41,7 +41,8 @@ def _gpu_packed(packed, scales):
 GEMM_CASES = [
     (128, 4864, 896, 64),   # gate / up at the Qwen prefill length
     (128, 896, 4864, 64),   # down
-    (16, 4864, 896, 64),    # config 2, M = 16
+    (16, 4864, 896, 64),    # config 2, M = 16: 896 -> 4864
+    (16, 896, 4864, 64),    # config 2, M = 16: 4864 -> 896
     (1, 896, 896, 64),      # a single row through the GEMM
     (200, 1152, 896, 32),   # ragged M, group 32
     (300, 2048, 512, 128),  # group 128, several m blocks
@@ -60,10 +61,11 @@ def test_w4_matmul_plain(m, n, k, group, tile):
     assert_bf16_parity(from_gpu_bf16(y), oracle.w4_matmul(x, packed, scales, group), max_ulp=1.0)
 
 
+@pytest.mark.parametrize("m", [128, 16])  # config 2's M: the bias form is the packed q/k/v 896 -> 1152
 @pytest.mark.parametrize("epilogue", ["bias", "residual", "gate"])
-def test_w4_matmul_epilogues(epilogue):
-    rng = np.random.default_rng({"bias": 1, "residual": 2, "gate": 3}[epilogue])
-    m, n, k = 128, 1152 if epilogue == "bias" else 896, 896
+def test_w4_matmul_epilogues(epilogue, m):
+    rng = np.random.default_rng({"bias": 1, "residual": 2, "gate": 3}[epilogue] + m)
+    n, k = 1152 if epilogue == "bias" else 896, 896
     packed, scales = _packed(rng, n, k)
     x = bf16_normal(rng, (m, k))
     kwargs = {}

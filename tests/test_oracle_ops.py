@@ -225,3 +225,62 @@ def test_w4_gemv_rows_are_output_features(layout):
     x[5] = 1.0
     w = dequantize_i4_exact(packed, scales, 32)
     np.testing.assert_array_equal(ops.w4_gemv(x, packed, scales, 32), round_bf16(w[:, 5]))
+
+
+# ------------------------------------------------------------------ RoPE + KV append (decode)
+def _tiny_decoder(seed=5, capacity=12):
+    from oracle.decoder import DecoderShape, OracleDecoder
+    from tests.helpers import random_oracle_state
+
+    shape = DecoderShape(vocab=48, hidden=64, intermediate=96, layers=2, heads=4, kv_heads=2, head_dim=16, eps=1e-6,
+                         theta=1e6, group_size=32)
+    return shape, OracleDecoder(shape, random_oracle_state(shape, seed=seed), capacity)
+
+
+def test_rope_kv_cache_append_is_the_decoders_cache_update():
+    """rope_kv_cache_append rolls layer 0's window exactly as the oracle decoder's decode
+    step does (the decoder is pinned against HuggingFace eager in test_oracle_decoder.py),
+    from the same projection row, at the step's position."""
+
+    shape, dec = _tiny_decoder()
+    ids = np.array([3, 17, 40, 9, 22], dtype=np.int64)
+    _, compact = dec.prefill(ids)
+    cache = dec.pad_cache(compact)
+    token, valid = 11, ids.shape[0] + 1
+    _, next_cache = dec.decode(token, valid, cache)
+    layer = dec.state["layers"][0]
+    row = dec._gemv(dec.state["embed"][token], layer["qkv"], norm=layer["input_norm"], bias=layer.get("qkv_bias"))
+    qd, kd = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
+    q, pair = ops.rope_kv_cache_append(cache, row[None], dec.cos[valid - 1], dec.sin[valid - 1], layer=0,
+                                       query_heads=shape.heads, query_start=0, key_start=qd, value_start=qd + kd)
+    np.testing.assert_array_equal(pair, next_cache[0])
+    assert q.shape == (1, shape.heads, 1, shape.head_dim)
+
+
+def test_rope_kv_cache_append_closed_forms():
+    """The window moves down one slot bit for bit, the value lands unrotated in the last
+    slot, and at position 0 (cos 1, sin 0) q and k are the projection row's own values;
+    at another position q and k keep each rotated pair's norm (to bf16 rounding)."""
+
+    rng = np.random.default_rng(8)
+    layers, batch, hkv, cap, d, hq = 3, 1, 2, 7, 16, 4
+    cache = bf16_normal(rng, (layers, 2, batch, hkv, cap, d))
+    width = (hq + 2 * hkv) * d
+    row = bf16_normal(rng, (batch, width))
+    cos, sin = ops.rope_tables(16, d, 1e6)
+    kw = dict(layer=1, query_heads=hq, query_start=0, key_start=hq * d, value_start=(hq + hkv) * d)
+    q, pair = ops.rope_kv_cache_append(cache, row, cos[0], sin[0], **kw)
+    np.testing.assert_array_equal(pair[:, :, :, :-1], cache[1][:, :, :, 1:])
+    np.testing.assert_array_equal(pair[1, :, :, -1], row[:, (hq + hkv) * d:].reshape(batch, hkv, d))
+    np.testing.assert_array_equal(pair[0, :, :, -1], row[:, hq * d:(hq + hkv) * d].reshape(batch, hkv, d))
+    np.testing.assert_array_equal(q.reshape(batch, hq, d), row[:, :hq * d].reshape(batch, hq, d))
+    q, pair = ops.rope_kv_cache_append(cache, row, cos[9], sin[9], **kw)
+    k_in = row[:, hq * d:(hq + hkv) * d].reshape(batch, hkv, d).astype(np.float64)
+    k_out = pair[0, :, :, -1].astype(np.float64)
+    half = d // 2
+    pair_norm_in = np.hypot(k_in[..., :half], k_in[..., half:])
+    pair_norm_out = np.hypot(k_out[..., :half], k_out[..., half:])
+    np.testing.assert_allclose(pair_norm_out, pair_norm_in, rtol=2 ** -7, atol=1e-3)
+    assert not np.array_equal(k_out, k_in), "position 9 rotates"
+    # the other layers' windows are not part of the result
+    assert pair.shape == (2, batch, hkv, cap, d)
