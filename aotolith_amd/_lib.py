@@ -12,6 +12,7 @@ import ctypes
 import hashlib
 import os
 import threading
+import weakref
 
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(PACKAGE_DIR, "libaoto_hip.so")
@@ -38,6 +39,8 @@ SIGNATURES: dict[str, tuple] = {
     "aoto_hip_last_error": (ctypes.c_char_p, _c_size),
     "aoto_hip_load_code_object": (_p, _c_size),
     "aoto_hip_unload_code_object": (),
+    "aoto_hip_hold_graphs": (_c_int,),
+    "aoto_hip_graph_holds": (),
     "aoto_hip_code_object_loaded": (),
     "aoto_hip_w4_quantize": (_p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p, _p),
     "aoto_hip_w4_dequantize": (_p, _p, _c_int, _c_int, _c_int, _p, _p),
@@ -204,6 +207,20 @@ def install_code_object(image: bytes, device: int | None = None) -> str:
     _loaded_devices[device] = digest
     _loaded_images[device] = bytes(image)
     return digest
+
+
+def _release_graph_hold() -> None:
+    library().aoto_hip_hold_graphs(-1)
+
+
+def hold_graph(graph) -> None:
+    """Count a captured graph whose nodes launch this library's kernels until it is
+    garbage-collected: while any is held, a code-object reload keeps the replaced
+    module loaded and ``aoto_hip_unload_code_object`` refuses (the graph launches
+    kernels by handle)."""
+
+    check(library().aoto_hip_hold_graphs(1))
+    weakref.finalize(graph, _release_graph_hold)
 
 
 def ensure_code_object(device: int | None = None) -> str:

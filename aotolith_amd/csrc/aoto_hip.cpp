@@ -54,15 +54,32 @@ namespace {
 struct DeviceModule {
   hipModule_t module = nullptr;
   std::unordered_map<std::string, hipFunction_t> functions;
-  // Modules replaced by a later load. They stay loaded: a HIP graph captured
-  // earlier holds their kernel handles, and replaying it after an unload would
-  // execute freed code (a GPU memory fault). Released by
-  // aoto_hip_unload_code_object only.
+  // Modules replaced by a later load while captured graphs were held: such a
+  // graph holds their kernel handles, and replaying it after an unload would
+  // execute freed code (a GPU memory fault). Released when the last hold goes.
   std::vector<hipModule_t> retired;
 };
 
 std::mutex g_mutex;
 std::map<int, DeviceModule> g_modules;
+// Captured HIP graphs (process-wide) whose nodes launch kernels of the loaded
+// modules: aoto_hip_hold_graphs(+1 / -1). While any is held, no module is unloaded.
+int g_graph_holds = 0;
+
+// With g_mutex held and no graph held: unload every retired module (after the
+// device's queued work, which may still run their kernels).
+void release_retired_locked() {
+  for (auto& entry : g_modules) {
+    if (entry.second.retired.empty()) continue;
+    int current = 0;
+    hipGetDevice(&current);
+    hipSetDevice(entry.first);
+    hipDeviceSynchronize();
+    for (hipModule_t old : entry.second.retired) hipModuleUnload(old);
+    entry.second.retired.clear();
+    hipSetDevice(current);
+  }
+}
 
 int current_device(int* device) {
   hipError_t err = hipGetDevice(device);
@@ -359,10 +376,31 @@ int aoto_hip_load_code_object(const void* image, size_t size) {
   slot.module = module;
   slot.functions.clear();
   aoto::noalloc_prepare_device(device);
+  if (g_graph_holds == 0) release_retired_locked();
   return AOTO_OK;
 }
 
+int aoto_hip_hold_graphs(int delta) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  if (delta == 0 || g_graph_holds + delta < 0)
+    return fail(AOTO_ERR_ARGUMENT, "hold_graphs: %d held, cannot change by %d", g_graph_holds, delta);
+  g_graph_holds += delta;
+  if (g_graph_holds == 0) release_retired_locked();
+  return AOTO_OK;
+}
+
+int aoto_hip_graph_holds(void) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  return g_graph_holds;
+}
+
 int aoto_hip_unload_code_object(void) {
+  {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (g_graph_holds > 0)
+      return fail(AOTO_ERR_ARGUMENT, "unload_code_object: %d captured graphs still launch kernels of the loaded "
+                  "code objects; release them (aoto_hip_hold_graphs(-1)) first", g_graph_holds);
+  }
   int device = 0;
   if (int s = current_device(&device)) return s;
   std::lock_guard<std::mutex> lock(g_mutex);

@@ -36,7 +36,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, ops
 from .errors import (
     BucketRangeError,
     CompilationError,
@@ -770,6 +770,7 @@ class _Engine:
                 with _graph_capture(graph):
                     for _ in range(size):
                         self._ring_step()
+                _lib.hold_graph(graph)
                 graphs[size] = graph
                 size *= 2
             self._graphs = graphs
@@ -846,6 +847,7 @@ class _Engine:
             graph = torch.cuda.CUDAGraph()
             with _graph_capture(graph, pool=self._prefill_pool):
                 captured = self._ring_prefill_body(key_start)
+            _lib.hold_graph(graph)
             self._prefill_graphs[key_start] = (graph, captured)
         except Exception as error:  # noqa: BLE001 - eager prefill stays correct, recorded
             self.prefill_graph_error = f"{type(error).__name__}: {error}"

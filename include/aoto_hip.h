@@ -56,16 +56,26 @@ size_t aoto_hip_take_launches(char* buf, size_t size);
 size_t aoto_hip_last_error(char* buf, size_t size);
 
 /* Install a gfx950 code object (the bytes of an .hsaco) as the kernel module of
- * the current device: later launches use its kernels. The module it replaces
- * stays loaded, because HIP graphs captured earlier launch its kernels by handle.
- * Replaces the reference's kernel shell and cache (codegen/msl.py:625-646) and,
- * on artifact reload, its re-emission of MSL (artifact.py:367-384): the stored
- * code object is loaded as-is instead of regenerating source. */
+ * the current device: later launches use its kernels. The module it replaces is
+ * unloaded at once when no captured graph is held (aoto_hip_hold_graphs), else
+ * kept until the last hold is released, because those graphs launch its kernels
+ * by handle. Replaces the reference's kernel shell and cache
+ * (codegen/msl.py:625-646) and, on artifact reload, its re-emission of MSL
+ * (artifact.py:367-384): the stored code object is loaded as-is instead of
+ * regenerating source. */
 int aoto_hip_load_code_object(const void* image, size_t size);
 
-/* Unload the current device's module and every module it replaced. The caller
- * must first drop every graph captured over them: replaying one afterwards
- * executes unloaded code. */
+/* No counterpart in the reference (its runtime has no captured graphs). Count
+ * (+1) or release (-1) a captured HIP graph whose nodes launch kernels of the
+ * loaded code objects; process-wide. A release that brings the count to zero
+ * unloads the modules replaced in the meantime. A count below zero is refused. */
+int aoto_hip_hold_graphs(int delta);
+/* The current number of held graphs. */
+int aoto_hip_graph_holds(void);
+
+/* Unload the current device's module and every module it replaced. Refused
+ * (AOTO_ERR_ARGUMENT) while any captured graph is held: replaying one afterwards
+ * would execute unloaded code. */
 int aoto_hip_unload_code_object(void);
 
 /* 1 when a module is installed on the current device, else 0. */

@@ -92,3 +92,42 @@ def test_wide_plan_matches_the_workspace_queries():
     # explicit codes are taken as given
     assert ops.gemm_workspace_bytes(2048, 4096, 4096, 28, 1) == 0
     assert ops.gemm_workspace_bytes(2048, 4096, 4096, 441, 2) == 2 * 2048 * 4096 * 4
+
+
+def test_unload_is_refused_while_captured_graphs_are_held():
+    """Host logic only: with a captured graph held, aoto_hip_unload_code_object refuses
+    before touching any device (its modules would back the graph's kernel handles); a
+    release below zero is refused; after the release the unload no longer names graphs."""
+
+    from aotolith_amd import _lib
+
+    lib = _lib.library()
+    assert lib.aoto_hip_graph_holds() == 0
+    assert lib.aoto_hip_hold_graphs(1) == _lib.AOTO_OK
+    try:
+        assert lib.aoto_hip_graph_holds() == 1
+        assert lib.aoto_hip_unload_code_object() == _lib.AOTO_ERR_ARGUMENT
+        assert "captured graphs still launch kernels" in _lib.last_error()
+    finally:
+        assert lib.aoto_hip_hold_graphs(-1) == _lib.AOTO_OK
+    assert lib.aoto_hip_hold_graphs(-1) == _lib.AOTO_ERR_ARGUMENT
+    assert lib.aoto_hip_graph_holds() == 0
+    lib.aoto_hip_unload_code_object()  # no GPU here: a device error at most, never the graph refusal
+    assert "captured graphs" not in _lib.last_error()
+
+
+def test_hold_graph_is_released_when_the_graph_is_collected():
+    import gc
+
+    from aotolith_amd import _lib
+
+    class Graph:  # stands in for torch.cuda.CUDAGraph (no GPU here)
+        pass
+
+    lib = _lib.library()
+    graph = Graph()
+    _lib.hold_graph(graph)
+    assert lib.aoto_hip_graph_holds() == 1
+    del graph
+    gc.collect()
+    assert lib.aoto_hip_graph_holds() == 0
