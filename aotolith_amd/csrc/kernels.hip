@@ -41,7 +41,9 @@ AOTO_GEMV_STREAM_SINGLE(64, 3, 0, true)
 AOTO_GEMV_ROWS_SHAPE(32, 1, 2)
 AOTO_GEMV_ROWS_SHAPE(32, 1, 4)
 // Block-staged x for long reductions with short or mid outputs: K = 4096
-// (Llama-8B q/k/v, o, gate/up) 32x4, K = 14336 (Llama-8B down) 64x7.
+// (Llama-8B q/k/v, o, gate/up) 32x4, K = 14336 (Llama-8B down) 64x7. The single
+// forms hold x in registers (same-process A/B: down 10.9-11.3 -> 9.6-9.8 us,
+// q/k/v -0.1 us, o unchanged); the paired form reads it from LDS (no gain).
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(32, 4, 2)
 AOTO_GEMV_STREAM_BLOCKX_PAIRED(32, 4, 2)
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 7, 7)
@@ -49,8 +51,9 @@ AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 7, 7)
 // and direct 64-lane forms for any other K up to 2048 / 6144.
 AOTO_GEMV_STREAM_ARGMAX(8, 4, 2, false)
 // the K = 896 and K = 4096 LM heads with their final norm, x staged once per block
-AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x8x4_n1_argmax, 8, 4, 1, false, 1, 0, 0, true, true)
-AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x32x4_n1_argmax, 32, 4, 2, false, 1, 0, 0, true, true)
+// and copied into registers (same-process A/B, Qwen head 14.7-15.7 -> 14.0-14.1 us)
+AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x8x4_n1_argmax, 8, 4, 1, true, 1, 0, 0, true, true)
+AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x32x4_n1_argmax, 32, 4, 2, true, 1, 0, 0, true, true)
 AOTO_GEMV_STREAM_ARGMAX(32, 4, 8, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 1, 0, true)
 AOTO_GEMV_STREAM_ARGMAX(64, 3, 0, true)

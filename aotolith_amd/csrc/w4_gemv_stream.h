@@ -220,7 +220,8 @@ struct DirectActivation {
 // the stored bf16 value and its row) and store it at keys[global wave index],
 // 0 for a wave without rows; aoto_argmax_finish reduces the keys.
 // BLOCKX: x staged once per block (StagedActivation; XV >= K/2048) into
-// one LDS region the block's waves share; needs 4-wave blocks.
+// one LDS region the block's waves share; needs 4-wave blocks. With XREG the
+// lanes copy their chunks out of it after the block's staging barrier.
 template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX, bool BLOCKX = false>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                     const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
@@ -360,6 +361,14 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
     load(tile, ra);
     __builtin_amdgcn_sched_barrier(0);  // x, then the first tile's loads, then the staging
     act.finish(eps, K, xp, csum);
+    if constexpr (XREG) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xr[j][k] = xp[cidx[j] * 4 + k];
+        cr[j] = csum[cidx[j]];
+      }
+    }
   }
   if (tile >= tiles) {
     if (ARGMAX && lane == 0) keys[tile] = 0;
@@ -480,15 +489,17 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n1_argmax, LPR, CPL, XV, XREG, 1, 0, 0, true)  \
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n0_argmax, LPR, CPL, XV, XREG, 0, 0, 0, true)
 // Block-staged forms (x shared by the block's 4 waves) for long reductions:
-// names aoto_w4_gemv_x{LPR}x{CPL}_n*_p*_b*.
-#define AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, NORM, PAIRED, BIAS)                               \
+// names aoto_w4_gemv_x{LPR}x{CPL}_n*_p*_b*. XREG: each lane then copies its
+// chunks of x into registers (single projections; the paired form, with two
+// weight sets in flight, keeps reading x from LDS).
+#define AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, XREG, NORM, PAIRED, BIAS)                         \
   AOTO_GEMV_STREAM_KERNEL_X(aoto_w4_gemv_x##LPR##x##CPL##_n##NORM##_p##PAIRED##_b##BIAS, LPR, CPL, XV,   \
-                            false, NORM, PAIRED, BIAS, false, true)
-#define AOTO_GEMV_STREAM_BLOCKX_SINGLE(LPR, CPL, XV)          \
-  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 1, 0, 1)    \
-  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 1, 0, 0)    \
-  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 0, 0, 1)    \
-  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 0, 0, 0)
-#define AOTO_GEMV_STREAM_BLOCKX_PAIRED(LPR, CPL, XV)          \
-  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 1, 1, 0)    \
-  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, 0, 1, 0)
+                            XREG, NORM, PAIRED, BIAS, false, true)
+#define AOTO_GEMV_STREAM_BLOCKX_SINGLE(LPR, CPL, XV)                \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, true, 1, 0, 1)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, true, 1, 0, 0)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, true, 0, 0, 1)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, true, 0, 0, 0)
+#define AOTO_GEMV_STREAM_BLOCKX_PAIRED(LPR, CPL, XV)                 \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, false, 1, 1, 0)    \
+  AOTO_GEMV_STREAM_BLOCKX_INSTANCE(LPR, CPL, XV, false, 0, 1, 0)
