@@ -16,10 +16,11 @@
 //   A (32 n x 16 k): lane l holds W[n0 + l%32][k-unit of half l/32]   -> one packed word
 //   B (16 k x 32 m): lane l holds X[m0 + l%32][k-unit of half l/32]   -> 16 B of an X row
 //   C (32 n x 32 m): lane l, register e holds Y[m0 + l%32][n0 + 8(e/4) + 4(l/32) + e%4]
-// A step is 64 k (eight 8-code units); lane half h supplies units 4h .. 4h+3 (one
-// 16-byte load of 4-bit words) and product j of the step takes unit 4h + j from
-// both operands, so the sum over k is the same, in another order. The 32 k of a
-// lane half lie in one group (group % 32 == 0): one scale per lane and step.
+// A sub-step is 16 k: lane half h supplies one 8-code unit of its row (A) and the
+// matching 16 bytes of its X row (B); over a 128-k step lane half h covers units
+// 8h .. 8h+7 and sub-step j takes unit 8h + j from both operands, so the sum over
+// k is the same, in another order. Each 32 k of a lane half lie in one group
+// (group % 32 == 0): two scales per lane and step.
 //
 // Exact dequant: with n = code + 8 (the nibble's sign bit flipped, 0..15), an
 // f16 lane holding 1024 + n (n OR-ed into the mantissa of 1024.0) goes through
@@ -30,11 +31,11 @@
 // exact for every bf16 s). Per 8 codes: one shift, four v_bitop3 (mask, sign
 // flip and exponent in one op), eight v_fma_mix_f32, four packs.
 //
-// Block: NW (4 or 8) waves side by side along n; the X tile [BM][64] is
-// staged in LDS (rows 144 bytes apart, so each 16-lane phase of an operand read
-// touches all 64 banks once), double-buffered, one barrier per step. The next
-// step's X chunks and words are loaded into registers while the current step
-// computes.
+// Block: NW (4 or 8) waves side by side along n. A step is 128 k: its X tile
+// [BM][128] and each wave's packed words and scales go from global memory straight
+// into LDS (global-to-LDS loads, no VGPRs on the way; X chunks XOR-swizzled so each
+// 16-lane phase of an operand read touches 16 bank groups), two or three steps in
+// flight, one barrier per step (w4_gemm_wide_body).
 #pragma once
 
 #include "common.h"
@@ -397,6 +398,9 @@ __device__ void w4_gemm_wide_body(const uint16_t* __restrict__ X, const typename
       step(st + 1, xs1, ws1, ss1, xs0, ws0, ss0);
     }
   }
+  // The last rounds' loads (of steps past the slice) still land in LDS: wait for
+  // them before the block ends (split-K) or reuses the buffers (epilogue).
+  AOTO_WAIT_VMCNT(0);
 
   if (partials != nullptr) {
 #pragma unroll

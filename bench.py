@@ -199,21 +199,45 @@ def _row(name: str, kernel: str, us: float, *, nbytes: int | None = None, flops:
     return row
 
 
-def decode_kernel_table(runtime, torch, ops, valid: int | None = None) -> list[dict]:
+def _rotation(weights: list, torch, pool_bytes: float) -> list:
+    """The weights to cycle through: the given ones, then copies of them until their
+    packed words and scales exceed ``pool_bytes`` (more than the 256 MB Infinity
+    Cache and the L2s hold), so no launch finds its weights cached from an earlier one."""
+
+    from dataclasses import replace
+
+    out = list(weights)
+    size = sum(w.packed.numel() * 4 + w.scales.numel() * 2 for w in weights)
+    while size < pool_bytes:
+        w = weights[len(out) % len(weights)]
+        out.append(replace(w, packed=w.packed.clone(), scales=w.scales.clone()))
+        size += w.packed.numel() * 4 + w.scales.numel() * 2
+    return out
+
+
+def decode_kernel_table(runtime, torch, ops, valid: int | None = None, pool_bytes: float = 0.6e9) -> list[dict]:
     """Per-kernel times of the greedy loop's decode step, one row per kernel kind.
 
-    Each kernel is launched once per layer with that layer's weights (so, as in the
-    loop, no launch finds its weights in the Infinity Cache from the previous
-    launch of the same kind) inside one HIP graph; the time is the median replay /
-    layer count. Bytes are the algorithmic bytes of one launch (weights, scales, x,
-    y, bias or residual, norm weight; the attention's K/V window of ``valid``
-    keys). The loop's state is left as a fresh loop would find it.
+    Each GEMV kind is launched over a rotation of its layers' weights, extended with
+    copies to more than ``pool_bytes`` (a small model's 24 layers of one kind fit in
+    the Infinity Cache, where the loop, which streams a whole step between two reads
+    of one layer, does not find them), inside one HIP graph; the time is the median
+    replay / launch count. The attention runs once per layer over the layers' own
+    KV windows (as in the loop). Bytes are the algorithmic bytes of one launch
+    (weights, scales, x, y, bias or residual, norm weight; the attention's K/V window
+    of ``valid`` keys). The loop's state is left as a fresh loop would find it.
     """
 
     eng = runtime.engine
     spec = runtime.spec
     layers = eng.state.layers
     n = len(layers)
+    # per kind: (weight, its layer's norm / bias / up weights), cycled
+    qkv_w = _rotation([l.qkv for l in layers], torch, pool_bytes)
+    o_w = _rotation([l.o for l in layers], torch, pool_bytes)
+    down_w = _rotation([l.down for l in layers], torch, pool_bytes)
+    gate_w = _rotation([l.gate for l in layers], torch, pool_bytes / 2)
+    up_w = _rotation([l.up for l in layers], torch, pool_bytes / 2)
     bits = eng.state.bits
     h, i = spec.hidden, spec.intermediate
     qd, kd = spec.heads * spec.head_dim, spec.kv_heads * spec.head_dim
@@ -227,9 +251,9 @@ def decode_kernel_table(runtime, torch, ops, valid: int | None = None) -> list[d
     rows = []
 
     def qkv():
-        for layer in layers:
-            eng._gemv(eng.hidden, layer.qkv, eng.qkv, norm_weight=layer.input_norm, eps=spec.eps,
-                      bias=layer.qkv_bias)
+        for index, w in enumerate(qkv_w):
+            layer = layers[index % n]
+            eng._gemv(eng.hidden, w, eng.qkv, norm_weight=layer.input_norm, eps=spec.eps, bias=layer.qkv_bias)
 
     def attention():
         for index in range(n):
@@ -240,29 +264,34 @@ def decode_kernel_table(runtime, torch, ops, valid: int | None = None) -> list[d
                                       rope_rows=eng.rope_rows if eng.keys is not None else None, out=eng.attn)
 
     def o_proj():
-        for layer in layers:
-            eng._gemv(eng.attn.view(-1), layer.o, eng.hidden, bias=eng.hidden)
+        for w in o_w:
+            eng._gemv(eng.attn.view(-1), w, eng.hidden, bias=eng.hidden)
 
     def gate_up():
-        for layer in layers:
-            eng._gemv(eng.hidden, layer.gate, eng.act, norm_weight=layer.post_norm, eps=spec.eps,
-                      up=(layer.up.packed, layer.up.scales))
+        for index, (g, u) in enumerate(zip(gate_w, up_w)):
+            eng._gemv(eng.hidden, g, eng.act, norm_weight=layers[index % n].post_norm, eps=spec.eps,
+                      up=(u.packed, u.scales))
 
     def down():
-        for layer in layers:
-            eng._gemv(eng.act, layer.down, eng.hidden, bias=eng.hidden)
+        for w in down_w:
+            eng._gemv(eng.act, w, eng.hidden, bias=eng.hidden)
 
     w = f"w{bits}"
-    rows.append(_row("qkv", f"aoto_{w}_gemv (RMSNorm prologue, bias)", _graph_us(torch, qkv, n),
+    rows.append(_row("qkv", f"aoto_{w}_gemv (RMSNorm prologue, bias)", _graph_us(torch, qkv, len(qkv_w)),
                      nbytes=gemv_bytes(spec.qkv_width, h, norm=True, bias=spec.qkv_bias, bits=bits)))
     rows.append(_row("attention", f"aoto_decode_rope_attention_d{spec.head_dim} (RoPE, KV write, {valid} keys)",
                      _graph_us(torch, attention, n), nbytes=2 * spec.kv_heads * valid * spec.head_dim * 2))
-    rows.append(_row("o", f"aoto_{w}_gemv (residual)", _graph_us(torch, o_proj, n),
+    rows.append(_row("o", f"aoto_{w}_gemv (residual)", _graph_us(torch, o_proj, len(o_w)),
                      nbytes=gemv_bytes(h, spec.attention_width, bias=True, bits=bits)))
-    rows.append(_row("gate_up", f"aoto_{w}_gemv paired (RMSNorm prologue, silu_mul)", _graph_us(torch, gate_up, n),
+    rows.append(_row("gate_up", f"aoto_{w}_gemv paired (RMSNorm prologue, silu_mul)",
+                     _graph_us(torch, gate_up, len(gate_w)),
                      nbytes=gemv_bytes(i, h, norm=True, paired=True, bits=bits)))
-    rows.append(_row("down", f"aoto_{w}_gemv (residual)", _graph_us(torch, down, n),
+    rows.append(_row("down", f"aoto_{w}_gemv (residual)", _graph_us(torch, down, len(down_w)),
                      nbytes=gemv_bytes(h, i, bias=True, bits=bits)))
+    for row, weights in zip(rows, (qkv_w, None, o_w, gate_w, down_w)):
+        if weights is not None:
+            row["rotation"] = len(weights)
+    del qkv_w, o_w, down_w, gate_w, up_w
     if eng.keys is not None:
         head = eng.state.lm_head
 
