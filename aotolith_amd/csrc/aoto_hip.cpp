@@ -192,7 +192,7 @@ int gemv_rows(int lpr, int shape_default) {
   return exists ? value : shape_default;
 }
 
-bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) {
+bool stream_shape(int K, int N, bool paired, StreamShape* s) {
   const bool short_out = N <= 8192;
   switch (K) {
     case 896:
@@ -202,13 +202,18 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) 
       // tiles, over which its x staging and pipeline fill and drain amortize
       // (greedy loop's LM-head kernel, 151936 rows, 1 / 2 / 3 / 4 / 5 / 6 / 8
       // blocks per CU: 16.7 / 14.9 / 15.5 / 16.0 / 16.8 / 17.0 / 17.5 us).
-      // Short outputs: the multi-row direct form where one normalized copy of x
-      // serves several rows (paired gate/up: 4 rows per lane, 3.9 vs 4.3 us for
-      // Qwen's 2 x 4864 rows; normed q/k/v: 2, 2.45 vs 2.6 us); without a norm
-      // prologue (o projection) the streaming form is as fast (2.0 us).
-      if (short_out) {
+      // Short outputs, paired gate/up: the multi-row direct form, one normalized
+      // copy of x per lane serving 4 rows (3.9 vs 4.3 us for Qwen's 2 x 4864 rows).
+      // Single projections (q/k/v, o): one copy of x per 4-wave block, held in
+      // registers - in the direct forms every wave loaded all of x and the norm
+      // weight, more bytes per CU than its weights (Qwen q/k/v 2.87 -> 2.74 us, o
+      // 2.91 -> 2.51, decode 2385-2391 -> 2414-2417 tok/s in alternating runs on
+      // one box; the paired form this way: 4.15 -> 4.40 us).
+      if (short_out && paired) {
         *s = {32, 1, true};
-        s->rows = gemv_rows(32, paired ? 4 : (norm ? 2 : 0));
+        s->rows = gemv_rows(32, 4);
+      } else if (short_out) {
+        *s = {32, 1, false, 1, true};
       } else
         *s = paired ? StreamShape{8, 4, false} : StreamShape{8, 4, false, 2};
       return true;
@@ -224,8 +229,12 @@ bool stream_shape(int K, int N, bool paired, StreamShape* s, bool norm = false) 
         *s = {32, 4, false};
       return true;
     case 4864:
+      // One copy of x per 4-wave block, held in registers: the direct form had
+      // every wave load all 9.7 KB of x, ~40 KB per CU beside ~9 KB of weights
+      // (Qwen down projection 3.58 -> 3.29 us, decode 2345-2359 -> 2379-2382
+      // tok/s in alternating runs on one box).
       if (paired || !short_out) return false;
-      *s = {64, 3, true};
+      *s = {64, 3, false, 1, true};
       return true;
     case 14336:
       // 28 KB of x per block: one block per CU (down projection 10.28 against
@@ -472,7 +481,7 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   // The streaming form reads scales and bias as aligned 32-bit pairs.
   const bool pairs_ok = (K / group) % 2 == 0 && aligned4(scales) && (!up_scales || aligned4(up_scales)) &&
                         (!bias || (N % 2 == 0 && aligned4(bias)));
-  if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss, norm) && ss.rows > 0) {
+  if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss) && ss.rows > 0) {
     // one 1-wave block per tile of (64 / lpr) * rows rows
     const int rows_per_wave = (64 / ss.lpr) * ss.rows;
     const unsigned grid = (unsigned)((N + rows_per_wave - 1) / rows_per_wave);

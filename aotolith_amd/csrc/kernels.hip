@@ -25,27 +25,27 @@ AOTO_GEMV_LPR(1, 1, 0)
 // {x vectors each lane stages, ceil(K / 512); 0 = each lane loads its own
 // chunks directly} x {x held in registers}.
 // K = 896: 8x4 for long outputs (single: x read from LDS; paired: x in
-// registers), 32x1 direct for short ones (single and paired); K = 4096: 32x4;
-// K = 4864: 64x3 direct.
+// registers), 32x1 direct for short paired ones (AOTO_GEMV_ROWS=0); K = 4096: 32x4.
 AOTO_GEMV_STREAM_SINGLE(8, 4, 2, false)
 AOTO_GEMV_STREAM_PAIRED(8, 4, 2, true)
-AOTO_GEMV_STREAM_SINGLE(32, 1, 0, true)
 AOTO_GEMV_STREAM_PAIRED(32, 1, 0, true)
 AOTO_GEMV_STREAM_SINGLE(32, 4, 8, true)
 AOTO_GEMV_STREAM_PAIRED(32, 4, 8, true)
-AOTO_GEMV_STREAM_SINGLE(64, 3, 0, true)
-// Multi-row direct GEMV for a decoder layer's short outputs at K = 896:
-// {lanes per row} x {chunks per lane} x {rows per lane}. (Measured and not
-// kept: 8 rows per lane at K = 896, and 2 or 4 rows of the 64x3 layout at
-// K = 4864, no faster than the streaming form.)
+// Multi-row direct GEMV for the paired gate/up at K = 896 (4 rows per lane; 2
+// by AOTO_GEMV_ROWS): {lanes per row} x {chunks per lane} x {rows per lane}. (Measured and not
+// kept: 8 rows per lane at K = 896, and 2 or 4 rows of a direct 64x3 layout
+// at K = 4864, no faster than the streaming form.)
 AOTO_GEMV_ROWS_SHAPE(32, 1, 2)
 AOTO_GEMV_ROWS_SHAPE(32, 1, 4)
-// Block-staged x for long reductions with short or mid outputs: K = 4096
-// (Llama-8B q/k/v, o, gate/up) 32x4, K = 14336 (Llama-8B down) 64x7. The single
-// forms hold x in registers (same-process A/B: down 10.9-11.3 -> 9.6-9.8 us,
-// q/k/v -0.1 us, o unchanged); the paired form reads it from LDS (no gain).
+// Block-staged x for short or mid outputs: K = 896 (Qwen q/k/v, o) 32x1,
+// K = 4096 (Llama-8B q/k/v, o, gate/up) 32x4, K = 4864 (Qwen down) 64x3,
+// K = 14336 (Llama-8B down) 64x7. The single
+// forms hold x in registers (same-process A/B, Llama-8B: down 10.9-11.3 -> 9.6-9.8
+// us, q/k/v -0.1 us, o unchanged); the paired form reads it from LDS (no gain).
+AOTO_GEMV_STREAM_BLOCKX_SINGLE(32, 1, 1)
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(32, 4, 2)
 AOTO_GEMV_STREAM_BLOCKX_PAIRED(32, 4, 2)
+AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 3, 3)
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 7, 7)
 // LM heads with the fused greedy-argmax keys: K = 896 (8x4), K = 4096 (32x4),
 // and direct 64-lane forms for any other K up to 2048 / 6144.
