@@ -542,12 +542,12 @@ struct GemmPlan {
 // Wide-tile codes: 100 * (waves per block / 2) + 10 * (32-row tiles per wave) +
 // (32-column tiles per wave), the waves side by side along n (w4_gemm_wide.h).
 bool wide_code(int tile) {
-  return tile == 241 || tile == 242 || tile == 243 || tile == 281 || tile == 441 || tile == 442;
+  return tile == 241 || tile == 242 || tile == 243 || tile == 281 || tile == 441;
 }
 
 // The wide instances in the code object (their staging fits 160 KB of LDS).
 bool wide_instance(int tile, int bits, bool paired) {
-  if (paired) return tile == 241 || (bits == 4 && tile == 441);
+  if (paired) return tile == 241;
   return bits == 4 || tile == 241 || tile == 242 || tile == 441;
 }
 
@@ -731,7 +731,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
     return fail(AOTO_ERR_ARGUMENT, "%s: x and words must be 16-byte aligned, y/bias/residual/gate 8-byte aligned",
                 what);
   if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile))
-    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441, 442", what,
+    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441", what,
                 tile);
   if (wide_code(tile)) {
     if (!wide_instance(tile, bits, paired))

@@ -88,12 +88,10 @@ AOTO_GEMM_WIDE_EPILOGUES(4, 4, 2, 4)
 AOTO_GEMM_WIDE_EPILOGUES(4, 4, 3, 4)
 AOTO_GEMM_WIDE_EPILOGUES(4, 8, 1, 4)
 AOTO_GEMM_WIDE_EPILOGUES(4, 4, 1, 8)
-AOTO_GEMM_WIDE_EPILOGUES(4, 4, 2, 8)
 AOTO_GEMM_WIDE_EPILOGUES(8, 4, 1, 4)
 AOTO_GEMM_WIDE_EPILOGUES(8, 4, 2, 4)
 AOTO_GEMM_WIDE_EPILOGUES(8, 4, 1, 8)
 AOTO_GEMM_WIDE_PAIRED_INSTANCE(4, 4, 1, 4)
-AOTO_GEMM_WIDE_PAIRED_INSTANCE(4, 4, 1, 8)
 AOTO_GEMM_WIDE_PAIRED_INSTANCE(8, 4, 1, 4)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)
