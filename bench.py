@@ -693,6 +693,8 @@ def main() -> int:
                         help="only the causal prefill attention of one layer at TOKENS queries (timing, counter runs)")
     parser.add_argument("--input-std", type=float, default=1.0,
                         help="standard deviation of the --prefill-attention-only inputs")
+    parser.add_argument("--decode-kernels-only", action="store_true",
+                        help="only the decode step's per-kernel table (after a 256 MiB calibration copy)")
     parser.add_argument("--prefill-gemm-only", type=int, default=0, metavar="TOKENS",
                         help="only one layer's prefill GEMMs at TOKENS rows (for MFMA counter runs)")
     args = parser.parse_args()
@@ -728,6 +730,23 @@ def main() -> int:
         gemms = measure_prefill_gemms(spec, torch, ops, args.prefill_gemm_only)
         print(json.dumps({"workload": f"{args.workload} prefill GEMMs", "tokens": args.prefill_gemm_only,
                           "peak_tflops": MFMA_BF16_PEAK_TFLOPS, **gemms}), flush=True)
+        return 0
+    if args.decode_kernels_only:
+        # the decode step's per-kernel table alone (after a 256 MiB calibration copy, for
+        # counter runs): the workload's full-depth random-init state, bucket = --prompt
+        spec = qwen_spec() if args.workload == "qwen0.5b" else llama8b_spec()
+        src = torch.empty(1 << 26, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        prompt = args.prompt if args.workload == "qwen0.5b" else 512
+        new = args.new if args.workload == "qwen0.5b" else 256
+        std = {"std": STATE_STD} if args.workload == "qwen0.5b" else {}  # as the workload's own bench line
+        state = random_state(spec, 64, seed=0, norm_std=STATE_NORM_STD, bits=args.bits, **std)
+        runtime = compile_decoder_state(spec, state, prompt_length=prompt, max_new_tokens=new)
+        rows = decode_kernel_table(runtime, torch, ops)
+        print(json.dumps({"workload": f"{args.workload} decode kernels", "prompt": prompt, "new_tokens": new,
+                          "calibration_copy_bytes": src.numel() * 4, "decode": rows}), flush=True)
         return 0
     if args.workload == "llama8b":
         result = run_llama8b(args, torch, ops)
