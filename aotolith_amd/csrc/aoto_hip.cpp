@@ -481,18 +481,16 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
   // The streaming form reads scales and bias as aligned 32-bit pairs.
   const bool pairs_ok = (K / group) % 2 == 0 && aligned4(scales) && (!up_scales || aligned4(up_scales)) &&
                         (!bias || (N % 2 == 0 && aligned4(bias)));
-  if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss) && ss.rows > 0) {
+  // (the multi-row instances take 64-code groups; other groups use the streaming form)
+  if (lanes_per_row == 0 && pairs_ok && group == 64 && stream_shape(K, N, paired, &ss) && ss.rows > 0) {
     // one 1-wave block per tile of (64 / lpr) * rows rows
     const int rows_per_wave = (64 / ss.lpr) * ss.rows;
     const unsigned grid = (unsigned)((N + rows_per_wave - 1) / rows_per_wave);
-    int shift = 0;
-    while ((32 << shift) < group) ++shift;
     char rname[64];
     snprintf(rname, sizeof(rname), "aoto_w4_gemv_r%dx%dx%d_n%d_p%d_b%d", ss.lpr, ss.cpl, ss.rows, norm,
              paired ? 1 : 0, has_bias);
-    const int one_wave = 1;
-    return launch(rname, dim3(grid), dim3(64), 0u, stream, x, words, scales, up_words, up_scales, norm_weight,
-                  eps, bias, alpha, beta, y, K, N, shift, one_wave);
+    return launch(rname, dim3(grid), dim3(64), 0u, stream, words, scales, up_words, up_scales, x, norm_weight, K,
+                  N, bias, eps, alpha, beta, y);
   }
   if (lanes_per_row == 0 && pow2_group && pairs_ok && stream_shape(K, N, paired, &ss)) {
     const StreamLaunch l = stream_launch(ss, K, N, group);
@@ -500,8 +498,8 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales, co
     snprintf(sname, sizeof(sname), "aoto_w4_gemv_%c%dx%d_n%d_p%d_b%d", ss.block_x ? 'x' : 's', ss.lpr, ss.cpl,
              norm, paired ? 1 : 0, has_bias);
     unsigned long long* no_keys = nullptr;
-    return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, x, words, scales, up_words,
-                  up_scales, norm_weight, eps, bias, alpha, beta, y, K, N, l.shift, l.wpb, no_keys);
+    return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, words, scales, x, norm_weight,
+                  K, N, l.shift, l.wpb, bias, up_words, up_scales, eps, alpha, beta, y, no_keys);
   }
   int lpr = lanes_per_row;
   if (lpr == 0) {
@@ -1220,8 +1218,8 @@ int aoto_hip_w4_gemv_argmax(const void* x, const int32_t* words, const void* sca
   snprintf(sname, sizeof(sname), "aoto_w4_gemv_%s%dx%d_n%d_argmax", blockx ? "x" : "s", ss.lpr, ss.cpl,
            norm_weight ? 1 : 0);
   const void* none = nullptr;
-  return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, x, words, scales, none, none,
-                norm_weight, eps, none, 1.0f, 0.0f, y, K, N, l.shift, l.wpb, keys);
+  return launch(sname, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, words, scales, x, norm_weight, K,
+                N, l.shift, l.wpb, none, none, none, eps, 1.0f, 0.0f, y, keys);
 }
 
 int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_out, int64_t* history,

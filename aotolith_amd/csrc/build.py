@@ -26,7 +26,10 @@ CODE_OBJECT = os.path.join(PACKAGE, "aoto_gfx950.hsaco")
 LIBRARY = os.path.join(PACKAGE, "libaoto_hip.so")
 
 # Device flags: gfx950 only; packed-FP32 VALU forms disabled (they are not used
-# by hand and the compiler is told not to form them).
+# by hand and the compiler is told not to form them); kernel arguments preloaded
+# into SGPRs (up to 14 dwords on gfx950, so a kernel's first loads need not wait
+# for a scalar load of its argument buffer; kernels order their arguments for
+# it).
 DEVICE_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -35,6 +38,8 @@ DEVICE_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-I" + CSRC,
     "-I" + INCLUDE,
 ]

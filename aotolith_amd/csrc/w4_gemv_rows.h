@@ -23,19 +23,21 @@
 
 namespace aoto {
 
+// One-wave blocks (tile = block); 64-code scale groups (GS = log2(64 / 32)).
 template <int LPR, int CPL, int R, bool NORM, bool PAIRED, bool BIAS>
 __device__ void w4_gemv_rows_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                   const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
                                   const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ norm_w,
                                   float eps, const uint16_t* __restrict__ bias, float alpha, float beta,
-                                  uint16_t* __restrict__ y, int K, int N, int group_shift, int waves_per_block) {
+                                  uint16_t* __restrict__ y, int K, int N) {
+  constexpr int group_shift = 1;
   static_assert(R <= LPR, "a row group's lanes finish its R rows");
   constexpr int RPW = (64 / LPR) * R;  // rows per wave
   const int nchunks = K >> 5;
   const int ngroups = nchunks >> group_shift;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int li = lane & (LPR - 1);
-  const int tile = blockIdx.x * waves_per_block + wave;
+  const int tile = blockIdx.x;
   if (tile * RPW >= N) return;  // uniform: the wave has no rows
   const int row0 = tile * RPW + (lane / LPR) * R;
 
@@ -114,16 +116,17 @@ __device__ void w4_gemv_rows_body(const uint16_t* __restrict__ x, const uint4* _
 
 }  // namespace aoto
 
-// aoto_w4_gemv_r{LPR}x{CPL}x{R}_n{NORM}_p{PAIRED}_b{BIAS}
+// aoto_w4_gemv_r{LPR}x{CPL}x{R}_n{NORM}_p{PAIRED}_b{BIAS}: 64-thread blocks, one
+// tile each. Argument order: what the first loads need comes first, within the
+// 14 preloaded argument dwords (weights, up weights, x, norm weight, shape).
 #define AOTO_GEMV_ROWS_INSTANCE(LPR, CPL, R, NORM, PAIRED, BIAS)                                             \
   extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void                                         \
       aoto_w4_gemv_r##LPR##x##CPL##x##R##_n##NORM##_p##PAIRED##_b##BIAS(                                   \
-          const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,            \
-          const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias, float alpha, \
-          float beta, uint16_t* y, int K, int N, int group_shift, int waves_per_block) {                  \
+          const uint4* words, const uint16_t* scales, const uint4* up_words, const uint16_t* up_scales,    \
+          const uint16_t* x, const uint16_t* norm_w, int K, int N, const uint16_t* bias, float eps,        \
+          float alpha, float beta, uint16_t* y) {                                                         \
     aoto::w4_gemv_rows_body<LPR, CPL, R, NORM, PAIRED, BIAS>(x, words, scales, up_words, up_scales,        \
-                                                              norm_w, eps, bias, alpha, beta, y, K, N,     \
-                                                              group_shift, waves_per_block);               \
+                                                              norm_w, eps, bias, alpha, beta, y, K, N);    \
   }
 // The decoder-layer variants of one lane layout: q/k/v (norm, with or without
 // bias), o / down (+residual), plain, and the paired gate/up (norm or not).

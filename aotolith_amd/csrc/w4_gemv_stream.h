@@ -455,11 +455,15 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
 
 }  // namespace aoto
 
+// Argument order: what the first loads need comes first, so it arrives in the
+// preloaded SGPRs (the code object is built with kernel-argument preloading,
+// 14 dwords on gfx950) instead of behind a scalar load from the argument
+// buffer: the weights, x, the norm weight, the shape, then the bias element.
 #define AOTO_GEMV_STREAM_KERNEL_X(NAME, LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX, BLOCKX)       \
   extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void NAME(                                 \
-      const uint16_t* x, const uint4* words, const uint16_t* scales, const uint4* up_words,              \
-      const uint16_t* up_scales, const uint16_t* norm_w, float eps, const uint16_t* bias, float alpha,   \
-      float beta, uint16_t* y, int K, int N, int group_shift, int waves_per_block,                       \
+      const uint4* words, const uint16_t* scales, const uint16_t* x, const uint16_t* norm_w, int K,      \
+      int N, int group_shift, int waves_per_block, const uint16_t* bias, const uint4* up_words,          \
+      const uint16_t* up_scales, float eps, float alpha, float beta, uint16_t* y,                        \
       unsigned long long* keys) {                                                                        \
     aoto::w4_gemv_stream_body<LPR, CPL, XV, XREG, NORM, PAIRED, BIAS, ARGMAX, BLOCKX>(                   \
         x, words, scales, up_words, up_scales, norm_w, eps, bias, alpha, beta, y, K, N, group_shift,     \
