@@ -1113,14 +1113,22 @@ int aoto_hip_decode_rope_attention(const void* row, int row_width, int query_sta
       !aligned16(row) || !aligned16(cos_table) || !aligned16(sin_table) || (row_width % 8) || (query_start % 8))
     return fail(AOTO_ERR_ARGUMENT, "decode_rope_attention: keys/values/row/tables must be 16-byte aligned, "
                 "row width and query start multiples of 8");
+  // the kernel takes these packed (decode.h): 16-bit heads, starts and width,
+  // a 9-bit chunk with a 22-bit capacity, 31-bit strides
+  if (query_heads >= 65536 || kv_heads >= 65536 || row_width >= 65536 || chunk >= 512 || capacity >= (1 << 22) ||
+      kv_batch_stride >= (int64_t)1 << 31 || kv_head_stride >= (int64_t)1 << 31 || kv_batch_stride < 0 ||
+      kv_head_stride < 0)
+    return fail(AOTO_ERR_UNSUPPORTED, "decode_rope_attention: heads, row width < 65536, capacity < 2^22 and "
+                "strides < 2^31 elements needed");
   char name[64];
   const AttnShape as = attention_shape(head_dim, chunk);
   snprintf(name, sizeof(name), "aoto_decode_rope_attention_d%d_w%dj%d", head_dim, as.waves, as.loads);
-  if (int st = launch(name, dim3(s, batch * query_heads), dim3(64 * as.waves), 0, stream, row, row_width,
-                      query_start,
-                      key_start, value_start, cos_table, sin_table, keys, values, (long long)kv_batch_stride,
-                      (long long)kv_head_stride, valid, ring_offset, position, slot, capacity, query_heads,
-                      kv_heads, scale, chunk, (float*)workspace, step_state, rope_rows, out))
+  const int heads = query_heads | (kv_heads << 16), starts_qk = query_start | (key_start << 16);
+  const int start_v_width = value_start | (row_width << 16), chunk_cap = chunk | (capacity << 9);
+  if (int st = launch(name, dim3(s, batch * query_heads), dim3(64 * as.waves), 0, stream, row, rope_rows, keys,
+                      values, (int)kv_head_stride, (int)kv_batch_stride, heads, starts_qk, start_v_width, chunk_cap,
+                      valid, ring_offset, position, slot, scale, (float*)workspace, step_state, cos_table, sin_table,
+                      out))
     return st;
   return s > 1 ? launch_merge(batch * query_heads, s, head_dim, workspace, out, stream) : AOTO_OK;
 }
@@ -1237,9 +1245,12 @@ int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_o
   if (rope_rows && (!step_state || !cos_table || !sin_table || head_dim <= 0 || head_dim > 256))
     return fail(AOTO_ERR_ARGUMENT, "argmax_finish: RoPE rows need the step state, both tables and "
                 "0 < head_dim <= 256");
-  return launch("aoto_argmax_finish", dim3(1), dim3(256), 0, stream, keys, key_count, token_out, history,
-                history_len, step_state, capacity, embedding, (long long)embedding_rows, hidden, hidden_out, error,
-                cos_table, sin_table, head_dim, rope_rows);
+  // the kernel takes the capacity and head size packed (cap | head_dim << 22)
+  if (capacity >= (1 << 22)) return fail(AOTO_ERR_UNSUPPORTED, "argmax_finish: capacity must be below 2^22");
+  const int cap_hd = (capacity > 0 ? capacity : 0) | ((rope_rows ? head_dim : 0) << 22);
+  return launch("aoto_argmax_finish", dim3(1), dim3(256), 0, stream, keys, step_state, cos_table, sin_table, history,
+                history_len, key_count, cap_hd, rope_rows, token_out, embedding, (long long)embedding_rows, hidden,
+                hidden_out, error);
 }
 
 int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,

@@ -488,13 +488,16 @@ extern "C" __global__ __launch_bounds__(1024) void aoto_argmax(const uint16_t* _
 //   rope_rows (with step) the cos and sin rows of the advanced position
 //             (tables [cap, D]) - the next step's RoPE rows, so its attention
 //             kernels need not read the step state before loading them.
-// One block of 256 threads; hidden % 8 == 0.
+// One block of 256 threads; hidden % 8 == 0. The arguments of the loads that
+// start the kernel come first, within the 14 preloaded argument dwords
+// (cap_hd = cap | head_dim << 22; cap < 2^22, head_dim < 512).
 extern "C" __global__ __launch_bounds__(256) void aoto_argmax_finish(
-    const unsigned long long* __restrict__ keys, int count, long long* __restrict__ token_out,
-    long long* __restrict__ history, int* __restrict__ history_len, int* __restrict__ step, int cap,
+    const unsigned long long* __restrict__ keys, int* __restrict__ step, const uint16_t* __restrict__ cos_table,
+    const uint16_t* __restrict__ sin_table, long long* __restrict__ history, int* __restrict__ history_len,
+    int count, int cap_hd, uint16_t* __restrict__ rope_rows, long long* __restrict__ token_out,
     const uint16_t* __restrict__ embed, long long embed_rows, int hidden, uint16_t* __restrict__ hidden_out,
-    int* __restrict__ error, const uint16_t* __restrict__ cos_table, const uint16_t* __restrict__ sin_table,
-    int head_dim, uint16_t* __restrict__ rope_rows) {
+    int* __restrict__ error) {
+  const int cap = cap_hd & 0x3FFFFF, head_dim = (int)((unsigned)cap_hd >> 22);
   __shared__ unsigned long long s_best[4];
   constexpr int kUnroll = 16;  // keys per thread loaded at once (count <= 4096)
   // Everything that does not depend on the token is read up front, in parallel
@@ -573,6 +576,12 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
 }  // namespace aoto
 
 // aoto_decode_attention_d{D}_w{WAVES}j{J} and aoto_decode_rope_attention_d{D}_w{WAVES}j{J}.
+// The fused ring-step kernel takes the arguments its first loads need in the
+// 14 preloaded argument dwords: the row, the RoPE rows, the cache bases, the
+// strides (elements, < 2^31) and packed small integers - heads = query_heads |
+// kv_heads << 16, starts_qk = query_start | key_start << 16, start_v_width =
+// value_start | row_width << 16 (each < 2^16), chunk_cap = chunk | cap << 9
+// (chunk < 512, cap < 2^22); the launcher checks the ranges.
 #define AOTO_DECODE_ATTENTION_INSTANCE(D, WAVES, J)                                                       \
   extern "C" __global__ __launch_bounds__(64 * WAVES) void aoto_decode_attention_d##D##_w##WAVES##j##J(  \
       const uint16_t* q, uint16_t* kbase, uint16_t* vbase, long long kv_batch_stride,                    \
@@ -586,11 +595,15 @@ extern "C" __global__ void aoto_step_advance(int* __restrict__ state, int cap) {
   }                                                                                                      \
   extern "C" __global__ __launch_bounds__(64 * WAVES) void                                               \
       aoto_decode_rope_attention_d##D##_w##WAVES##j##J(                                                  \
-          const uint16_t* row, int row_width, int query_start, int key_start, int value_start,           \
-          const uint16_t* cos_table, const uint16_t* sin_table, uint16_t* kbase, uint16_t* vbase,        \
-          long long kv_batch_stride, long long kv_head_stride, int valid, int ring_offset, int position, \
-          int slot, int cap, int query_heads, int kv_heads, float scale, int chunk, float* partials,      \
-          const int* step, const uint16_t* rope_rows, uint16_t* out) {                                   \
+          const uint16_t* row, const uint16_t* rope_rows, uint16_t* kbase, uint16_t* vbase,              \
+          int kv_head_stride, int kv_batch_stride, int heads, int starts_qk, int start_v_width,          \
+          int chunk_cap, int valid, int ring_offset, int position, int slot, float scale,                \
+          float* partials, const int* step, const uint16_t* cos_table, const uint16_t* sin_table,        \
+          uint16_t* out) {                                                                               \
+    const int query_heads = heads & 0xFFFF, kv_heads = (int)((unsigned)heads >> 16);                     \
+    const int query_start = starts_qk & 0xFFFF, key_start = (int)((unsigned)starts_qk >> 16);            \
+    const int value_start = start_v_width & 0xFFFF, row_width = (int)((unsigned)start_v_width >> 16);    \
+    const int chunk = chunk_cap & 0x1FF, cap = (int)((unsigned)chunk_cap >> 9);                          \
     if (rope_rows != nullptr)                                                                            \
       aoto::decode_attention_body<D, WAVES, J, true, true>(                                              \
           nullptr, row, row_width, query_start, key_start, value_start, cos_table, sin_table, kbase,     \
