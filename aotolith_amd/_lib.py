@@ -104,6 +104,11 @@ SIGNATURES: dict[str, tuple] = {
     "aoto_hip_argmax_finish": (
         _p, _c_int, _p, _p, _p, _p, _c_int, _p, _i64, _c_int, _p, _p, _p, _p, _c_int, _p, _p,
     ),
+    "aoto_hip_w4_gemv_finish_max_keys": (),
+    "aoto_hip_w4_gemv_finish": (
+        _p, _c_int, _p, _i64, _p, _p, _p, _c_float, _p, _c_float, _c_float, _p, _c_int, _c_int, _c_int,
+        _p, _p, _p, _p, _c_int, _p, _p, _c_int, _p, _p, _p, _p,
+    ),
     "aoto_hip_generic_elementwise": (_c_int, _p, _p, _p, _p, ctypes.c_double, _p),
     "aoto_hip_generic_reduce": (_c_int, _p, _p, _p),
     "aoto_hip_generic_matmul": (_p, _p, _p, _p, _c_float, _c_float, _p),
@@ -117,7 +122,7 @@ SIGNATURES: dict[str, tuple] = {
 #: Entry points returning a size rather than a status.
 SIZE_RETURNING = {"aoto_hip_last_error", "aoto_hip_take_launches", "aoto_hip_decode_attention_workspace",
                   "aoto_hip_w4_gemm_workspace", "aoto_hip_w4_gemm_gate_up_workspace", "aoto_hip_w4_gemm_qkv_rope_workspace",
-                  "aoto_hip_w4_gemv_argmax_keys"}
+                  "aoto_hip_w4_gemv_argmax_keys", "aoto_hip_w4_gemv_finish_max_keys"}
 
 
 class HipBackendUnavailable(RuntimeError):

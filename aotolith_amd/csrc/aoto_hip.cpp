@@ -21,6 +21,7 @@
 #include "gemm_args.h"
 #include "generic_args.h"
 #include "internal.h"
+#include "gemv_finish_args.h"
 
 
 namespace {
@@ -1251,6 +1252,62 @@ int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_o
   return launch("aoto_argmax_finish", dim3(1), dim3(256), 0, stream, keys, step_state, cos_table, sin_table, history,
                 history_len, key_count, cap_hd, rope_rows, token_out, embedding, (long long)embedding_rows, hidden,
                 hidden_out, error);
+}
+
+size_t aoto_hip_w4_gemv_finish_max_keys(void) { return 2048; }
+
+int aoto_hip_w4_gemv_finish(const uint64_t* keys, int key_count, const void* embedding, int64_t embedding_rows,
+                            const int32_t* words, const void* scales, const void* norm_weight, float eps,
+                            const void* bias, float alpha, float beta, void* y, int K, int N, int group,
+                            int64_t* token_out, int64_t* history, int* history_len, int32_t* step_state,
+                            int capacity, const void* cos_table, const void* sin_table, int head_dim,
+                            void* rope_rows, void* hidden_out, int* error, void* stream) {
+  if (!keys || !embedding || !words || !scales || !norm_weight || !y || !token_out || !hidden_out)
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: null pointer");
+  if (key_count <= 0 || (size_t)key_count > aoto_hip_w4_gemv_finish_max_keys())
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: %d keys, the prologue takes 1 .. %zu", key_count,
+                aoto_hip_w4_gemv_finish_max_keys());
+  if (embedding_rows <= 0 || N <= 0 || K <= 0)
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: empty shape K=%d N=%d rows=%lld", K, N, (long long)embedding_rows);
+  if ((history == nullptr) != (history_len == nullptr))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: a token history needs both pointers");
+  if (step_state && (capacity <= 0 || capacity >= (1 << 22)))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: step state needs a capacity in (0, 2^22)");
+  if (rope_rows && (!step_state || !cos_table || !sin_table || head_dim <= 0 || head_dim > 256))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: RoPE rows need the step state, both tables and "
+                "0 < head_dim <= 256");
+  StreamShape ss{};
+  const bool pow2_group = group > 0 && (group & (group - 1)) == 0;
+  if (!pow2_group || group < 32 || K % group != 0 || (K / group) % 2 != 0 || !stream_shape(K, N, false, &ss) ||
+      !ss.block_x || ss.lpr != 32 || (ss.cpl != 1 && ss.cpl != 4) || ss.rows != 0)
+    return fail(AOTO_ERR_UNSUPPORTED, "w4_gemv_finish: the finish prologue is built for the block-staged "
+                "q/k/v GEMV shapes (K = 896 or 4096, N <= 16384, power-of-two groups; K=%d N=%d group=%d)",
+                K, N, group);
+  if (!aligned16(embedding) || !aligned16(words) || !aligned16(norm_weight) || !aligned16(hidden_out) ||
+      !aligned4(scales) || !aligned8(keys) || (bias && (N % 2 != 0 || !aligned4(bias))))
+    return fail(AOTO_ERR_ARGUMENT, "w4_gemv_finish: embedding, words, norm weight and hidden_out must be 16-byte "
+                "aligned, scales and bias 4-byte (N even with a bias), keys 8-byte");
+  const StreamLaunch l = stream_launch(ss, K, N, group);
+  if (l.shift > 15 || l.wpb > 255) return fail(AOTO_ERR_UNSUPPORTED, "w4_gemv_finish: launch shape out of range");
+  aoto::GemvFinishArgs fin{};
+  fin.token_out = reinterpret_cast<long long*>(token_out);
+  fin.history = reinterpret_cast<long long*>(history);
+  fin.history_len = history_len;
+  fin.step = step_state;
+  fin.cos_table = static_cast<const uint16_t*>(cos_table);
+  fin.sin_table = static_cast<const uint16_t*>(sin_table);
+  fin.rope_rows = static_cast<uint16_t*>(rope_rows);
+  fin.hidden_out = static_cast<uint16_t*>(hidden_out);
+  fin.error = error;
+  fin.embed_rows = (long long)embedding_rows;
+  fin.count = key_count;
+  fin.cap = step_state ? capacity : 0;
+  fin.head_dim = rope_rows ? head_dim : 0;
+  const int shape = l.shift | (l.wpb << 4) | (key_count << 12);
+  char name[64];
+  snprintf(name, sizeof(name), "aoto_w4_gemv_x%dx%d_n1_b%d_finish", ss.lpr, ss.cpl, bias ? 1 : 0);
+  return launch(name, dim3((unsigned)l.grid), dim3(64 * l.wpb), l.shared, stream, keys, words, scales, embedding, K,
+                N, shape, bias, norm_weight, eps, alpha, beta, y, fin);
 }
 
 int aoto_hip_argmax(const void* logits, int rows, int n, int64_t row_stride, int64_t* out, int64_t* history,

@@ -47,6 +47,12 @@ AOTO_GEMV_STREAM_BLOCKX_SINGLE(32, 4, 2)
 AOTO_GEMV_STREAM_BLOCKX_PAIRED(32, 4, 2)
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 3, 3)
 AOTO_GEMV_STREAM_BLOCKX_SINGLE(64, 7, 7)
+// The greedy loop's first q/k/v GEMV of a step with the previous step's argmax
+// finish in its prologue (K = 896: 32x1, K = 4096: 32x4; with and without bias).
+AOTO_GEMV_STREAM_FINISH_KERNEL(32, 1, 1, 1, 1)
+AOTO_GEMV_STREAM_FINISH_KERNEL(32, 1, 1, 1, 0)
+AOTO_GEMV_STREAM_FINISH_KERNEL(32, 4, 2, 1, 1)
+AOTO_GEMV_STREAM_FINISH_KERNEL(32, 4, 2, 1, 0)
 // LM heads with the fused greedy-argmax keys: K = 896 (8x4), K = 4096 (32x4),
 // and direct 64-lane forms for any other K up to 2048 / 6144.
 AOTO_GEMV_STREAM_ARGMAX(8, 4, 2, false)

@@ -22,6 +22,7 @@
 
 #include "common.h"
 #include "w4_gemv.h"
+#include "gemv_finish_args.h"
 
 namespace aoto {
 
@@ -108,11 +109,22 @@ struct StagedActivation {
                                                      : (int)threadIdx.x + kGemvThreads * i; }
 
   AOTO_DEVICE void issue(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w, int K) {
+    issue_x(x, K);
+    issue_norm(norm_w, K);
+  }
+  // zero: stage a zero vector instead of x (x is still a valid address)
+  AOTO_DEVICE void issue_x(const uint16_t* __restrict__ x, int K, bool zero = false) {
     const int vecs = K >> 3;
     const uint4* xv = reinterpret_cast<const uint4*>(x);
-    const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
 #pragma unroll
-    for (int i = 0; i < XV; ++i) xr[i] = xv[min(index(i), vecs - 1)];
+    for (int i = 0; i < XV; ++i) {
+      const uint4 v = xv[min(index(i), vecs - 1)];
+      xr[i] = zero ? make_uint4(0u, 0u, 0u, 0u) : v;
+    }
+  }
+  AOTO_DEVICE void issue_norm(const uint16_t* __restrict__ norm_w, int K) {
+    const int vecs = K >> 3;
+    const uint4* wv = reinterpret_cast<const uint4*>(norm_w);
     if (NORM) {
 #pragma unroll
       for (int i = 0; i < XV; ++i) wr[i] = wv[min(index(i), vecs - 1)];
@@ -222,13 +234,18 @@ struct DirectActivation {
 // BLOCKX: x staged once per block (StagedActivation; XV >= K/2048) into
 // one LDS region the block's waves share; needs 4-wave blocks. With XREG the
 // lanes copy their chunks out of it after the block's staging barrier.
-template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX, bool BLOCKX = false>
+// FINISH (block-staged forms): x is the embedding table and `keys` the previous
+// LM head's argmax keys (GemvFinishArgs above).
+template <int LPR, int CPL, int XV, bool XREG, bool NORM, bool PAIRED, bool BIAS, bool ARGMAX, bool BLOCKX = false,
+          bool FINISH = false>
 __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4* __restrict__ words,
                                     const uint16_t* __restrict__ scales, const uint4* __restrict__ up_words,
                                     const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ norm_w,
                                     float eps, const uint16_t* __restrict__ bias, float alpha, float beta,
                                     uint16_t* __restrict__ y, int K, int N, int group_shift,
-                                    int waves_per_block, unsigned long long* __restrict__ keys) {
+                                    int waves_per_block, unsigned long long* __restrict__ keys,
+                                    const GemvFinishArgs& fin = GemvFinishArgs{}) {
+  static_assert(!FINISH || (BLOCKX && !ARGMAX), "the finish prologue is a block-staged GEMV's");
   extern __shared__ uint4 lds[];
   constexpr int RPW = 64 / LPR;  // rows per wave tile
   const int nchunks = K >> 5;
@@ -354,7 +371,93 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
   };
 
   int tile = blockIdx.x * waves_per_block + wave;
-  if constexpr (BLOCKX) {
+  if constexpr (BLOCKX && FINISH) {
+    // The first tile's loads, the norm weight and the keys (and block 0's step
+    // state, history length and, once the position is known, RoPE rows), then
+    // the token's embedding row as x.
+    StagedActivation<NORM, (XV > 0 ? XV : 1), false> act;
+    load(tile, ra);
+    // keys per thread (count <= 8 * 256, checked on the host); unconditional
+    // loads (index clamped), so they are all in flight at once
+    constexpr int kUnroll = 8;
+    unsigned long long kv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = threadIdx.x + kGemvThreads * u;
+      kv[u] = keys[min(i, fin.count - 1)];
+    }
+    // the tile's and the keys' loads need only preloaded arguments: keep them
+    // ahead of the wait for the others
+    __builtin_amdgcn_sched_barrier(0);
+    act.issue_norm(norm_w, K);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if ((int)threadIdx.x + kGemvThreads * u >= fin.count) kv[u] = 0ull;
+    const bool recorder = blockIdx.x == 0;
+    int st[4] = {0, 0, 0, 0};
+    if (recorder && fin.step != nullptr) {
+      st[0] = fin.step[0];
+      st[1] = fin.step[1];
+      st[2] = fin.step[2];
+      st[3] = fin.step[3];
+    }
+    const int at = recorder && fin.history != nullptr ? fin.history_len[0] : 0;
+    const int p = st[0] + 1;
+    const bool rows = recorder && fin.rope_rows != nullptr && fin.step != nullptr && p < fin.cap &&
+                      (int)threadIdx.x < fin.head_dim;
+    uint16_t cs = 0, sn = 0;
+    if (rows) {
+      cs = fin.cos_table[(size_t)p * fin.head_dim + threadIdx.x];
+      sn = fin.sin_table[(size_t)p * fin.head_dim + threadIdx.x];
+    }
+    unsigned long long best = 0;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) best = max_u64(best, kv[u]);
+    best = wave_max_u64(best);
+    __shared__ unsigned long long s_best[kGemvThreads / 64];
+    if (lane == 0) s_best[wave] = best;
+    __syncthreads();
+    best = max_u64(max_u64(s_best[0], s_best[1]), max_u64(s_best[2], s_best[3]));
+    const long long token = argmax_key_index(best);
+    const bool ok = token >= 0 && token < fin.embed_rows;
+    act.issue_x(x + (size_t)(ok ? token : 0) * K, K, !ok);
+    if (recorder) {
+      if (threadIdx.x == 0) {
+        fin.token_out[0] = token;
+        if (fin.history != nullptr) {
+          fin.history[at] = token;
+          fin.history_len[0] = at + 1;
+        }
+        if (fin.step != nullptr) {
+          fin.step[0] = st[0] + 1;
+          fin.step[1] = st[1] + 1;
+          fin.step[2] = st[2] + 1 == fin.cap ? 0 : st[2] + 1;
+          fin.step[3] = st[3] + 1 == fin.cap ? 0 : st[3] + 1;
+        }
+        if (!ok && fin.error != nullptr) fin.error[0] = 1;
+      }
+      if (rows) {
+        fin.rope_rows[threadIdx.x] = cs;
+        fin.rope_rows[fin.head_dim + threadIdx.x] = sn;
+      }
+      // the raw row is the step's residual
+      uint4* hid = reinterpret_cast<uint4*>(fin.hidden_out);
+#pragma unroll
+      for (int i = 0; i < (XV > 0 ? XV : 1); ++i) {
+        const int v = (int)threadIdx.x + kGemvThreads * i;
+        if (v < (K >> 3)) hid[v] = act.xr[i];
+      }
+    }
+    act.finish(eps, K, xp, csum);
+    if constexpr (XREG) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xr[j][k] = xp[cidx[j] * 4 + k];
+        cr[j] = csum[cidx[j]];
+      }
+    }
+  } else if constexpr (BLOCKX) {
     // every wave takes part in the block's staging barrier, tile or not
     StagedActivation<NORM, (XV > 0 ? XV : 1), false> act;
     act.issue(x, norm_w, K);
@@ -492,6 +595,23 @@ __device__ void w4_gemv_stream_body(const uint16_t* __restrict__ x, const uint4*
 #define AOTO_GEMV_STREAM_ARGMAX(LPR, CPL, XV, XREG)                                                      \
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n1_argmax, LPR, CPL, XV, XREG, 1, 0, 0, true)  \
   AOTO_GEMV_STREAM_KERNEL(aoto_w4_gemv_s##LPR##x##CPL##_n0_argmax, LPR, CPL, XV, XREG, 0, 0, 0, true)
+// Block-staged single projection with the greedy loop's argmax finish in its
+// prologue: aoto_w4_gemv_x{LPR}x{CPL}_n{NORM}_b{BIAS}_finish. What the first
+// tile's and the keys' loads need comes first, within the 14 preloaded argument
+// dwords: keys, weights, scales, embedding table, K, N, shape = group_shift |
+// waves_per_block << 4 | key count << 12, bias.
+#define AOTO_GEMV_STREAM_FINISH_KERNEL(LPR, CPL, XV, NORM, BIAS)                                          \
+  extern "C" __global__ __launch_bounds__(aoto::kGemvThreads) void                                       \
+      aoto_w4_gemv_x##LPR##x##CPL##_n##NORM##_b##BIAS##_finish(                                          \
+          unsigned long long* keys, const uint4* words, const uint16_t* scales, const uint16_t* embed,   \
+          int K, int N, int shape, const uint16_t* bias, const uint16_t* norm_w, float eps, float alpha,  \
+          float beta, uint16_t* y, aoto::GemvFinishArgs fin) {                                            \
+    aoto::GemvFinishArgs f = fin;                                                                        \
+    f.count = (int)((unsigned)shape >> 12);                                                              \
+    aoto::w4_gemv_stream_body<LPR, CPL, XV, true, NORM, false, BIAS, false, true, true>(                 \
+        embed, words, scales, nullptr, nullptr, norm_w, eps, bias, alpha, beta, y, K, N, shape & 0xF,    \
+        (shape >> 4) & 0xFF, keys, f);                                                                   \
+  }
 // Block-staged forms (x shared by the block's 4 waves) for long reductions:
 // names aoto_w4_gemv_x{LPR}x{CPL}_n*_p*_b*. XREG: each lane then copies its
 // chunks of x into registers (single projections; the paired form, with two

@@ -621,6 +621,16 @@ class _Engine:
         # cos/sin rows of the current decode position, kept by the finish kernel,
         # so attention does not wait for the step state before its table loads
         self.rope_rows = torch.zeros((2, s.head_dim), dtype=BF16, device=dev)
+        # The graph loop folds each step's finish into the next step's first
+        # q/k/v GEMV (ops.w4_gemv_finish: one launch fewer per token) where that
+        # GEMV's shape has the fused form; the last token's finish runs alone.
+        qkv0 = self.state.layers[0].qkv if self.state.layers else None
+        self.fold_finish = bool(
+            self.keys is not None and qkv0 is not None and qkv0.bits == 4
+            and tuple(self.state.embed.shape[1:]) == (s.hidden,)
+            and ops.gemv_finish_supported(s.hidden, qkv0.packed.shape[0], qkv0.group, self.key_count)
+            and os.environ.get("AOTOLITH_FOLD_FINISH", "1") != "0"
+        )
         # ring prefill inputs (captured prefill graphs read these) and the graphs,
         # one per left-pad width (the attention's key start), sharing one pool
         self.prefill_ids = torch.zeros((1, self.prompt_length), dtype=torch.int64, device=dev)
@@ -630,6 +640,7 @@ class _Engine:
         self.prefill_graph_error: str | None = None
         self._graph = None
         self._graphs: dict[int, object] = {}
+        self._first_graph = None
         self.graph_error: str | None = None
 
     #: longest run of decode steps captured in one graph (AOTOLITH_GRAPH_STEPS
@@ -647,18 +658,35 @@ class _Engine:
         matmul = ops.w4_matmul if w.bits == 4 else ops.w8_matmul
         return matmul(x, w.packed, w.scales, w.group, **kwargs)
 
-    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool, lm_head: bool = True, rec=None):
-        """Run the per-layer decode kernels (and the LM head); ``hidden`` holds the embedded token."""
+    def _decode_layers(self, cache_in, cache_out, *, valid=None, ring: bool, lm_head: bool = True, rec=None,
+                       finish: bool = False):
+        """Run the per-layer decode kernels (and the LM head); ``hidden`` holds the embedded token.
+
+        ``finish``: the previous step's argmax finish runs in layer 0's q/k/v GEMV
+        (``ops.w4_gemv_finish``), which embeds the token into ``hidden`` itself.
+        """
 
         s = self.spec
         qd, kd = s.heads * s.head_dim, s.kv_heads * s.head_dim
         bits = self.state.bits
         gemv = f"w{bits}_gemv"
         for index, layer in enumerate(self.state.layers):
-            _mark(rec, "addmm", f"qkv_{index}", gemv,
-                  f"packed W{bits} GEMV (M=1) with RMSNorm prologue" + (" and q/k/v bias epilogue" if s.qkv_bias else ""))
-            self._gemv(self.hidden, layer.qkv, self.qkv, norm_weight=layer.input_norm, eps=s.eps,
-                       bias=layer.qkv_bias)
+            if finish and index == 0:
+                _mark(rec, "addmm", f"qkv_{index}", gemv,
+                      "the previous step's argmax finish (token, history, step state, RoPE rows, embedding) in "
+                      "the prologue of the packed W4 GEMV (M=1) with RMSNorm prologue"
+                      + (" and q/k/v bias epilogue" if s.qkv_bias else ""))
+                ops.w4_gemv_finish(self.keys, self.key_count, self.state.embed, layer.qkv.packed, layer.qkv.scales,
+                                   layer.qkv.group, norm_weight=layer.input_norm, eps=s.eps, bias=layer.qkv_bias,
+                                   out=self.qkv, token_out=self.token, hidden_out=self.hidden,
+                                   history=self.history, history_len=self.history_len, step_state=self.step_state,
+                                   capacity=self.capacity, rope_tables=(self.cos, self.sin), rope_rows=self.rope_rows)
+            else:
+                _mark(rec, "addmm", f"qkv_{index}", gemv,
+                      f"packed W{bits} GEMV (M=1) with RMSNorm prologue"
+                      + (" and q/k/v bias epilogue" if s.qkv_bias else ""))
+                self._gemv(self.hidden, layer.qkv, self.qkv, norm_weight=layer.input_norm, eps=s.eps,
+                           bias=layer.qkv_bias)
             pair_out = cache_out[index]
             if ring:
                 _mark(rec, "attention", f"attention_{index}", "decode_attention",
@@ -735,6 +763,32 @@ class _Engine:
                           embedding=self.state.embed, hidden_out=self.hidden, rope_tables=(self.cos, self.sin),
                           rope_rows=self.rope_rows)
 
+    def _ring_step_folded(self, first: bool, rec=None) -> None:
+        """One step of the folded graph loop: [finish of the previous keys + layer-0 q/k/v, ..., LM-head keys].
+
+        ``first``: the loop's first step, whose token ``_enter_loop`` embedded, runs
+        the plain q/k/v GEMV. After the last step ``_finish_keys`` turns the keys
+        into the final token.
+        """
+
+        head = self.state.lm_head
+        self._decode_layers(None, self.ring, ring=True, lm_head=False, rec=rec, finish=not first)
+        _mark(rec, "matmul", "logits", "w4_gemv",
+              "LM-head W4 GEMV with final RMSNorm prologue, writing per-wave greedy-argmax keys")
+        ops.w4_gemv_argmax(self.hidden, head.packed, head.scales, head.group, self.keys,
+                           norm_weight=self.state.final_norm, eps=self.spec.eps, out=self.logits.view(-1))
+
+    def _finish_keys(self, rec=None) -> None:
+        """The standalone argmax finish of the last LM-head keys (the folded loop's last token)."""
+
+        _mark(rec, "argmax", "token", "argmax",
+              "reduces the last step's argmax keys to the token; appends it to the history, advances the step "
+              "state, copies the next position's RoPE rows and gathers the next token's embedding")
+        ops.argmax_finish(self.keys, self.key_count, out=self.token, history=self.history,
+                          history_len=self.history_len, step_state=self.step_state, capacity=self.capacity,
+                          embedding=self.state.embed, hidden_out=self.hidden, rope_tables=(self.cos, self.sin),
+                          rope_rows=self.rope_rows)
+
     def _enter_loop(self, position: int) -> None:
         """The loop's entry condition: the RoPE rows of ``position`` and (fused tail) ``token``'s embedding."""
 
@@ -756,29 +810,43 @@ class _Engine:
         self.history_len.zero_()
         self._enter_loop(0)
         self._ring_step()
+        if self.fold_finish:
+            self._ring_step_folded(first=True)
+            self._ring_step_folded(first=False)
+            self._finish_keys()
         torch.cuda.synchronize()
         try:
             # Graphs of 1, 2, 4, ... consecutive steps: a loop of n steps replays
             # the binary decomposition of n, so back-to-back graph launches
-            # (each with its own launch cost) are few.
+            # (each with its own launch cost) are few. With the folded finish the
+            # loop's first step has a graph of its own (plain q/k/v GEMV) and the
+            # others fold the previous step's finish into theirs.
             longest = int(os.environ.get("AOTOLITH_GRAPH_STEPS", self.MAX_GRAPH_STEPS))
             limit = min(max(1, longest), max(1, self.capacity - self.prompt_length - 1))
+            step = (lambda: self._ring_step_folded(first=False)) if self.fold_finish else self._ring_step
             graphs = {}
             size = 1
             while size <= limit:
                 graph = torch.cuda.CUDAGraph()
                 with _graph_capture(graph):
                     for _ in range(size):
-                        self._ring_step()
+                        step()
                 _lib.hold_graph(graph)
                 graphs[size] = graph
                 size *= 2
+            if self.fold_finish:
+                graph = torch.cuda.CUDAGraph()
+                with _graph_capture(graph):
+                    self._ring_step_folded(first=True)
+                _lib.hold_graph(graph)
+                self._first_graph = graph
             self._graphs = graphs
             self._graph = graphs[1]
         except Exception as error:  # noqa: BLE001 - fall back to eager replay, recorded
             self.graph_error = f"{type(error).__name__}: {error}"
             self._graph = None
             self._graphs = {}
+            self._first_graph = None
         torch.cuda.synchronize()
 
     def ring_loop(self, steps: int, start_valid: int, first_token: torch.Tensor, *, sync_each_step: bool,
@@ -793,9 +861,19 @@ class _Engine:
             torch.tensor([start_valid, start_valid + 1, 1 % self.capacity, 0], dtype=torch.int32)
         )
         self._enter_loop(start_valid)
+        graphs = use_graph and bool(self._graphs)
         remaining = steps
+        if self.fold_finish and remaining > 0:
+            # the loop's first step (its token embedded on entry), then the folded steps
+            if graphs and self._first_graph is not None:
+                self._first_graph.replay()
+            else:
+                self._ring_step_folded(first=True)
+            remaining -= 1
+            if sync_each_step:
+                torch.cuda.synchronize()
         while remaining > 0:
-            if use_graph and self._graphs:
+            if graphs:
                 size = 1
                 if not sync_each_step:
                     while size * 2 in self._graphs and size * 2 <= remaining:
@@ -803,8 +881,15 @@ class _Engine:
                 self._graphs[size].replay()
             else:
                 size = 1
-                self._ring_step()
+                if self.fold_finish:
+                    self._ring_step_folded(first=False)
+                else:
+                    self._ring_step()
             remaining -= size
+            if sync_each_step:
+                torch.cuda.synchronize()
+        if self.fold_finish and steps > 0:
+            self._finish_keys()  # the last step's token
             if sync_each_step:
                 torch.cuda.synchronize()
         return self.history
@@ -1000,8 +1085,17 @@ class _Engine:
                 _mark(rec, "embedding", "hidden_0", "gather",
                       "the first token's embedding row, gathered once when the loop starts (each step's finish "
                       "gathers the next one)")
-            self._enter_loop(0)
-            self._ring_step(rec=rec)
+            if self.fold_finish:
+                # the loop's first step runs the plain q/k/v GEMV (recorded below as
+                # layer 1's); a token's step is the folded one, the last token's
+                # finish runs alone
+                self._enter_loop(0)
+                self._ring_step_folded(first=True)
+                self._ring_step_folded(first=False, rec=rec)
+                self._finish_keys(rec=rec)
+            else:
+                self._enter_loop(0)
+                self._ring_step(rec=rec)
             out["decode_loop"] = rec.selections()
         torch.cuda.synchronize()
         return out

@@ -1018,6 +1018,101 @@ def argmax_finish(
     return out
 
 
+def gemv_finish_supported(k: int, n: int, group_size: int, key_count: int) -> bool:
+    """Whether ``w4_gemv_finish`` takes a ``[n, k]`` weight and ``key_count`` keys (a shape check, no launch)."""
+
+    if not 0 < key_count <= int(_lib.library().aoto_hip_w4_gemv_finish_max_keys()):
+        return False
+    if group_size < 32 or group_size & (group_size - 1) or k % group_size or (k // group_size) % 2:
+        return False
+    return (k == 896 and n <= 8192) or (k == 4096 and n <= 16384)
+
+
+def w4_gemv_finish(
+    keys: torch.Tensor,
+    count: int,
+    embedding: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int,
+    *,
+    norm_weight: torch.Tensor,
+    eps: float,
+    out: torch.Tensor,
+    token_out: torch.Tensor,
+    hidden_out: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    history: torch.Tensor | None = None,
+    history_len: torch.Tensor | None = None,
+    step_state: torch.Tensor | None = None,
+    capacity: int = 0,
+    error: torch.Tensor | None = None,
+    rope_tables: tuple[torch.Tensor, torch.Tensor] | None = None,
+    rope_rows: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``argmax_finish`` of ``count`` keys folded into the next step's first W4 GEMV.
+
+    The greedy token's ``embedding`` row is the GEMV's x (RMSNorm prologue with
+    ``norm_weight``, optional ``bias``): ``out`` [N] equals ``w4_gemv`` of that row.
+    The token, history, step state, RoPE rows and the raw row (into ``hidden_out``)
+    are recorded as ``argmax_finish`` records them.
+    """
+
+    _i64(keys, "keys")
+    _i64(token_out, "token_out")
+    _expect(packed, "packed", torch.int32)
+    if packed.dim() != 2:
+        raise ValueError("packed must be 2-D [N, K/8]")
+    n, words = packed.shape
+    k = words * 8
+    _expect(embedding, "embedding", BF16)
+    rows, hidden = embedding.shape
+    if hidden != k:
+        raise ValueError(f"embedding rows have {hidden} elements, the weight reduces over {k}")
+    if group_size <= 0 or k % group_size:
+        raise ValueError(f"group size {group_size} does not divide K={k}")
+    _expect(scales, "scales", BF16, (n, k // group_size))
+    _expect(norm_weight, "norm_weight", BF16)
+    if norm_weight.numel() != k:
+        raise ValueError(f"norm_weight has {norm_weight.numel()} elements, expected {k}")
+    if bias is not None:
+        _expect(bias, "bias", BF16)
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
+    _expect(out, "out", BF16)
+    if out.numel() != n:
+        raise ValueError(f"out has {out.numel()} elements, expected {n}")
+    _expect(hidden_out, "hidden_out", BF16)
+    if hidden_out.numel() != k:
+        raise ValueError("hidden_out must hold one embedding row")
+    if not 0 < count <= keys.numel():
+        raise ValueError(f"count {count} is outside (0, {keys.numel()}]")
+    if step_state is not None:
+        _expect(step_state, "step_state", torch.int32, (4,))
+    if error is not None:
+        _expect(error, "error", torch.int32)
+    cos_table = sin_table = None
+    head_dim = 0
+    if rope_rows is not None:
+        if rope_tables is None or step_state is None:
+            raise ValueError("rope_rows needs rope_tables and step_state")
+        cos_table, sin_table = rope_tables
+        head_dim = cos_table.shape[-1]
+        _expect(cos_table, "cos table", BF16, (int(capacity), head_dim))
+        _expect(sin_table, "sin table", BF16, (int(capacity), head_dim))
+        _expect(rope_rows, "rope_rows", BF16, (2, head_dim))
+    _ready(keys)
+    _lib.check(
+        _lib.library().aoto_hip_w4_gemv_finish(
+            _ptr(keys), int(count), _ptr(embedding), int(rows), _ptr(packed), _ptr(scales), _ptr(norm_weight),
+            float(eps), _ptr(bias), 1.0, 1.0, _ptr(out), k, n, int(group_size), _ptr(token_out), _ptr(history),
+            _ptr(history_len), _ptr(step_state), int(capacity), _ptr(cos_table), _ptr(sin_table), int(head_dim),
+            _ptr(rope_rows), _ptr(hidden_out), _ptr(error), _stream(),
+        )
+    )
+    return out
+
+
 def step_advance(step_state: torch.Tensor, capacity: int) -> None:
     """Advance the int32 device step state ``{position, valid, ring_offset, slot}`` by one token."""
 

@@ -301,7 +301,25 @@ def decode_kernel_table(runtime, torch, ops, valid: int | None = None, pool_byte
 
         ops.w4_gemv_argmax(eng.hidden, head.packed, head.scales, head.group, eng.keys,
                            norm_weight=eng.state.final_norm, eps=spec.eps, out=eng.logits.view(-1))
-        rows.append(_row("argmax_finish", "aoto_argmax_finish (token from the per-wave keys)",
+        if eng.fold_finish:
+            # the loop's per-token form: the finish in layer 0's q/k/v GEMV (the
+            # standalone finish runs once per generation, for the last token)
+            qkv_f = _rotation([layers[0].qkv], torch, pool_bytes)
+            hidden = torch.empty_like(eng.hidden)
+
+            def qkv_finish():
+                for w in qkv_f:
+                    ops.w4_gemv_finish(eng.keys, eng.key_count, eng.state.embed, w.packed, w.scales, w.group,
+                                       norm_weight=layers[0].input_norm, eps=spec.eps, bias=layers[0].qkv_bias,
+                                       out=eng.qkv, token_out=eng.token, hidden_out=hidden)
+
+            rows.append(_row("qkv_finish", f"aoto_{w}_gemv_*_finish (the previous token's argmax finish, then "
+                             "layer 0's q/k/v GEMV on its embedding row)", _graph_us(torch, qkv_finish, len(qkv_f)),
+                             nbytes=gemv_bytes(spec.qkv_width, h, norm=True, bias=spec.qkv_bias, bits=bits)))
+            rows[-1]["rotation"] = len(qkv_f)
+            del qkv_f
+        rows.append(_row("argmax_finish", "aoto_argmax_finish (token from the per-wave keys"
+                         + ("; once per generation with the folded loop)" if eng.fold_finish else ")"),
                          _graph_us(torch, finish, n)))
     torch.cuda.synchronize()
     return rows

@@ -35,7 +35,7 @@ extern "C" {
 #define AOTO_ERR_HIP 3            /* a HIP runtime call failed */
 #define AOTO_ERR_UNSUPPORTED 4    /* shape outside this kernel's limits: select another impl */
 
-#define AOTO_HIP_ABI_VERSION 18
+#define AOTO_HIP_ABI_VERSION 19
 
 /* ABI version of the loaded library (AOTO_HIP_ABI_VERSION at build time). */
 int aoto_hip_abi_version(void);
@@ -398,6 +398,28 @@ int aoto_hip_argmax_finish(const uint64_t* keys, int key_count, int64_t* token_o
                            int64_t embedding_rows, int hidden, void* hidden_out, int* error,
                            const void* cos_table, const void* sin_table, int head_dim, void* rope_rows,
                            void* stream);
+
+/* The greedy loop's argmax finish (aoto_hip_argmax_finish) folded into the
+ * prologue of the next step's first GEMV, the layer-0 q/k/v projection
+ * (models/decoder.py:1054-1087: the argmax, the next step's embedding take,
+ * runtime/bounds.py:104-107, and the packed q/k/v GEMV with its RMSNorm
+ * prologue and bias, codegen/matmul.py:542-739, codegen/norm.py:45-72). Every
+ * block reduces the keys an aoto_hip_w4_gemv_argmax launch wrote to the token
+ * and uses that token's embedding row as x; y = the GEMV aoto_hip_w4_gemv would
+ * write for x = that row. Block 0 also records the token as
+ * aoto_hip_argmax_finish does (token_out, history, step state, RoPE rows) and
+ * writes the raw embedding row to hidden_out (the step's residual stream; a
+ * token outside the table stages and writes zeros and sets *error = 1). For the
+ * block-staged q/k/v shapes (K = 896 or 4096, N <= 16384, norm weight
+ * required) and at most aoto_hip_w4_gemv_finish_max_keys() keys; other shapes
+ * return AOTO_ERR_UNSUPPORTED. */
+size_t aoto_hip_w4_gemv_finish_max_keys(void);
+int aoto_hip_w4_gemv_finish(const uint64_t* keys, int key_count, const void* embedding, int64_t embedding_rows,
+                            const int32_t* words, const void* scales, const void* norm_weight, float eps,
+                            const void* bias, float alpha, float beta, void* y, int K, int N, int group,
+                            int64_t* token_out, int64_t* history, int* history_len, int32_t* step_state,
+                            int capacity, const void* cos_table, const void* sin_table, int head_dim,
+                            void* rope_rows, void* hidden_out, int* error, void* stream);
 
 /* ---------------------------------------------------------------- generic graph kernels
  *

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.aoto_hip_abi_version() == 18
+    assert lib.aoto_hip_abi_version() == 19
 
 
 def test_no_code_object_without_a_gpu():

@@ -282,3 +282,84 @@ def test_gemv_argmax_refuses_unsupported_shapes():
         ops.w4_gemv_argmax(torch.zeros(96, dtype=torch.bfloat16, device="cuda"),
                            torch.zeros((64, 12), dtype=torch.int32, device="cuda"),
                            torch.zeros((64, 3), dtype=torch.bfloat16, device="cuda"), 32, keys)
+
+
+# (LM-head rows, K, q/k/v rows, bias): the Qwen2.5-0.5B and Llama-3-8B q/k/v shapes,
+# each after an LM head whose launch writes 2048 argmax keys
+FINISH_SHAPES = [(20000, 896, 1152, True), (8192, 4096, 6144, False)]
+
+
+@pytest.mark.parametrize("lm_n,k,n,bias", FINISH_SHAPES)
+def test_gemv_finish_matches_finish_then_gemv(lm_n, k, n, bias):
+    """The finish folded into the next q/k/v GEMV: the same token, history, step state, RoPE
+    rows and residual row as argmax_finish, and bit-identical GEMV output to w4_gemv on that
+    row; a token outside the embedding table stages zeros and sets the error flag."""
+
+    ops = _ops()
+    group = 64
+    count = ops.argmax_key_count(k, lm_n, group)
+    assert 0 < count <= 2048 and ops.gemv_finish_supported(k, n, group, count)
+    gen = torch.Generator(device="cuda").manual_seed(lm_n + k + n)
+    x = torch.randn(k, generator=gen, device="cuda").to(torch.bfloat16)
+    head = (torch.randn((lm_n, k), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    top = lm_n // 5
+    head[top] = (torch.sign(x.float()) * 0.05).to(torch.bfloat16)
+    hp, hs = ops.w4_quantize(head, group)
+    keys = torch.full((count,), -7, dtype=torch.int64, device="cuda")
+    ops.w4_gemv_argmax(x, hp, hs, group, keys, eps=1e-6)
+    embed = torch.randn((lm_n, k), generator=gen, device="cuda").to(torch.bfloat16)
+    qkv = (torch.randn((n, k), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    qp, qs = ops.w4_quantize(qkv, group)
+    normw = (1.0 + 0.1 * torch.randn(k, generator=gen, device="cuda")).to(torch.bfloat16)
+    qbias = (torch.randn(n, generator=gen, device="cuda") * 0.02).to(torch.bfloat16) if bias else None
+    cap, hd = 16, 64
+    cos_t = torch.randn((cap, hd), generator=gen, device="cuda").to(torch.bfloat16)
+    sin_t = torch.randn((cap, hd), generator=gen, device="cuda").to(torch.bfloat16)
+
+    def state():
+        return dict(token=torch.zeros((1,), dtype=torch.int64, device="cuda"),
+                    history=torch.zeros((8,), dtype=torch.int64, device="cuda"),
+                    history_len=torch.full((1,), 3, dtype=torch.int32, device="cuda"),
+                    step=torch.tensor([9, 10, cap - 1, 4], dtype=torch.int32, device="cuda"),
+                    rope=torch.zeros((2, hd), dtype=torch.bfloat16, device="cuda"),
+                    hidden=torch.full((k,), float("nan"), dtype=torch.bfloat16, device="cuda"),
+                    error=torch.zeros((1,), dtype=torch.int32, device="cuda"))
+
+    for table in (embed, embed[:top].contiguous()):
+        a, b = state(), state()
+        ops.argmax_finish(keys, count, out=a["token"], history=a["history"], history_len=a["history_len"],
+                          step_state=a["step"], capacity=cap, embedding=table, hidden_out=a["hidden"],
+                          error=a["error"], rope_tables=(cos_t, sin_t), rope_rows=a["rope"])
+        want = ops.w4_gemv(a["hidden"], qp, qs, group, norm_weight=normw, eps=1e-6, bias=qbias)
+        got = torch.full((n,), float("nan"), dtype=torch.bfloat16, device="cuda")
+        ops.w4_gemv_finish(keys, count, table, qp, qs, group, norm_weight=normw, eps=1e-6, bias=qbias, out=got,
+                           token_out=b["token"], hidden_out=b["hidden"], history=b["history"],
+                           history_len=b["history_len"], step_state=b["step"], capacity=cap, error=b["error"],
+                           rope_tables=(cos_t, sin_t), rope_rows=b["rope"])
+        torch.cuda.synchronize()
+        assert int(a["token"].item()) == top
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        for name in ("token", "history", "history_len", "step", "error"):
+            assert torch.equal(a[name], b[name]), name
+        for name in ("rope", "hidden"):
+            assert torch.equal(a[name].view(torch.int16), b[name].view(torch.int16)), name
+        assert b["step"].cpu().tolist() == [10, 11, 0, 5]
+        assert int(b["error"].item()) == (0 if table is embed else 1)
+
+
+def test_gemv_finish_refuses_other_shapes():
+    from aotolith_amd._lib import UnsupportedShape
+
+    ops = _ops()
+    assert not ops.gemv_finish_supported(1024, 1024, 64, 2048)   # not a block-staged q/k/v shape
+    assert not ops.gemv_finish_supported(896, 1152, 64, 4096)    # more keys than the prologue reads
+    keys = torch.zeros((2048,), dtype=torch.int64, device="cuda")
+    embed = torch.zeros((16, 896), dtype=torch.bfloat16, device="cuda")
+    packed = torch.zeros((20000, 112), dtype=torch.int32, device="cuda")  # a long output: the LM-head form
+    scales = torch.zeros((20000, 14), dtype=torch.bfloat16, device="cuda")
+    normw = torch.ones(896, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(UnsupportedShape):
+        ops.w4_gemv_finish(keys, 2048, embed, packed, scales, 64, norm_weight=normw, eps=1e-6,
+                           out=torch.empty(20000, dtype=torch.bfloat16, device="cuda"),
+                           token_out=torch.zeros((1,), dtype=torch.int64, device="cuda"),
+                           hidden_out=torch.empty(896, dtype=torch.bfloat16, device="cuda"))
