@@ -258,3 +258,36 @@ def test_runtime_rejects_bad_inputs():
         runtime.decode_token(torch.tensor([[1]]), cache, PROMPT + NEW)
     with pytest.raises(PlanInputError):
         runtime.greedy_generate(np.zeros(PROMPT, dtype=np.int64), max_new_tokens=NEW + 1)
+
+
+# hidden 896: the shapes whose q/k/v GEMV takes the argmax finish in its prologue
+NARROW = DecoderShape(vocab=4096, hidden=896, intermediate=1024, layers=2, heads=14, kv_heads=2, head_dim=64,
+                      eps=1e-6, theta=1e6)
+
+
+def test_folded_finish_loop_matches_the_unfolded_loop(monkeypatch):
+    """The graph loop with each step's finish folded into the next step's q/k/v GEMV gives the
+    same tokens and leaves the same loop state as the unfolded loop, graph-replayed or eager,
+    synchronized per step or not, for every generation length; and it tracks the oracle."""
+
+    runtime, oracle = _pair(NARROW, seed=21)
+    assert runtime.engine.fold_finish
+    monkeypatch.setenv("AOTOLITH_FOLD_FINISH", "0")
+    plain, _ = _pair(NARROW, seed=21)
+    assert not plain.engine.fold_finish
+    ids = np.random.default_rng(22).integers(0, NARROW.vocab, PROMPT)
+    want = plain.greedy_generate(ids).cpu().numpy()
+    state = plain.engine.step_state.cpu().tolist(), int(plain.engine.history_len.item())
+    for kwargs in ({}, {"use_graph": False}, {"sync_each_step": True}):
+        got = runtime.greedy_generate(ids, **kwargs).cpu().numpy()
+        np.testing.assert_array_equal(got, want, err_msg=str(kwargs))
+        assert (runtime.engine.step_state.cpu().tolist(), int(runtime.engine.history_len.item())) == state
+    for steps in (1, 2, 3, NEW - 1):
+        short = runtime.greedy_generate(ids, max_new_tokens=steps).cpu().numpy()
+        np.testing.assert_array_equal(short[0], want[0, :steps], err_msg=f"{steps} tokens")
+    assert runtime.engine.graph_error is None, runtime.engine.graph_error
+    reference, history = oracle.greedy_generate(ids, NEW, record_logits=True)
+    divergence = first_divergence(want, reference, history)
+    if divergence is not None:
+        scale = float(np.abs(history[divergence["step"]]).max())
+        assert _margin_ok(divergence, scale), divergence
