@@ -533,15 +533,38 @@ struct GemmPlan {
   int tn, tm, splits, kslice;
   // the wide-tile family (w4_gemm_wide.h): 32-row / 32-column tiles per wave, waves per block
   int wide_mt = 0, wide_nt = 0, wide_nw = 0;
-  int bm() const { return wide_mt ? 32 * wide_mt : 16 * tm; }
-  int bn() const { return wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
-  int threads() const { return wide_nw ? 64 * wide_nw : 256; }
+  // the dequant-once family (w4_gemm_lds.h): 8 waves, 256-row blocks of 128 (single)
+  // or 64 + 64 (paired) columns
+  bool lds = false, lds_paired = false;
+  int bm() const { return lds ? 256 : wide_mt ? 32 * wide_mt : 16 * tm; }
+  int bn() const { return lds ? (lds_paired ? 64 : 128) : wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
+  int threads() const { return lds ? 512 : wide_nw ? 64 * wide_nw : 256; }
 };
 
 // Wide-tile codes: 100 * (waves per block / 2) + 10 * (32-row tiles per wave) +
 // (32-column tiles per wave), the waves side by side along n (w4_gemm_wide.h).
 bool wide_code(int tile) {
   return tile == 241 || tile == 242 || tile == 243 || tile == 281 || tile == 441;
+}
+
+// Dequant-once codes (w4_gemm_lds.h, 4-bit codes, unsplit): 822 = 8 waves of 64 x 64
+// (256 x 128 blocks), 821 = the paired gate/up form (256 x (64 + 64) blocks).
+bool lds_code(int tile) { return tile == 821 || tile == 822; }
+
+// The automatic plan's choice of the dequant-once kernel: 4-bit codes, a power-of-two
+// group with an even count per row, no gate epilogue, and a grid whose last round of
+// 256 blocks (one per CU) is at least 90% full. Each packed tile is expanded once per
+// 256-row block instead of once per 128-row wave, which pays where the rounds are
+// full: measured on MI355X at 2048 rows (Llama-3-8B, same process, us): gate/up 484
+// against 513-528 for the paired 241, o 75 against 81 and down 232 against 241 for 441;
+// q/k/v (384 blocks, 1.5 rounds) stays on 243.
+bool lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate) {
+  if (bits != 4 || gate || M < 1024 || K % 64 != 0 || (group & (group - 1)) != 0 || group < 32 ||
+      (K / group) % 2 != 0)
+    return false;
+  const long long blocks = (long long)((N + (paired ? 63 : 127)) / (paired ? 64 : 128)) * ((M + 255) / 256);
+  const long long rounds = (blocks + 255) / 256;
+  return blocks >= 256 && blocks * 10 >= rounds * 256 * 9;
 }
 
 // The wide instances in the code object (their staging fits 160 KB of LDS).
@@ -592,6 +615,13 @@ void resolve_auto(int M, int N, int K, bool paired, int* tile, int* splits) {
 
 GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
+  if (lds_code(tile)) {
+    p.lds = true;
+    p.lds_paired = tile == 821;
+    p.splits = 1;
+    p.kslice = K;
+    return p;
+  }
   if (wide_code(tile)) {
     p.wide_nw = 2 * (tile / 100);
     p.wide_mt = (tile / 10) % 10;
@@ -654,7 +684,7 @@ namespace {
 // 128 rows (twice the blocks; each wave's dequant per step is the same: 7.5 against
 // 9.3 us on 64-row blocks for Qwen2-0.5B at 128 rows), else the auto split.
 void qkv_rope_plan(int M, int N, int K, int head_dim, int* tile, int* splits) {
-  if (*splits != 0 || head_dim <= 0 || wide_code(*tile)) return;
+  if (*splits != 0 || head_dim <= 0 || wide_code(*tile) || lds_code(*tile)) return;
   const int t = *tile == 0 && M <= 128 && 64 % head_dim == 0 ? 12 : *tile;
   const GemmPlan p = gemm_plan(M, N, K, t, 1, false);
   const int bn = 64 * p.tn;
@@ -729,9 +759,22 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       (gate && !aligned8(gate)) || !aligned16(words) || (paired && !aligned16(up_words)))
     return fail(AOTO_ERR_ARGUMENT, "%s: x and words must be 16-byte aligned, y/bias/residual/gate 8-byte aligned",
                 what);
-  if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile))
-    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441", what,
-                tile);
+  if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile) &&
+      !lds_code(tile))
+    return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441, "
+                "821, 822", what, tile);
+  if (lds_code(tile)) {
+    if (bits != 4 || (tile == 821) != paired || gate != nullptr || splits > 1)
+      return fail(AOTO_ERR_ARGUMENT, "%s: tile %d is the unsplit 4-bit %s form without a gate epilogue", what, tile,
+                  tile == 821 ? "paired" : "single");
+    if ((group & (group - 1)) != 0 || K % 64 != 0 || (K / group) % 2 != 0)
+      return fail(AOTO_ERR_UNSUPPORTED, "%s: tile %d needs K %% 64 == 0 and an even number of power-of-two groups "
+                  "per row (K=%d group=%d)", what, tile, K, group);
+    // the kernel's per-lane load offsets are 32-bit
+    if ((long long)M * K * 2 >= (1LL << 31) || (long long)N * K / 2 >= (1LL << 31))
+      return fail(AOTO_ERR_UNSUPPORTED, "%s: tile %d needs X and the packed words under 2 GiB (M=%d N=%d K=%d)", what,
+                  tile, M, N, K);
+  }
   if (wide_code(tile)) {
     if (!wide_instance(tile, bits, paired))
       return fail(AOTO_ERR_ARGUMENT, "%s: no wide tile %d instance for %d-bit%s codes", what, tile, bits,
@@ -740,6 +783,9 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       return fail(AOTO_ERR_UNSUPPORTED, "%s: wide tile %d needs K %% 128 == 0 and an even number of "
                   "power-of-two groups per row (K=%d group=%d)", what, tile, K, group);
   }
+  if (tile == 0 && splits == 0 && lds_auto(bits, M, N, K, group, paired, gate != nullptr) &&
+      (long long)M * K * 2 < (1LL << 31) && (long long)N * K / 2 < (1LL << 31))
+    tile = paired ? 821 : 822;
   resolve_auto(M, N, K, paired, &tile, &splits);
   if (bits == 8 && tile == 243) tile = 441;  // no 8-bit 243 instance; the same (unsplit) grid class
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
@@ -758,6 +804,23 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   float* partials = split ? static_cast<float*>(workspace) : nullptr;
   const long long quads = (long long)M * N / 4;
   char name[64];
+  if (p.lds) {
+    // dequant-once kernel: unsplit, its own epilogues; norm / RoPE launches follow as
+    // after any unsplit GEMM
+    int st;
+    if (paired) {
+      st = launch("aoto_w4_gemm_d8w2x1_paired", grid, dim3(p.threads()), 0, stream, x, words, scales, up_words,
+                  up_scales, y, M, N, K, group);
+    } else {
+      snprintf(name, sizeof(name), "aoto_w4_gemm_d8w2x2_b%d_r%d", bias != nullptr, residual != nullptr);
+      st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, bias, residual, y, M, N, K, group);
+    }
+    if (st || paired) return st;
+    if (norm_out != nullptr)
+      return launch("aoto_rms_norm", dim3((M + 3) / 4), dim3(256), 0, stream, y, norm_weight, eps, norm_out, M, N);
+    if (rope != nullptr) return rope_after_gemm(y, M, *rope, stream);
+    return AOTO_OK;
+  }
   if (paired) {
     snprintf(name, sizeof(name), "aoto_w%d_gemm_%s_paired", bits, family);
     if (int st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, up_words, up_scales, y, M, N, K, group,

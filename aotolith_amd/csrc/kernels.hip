@@ -7,6 +7,7 @@
 #include "w4_gemv_rows.h"
 #include "w4_gemm.h"
 #include "w4_gemm_wide.h"
+#include "w4_gemm_lds.h"
 #include "w8.h"
 #include "generic.h"
 #include "decode.h"
@@ -99,6 +100,13 @@ AOTO_GEMM_WIDE_EPILOGUES(8, 4, 2, 4)
 AOTO_GEMM_WIDE_EPILOGUES(8, 4, 1, 8)
 AOTO_GEMM_WIDE_PAIRED_INSTANCE(4, 4, 1, 4)
 AOTO_GEMM_WIDE_PAIRED_INSTANCE(8, 4, 1, 4)
+// Long prefills whose grids fill whole rounds of 256 blocks: each packed tile
+// expanded once per 256-row block into LDS (w4_gemm_lds.h), 8 waves of 64 x 64:
+// {waves} x {32-row tiles per wave} x {32-column tiles per wave} x {bias} x {residual}.
+AOTO_GEMM_LDS_INSTANCE(8, 2, 2, 0, 0)
+AOTO_GEMM_LDS_INSTANCE(8, 2, 2, 1, 0)
+AOTO_GEMM_LDS_INSTANCE(8, 2, 2, 0, 1)
+AOTO_GEMM_LDS_PAIRED_INSTANCE(8, 2, 1)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 1)

@@ -392,16 +392,21 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
     else:
         qkv_label = (f"aoto_w{bits}_gemm + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: RoPE "
                      "in the GEMM epilogue, or aoto_rope_qkv_rows after it)")
-    mlp_label = (f"{gemm} paired gate/up + silu_mul")
+    once = "aoto_w4_gemm_d8w* (packed tiles expanded once per 256-row block into LDS, 32x32x16 MFMA)"
+
+    def label(n_, k_, paired=False):
+        return once if ops.lds_plan(m, n_, k_, paired=paired, bits=bits) else gemm
+
+    mlp_label = f"{label(i, h, True)} paired gate/up + silu_mul"
     rows = [
         _row("qkv_rope", qkv_label, _graph_us(torch, qkv_rope, n), flops=2.0 * m * spec.qkv_width * h),
         _row("attention", f"aoto_flash_attention_d{spec.head_dim} (causal)", _graph_us(torch, attention, n),
              flops=4.0 * m * m * spec.head_dim * spec.heads / 2),
-        _row("o_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, o_norm, n),
-             flops=2.0 * m * h * spec.attention_width),
+        _row("o_norm", f"{label(h, spec.attention_width)} + residual, then the next RMSNorm",
+             _graph_us(torch, o_norm, n), flops=2.0 * m * h * spec.attention_width),
         _row("gate_up", mlp_label, _graph_us(torch, mlp, n),
              flops=2.0 * m * 2 * i * h),
-        _row("down_norm", f"{gemm} + residual, then the next RMSNorm", _graph_us(torch, down_norm, n),
+        _row("down_norm", f"{label(h, i)} + residual, then the next RMSNorm", _graph_us(torch, down_norm, n),
              flops=2.0 * m * h * i),
     ]
     torch.cuda.synchronize()
@@ -659,7 +664,10 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> 
     cases.append(("down", h, i, lambda: ops.w4_matmul(x_i, *down_w, 64, residual=res, out=out_h)))
     out = {}
     for name, n, k, run in cases:
-        run()  # allocates any split-K workspace outside the capture
+        with ops.recording_launches() as take:
+            take()
+            run()  # allocates any split-K workspace outside the capture
+            kernels = take()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -678,7 +686,7 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> 
         us = sorted(rounds)[1]
         tflops = 2.0 * tokens * n * k / (us * 1e-6) / 1e12
         out[name] = {"M": tokens, "N": n, "K": k, "us": round(us, 2), "tflops": round(tflops, 1),
-                     "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+                     "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "kernels": kernels}
     return out
 
 
