@@ -619,7 +619,7 @@ def measure_prefill_attention(spec, torch, ops, tokens: int, launches: int = 20,
             "tflops": round(flops / us / 1e6, 1), "frac": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
-def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> dict:
+def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10, library: bool = False) -> dict:
     """One decoder layer's prefill projections at ``tokens`` rows, timed alone.
 
     q/k/v (+bias when the model has it), o (+residual), gate/up (two GEMMs, or the
@@ -627,6 +627,10 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> 
     weights, each the median of 3 replays of a HIP graph of ``launches`` launches
     (no host overhead between them) between HIP events; TFLOP/s = 2 * tokens * N * K
     / duration (for counter runs: MFMA utilization against the bf16 peak).
+
+    ``library``: also time, as a comparison only (never a product path), the vendor
+    library's bf16 GEMM (``torch.matmul``, hipBLASLt) on the same weights unpacked to
+    bf16 ahead of time, and the unpack (``aoto_w4_dequantize``) of each weight.
     """
 
     from aotolith_amd.decoder import _prefill_pairs_gate_up
@@ -662,6 +666,17 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10) -> 
         cases.append(("gate", i, h, lambda: ops.w4_matmul(x_h, *gate_w, 64, out=gate)))
         cases.append(("up", i, h, lambda: ops.w4_matmul(x_h, *up_w, 64, gate=gate, out=out_i)))
     cases.append(("down", h, i, lambda: ops.w4_matmul(x_i, *down_w, 64, residual=res, out=out_h)))
+    if library:
+        dense = {}
+        for name, w in (("qkv", qkv_w), ("o", o_w), ("gate", gate_w), ("up", up_w), ("down", down_w)):
+            dense[name] = ops.w4_dequantize(*w, 64)
+        xs = {"qkv": x_h, "o": x_a, "gate": x_h, "up": x_h, "down": x_i}
+        for name in dense:
+            cases.append((f"library_{name}", dense[name].shape[0], dense[name].shape[1],
+                          lambda name=name: torch.matmul(xs[name], dense[name].t())))
+            w = {"qkv": qkv_w, "o": o_w, "gate": gate_w, "up": up_w, "down": down_w}[name]
+            cases.append((f"unpack_{name}", dense[name].shape[0], dense[name].shape[1],
+                          lambda w=w: ops.w4_dequantize(*w, 64)))
     out = {}
     for name, n, k, run in cases:
         with ops.recording_launches() as take:
@@ -721,6 +736,8 @@ def main() -> int:
                         help="standard deviation of the --prefill-attention-only inputs")
     parser.add_argument("--decode-kernels-only", action="store_true",
                         help="only the decode step's per-kernel table (after a 256 MiB calibration copy)")
+    parser.add_argument("--library-comparison", action="store_true",
+                        help="with --prefill-gemm-only: also time the vendor bf16 GEMM on unpacked weights")
     parser.add_argument("--prefill-gemm-only", type=int, default=0, metavar="TOKENS",
                         help="only one layer's prefill GEMMs at TOKENS rows (for MFMA counter runs)")
     args = parser.parse_args()
@@ -753,7 +770,7 @@ def main() -> int:
         return 0
     if args.prefill_gemm_only:
         spec = qwen_spec() if args.workload == "qwen0.5b" else llama8b_spec()
-        gemms = measure_prefill_gemms(spec, torch, ops, args.prefill_gemm_only)
+        gemms = measure_prefill_gemms(spec, torch, ops, args.prefill_gemm_only, library=args.library_comparison)
         print(json.dumps({"workload": f"{args.workload} prefill GEMMs", "tokens": args.prefill_gemm_only,
                           "peak_tflops": MFMA_BF16_PEAK_TFLOPS, **gemms}), flush=True)
         return 0
