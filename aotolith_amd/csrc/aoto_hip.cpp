@@ -562,6 +562,8 @@ bool lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate) 
   if (bits != 4 || gate || M < 1024 || K % 64 != 0 || (group & (group - 1)) != 0 || group < 32 ||
       (K / group) % 2 != 0)
     return false;
+  // the kernel's per-lane load offsets are 32-bit
+  if ((long long)M * K * 2 >= (1LL << 31) || (long long)N * K / 2 >= (1LL << 31)) return false;
   const long long blocks = (long long)((N + (paired ? 63 : 127)) / (paired ? 64 : 128)) * ((M + 255) / 256);
   const long long rounds = (blocks + 255) / 256;
   return blocks >= 256 && blocks * 10 >= rounds * 256 * 9;
@@ -671,7 +673,12 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
 
 // Automatic codes resolved to the explicit plan aoto_hip_w4_gemm would run (for
 // the allocation-free entry point, which sizes its split against its scratch).
-extern "C++" void aoto::resolve_gemm_codes(int M, int N, int K, int* tile, int* splits) {
+extern "C++" void aoto::resolve_gemm_codes(int M, int N, int K, int group, bool gate, int* tile, int* splits) {
+  if (*tile == 0 && *splits == 0 && lds_auto(4, M, N, K, group, false, gate)) {
+    *tile = 822;
+    *splits = 1;
+    return;
+  }
   resolve_auto(M, N, K, false, tile, splits);
 }
 
@@ -783,9 +790,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       return fail(AOTO_ERR_UNSUPPORTED, "%s: wide tile %d needs K %% 128 == 0 and an even number of "
                   "power-of-two groups per row (K=%d group=%d)", what, tile, K, group);
   }
-  if (tile == 0 && splits == 0 && lds_auto(bits, M, N, K, group, paired, gate != nullptr) &&
-      (long long)M * K * 2 < (1LL << 31) && (long long)N * K / 2 < (1LL << 31))
-    tile = paired ? 821 : 822;
+  if (tile == 0 && splits == 0 && lds_auto(bits, M, N, K, group, paired, gate != nullptr)) tile = paired ? 821 : 822;
   resolve_auto(M, N, K, paired, &tile, &splits);
   if (bits == 8 && tile == 243) tile = 441;  // no 8-bit 243 instance; the same (unsplit) grid class
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);

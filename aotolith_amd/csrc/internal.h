@@ -11,8 +11,9 @@ int set_error(int code, const char* fmt, ...);
 // object is installed on the device.
 void noalloc_prepare_device(int device);
 
-// Automatic (0) tile / split codes of the unpaired prefill GEMM resolved to the
-// explicit plan aoto_hip_w4_gemm runs (aoto_hip.cpp); other codes pass unchanged.
-void resolve_gemm_codes(int M, int N, int K, int* tile, int* splits);
+// Automatic (0) tile / split codes of the unpaired 4-bit prefill GEMM (group size,
+// gate epilogue or not) resolved to the explicit plan aoto_hip_w4_gemm runs
+// (aoto_hip.cpp); other codes pass unchanged.
+void resolve_gemm_codes(int M, int N, int K, int group, bool gate, int* tile, int* splits);
 
 }  // namespace aoto

@@ -70,7 +70,7 @@ extern "C" int aoto_hip_w4_gemm_noalloc(const void* x, const int32_t* words, con
   // (to one at least) until the partials fit the scratch; explicit codes are kept
   // and refused if they do not fit.
   const bool automatic = tile == 0 && splits == 0;
-  if (M > 0 && N > 0 && K > 0 && K % 64 == 0) aoto::resolve_gemm_codes(M, N, K, &tile, &splits);
+  if (M > 0 && N > 0 && K > 0 && K % 64 == 0) aoto::resolve_gemm_codes(M, N, K, group, gate != nullptr, &tile, &splits);
   size_t need = aoto_hip_w4_gemm_workspace(M, N, K, tile, splits);
   if (automatic && need > AOTO_HIP_NOALLOC_SCRATCH_BYTES) {
     if (splits == 0) splits = (int)(need / ((size_t)M * N * sizeof(float)));  // the 16x16 plan's own count

@@ -68,6 +68,34 @@ def test_noalloc_gemm_matches_the_workspace_entry_point_on_two_calls():
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"M={m} N={n} K={k}"
 
 
+def test_noalloc_gemm_takes_the_dequant_once_plan_where_the_workspace_entry_point_does():
+    """At 2048 rows an o-shaped GEMM (256 blocks of 256 x 128) runs on the dequant-once
+    kernel under automatic codes in both entry points - no split, so no scratch - and the
+    two outputs are bit-identical."""
+
+    from aotolith_amd import ops
+
+    m, n, k = 2048, 4096, 1024
+    assert ops.lds_plan(m, n, k) == ops.LDS_TILE
+    rng = np.random.default_rng(95)
+    packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
+    gp, gs = torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
+    x = to_gpu_bf16(bf16_normal(rng, (m, k)))
+    residual = to_gpu_bf16(bf16_normal(rng, (m, n)))
+    with ops.recording_launches() as take:
+        take()
+        want = ops.w4_matmul(x, gp, gs, 64, residual=residual)
+        got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
+        take()
+        status = _noalloc(x, gp, gs, 64, got, residual=residual)
+        names = take()
+    torch.cuda.synchronize()
+    assert status == 0, _last_error()
+    assert names == ["aoto_w4_gemm_d8w2x2_b0_r1"], names
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 def test_noalloc_gemm_refuses_explicit_plans_beyond_its_scratch():
     from aotolith_amd import ops
 
