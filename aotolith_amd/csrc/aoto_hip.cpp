@@ -533,11 +533,12 @@ struct GemmPlan {
   int tn, tm, splits, kslice;
   // the wide-tile family (w4_gemm_wide.h): 32-row / 32-column tiles per wave, waves per block
   int wide_mt = 0, wide_nt = 0, wide_nw = 0;
-  // the dequant-once family (w4_gemm_lds.h): 8 waves, 256-row blocks of 128 (single)
-  // or 64 + 64 (paired) columns
-  bool lds = false, lds_paired = false;
+  // the dequant-once family (w4_gemm_lds.h): 8 waves, 256-row blocks of 64 lds_nt
+  // columns (single: 128 or 192) or 64 + 64 (paired)
+  bool lds = false;
+  int lds_nt = 0;
   int bm() const { return lds ? 256 : wide_mt ? 32 * wide_mt : 16 * tm; }
-  int bn() const { return lds ? (lds_paired ? 64 : 128) : wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
+  int bn() const { return lds ? 64 * lds_nt : wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
   int threads() const { return lds ? 512 : wide_nw ? 64 * wide_nw : 256; }
 };
 
@@ -547,26 +548,32 @@ bool wide_code(int tile) {
   return tile == 241 || tile == 242 || tile == 243 || tile == 281 || tile == 441;
 }
 
-// Dequant-once codes (w4_gemm_lds.h, 4-bit codes, unsplit): 822 = 8 waves of 64 x 64
-// (256 x 128 blocks), 821 = the paired gate/up form (256 x (64 + 64) blocks).
-bool lds_code(int tile) { return tile == 821 || tile == 822; }
+// Dequant-once codes (w4_gemm_lds.h, 4-bit codes, unsplit): 822 / 823 = 8 waves of
+// 64 x 64 / 64 x 96 (256 x 128 / 256 x 192 blocks), 821 = the paired gate/up form
+// (256 x (64 + 64) blocks).
+bool lds_code(int tile) { return tile == 821 || tile == 822 || tile == 823; }
 
-// The automatic plan's choice of the dequant-once kernel: 4-bit codes, a power-of-two
-// group with an even count per row, no gate epilogue, and a grid whose last round of
-// 256 blocks (one per CU) is at least 90% full. Each packed tile is expanded once per
-// 256-row block instead of once per 128-row wave, which pays where the rounds are
-// full: measured on MI355X at 2048 rows (Llama-3-8B, same process, us): gate/up 484
-// against 513-528 for the paired 241, o 75 against 81 and down 232 against 241 for 441;
-// q/k/v (384 blocks, 1.5 rounds) stays on 243.
-bool lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate) {
+// The automatic plan's choice of the dequant-once kernel (its tile code, or 0):
+// 4-bit codes, a power-of-two group with an even count per row, no gate epilogue,
+// and a grid whose last round of 256 blocks (one per CU) is at least 90% full - 128
+// columns per block where that fills the rounds, else 192. Each packed tile is
+// expanded once per 256-row block instead of once per 128-row wave, which pays where
+// the rounds are full: measured on MI355X at 2048 rows (Llama-3-8B, same process,
+// us): gate/up 484 against 513-528 for the paired 241, o 75 against 81 and down 232
+// against 241 for 441.
+int lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate) {
   if (bits != 4 || gate || M < 1024 || K % 64 != 0 || (group & (group - 1)) != 0 || group < 32 ||
       (K / group) % 2 != 0)
-    return false;
+    return 0;
   // the kernel's per-lane load offsets are 32-bit
-  if ((long long)M * K * 2 >= (1LL << 31) || (long long)N * K / 2 >= (1LL << 31)) return false;
-  const long long blocks = (long long)((N + (paired ? 63 : 127)) / (paired ? 64 : 128)) * ((M + 255) / 256);
-  const long long rounds = (blocks + 255) / 256;
-  return blocks >= 256 && blocks * 10 >= rounds * 256 * 9;
+  if ((long long)M * K * 2 >= (1LL << 31) || (long long)N * K / 2 >= (1LL << 31)) return 0;
+  auto fills = [&](int bn) {
+    const long long blocks = (long long)((N + bn - 1) / bn) * ((M + 255) / 256);
+    const long long rounds = (blocks + 255) / 256;
+    return blocks >= 256 && blocks * 10 >= rounds * 256 * 9;
+  };
+  if (paired) return fills(64) ? 821 : 0;
+  return fills(128) ? 822 : fills(192) ? 823 : 0;
 }
 
 // The wide instances in the code object (their staging fits 160 KB of LDS).
@@ -619,7 +626,7 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
   if (lds_code(tile)) {
     p.lds = true;
-    p.lds_paired = tile == 821;
+    p.lds_nt = tile % 10;
     p.splits = 1;
     p.kslice = K;
     return p;
@@ -674,10 +681,12 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
 // Automatic codes resolved to the explicit plan aoto_hip_w4_gemm would run (for
 // the allocation-free entry point, which sizes its split against its scratch).
 extern "C++" void aoto::resolve_gemm_codes(int M, int N, int K, int group, bool gate, int* tile, int* splits) {
-  if (*tile == 0 && *splits == 0 && lds_auto(4, M, N, K, group, false, gate)) {
-    *tile = 822;
-    *splits = 1;
-    return;
+  if (*tile == 0 && *splits == 0) {
+    if (const int code = lds_auto(4, M, N, K, group, false, gate)) {
+      *tile = code;
+      *splits = 1;
+      return;
+    }
   }
   resolve_auto(M, N, K, false, tile, splits);
 }
@@ -769,7 +778,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile) &&
       !lds_code(tile))
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441, "
-                "821, 822", what, tile);
+                "821, 822, 823", what, tile);
   if (lds_code(tile)) {
     if (bits != 4 || (tile == 821) != paired || gate != nullptr || splits > 1)
       return fail(AOTO_ERR_ARGUMENT, "%s: tile %d is the unsplit 4-bit %s form without a gate epilogue", what, tile,
@@ -790,7 +799,9 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       return fail(AOTO_ERR_UNSUPPORTED, "%s: wide tile %d needs K %% 128 == 0 and an even number of "
                   "power-of-two groups per row (K=%d group=%d)", what, tile, K, group);
   }
-  if (tile == 0 && splits == 0 && lds_auto(bits, M, N, K, group, paired, gate != nullptr)) tile = paired ? 821 : 822;
+  if (tile == 0 && splits == 0) {
+    if (const int code = lds_auto(bits, M, N, K, group, paired, gate != nullptr)) tile = code;
+  }
   resolve_auto(M, N, K, paired, &tile, &splits);
   if (bits == 8 && tile == 243) tile = 441;  // no 8-bit 243 instance; the same (unsplit) grid class
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
@@ -817,7 +828,7 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
       st = launch("aoto_w4_gemm_d8w2x1_paired", grid, dim3(p.threads()), 0, stream, x, words, scales, up_words,
                   up_scales, y, M, N, K, group);
     } else {
-      snprintf(name, sizeof(name), "aoto_w4_gemm_d8w2x2_b%d_r%d", bias != nullptr, residual != nullptr);
+      snprintf(name, sizeof(name), "aoto_w4_gemm_d8w2x%d_b%d_r%d", p.lds_nt, bias != nullptr, residual != nullptr);
       st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, bias, residual, y, M, N, K, group);
     }
     if (st || paired) return st;

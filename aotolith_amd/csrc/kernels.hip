@@ -101,11 +101,14 @@ AOTO_GEMM_WIDE_EPILOGUES(8, 4, 1, 8)
 AOTO_GEMM_WIDE_PAIRED_INSTANCE(4, 4, 1, 4)
 AOTO_GEMM_WIDE_PAIRED_INSTANCE(8, 4, 1, 4)
 // Long prefills whose grids fill whole rounds of 256 blocks: each packed tile
-// expanded once per 256-row block into LDS (w4_gemm_lds.h), 8 waves of 64 x 64:
+// expanded once per 256-row block into LDS (w4_gemm_lds.h), 8 waves of 64 x 64 or 64 x 96:
 // {waves} x {32-row tiles per wave} x {32-column tiles per wave} x {bias} x {residual}.
 AOTO_GEMM_LDS_INSTANCE(8, 2, 2, 0, 0)
 AOTO_GEMM_LDS_INSTANCE(8, 2, 2, 1, 0)
 AOTO_GEMM_LDS_INSTANCE(8, 2, 2, 0, 1)
+AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 0, 0)
+AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 1, 0)
+AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 0, 1)
 AOTO_GEMM_LDS_PAIRED_INSTANCE(8, 2, 1)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)

@@ -11,7 +11,7 @@
 // keeps the expansion but feeds raw words to the products runs no faster than the
 // original: the cost is the VALU count, not the dependency). Here a block of 8
 // waves (two per SIMD) takes BM = 256 rows of X and 128 weight rows (128 columns,
-// or 64 gate + 64 up columns of the paired form). Each 64-k step of the block's
+// or 64 gate + 64 up columns of the paired form) or 192 (192 columns). Each 64-k step of the block's
 // packed words is expanded once, by all 512 lanes (two words each, 17 VALU per 8
 // codes, wide_dequant's exact bf16(code * s)), into a bf16 tile in LDS that the
 // four row-waves read as their A operands: each expanded word feeds the products
@@ -32,7 +32,9 @@
 // Rows of every staged tile are 128 bytes; 16-byte unit u of row r sits at slot
 // u ^ ((r >> 1) & 7), so each 16-lane phase of an operand read (16 consecutive
 // rows, one unit) and of the expansion's stores covers the 64 banks once.
-// LDS: 3 x 32 + 2 x 16 + 3 x 4.5 KB = 141.5 KB, one block per CU.
+// LDS at 128 weight rows: 3 x 32 + 2 x 16 + 3 x 4.5 KB = 141.5 KB; at 192 (the
+// q/k/v width of an 8B-class model: 6144 columns in 32 blocks) 2 x 32 + 2 x 24 +
+// 3 x 6.75 KB = 132.25 KB; one block per CU.
 #pragma once
 
 #include "common.h"
@@ -42,7 +44,6 @@
 namespace aoto {
 
 constexpr int kLdsBK = 64;     // k per step: four 16-k sub-steps
-constexpr int kLdsRows = 128;  // weight rows staged per block
 
 // Global -> LDS loads issued from inline assembly (lane l's 16 / 4 bytes land at
 // lds + 16 l / 4 l; lds is wave-uniform). The compiler then tracks none of them,
@@ -69,9 +70,11 @@ AOTO_DEVICE int lds_unit(int r, int u) { return r * 128 + ((u ^ ((r >> 1) & 7)) 
 
 // NW waves (8: two per SIMD, 4: one), NW / 2 along m and 2 along n; MT 32-row
 // tiles and NT 32-column tiles (per weight) per wave: BM = 256 rows (16 NW MT), 64 NT
-// columns per weight, NP weights (2 for the paired gate/up) - 128 weight rows in
-// all. Per sub-step a wave reads MT + NP NT operands for MT NP NT products: at 4
-// waves (MT = 4) 6 for 8, at 8 waves (MT = 2) 4 for 4.
+// columns per weight, NP weights (2 for the paired gate/up) - WR = 64 NP NT = 128 or
+// 192 weight rows. Per sub-step a wave reads MT + NP NT operands for MT NP NT
+// products: at 4 waves (MT = 4) 6 for 8, at 8 waves (MT = 2) 4 for 4, or 5 for 6 at
+// NT = 3. X takes three staging buffers where they fit 160 KB (WR = 128), else two
+// (WR = 192: each step's X is then loaded one step ahead).
 template <int NW, int MT, int NT, bool PAIRED, bool BIAS, bool RESIDUAL>
 __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t* __restrict__ words,
                                  const uint16_t* __restrict__ scales, const uint32_t* __restrict__ up_words,
@@ -83,20 +86,23 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   constexpr int WGM = NW / 2, WGN = 2;
   constexpr int BM = WGM * 32 * MT;
   constexpr int BNW = WGN * 32 * NT;  // columns per weight
-  static_assert(NP * BNW == kLdsRows, "128 weight rows per block");
+  constexpr int WR = NP * BNW;                       // weight rows per block
+  static_assert(WR == 128 || WR == 192, "128 or 192 weight rows per block");
   static_assert(BM == 256, "256 X rows per block");
   constexpr int XT = BM * 128;                       // bytes of a staged X tile
   constexpr int XDW = XT / 1024 / NW;                // 1-KB X loads per wave and step
-  constexpr int WT = kLdsRows * 128;                 // bytes of a bf16 weight tile
-  constexpr int PT = kLdsRows * 32;                  // bytes of a step's packed words
-  constexpr int PST = PT + kLdsRows * 4;             // ... and their scale dwords
-  constexpr int PW = kLdsRows / NW;                  // packed rows each wave loads: 16 or 32
-  constexpr int UPT = kLdsRows * 8 / (64 * NW);      // words each lane expands per step: 2 or 4
+  constexpr int WT = WR * 128;                       // bytes of a bf16 weight tile
+  constexpr int PT = WR * 32;                        // bytes of a step's packed words
+  constexpr int PST = PT + WR * 4;                   // ... and their scale dwords
+  constexpr int XS = 3 * XT + 2 * WT + 3 * PST <= 160 * 1024 ? 3 : 2;  // X staging buffers
+  constexpr int PW = WR / NW;                        // packed rows each wave loads: 16, 24 or 32
+  constexpr int UPT = WR * 8 / (64 * NW);            // words each lane expands per step: 2, 3 or 4
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  static_assert(2 * PW <= 64 && UPT <= 4, "one packed-word load per wave and step");
 
   __shared__ __attribute__((aligned(16))) uint8_t xs0[XT];
   __shared__ __attribute__((aligned(16))) uint8_t xs1[XT];
-  __shared__ __attribute__((aligned(16))) uint8_t xs2[XT];
+  __shared__ __attribute__((aligned(16))) uint8_t xs2[XS == 3 ? XT : 16];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[WT];
   __shared__ __attribute__((aligned(16))) uint8_t ws1[WT];
   __shared__ __attribute__((aligned(16))) uint8_t ps0[PST];  // words [128][32 B], then scales [128]
@@ -142,7 +148,7 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   const uint8_t* pbase = reinterpret_cast<const uint8_t*>(up_rows ? up_words : words);
   const uint8_t* sbase = reinterpret_cast<const uint8_t*>(up_rows ? up_scales : scales);
   const uint32_t poff = (uint32_t)(((size_t)pn * kw) * 4 + 16 * (lane & 1));
-  const int srow = PW * wave + (lane & (PW - 1));
+  const int srow = PW * wave + lane % PW;
   const uint32_t soff = (uint32_t)((size_t)min(n_block + srow % BNW, N - 1) * groups * 2);
 
   // Step st's loads (steps past the end re-read the last one).
@@ -214,13 +220,13 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   };
   constexpr int DPS = XDW + 2;  // a wave's loads per step
 
-  // Step s: issue step s + 2's X and step s + 3's words; expand step s + 1's words
-  // (read at the start, stored in sub-steps 2 and 3) while the products of step s
-  // run; wait for step s + 1's X and step s + 2's words, barrier, read sub-step 0's
-  // operands of step s + 1.
+  // Step s: issue step s + XS - 1's X and step s + 3's words; expand step s + 1's
+  // words (read at the start, stored over the sub-steps) while the products of
+  // step s run; wait for step s + 1's X and step s + 2's words, barrier, read
+  // sub-step 0's operands of step s + 1.
   auto step = [&](int s, const uint8_t* xc, const uint8_t* wc, uint8_t* wn_, const uint8_t* pd, uint8_t* xi,
                   uint8_t* pi, const uint8_t* xn) __attribute__((always_inline)) {
-    issue_x(s + 2, xi);
+    issue_x(s + XS - 1, xi);
     issue_p(s + 3, pi);
     expand_read(pd);
     // word v is expanded in sub-step ex(v) and stored in the next (the last in the last)
@@ -246,38 +252,40 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    AOTO_WAIT_VMCNT(DPS);  // step s + 1's X and step s + 2's words are in
+    // step s + 1's X and step s + 2's words are in (with two X buffers step s + 1's X
+    // went out at this step's start, ahead of its words)
+    AOTO_WAIT_VMCNT(XS == 3 ? DPS : 2);
     AOTO_WAIT_LGKMCNT(0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access moves across the barrier
     read_ops(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, wn_, xn);
   };
 
-  // Prologue: X 0 and 1, words 0, 1 and 2 in flight; step 0's words expanded;
-  // step 1's words in; sub-step 0's operands of step 0 read.
+  // Prologue: X 0 (and 1 with three buffers), words 0, 1 and 2 in flight; step 0's
+  // words expanded; step 1's words in; sub-step 0's operands of step 0 read.
   issue_x(0, xs0);
   issue_p(0, ps0);
-  issue_x(1, xs1);
+  if constexpr (XS == 3) issue_x(1, xs1);
   issue_p(1, ps1);
   issue_p(2, ps2);
-  AOTO_WAIT_VMCNT(DPS + 2);  // X 0 and words 0
+  AOTO_WAIT_VMCNT(XS == 3 ? DPS + 2 : 4);  // X 0 and words 0
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   expand_read(ps0);
 #pragma unroll
   for (int v = 0; v < UPT; ++v) *reinterpret_cast<bf16x8_v*>(ws0 + dwr[v]) = expand(v, 0);
-  AOTO_WAIT_VMCNT(2);  // X 1 and words 1
+  AOTO_WAIT_VMCNT(2);  // (X 1 and) words 1
   AOTO_WAIT_LGKMCNT(0);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_ops(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, ws0, xs0);
 
-  // Six steps per trip (X and words in 3 buffers, weight tiles in 2), then the
+  // Six steps per trip (X in XS buffers, words in 3, weight tiles in 2), then the
   // remaining steps % 6.
   auto step6 = [&](auto i_c, int s) __attribute__((always_inline)) {
     constexpr int i = decltype(i_c)::value;
     auto X3 = [&](auto b_c) __attribute__((always_inline)) -> uint8_t* {
-      constexpr int b = decltype(b_c)::value % 3;
+      constexpr int b = decltype(b_c)::value % XS;
       if constexpr (b == 0) return xs0; else if constexpr (b == 1) return xs1; else return xs2;
     };
     auto P3 = [&](auto b_c) __attribute__((always_inline)) -> uint8_t* {
@@ -289,8 +297,8 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
     };
     using I0 = std::integral_constant<int, i>;
     using I1 = std::integral_constant<int, i + 1>;
-    using I2 = std::integral_constant<int, i + 2>;
-    step(s, X3(I0{}), W2(I0{}), W2(I1{}), P3(I1{}), X3(I2{}), P3(I0{}), X3(I1{}));
+    using IX = std::integral_constant<int, i + XS - 1>;
+    step(s, X3(I0{}), W2(I0{}), W2(I1{}), P3(I1{}), X3(IX{}), P3(I0{}), X3(I1{}));
   };
   int s = 0;
   for (; s + 6 <= steps; s += 6) {

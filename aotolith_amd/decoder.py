@@ -987,7 +987,10 @@ class _Engine:
                 ops.rms_norm(x, layer.input_norm, s.eps, out=xn)
             pair = pair_of(index)
             _mark(rec, "addmm" if s.qkv_bias else "matmul", f"qkv_{index}", gemm,
-                  (f"wide-tile fused-dequant W{bits} GEMM on 32x32x16 bf16 MFMA"
+                  (f"dequant-once W{bits} GEMM (packed tiles expanded once per 256-row block into LDS) on "
+                   "32x32x16 bf16 MFMA"
+                   if ops.lds_plan(m, s.qkv_width, s.hidden, group_size=layer.qkv.group, bits=bits) is not None
+                   else f"wide-tile fused-dequant W{bits} GEMM on 32x32x16 bf16 MFMA"
                    if ops.wide_plan(m, s.qkv_width, s.hidden) is not None
                    else f"fused-dequant W{bits} GEMM on bf16 MFMA") + (" with q/k/v bias" if s.qkv_bias else "")
                   + ", RoPE of q/k and the layer's cache fill (with the split-K sum when the plan splits)")

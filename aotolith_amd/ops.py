@@ -387,8 +387,8 @@ def wide_plan(m: int, n: int, k: int, *, paired: bool = False) -> tuple[int, int
 
 
 #: Tile codes of the dequant-once long-prefill kernel (``csrc/w4_gemm_lds.h``): the
-#: single form (256 x 128 blocks) and the paired gate/up form (256 x (64 + 64)).
-LDS_TILE, LDS_PAIRED_TILE = 822, 821
+#: single forms (256 x 128 and 256 x 192 blocks) and the paired gate/up form (256 x (64 + 64)).
+LDS_TILE, LDS_WIDE_TILE, LDS_PAIRED_TILE = 822, 823, 821
 
 
 def lds_plan(m: int, n: int, k: int, *, group_size: int = 64, paired: bool = False, bits: int = 4,
@@ -396,17 +396,21 @@ def lds_plan(m: int, n: int, k: int, *, group_size: int = 64, paired: bool = Fal
     """The tile code the automatic plan runs on the dequant-once kernel for this shape, else
     None: the Python mirror of the C ABI's ``lds_auto`` (4-bit codes, no gate epilogue,
     from 1024 rows, K % 64 == 0, a power-of-two group with an even count per row, and a
-    grid of at least 256 blocks whose last round of 256 is at least 90% full)."""
+    grid of at least 256 blocks whose last round of 256 is at least 90% full: 128 columns
+    per block where that fills the rounds, else 192)."""
 
     if bits != 4 or gate or m < 1024 or k % 64 or group_size < 32 or group_size & (group_size - 1):
         return None
     if (k // group_size) % 2 or m * k * 2 >= 2 ** 31 or n * k // 2 >= 2 ** 31:
         return None
-    blocks = -(-n // (64 if paired else 128)) * -(-m // 256)
-    rounds = -(-blocks // 256)
-    if blocks >= 256 and blocks * 10 >= rounds * 256 * 9:
-        return LDS_PAIRED_TILE if paired else LDS_TILE
-    return None
+    def fills(bn):
+        blocks = -(-n // bn) * -(-m // 256)
+        rounds = -(-blocks // 256)
+        return blocks >= 256 and blocks * 10 >= rounds * 256 * 9
+
+    if paired:
+        return LDS_PAIRED_TILE if fills(64) else None
+    return LDS_TILE if fills(128) else LDS_WIDE_TILE if fills(192) else None
 
 
 def gemm_workspace_bytes(m: int, n: int, k: int, tile: int = 0, splits: int = 0) -> int:

@@ -385,7 +385,10 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
     bits = eng.state.bits
     plan = ops.wide_plan(m, spec.qkv_width, h)
     gemm = f"aoto_w{bits}_gemm_w* (wide tiles, 32x32x16 MFMA)" if ops.wide_plan(m, h, h) else f"aoto_w{bits}_gemm_n*"
-    if plan is not None:
+    if ops.lds_plan(m, spec.qkv_width, h, bits=bits) is not None:
+        qkv_label = ("aoto_w4_gemm_d8w* (packed tiles expanded once per 256-row block into LDS) + bias, then "
+                     "aoto_rope_qkv_rows (RoPE and cache fill)")
+    elif plan is not None:
         qkv_label = (f"aoto_w{bits}_gemm_w* tile {plan[0]} + bias, then aoto_rope_qkv_rows (RoPE and cache fill)"
                      if plan[1] == 1 else f"aoto_w{bits}_gemm_w* tile {plan[0]}, {plan[1]}-way split, then "
                      "aoto_w4_gemm_reduce_rope (sum, bias, RoPE and cache fill)")

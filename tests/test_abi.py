@@ -97,23 +97,25 @@ def test_wide_plan_matches_the_workspace_queries():
 def test_lds_plan_takes_the_full_rounds_at_long_prompts():
     """ops.lds_plan (the Python mirror of the C ABI's choice of the dequant-once kernel):
     at 2048 rows the Llama-3-8B o, down and paired gate/up projections (256 / 256 / 1792
-    blocks: whole rounds of 256) take it, q/k/v (384 blocks, 1.5 rounds) does not; nor do
-    1024-row o / down grids (128 blocks), 8-bit codes, gate epilogues, odd group counts;
-    its tiles need no split-K workspace - host logic only."""
+    blocks: whole rounds of 256) take it, and q/k/v on 192-column blocks (384 blocks of 128
+    columns would be 1.5 rounds, 256 of 192 are one); 1024-row o / down grids (128 blocks),
+    8-bit codes, gate epilogues and odd group counts do not; its tiles need no split-K
+    workspace - host logic only."""
 
     from aotolith_amd import ops
 
     assert ops.lds_plan(2048, 4096, 4096) == ops.LDS_TILE
     assert ops.lds_plan(2048, 4096, 14336) == ops.LDS_TILE
     assert ops.lds_plan(2048, 14336, 4096, paired=True) == ops.LDS_PAIRED_TILE
-    assert ops.lds_plan(2048, 6144, 4096) is None
+    assert ops.lds_plan(2048, 6144, 4096) == ops.LDS_WIDE_TILE
+    assert ops.lds_plan(2048, 5120, 4096) is None  # 20 x 8 = 160 blocks of 256 x 128 columns
     assert ops.lds_plan(1024, 4096, 4096) is None and ops.lds_plan(1024, 14336, 4096, paired=True) is None
     assert ops.lds_plan(4096, 4096, 4096) == ops.LDS_TILE
     assert ops.lds_plan(2048, 4096, 4096, bits=8) is None
     assert ops.lds_plan(2048, 4096, 4096, gate=True) is None
     assert ops.lds_plan(2048, 4096, 4096 - 64, group_size=64) is None  # 63 groups per row
     assert ops.lds_plan(2048, 4096, 4096, group_size=96) is None
-    for tile in (ops.LDS_TILE, ops.LDS_PAIRED_TILE):
+    for tile in (ops.LDS_TILE, ops.LDS_WIDE_TILE, ops.LDS_PAIRED_TILE):
         assert ops.gemm_workspace_bytes(2048, 4096, 4096, tile, 0) == 0
         assert ops.gate_up_workspace_bytes(2048, 4096, 4096, tile, 0) == 0
 

@@ -79,6 +79,30 @@ def test_lds_gemm_explicit(epilogue, group, k):
         assert_bf16_parity(from_gpu_bf16(y), from_gpu_bf16(wide), max_ulp=1.0, atol=_atol(expected))
 
 
+@pytest.mark.parametrize("group,k", [(32, 448), (64, 640), (128, 768), (32, 1216)])
+@pytest.mark.parametrize("epilogue", ["none", "bias", "residual"])
+def test_lds_gemm_192_columns_explicit(epilogue, group, k):
+    """Tile 823 (256 x 192 blocks, X in two staging buffers) on 300 rows and N = 720 (three
+    full 192-column blocks and a ragged one); K = 448 / 640 / 768 / 1216: 7 / 10 / 12 / 19
+    steps of 64."""
+
+    ops = _ops()
+    m, n = 300, 720
+    rng = np.random.default_rng(710 + group + k + len(epilogue))
+    packed, scales, gp, gs = _weights(rng, n, k, group)
+    x = bf16_normal(rng, (m, k))
+    kwargs = {}
+    if epilogue == "bias":
+        kwargs["bias"] = bf16_normal(rng, (n,), 0.5)
+    elif epilogue == "residual":
+        kwargs["residual"] = bf16_normal(rng, (m, n), 2.0)
+    gkw = {key: to_gpu_bf16(value) for key, value in kwargs.items()}
+    y, names = _traced(lambda: ops.w4_matmul(to_gpu_bf16(x), gp, gs, group, tile=823, **gkw))
+    assert names == [f"aoto_w4_gemm_d8w2x3_b{int(epilogue == 'bias')}_r{int(epilogue == 'residual')}"], names
+    expected = oracle.w4_matmul(x, packed, scales, group, **kwargs)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0, atol=_atol(expected))
+
+
 @pytest.mark.parametrize("group,k", [(64, 640), (32, 1088)])
 def test_lds_gate_up_explicit(group, k):
     """Tile 821: bf16(up * silu(bf16(gate))), N = 608 (nine full 64-column blocks and a
