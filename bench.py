@@ -680,6 +680,13 @@ def measure_prefill_gemms(spec, torch, ops, tokens: int, launches: int = 10, lib
             w = {"qkv": qkv_w, "o": o_w, "gate": gate_w, "up": up_w, "down": down_w}[name]
             cases.append((f"unpack_{name}", dense[name].shape[0], dense[name].shape[1],
                           lambda w=w: ops.w4_dequantize(*w, 64)))
+        # the epilogues the library GEMM leaves to elementwise kernels: the residual add
+        # (o, down) and silu_mul (gate/up); FLOP columns of these rows are not meaningful
+        lib_out = torch.empty(tokens, h, device=dev, dtype=torch.bfloat16)
+        cases.append(("library_residual_add", h, 1, lambda: torch.add(out_h, res, out=lib_out)))
+        lib_g = torch.empty(tokens, i, device=dev, dtype=torch.bfloat16)
+        cases.append(("library_silu_mul", i, 1,
+                      lambda: torch.mul(torch.nn.functional.silu(out_i), gate, out=lib_g)))
     out = {}
     for name, n, k, run in cases:
         with ops.recording_launches() as take:
