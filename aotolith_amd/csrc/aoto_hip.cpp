@@ -533,13 +533,13 @@ struct GemmPlan {
   int tn, tm, splits, kslice;
   // the wide-tile family (w4_gemm_wide.h): 32-row / 32-column tiles per wave, waves per block
   int wide_mt = 0, wide_nt = 0, wide_nw = 0;
-  // the dequant-once family (w4_gemm_lds.h): 8 waves, 256-row blocks of 64 lds_nt
-  // columns (single: 128 or 192) or 64 + 64 (paired)
+  // the dequant-once family (w4_gemm_lds.h): lds_waves waves, lds_bm-row blocks of
+  // lds_bn columns per weight
   bool lds = false;
-  int lds_nt = 0;
-  int bm() const { return lds ? 256 : wide_mt ? 32 * wide_mt : 16 * tm; }
-  int bn() const { return lds ? 64 * lds_nt : wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
-  int threads() const { return lds ? 512 : wide_nw ? 64 * wide_nw : 256; }
+  int lds_bm = 0, lds_bn = 0, lds_waves = 0;
+  int bm() const { return lds ? lds_bm : wide_mt ? 32 * wide_mt : 16 * tm; }
+  int bn() const { return lds ? lds_bn : wide_nt ? wide_nw * 32 * wide_nt : 64 * tn; }
+  int threads() const { return lds ? 64 * lds_waves : wide_nw ? 64 * wide_nw : 256; }
 };
 
 // Wide-tile codes: 100 * (waves per block / 2) + 10 * (32-row tiles per wave) +
@@ -550,8 +550,11 @@ bool wide_code(int tile) {
 
 // Dequant-once codes (w4_gemm_lds.h, 4-bit codes, unsplit): 822 / 823 = 8 waves of
 // 64 x 64 / 64 x 96 (256 x 128 / 256 x 192 blocks), 821 = the paired gate/up form
-// (256 x (64 + 64) blocks).
-bool lds_code(int tile) { return tile == 821 || tile == 822 || tile == 823; }
+// (256 x (64 + 64) blocks); for short prompts the paired form on 128-row blocks of
+// 4 waves, 812 = 64 x (32 + 32) per wave (128 x (64 + 64) blocks), 811 = 32 x (32 + 32)
+// per wave, one wave along n (128 x (32 + 32) blocks).
+bool lds_code(int tile) { return tile == 811 || tile == 812 || tile == 821 || tile == 822 || tile == 823; }
+bool lds_paired_code(int tile) { return tile == 811 || tile == 812 || tile == 821; }
 
 // The automatic plan's choice of the dequant-once kernel (its tile code, or 0):
 // 4-bit codes, a power-of-two group with an even count per row, no gate epilogue,
@@ -561,12 +564,26 @@ bool lds_code(int tile) { return tile == 821 || tile == 822 || tile == 823; }
 // the rounds are full: measured on MI355X at 2048 rows (Llama-3-8B, same process,
 // us): gate/up 484 against 513-528 for the paired 241, o 75 against 81 and down 232
 // against 241 for 441.
+//
+// Short prompts (32-256 rows), the paired gate/up only: 128-row blocks of 4 waves,
+// 64 + 64 columns (812) where that gives at least 128 blocks (from 65 rows), else
+// 32 + 32 (811) where that fits one round of 256 blocks. Every wave of the 16x16
+// kernel those replace expands its own columns' words; here the four row waves share
+// one expansion. Measured on MI355X (us, automatic plan -> dequant-once): K = 896 ->
+// 2 x 4864 at 32 / 64 / 128 / 256 rows 11.0 / 14.4 / 11.4 / 17.4 -> 9.6 / 9.6 / 9.6
+// (811) / 14.0 (812); K = 4096 -> 2 x 14336 at 128 / 256 rows 61.8 / 90.2 -> 47.8 /
+// 88.6 (812), at 64 rows 40.1 against 47.7 (kept on the 16x16 kernel).
 int lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate) {
-  if (bits != 4 || gate || M < 1024 || K % 64 != 0 || (group & (group - 1)) != 0 || group < 32 ||
-      (K / group) % 2 != 0)
+  if (bits != 4 || gate || K % 64 != 0 || (group & (group - 1)) != 0 || group < 32 || (K / group) % 2 != 0)
     return 0;
   // the kernel's per-lane load offsets are 32-bit
   if ((long long)M * K * 2 >= (1LL << 31) || (long long)N * K / 2 >= (1LL << 31)) return 0;
+  if (M < 1024) {
+    if (!paired || M < 32 || M > 256) return 0;
+    const long long mb = (M + 127) / 128;
+    if (M > 64 && (long long)((N + 63) / 64) * mb >= 128) return 812;
+    return (long long)((N + 31) / 32) * mb <= 256 ? 811 : 0;
+  }
   auto fills = [&](int bn) {
     const long long blocks = (long long)((N + bn - 1) / bn) * ((M + 255) / 256);
     const long long rounds = (blocks + 255) / 256;
@@ -626,7 +643,9 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
   GemmPlan p{};
   if (lds_code(tile)) {
     p.lds = true;
-    p.lds_nt = tile % 10;
+    p.lds_bm = tile / 10 == 82 ? 256 : 128;
+    p.lds_waves = tile / 10 == 82 ? 8 : 4;
+    p.lds_bn = tile == 811 ? 32 : tile == 823 ? 192 : tile == 822 ? 128 : 64;
     p.splits = 1;
     p.kslice = K;
     return p;
@@ -778,11 +797,11 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile) &&
       !lds_code(tile))
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441, "
-                "821, 822, 823", what, tile);
+                "811, 812, 821, 822, 823", what, tile);
   if (lds_code(tile)) {
-    if (bits != 4 || (tile == 821) != paired || gate != nullptr || splits > 1)
+    if (bits != 4 || lds_paired_code(tile) != paired || gate != nullptr || splits > 1)
       return fail(AOTO_ERR_ARGUMENT, "%s: tile %d is the unsplit 4-bit %s form without a gate epilogue", what, tile,
-                  tile == 821 ? "paired" : "single");
+                  lds_paired_code(tile) ? "paired" : "single");
     if ((group & (group - 1)) != 0 || K % 64 != 0 || (K / group) % 2 != 0)
       return fail(AOTO_ERR_UNSUPPORTED, "%s: tile %d needs K %% 64 == 0 and an even number of power-of-two groups "
                   "per row (K=%d group=%d)", what, tile, K, group);
@@ -825,10 +844,14 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
     // after any unsplit GEMM
     int st;
     if (paired) {
-      st = launch("aoto_w4_gemm_d8w2x1_paired", grid, dim3(p.threads()), 0, stream, x, words, scales, up_words,
-                  up_scales, y, M, N, K, group);
+      const char* kernel = p.lds_bm == 256 ? "aoto_w4_gemm_d8w2x1_paired"
+                           : p.lds_bn == 64 ? "aoto_w4_gemm_d4w2x1_paired"
+                                            : "aoto_w4_gemm_d4c1w1x1_paired";
+      st = launch(kernel, grid, dim3(p.threads()), 0, stream, x, words, scales, up_words, up_scales, y, M, N, K,
+                  group);
     } else {
-      snprintf(name, sizeof(name), "aoto_w4_gemm_d8w2x%d_b%d_r%d", p.lds_nt, bias != nullptr, residual != nullptr);
+      snprintf(name, sizeof(name), "aoto_w4_gemm_d8w2x%d_b%d_r%d", p.lds_bn / 64, bias != nullptr,
+               residual != nullptr);
       st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, bias, residual, y, M, N, K, group);
     }
     if (st || paired) return st;

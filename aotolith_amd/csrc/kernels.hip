@@ -110,6 +110,8 @@ AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 0, 0)
 AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 1, 0)
 AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 0, 1)
 AOTO_GEMM_LDS_PAIRED_INSTANCE(8, 2, 1)
+AOTO_GEMM_LDS_PAIRED_INSTANCE(4, 2, 1)
+AOTO_GEMM_LDS_PAIRED_COLUMN_INSTANCE(4, 1, 1)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 1)

@@ -68,14 +68,15 @@ AOTO_DEVICE void dma4_raw(const void* base, uint32_t off, const void* lds) {
 // Byte offset of 16-byte unit u of row r in a tile of 128-byte rows.
 AOTO_DEVICE int lds_unit(int r, int u) { return r * 128 + ((u ^ ((r >> 1) & 7)) << 4); }
 
-// NW waves (8: two per SIMD, 4: one), NW / 2 along m and 2 along n; MT 32-row
-// tiles and NT 32-column tiles (per weight) per wave: BM = 256 rows (16 NW MT), 64 NT
-// columns per weight, NP weights (2 for the paired gate/up) - WR = 64 NP NT = 128 or
-// 192 weight rows. Per sub-step a wave reads MT + NP NT operands for MT NP NT
-// products: at 4 waves (MT = 4) 6 for 8, at 8 waves (MT = 2) 4 for 4, or 5 for 6 at
-// NT = 3. X takes three staging buffers where they fit 160 KB (WR = 128), else two
-// (WR = 192: each step's X is then loaded one step ahead).
-template <int NW, int MT, int NT, bool PAIRED, bool BIAS, bool RESIDUAL>
+// NW waves (8: two per SIMD, 4: one), NW / WGN along m and WGN (1 or 2) along n;
+// MT 32-row tiles and NT 32-column tiles (per weight) per wave: BM = 32 MT NW / WGN
+// = 256 or 128 rows, 32 WGN NT columns per weight, NP weights (2 for the paired
+// gate/up) - WR = 32 NP WGN NT = 64, 128 or 192 weight rows. Per sub-step a wave
+// reads MT + NP NT operands for MT NP NT products: at 8 waves (MT = 2) 4 for 4, or 5
+// for 6 at NT = 3; the 128-row paired form (4 waves, WGN = 1, MT = NT = 1) 3 for 2.
+// X takes three staging buffers where they fit 160 KB, else two (WR = 192 at 256
+// rows: each step's X is then loaded one step ahead).
+template <int NW, int WGN, int MT, int NT, bool PAIRED, bool BIAS, bool RESIDUAL>
 __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t* __restrict__ words,
                                  const uint16_t* __restrict__ scales, const uint32_t* __restrict__ up_words,
                                  const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ bias,
@@ -83,12 +84,13 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
                                  int K, int group) {
   static_assert(!(PAIRED && (BIAS || RESIDUAL)), "the paired form has its own epilogue");
   constexpr int NP = PAIRED ? 2 : 1;
-  constexpr int WGM = NW / 2, WGN = 2;
+  static_assert(WGN == 1 || WGN == 2, "one or two waves along n");
+  constexpr int WGM = NW / WGN;
   constexpr int BM = WGM * 32 * MT;
   constexpr int BNW = WGN * 32 * NT;  // columns per weight
   constexpr int WR = NP * BNW;                       // weight rows per block
-  static_assert(WR == 128 || WR == 192, "128 or 192 weight rows per block");
-  static_assert(BM == 256, "256 X rows per block");
+  static_assert(WR == 64 || WR == 128 || WR == 192, "64, 128 or 192 weight rows per block");
+  static_assert(BM == 256 || BM == 128, "256 or 128 X rows per block");
   constexpr int XT = BM * 128;                       // bytes of a staged X tile
   constexpr int XDW = XT / 1024 / NW;                // 1-KB X loads per wave and step
   constexpr int WT = WR * 128;                       // bytes of a bf16 weight tile
@@ -97,6 +99,7 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   constexpr int XS = 3 * XT + 2 * WT + 3 * PST <= 160 * 1024 ? 3 : 2;  // X staging buffers
   constexpr int PW = WR / NW;                        // packed rows each wave loads: 16, 24 or 32
   constexpr int UPT = WR * 8 / (64 * NW);            // words each lane expands per step: 2, 3 or 4
+  static_assert(UPT >= 1 && WR % NW == 0, "every lane expands whole words");
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(2 * PW <= 64 && UPT <= 4, "one packed-word load per wave and step");
 
@@ -113,7 +116,7 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   const int lane = t & 63, wave = t >> 6;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int col = lane & 31, half = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int m_block = blockIdx.y * BM, n_block = blockIdx.x * BNW;
   const int kw = K >> 3;
   const int groups = K / group;
@@ -331,8 +334,9 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   // Epilogue: each 32 x 32 sub-tile through the wave's own 4.5-KB LDS slot (f32
   // rows 144 bytes apart), read back eight lanes per row: 64 contiguous bytes of
   // residual and output per row.
-  float* slot = reinterpret_cast<float*>((wave < 4 ? xs0 : xs1) + (wave & 3) * 4608);  // NW <= 8
-  static_assert(XT >= 4 * 4608, "four epilogue slots per X buffer");
+  constexpr int SLOTS = XT / 4608;  // epilogue slots per X buffer: 7 at 256 rows, 3 at 128
+  static_assert(NW <= 2 * SLOTS, "a slot per wave in the first two X buffers");
+  float* slot = reinterpret_cast<float*>((wave < SLOTS ? xs0 : xs1) + (wave % SLOTS) * 4608);
   const int m_wave = m_block + 32 * MT * wm;
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
@@ -385,19 +389,30 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
 
 }  // namespace aoto
 
-// aoto_w4_gemm_d{NW}w{MT}x{NT}_b{BIAS}_r{RES}: 256 x 128 blocks of NW waves.
+// aoto_w4_gemm_d{NW}w{MT}x{NT}_b{BIAS}_r{RES}: 256-row blocks of NW waves, two along n.
 #define AOTO_GEMM_LDS_INSTANCE(NW, MT, NT, BIAS, RES)                                                         \
   extern "C" __global__ __launch_bounds__(64 * NW, 1) void aoto_w4_gemm_d##NW##w##MT##x##NT##_b##BIAS##_r##RES( \
       const uint16_t* X, const uint32_t* words, const uint16_t* scales, const uint16_t* bias,                 \
       const uint16_t* residual, uint16_t* Y, int M, int N, int K, int group) {                                \
-    aoto::w4_gemm_lds_body<NW, MT, NT, false, BIAS, RES>(X, words, scales, nullptr, nullptr, bias, residual, Y,  \
-                                                         M, N, K, group);                                    \
+    aoto::w4_gemm_lds_body<NW, 2, MT, NT, false, BIAS, RES>(X, words, scales, nullptr, nullptr, bias, residual, \
+                                                            Y, M, N, K, group);                              \
   }
-// aoto_w4_gemm_d{NW}w{MT}x{NT}_paired: the MLP's gate/up pair, 256 x (64 + 64) blocks.
+// aoto_w4_gemm_d{NW}w{MT}x{NT}_paired: the MLP's gate/up pair, two waves along n
+// (256 x (64 + 64) blocks at NW = 8, MT = 2; 128 x (64 + 64) at NW = 4, MT = 2).
 #define AOTO_GEMM_LDS_PAIRED_INSTANCE(NW, MT, NT)                                                             \
   extern "C" __global__ __launch_bounds__(64 * NW, 1) void aoto_w4_gemm_d##NW##w##MT##x##NT##_paired(          \
       const uint16_t* X, const uint32_t* words, const uint16_t* scales, const uint32_t* up_words,             \
       const uint16_t* up_scales, uint16_t* Y, int M, int N, int K, int group) {                               \
-    aoto::w4_gemm_lds_body<NW, MT, NT, true, false, false>(X, words, scales, up_words, up_scales, nullptr,      \
-                                                           nullptr, Y, M, N, K, group);                      \
+    aoto::w4_gemm_lds_body<NW, 2, MT, NT, true, false, false>(X, words, scales, up_words, up_scales, nullptr,   \
+                                                              nullptr, Y, M, N, K, group);                   \
+  }
+// aoto_w4_gemm_d{NW}c1w{MT}x{NT}_paired: the same with one wave along n (at NW = 4,
+// MT = NT = 1: 128 x (32 + 32) blocks, twice the blocks of the 64-column form for
+// short prompts).
+#define AOTO_GEMM_LDS_PAIRED_COLUMN_INSTANCE(NW, MT, NT)                                                      \
+  extern "C" __global__ __launch_bounds__(64 * NW, 1) void aoto_w4_gemm_d##NW##c1w##MT##x##NT##_paired(       \
+      const uint16_t* X, const uint32_t* words, const uint16_t* scales, const uint32_t* up_words,             \
+      const uint16_t* up_scales, uint16_t* Y, int M, int N, int K, int group) {                               \
+    aoto::w4_gemm_lds_body<NW, 1, MT, NT, true, false, false>(X, words, scales, up_words, up_scales, nullptr,   \
+                                                              nullptr, Y, M, N, K, group);                   \
   }

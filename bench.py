@@ -395,10 +395,19 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
     else:
         qkv_label = (f"aoto_w{bits}_gemm + bias, RoPE and cache fill (split: aoto_w4_gemm_reduce_rope; unsplit: RoPE "
                      "in the GEMM epilogue, or aoto_rope_qkv_rows after it)")
-    once = "aoto_w4_gemm_d8w* (packed tiles expanded once per 256-row block into LDS, 32x32x16 MFMA)"
+    once = {
+        ops.LDS_SHORT_NARROW_TILE: "aoto_w4_gemm_d4c1w1x1_paired (packed tiles expanded once per 128 x (32 + 32) "
+                                   "block into LDS, 32x32x16 MFMA)",
+        ops.LDS_SHORT_PAIRED_TILE: "aoto_w4_gemm_d4w2x1_paired (packed tiles expanded once per 128 x (64 + 64) "
+                                   "block into LDS, 32x32x16 MFMA)",
+    }
 
     def label(n_, k_, paired=False):
-        return once if ops.lds_plan(m, n_, k_, paired=paired, bits=bits) else gemm
+        tile = ops.lds_plan(m, n_, k_, paired=paired, bits=bits)
+        if tile is None:
+            return gemm
+        return once.get(tile, "aoto_w4_gemm_d8w* (packed tiles expanded once per 256-row block into LDS, "
+                              "32x32x16 MFMA)")
 
     mlp_label = f"{label(i, h, True)} paired gate/up + silu_mul"
     rows = [

@@ -99,8 +99,9 @@ def test_lds_plan_takes_the_full_rounds_at_long_prompts():
     at 2048 rows the Llama-3-8B o, down and paired gate/up projections (256 / 256 / 1792
     blocks: whole rounds of 256) take it, and q/k/v on 192-column blocks (384 blocks of 128
     columns would be 1.5 rounds, 256 of 192 are one); 1024-row o / down grids (128 blocks),
-    8-bit codes, gate epilogues and odd group counts do not; its tiles need no split-K
-    workspace - host logic only."""
+    8-bit codes, gate epilogues and odd group counts do not; at 32-256 rows the paired
+    gate/up takes the 128-row forms (64 + 64 columns where that gives 128 blocks, else 32 +
+    32 within one round); its tiles need no split-K workspace - host logic only."""
 
     from aotolith_amd import ops
 
@@ -115,6 +116,14 @@ def test_lds_plan_takes_the_full_rounds_at_long_prompts():
     assert ops.lds_plan(2048, 4096, 4096, gate=True) is None
     assert ops.lds_plan(2048, 4096, 4096 - 64, group_size=64) is None  # 63 groups per row
     assert ops.lds_plan(2048, 4096, 4096, group_size=96) is None
+    # short prompts: the paired gate/up only, 128-row blocks
+    assert ops.lds_plan(128, 4864, 896, paired=True) == ops.LDS_SHORT_NARROW_TILE  # 152 blocks of 32 + 32
+    assert ops.lds_plan(64, 4864, 896, paired=True) == ops.LDS_SHORT_NARROW_TILE
+    assert ops.lds_plan(256, 4864, 896, paired=True) == ops.LDS_SHORT_PAIRED_TILE  # 2 x 76 blocks of 64 + 64
+    assert ops.lds_plan(128, 14336, 4096, paired=True) == ops.LDS_SHORT_PAIRED_TILE  # 224 blocks
+    assert ops.lds_plan(64, 14336, 4096, paired=True) is None  # 448 blocks of 32 + 32: more than a round
+    assert ops.lds_plan(16, 4864, 896, paired=True) is None and ops.lds_plan(300, 4864, 896, paired=True) is None
+    assert ops.lds_plan(128, 4864, 896) is None and ops.lds_plan(128, 4864, 896, paired=True, bits=8) is None
     for tile in (ops.LDS_TILE, ops.LDS_WIDE_TILE, ops.LDS_PAIRED_TILE):
         assert ops.gemm_workspace_bytes(2048, 4096, 4096, tile, 0) == 0
         assert ops.gate_up_workspace_bytes(2048, 4096, 4096, tile, 0) == 0

@@ -1,11 +1,13 @@
-"""GPU parity of the dequant-once long-prefill GEMM (csrc/w4_gemm_lds.h, tile codes 821 / 822).
+"""GPU parity of the dequant-once prefill GEMM (csrc/w4_gemm_lds.h, tile codes 811 / 812 /
+821 / 822 / 823).
 
 Each 64-k step of a block's packed words is expanded once into an LDS bf16 tile that the
-block's 8 waves read as MFMA operands. Every form is compared with the CPU oracle within one
-bf16 ulp (two for the silu_mul products) and with the wide-tile kernel under an explicit plan:
-ragged M and N tails, step counts that leave every remainder of the six-step unrolled loop,
-groups of 32 / 64 / 128, the bias and residual epilogues (in place too), the paired gate/up;
-the automatic plan's choice at 2048 rows; graph replays against eager; the refusals.
+block's waves (8 on 256-row blocks, 4 on the short prompts' 128-row paired blocks) read as
+MFMA operands. Every form is compared with the CPU oracle within one bf16 ulp (two for the
+silu_mul products) and with the wide-tile kernel under an explicit plan: ragged M and N
+tails, step counts that leave every remainder of the six-step unrolled loop, groups of 32 /
+64 / 128, the bias and residual epilogues (in place too), the paired gate/up; the automatic
+plan's choice at 2048 rows and at short prompts; graph replays against eager; the refusals.
 """
 
 from __future__ import annotations
@@ -47,7 +49,10 @@ def _traced(fn):
 
 
 def _lds(names):
-    return [name for name in names if name.startswith("aoto_w4_gemm_d8w")]
+    return [name for name in names if name.startswith(("aoto_w4_gemm_d8w", "aoto_w4_gemm_d4"))]
+
+
+SHORT_PAIRED = {811: "aoto_w4_gemm_d4c1w1x1_paired", 812: "aoto_w4_gemm_d4w2x1_paired"}
 
 
 @pytest.mark.parametrize("group,k", [(32, 448), (32, 896), (32, 576), (64, 640), (32, 704), (128, 768),
@@ -122,6 +127,59 @@ def test_lds_gate_up_explicit(group, k):
     assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0)
 
 
+@pytest.mark.parametrize("tile", [811, 812])
+@pytest.mark.parametrize("m,group,k", [(1, 64, 640), (16, 32, 448), (96, 64, 896), (128, 128, 768),
+                                       (200, 32, 704), (128, 64, 1152)])
+def test_lds_gate_up_short_prompt_tiles(tile, m, group, k):
+    """Tiles 811 / 812 (128-row blocks of 4 waves, 32 + 32 / 64 + 64 columns): ragged and
+    partial row blocks (1-200 rows), N = 608 (19 / 9.5 column blocks), K of 7 / 14 / 12 /
+    11 / 18 steps (every remainder of the six-step loop but 3, which 9 steps of the next
+    test cover), groups 32-128, within the bars of the oracle's two-step result; both
+    tiles give the same bits (one summation order)."""
+
+    ops = _ops()
+    n = 608
+    rng = np.random.default_rng(725 + m + group + k)
+    gpk, gsc, g_packed, g_scales = _weights(rng, n, k, group)
+    upk, usc, u_packed, u_scales = _weights(rng, n, k, group)
+    x = bf16_normal(rng, (m, k))
+    gx = to_gpu_bf16(x)
+    y, names = _traced(lambda: ops.w4_matmul_gate_up(gx, g_packed, g_scales, u_packed, u_scales, group, tile=tile))
+    assert names == [SHORT_PAIRED[tile]], names
+    want_gate = round_bf16(oracle.w4_matmul(x, gpk, gsc, group))
+    expected = oracle.w4_matmul(x, upk, usc, group, gate=want_gate)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0)
+    other = ops.w4_matmul_gate_up(gx, g_packed, g_scales, u_packed, u_scales, group, tile=1623 - tile)
+    assert torch.equal(y, other)
+
+
+def test_lds_gate_up_is_the_automatic_plan_at_short_prompts():
+    """The paired gate/up of a 0.5B-class MLP (896 -> 2 x 4864) at 128 rows takes tile 811
+    (152 blocks) by itself, an 8B-class one (4096 -> 2 x 14336) tile 812 (224 blocks), and
+    16 rows stay on the 16x16 kernel; K = 576 in groups of 32 (9 steps) covers the loop's
+    remainder 3."""
+
+    ops = _ops()
+    assert ops.lds_plan(128, 4864, 896, paired=True) == ops.LDS_SHORT_NARROW_TILE
+    assert ops.lds_plan(128, 14336, 4096, paired=True) == ops.LDS_SHORT_PAIRED_TILE
+    assert ops.lds_plan(16, 4864, 896, paired=True) is None
+    rng = np.random.default_rng(745)
+    for m, n, k, group, want in [(128, 4864, 576, 32, 811), (128, 14336, 4096, 64, 812)]:
+        gpk, gsc, g_packed, g_scales = _weights(rng, n, k, group)
+        upk, usc, u_packed, u_scales = _weights(rng, n, k, group)
+        x = bf16_normal(rng, (m, k))
+        y, names = _traced(lambda: ops.w4_matmul_gate_up(to_gpu_bf16(x), g_packed, g_scales, u_packed, u_scales,
+                                                         group))
+        assert names == [SHORT_PAIRED[want]], names
+        want_gate = round_bf16(oracle.w4_matmul(x, gpk, gsc, group))
+        expected = oracle.w4_matmul(x, upk, usc, group, gate=want_gate)
+        assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=2.0, atol=_atol(expected))
+    x = to_gpu_bf16(bf16_normal(rng, (16, 576)))
+    gpk, gsc, g_packed, g_scales = _weights(rng, 4864, 576)
+    _, names = _traced(lambda: ops.w4_matmul_gate_up(x, g_packed, g_scales, g_packed, g_scales, 64))
+    assert not _lds(names), names
+
+
 def test_lds_gemm_in_place_residual():
     ops = _ops()
     m, n, k = 512, 512, 1024
@@ -171,9 +229,9 @@ def test_lds_gemm_is_the_automatic_plan_at_2048_rows():
 
 
 def test_lds_gemms_replay_in_a_graph_like_eager():
-    """A captured bias, residual (in place) and paired sequence on tiles 822 / 821 replays
-    three times, with eager work and synchronizations between, bit-identical to its eager
-    pass each time."""
+    """A captured bias, residual (in place) and paired sequence on tiles 822 / 821 / 811
+    replays three times, with eager work and synchronizations between, bit-identical to its
+    eager pass each time."""
 
     ops = _ops()
     m, n, k = 512, 640, 768
@@ -185,13 +243,16 @@ def test_lds_gemms_replay_in_a_graph_like_eager():
     outs = {name: torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for name in ("bias", "paired")}
     residual = residual0.clone()
 
+    outs["short"] = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+
     def body():
         ops.w4_matmul(x, *weights[0], 64, bias=bias, out=outs["bias"], tile=822)
         ops.w4_matmul_gate_up(x, *weights[1], *weights[2], 64, out=outs["paired"], tile=821)
+        ops.w4_matmul_gate_up(x, *weights[1], *weights[2], 64, out=outs["short"], tile=811)
         ops.w4_matmul(x, *weights[0], 64, residual=residual, out=residual, tile=822)
 
     _, names = _traced(body)
-    assert len(_lds(names)) == 3, names
+    assert len(_lds(names)) == 4, names
     torch.cuda.synchronize()
     eager = {name: t.clone() for name, t in outs.items()}
     eager["residual"] = residual.clone()
@@ -229,6 +290,12 @@ def test_lds_tiles_refuse_what_they_cannot_run():
         ops.w4_matmul(x, gp, gs, 64, tile=822, gate=to_gpu_bf16(bf16_normal(rng, (64, 256))))
     with pytest.raises(HipKernelError, match="tile 821"):
         ops.w4_matmul(x, gp, gs, 64, tile=821)
+    with pytest.raises(HipKernelError, match="tile 811"):
+        ops.w4_matmul(x, gp, gs, 64, tile=811)
+    with pytest.raises(HipKernelError, match="tile 812"):
+        ops.w4_matmul_gate_up(x, gp, gs, gp, gs, 64, tile=812, splits=2)
+    with pytest.raises(HipKernelError, match="tile 822"):
+        ops.w4_matmul_gate_up(x, gp, gs, gp, gs, 64, tile=822)
     with pytest.raises(HipKernelError, match="tile 822"):
         ops.w4_matmul(x, gp, gs, 64, tile=822, splits=2)
     packed8, scales8 = pack_weight_bits_bf16(bf16_normal(rng, (256, 512), 0.02), 64, 8)
