@@ -553,8 +553,14 @@ bool wide_code(int tile) {
 // (256 x (64 + 64) blocks); for short prompts the paired form on 128-row blocks of
 // 4 waves, 812 = 64 x (32 + 32) per wave (128 x (64 + 64) blocks), 811 = 32 x (32 + 32)
 // per wave, one wave along n (128 x (32 + 32) blocks).
-bool lds_code(int tile) { return tile == 811 || tile == 812 || tile == 821 || tile == 822 || tile == 823; }
+// 813 / 814 = the single form's split-K partials on 128-row blocks of 4 waves, 128 x 32
+// (one wave along n, 32 x 32 per wave) / 128 x 64 (64 x 32 per wave) blocks, summed and
+// given their epilogue by the split reduce kernels (at any split count, 1 included).
+bool lds_code(int tile) {
+  return tile == 811 || tile == 812 || tile == 813 || tile == 814 || tile == 821 || tile == 822 || tile == 823;
+}
 bool lds_paired_code(int tile) { return tile == 811 || tile == 812 || tile == 821; }
+bool lds_split_code(int tile) { return tile == 813 || tile == 814; }
 
 // The automatic plan's choice of the dequant-once kernel (its tile code, or 0):
 // 4-bit codes, a power-of-two group with an even count per row, no gate epilogue,
@@ -573,13 +579,28 @@ bool lds_paired_code(int tile) { return tile == 811 || tile == 812 || tile == 82
 // 2 x 4864 at 32 / 64 / 128 / 256 rows 11.0 / 14.4 / 11.4 / 17.4 -> 9.6 / 9.6 / 9.6
 // (811) / 14.0 (812); K = 4096 -> 2 x 14336 at 128 / 256 rows 61.8 / 90.2 -> 47.8 /
 // 88.6 (812), at 64 rows 40.1 against 47.7 (kept on the 16x16 kernel).
-int lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate) {
+//
+// Short prompts, single projections with long reductions (K >= 2048: down, and o at
+// 8B widths) and no RoPE epilogue: the split-K form, 128 x 64 blocks (814) where
+// those give >= 64 column blocks, else 128 x 32 (813), split to ~232 blocks and summed
+// with the epilogue by the 16x16 kernel's reduce launches. Measured on MI355X (us,
+// with the residual + next-RMSNorm reduce): 4864 -> 896 at 64 / 128 / 256 rows 9.8 /
+// 12.1 / 23.2 -> 9.7 / 10.7 / 13.5 (813); 4096 -> 4096 at 64 / 128 / 256 rows 24.4 /
+// 25.7 / 29.1 -> 15.1 / 17.9 / 22.3 (814); 14336 -> 4096 at 128 rows 65.9 -> 31.4; at
+// K = 896 (0.5B o, q/k/v) the 16x16 plan stays (7.3 / 7.8 against 7.5 / 7.8 at best).
+int lds_short_single(int M, int N, int K) {
+  if (M < 32 || M > 256 || K < 2048 || K % 64 != 0) return 0;
+  return (long long)((N + 63) / 64) * ((M + 127) / 128) >= 64 ? 814 : 813;
+}
+
+int lds_auto(int bits, int M, int N, int K, int group, bool paired, bool gate, bool rope) {
   if (bits != 4 || gate || K % 64 != 0 || (group & (group - 1)) != 0 || group < 32 || (K / group) % 2 != 0)
     return 0;
   // the kernel's per-lane load offsets are 32-bit
   if ((long long)M * K * 2 >= (1LL << 31) || (long long)N * K / 2 >= (1LL << 31)) return 0;
   if (M < 1024) {
-    if (!paired || M < 32 || M > 256) return 0;
+    if (!paired) return rope ? 0 : lds_short_single(M, N, K);
+    if (M < 32 || M > 256) return 0;
     const long long mb = (M + 127) / 128;
     if (M > 64 && (long long)((N + 63) / 64) * mb >= 128) return 812;
     return (long long)((N + 31) / 32) * mb <= 256 ? 811 : 0;
@@ -645,9 +666,24 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
     p.lds = true;
     p.lds_bm = tile / 10 == 82 ? 256 : 128;
     p.lds_waves = tile / 10 == 82 ? 8 : 4;
-    p.lds_bn = tile == 811 ? 32 : tile == 823 ? 192 : tile == 822 ? 128 : 64;
+    p.lds_bn = tile == 811 || tile == 813 ? 32 : tile == 823 ? 192 : tile == 822 ? 128 : 64;
     p.splits = 1;
     p.kslice = K;
+    if (lds_split_code(tile)) {
+      // k slices of whole 64-k steps; automatic: ~232 blocks (232 / column blocks,
+      // rounded), at least two steps a slice
+      const int steps = K / 64;
+      int s = splits;
+      if (s <= 0) {
+        const long long cols = (long long)((N + p.lds_bn - 1) / p.lds_bn) * ((M + 127) / 128);
+        s = (int)((232 + cols / 2) / cols);
+        if (s > steps / 2) s = steps / 2;
+      }
+      if (s < 1) s = 1;
+      if (s > steps) s = steps;
+      p.kslice = ((steps + s - 1) / s) * 64;
+      p.splits = (K + p.kslice - 1) / p.kslice;
+    }
     return p;
   }
   if (wide_code(tile)) {
@@ -701,9 +737,9 @@ GemmPlan gemm_plan(int M, int N, int K, int tile, int splits, bool paired) {
 // the allocation-free entry point, which sizes its split against its scratch).
 extern "C++" void aoto::resolve_gemm_codes(int M, int N, int K, int group, bool gate, int* tile, int* splits) {
   if (*tile == 0 && *splits == 0) {
-    if (const int code = lds_auto(4, M, N, K, group, false, gate)) {
+    if (const int code = lds_auto(4, M, N, K, group, false, gate, false)) {
       *tile = code;
-      *splits = 1;
+      *splits = gemm_plan(M, N, K, code, 0, false).splits;  // 1 unless the short split form
       return;
     }
   }
@@ -733,9 +769,17 @@ void qkv_rope_plan(int M, int N, int K, int head_dim, int* tile, int* splits) {
 
 size_t aoto_hip_w4_gemm_workspace(int M, int N, int K, int tile, int splits) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  // automatic codes: enough for the short prompts' split dequant-once plan too, which
+  // the group, code width and epilogue (not known here) may select
+  const int short_split = tile == 0 && splits == 0 ? lds_short_single(M, N, K) : 0;
   resolve_auto(M, N, K, false, &tile, &splits);
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, false);
-  return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+  size_t bytes = p.splits > 1 || lds_split_code(tile) ? (size_t)p.splits * M * N * sizeof(float) : 0;
+  if (short_split) {
+    const size_t lds_bytes = (size_t)gemm_plan(M, N, K, short_split, 0, false).splits * M * N * sizeof(float);
+    if (lds_bytes > bytes) bytes = lds_bytes;
+  }
+  return bytes;
 }
 
 size_t aoto_hip_w4_gemm_gate_up_workspace(int M, int N, int K, int tile, int splits) {
@@ -797,9 +841,9 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   if (tile != 0 && tile != 12 && tile != 14 && tile != 18 && tile != 24 && tile != 28 && !wide_code(tile) &&
       !lds_code(tile))
     return fail(AOTO_ERR_ARGUMENT, "%s: tile code %d is not one of 12, 14, 18, 24, 28, 241, 242, 243, 281, 441, "
-                "811, 812, 821, 822, 823", what, tile);
+                "811, 812, 813, 814, 821, 822, 823", what, tile);
   if (lds_code(tile)) {
-    if (bits != 4 || lds_paired_code(tile) != paired || gate != nullptr || splits > 1)
+    if (bits != 4 || lds_paired_code(tile) != paired || gate != nullptr || (splits > 1 && !lds_split_code(tile)))
       return fail(AOTO_ERR_ARGUMENT, "%s: tile %d is the unsplit 4-bit %s form without a gate epilogue", what, tile,
                   lds_paired_code(tile) ? "paired" : "single");
     if ((group & (group - 1)) != 0 || K % 64 != 0 || (K / group) % 2 != 0)
@@ -819,16 +863,17 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
                   "power-of-two groups per row (K=%d group=%d)", what, tile, K, group);
   }
   if (tile == 0 && splits == 0) {
-    if (const int code = lds_auto(bits, M, N, K, group, paired, gate != nullptr)) tile = code;
+    if (const int code = lds_auto(bits, M, N, K, group, paired, gate != nullptr, rope != nullptr)) tile = code;
   }
   resolve_auto(M, N, K, paired, &tile, &splits);
   if (bits == 8 && tile == 243) tile = 441;  // no 8-bit 243 instance; the same (unsplit) grid class
   const GemmPlan p = gemm_plan(M, N, K, tile, splits, paired);
-  if (p.splits > 1 && (workspace == nullptr || !aligned16(workspace)))
+  const bool lds_split = lds_split_code(tile);  // partials at every split count, 1 included
+  if ((p.splits > 1 || lds_split) && (workspace == nullptr || !aligned16(workspace)))
     return fail(AOTO_ERR_ARGUMENT, "%s: %d-way split-K needs a 16-byte aligned workspace of "
                 "aoto_hip_w4_gemm%s_workspace() bytes", what, p.splits, paired ? "_gate_up" : "");
   const int bn = p.bn(), bm = p.bm();
-  const bool split = p.splits > 1;
+  const bool split = p.splits > 1 || lds_split;
   const bool wide = p.wide_mt != 0;
   char family[24];
   if (wide)
@@ -839,7 +884,13 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
   float* partials = split ? static_cast<float*>(workspace) : nullptr;
   const long long quads = (long long)M * N / 4;
   char name[64];
-  if (p.lds) {
+  if (lds_split) {
+    // dequant-once split partials; the reduce launches below sum them with the epilogue
+    snprintf(name, sizeof(name), "aoto_w4_gemm_d4c%dw%dx1_split", p.lds_bn / 32, p.lds_bn / 32);
+    if (int st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, partials, M, N, K, group,
+                        p.kslice))
+      return st;
+  } else if (p.lds) {
     // dequant-once kernel: unsplit, its own epilogues; norm / RoPE launches follow as
     // after any unsplit GEMM
     int st;
@@ -874,11 +925,13 @@ int packed_gemm(int bits, const void* x, const int32_t* words, const void* scale
     snprintf(name, sizeof(name), "aoto_w%d_gemm_n%d_m%d_rope_b%d", bits, p.tn, p.tm, bias != nullptr);
     return launch(name, grid, dim3(256), 0, stream, x, words, scales, bias, y, M, N, K, group, *rope);
   }
-  const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
-  snprintf(name, sizeof(name), "aoto_w%d_gemm_%s_b%d_r%d_g%d", bits, family, b, r, g);
-  if (int st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, bias, residual, gate, y, M, N, K, group,
-                      p.kslice, partials))
-    return st;
+  if (!lds_split) {
+    const int b = !split && bias != nullptr, r = !split && residual != nullptr, g = !split && gate != nullptr;
+    snprintf(name, sizeof(name), "aoto_w%d_gemm_%s_b%d_r%d_g%d", bits, family, b, r, g);
+    if (int st = launch(name, grid, dim3(p.threads()), 0, stream, x, words, scales, bias, residual, gate, y, M, N, K,
+                        group, p.kslice, partials))
+      return st;
+  }
   if (norm_out != nullptr) {
     if (!split)
       return launch("aoto_rms_norm", dim3((M + 3) / 4), dim3(256), 0, stream, y, norm_weight, eps, norm_out, M, N);

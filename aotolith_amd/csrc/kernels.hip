@@ -112,6 +112,8 @@ AOTO_GEMM_LDS_INSTANCE(8, 2, 3, 0, 1)
 AOTO_GEMM_LDS_PAIRED_INSTANCE(8, 2, 1)
 AOTO_GEMM_LDS_PAIRED_INSTANCE(4, 2, 1)
 AOTO_GEMM_LDS_PAIRED_COLUMN_INSTANCE(4, 1, 1)
+AOTO_GEMM_LDS_SPLIT_INSTANCE(4, 1, 1, 1)
+AOTO_GEMM_LDS_SPLIT_INSTANCE(4, 2, 2, 1)
 // The q/k/v projection with bias, RoPE and cache fill: {code width} x {n tiles} x {m tiles} x {bias}.
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 0)
 AOTO_GEMM_ROPE_INSTANCE(4, 1, 2, 1)

@@ -76,20 +76,24 @@ AOTO_DEVICE int lds_unit(int r, int u) { return r * 128 + ((u ^ ((r >> 1) & 7)) 
 // for 6 at NT = 3; the 128-row paired form (4 waves, WGN = 1, MT = NT = 1) 3 for 2.
 // X takes three staging buffers where they fit 160 KB, else two (WR = 192 at 256
 // rows: each step's X is then loaded one step ahead).
-template <int NW, int WGN, int MT, int NT, bool PAIRED, bool BIAS, bool RESIDUAL>
+// PARTIAL (split-K, the single form): block z of the grid's third dimension takes k
+// in [z kslice, min(K, (z + 1) kslice)) and stores its f32 tile to partials[z][m][n]
+// (the layout the split reduce kernels of w4_gemm.h read); no epilogue.
+template <int NW, int WGN, int MT, int NT, bool PAIRED, bool BIAS, bool RESIDUAL, bool PARTIAL = false>
 __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t* __restrict__ words,
                                  const uint16_t* __restrict__ scales, const uint32_t* __restrict__ up_words,
                                  const uint16_t* __restrict__ up_scales, const uint16_t* __restrict__ bias,
                                  const uint16_t* __restrict__ residual, uint16_t* __restrict__ Y, int M, int N,
-                                 int K, int group) {
+                                 int K, int group, float* __restrict__ partials = nullptr, int kslice = 0) {
   static_assert(!(PAIRED && (BIAS || RESIDUAL)), "the paired form has its own epilogue");
+  static_assert(!(PARTIAL && (PAIRED || BIAS || RESIDUAL)), "split partials carry no epilogue");
   constexpr int NP = PAIRED ? 2 : 1;
   static_assert(WGN == 1 || WGN == 2, "one or two waves along n");
   constexpr int WGM = NW / WGN;
   constexpr int BM = WGM * 32 * MT;
   constexpr int BNW = WGN * 32 * NT;  // columns per weight
   constexpr int WR = NP * BNW;                       // weight rows per block
-  static_assert(WR == 64 || WR == 128 || WR == 192, "64, 128 or 192 weight rows per block");
+  static_assert(WR == 32 || WR == 64 || WR == 128 || WR == 192, "32, 64, 128 or 192 weight rows per block");
   static_assert(BM == 256 || BM == 128, "256 or 128 X rows per block");
   constexpr int XT = BM * 128;                       // bytes of a staged X tile
   constexpr int XDW = XT / 1024 / NW;                // 1-KB X loads per wave and step
@@ -121,7 +125,8 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   const int kw = K >> 3;
   const int groups = K / group;
   const int gshift = __builtin_ctz(group);
-  const int steps = K / kLdsBK;
+  const int kbase = PARTIAL ? (int)blockIdx.z * kslice : 0;  // kslice % 64 == 0 (host)
+  const int steps = ((PARTIAL ? min(K, kbase + kslice) : K) - kbase) / kLdsBK;
 
   wide_f32x16 acc[NP][NT][MT];
 #pragma unroll
@@ -156,7 +161,7 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
 
   // Step st's loads (steps past the end re-read the last one).
   auto issue_x = [&](int st, uint8_t* xb) __attribute__((always_inline)) {
-    const int k0 = min(st, steps - 1) * kLdsBK;
+    const int k0 = kbase + min(st, steps - 1) * kLdsBK;
     const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(X) + 2 * k0;
 #pragma unroll
     for (int i = 0; i < XDW; ++i) dma16_raw(xsrc, xoff[i], xb + (wave_u * XDW + i) * 1024);
@@ -164,7 +169,7 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   // units k0 / 8 .. + 8 of the row (4 bytes each); the scale dword holding group k0 >> gshift
   // (groups per row are even, so the aligned pair never leaves the row)
   auto issue_p = [&](int st, uint8_t* pb) __attribute__((always_inline)) {
-    const int k0 = min(st, steps - 1) * kLdsBK;
+    const int k0 = kbase + min(st, steps - 1) * kLdsBK;
     if (2 * PW == 64 || lane < 2 * PW) dma16_raw(pbase + (k0 >> 3) * 4, poff, pb + wave_u * 32 * PW);
     if (lane < PW) dma4_raw(sbase + ((k0 >> gshift) & ~1) * 2, soff, pb + PT + wave_u * 4 * PW);
   };
@@ -187,7 +192,7 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   // the scale of this thread's unit: group 32 -> group du / 4 of the step's pair;
   // larger -> the step's group, the low or high half of its aligned pair
   auto expand = [&](int v, int st) __attribute__((always_inline)) {
-    const int k0 = min(st, steps - 1) * kLdsBK;
+    const int k0 = kbase + min(st, steps - 1) * kLdsBK;
     const int hsel = group == 32 ? (du >> 2) : ((k0 >> gshift) & 1);
     const float s = bf16_to_f32((dscale[v] >> (16 * hsel)) & 0xFFFFu);
     return wide_dequant(dword[v], wide_scale<4>(s), km);
@@ -338,6 +343,29 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
   static_assert(NW <= 2 * SLOTS, "a slot per wave in the first two X buffers");
   float* slot = reinterpret_cast<float*>((wave < SLOTS ? xs0 : xs1) + (wave % SLOTS) * 4608);
   const int m_wave = m_block + 32 * MT * wm;
+  if constexpr (PARTIAL) {
+    float* part = partials + (size_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int n = n_block + 32 * (NT * wn + i) + 4 * (lane & 7);
+#pragma unroll
+      for (int u = 0; u < MT; ++u) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(slot + col * 36 + 8 * g + 4 * half) =
+              make_float4(acc[0][i][u][4 * g], acc[0][i][u][4 * g + 1], acc[0][i][u][4 * g + 2],
+                          acc[0][i][u][4 * g + 3]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = (lane >> 3) + 8 * q;
+          const int m = m_wave + 32 * u + r;
+          const float4 f = *reinterpret_cast<const float4*>(slot + r * 36 + 4 * (lane & 7));
+          if (m < M && n < N) *reinterpret_cast<float4*>(part + (size_t)m * N + n) = f;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
     const int n0 = n_block + 32 * (NT * wn + i);
@@ -405,6 +433,16 @@ __device__ void w4_gemm_lds_body(const uint16_t* __restrict__ X, const uint32_t*
       const uint16_t* up_scales, uint16_t* Y, int M, int N, int K, int group) {                               \
     aoto::w4_gemm_lds_body<NW, 2, MT, NT, true, false, false>(X, words, scales, up_words, up_scales, nullptr,   \
                                                               nullptr, Y, M, N, K, group);                   \
+  }
+// aoto_w4_gemm_d{NW}c{WGN}w{MT}x{NT}_split: the single form's split-K partials (f32
+// partials[z][m][n], k slice z of kslice), for short prompts whose column blocks alone
+// do not fill the chip; a reduce kernel applies the epilogue.
+#define AOTO_GEMM_LDS_SPLIT_INSTANCE(NW, WGN, MT, NT)                                                         \
+  extern "C" __global__ __launch_bounds__(64 * NW, 1) void aoto_w4_gemm_d##NW##c##WGN##w##MT##x##NT##_split(   \
+      const uint16_t* X, const uint32_t* words, const uint16_t* scales, float* partials, int M, int N, int K, \
+      int group, int kslice) {                                                                                \
+    aoto::w4_gemm_lds_body<NW, WGN, MT, NT, false, false, false, true>(                                       \
+        X, words, scales, nullptr, nullptr, nullptr, nullptr, nullptr, M, N, K, group, partials, kslice);     \
   }
 // aoto_w4_gemm_d{NW}c1w{MT}x{NT}_paired: the same with one wave along n (at NW = 4,
 // MT = NT = 1: 128 x (32 + 32) blocks, twice the blocks of the 64-column form for

@@ -989,7 +989,8 @@ class _Engine:
             _mark(rec, "addmm" if s.qkv_bias else "matmul", f"qkv_{index}", gemm,
                   (f"dequant-once W{bits} GEMM (packed tiles expanded once per 256-row block into LDS) on "
                    "32x32x16 bf16 MFMA"
-                   if ops.lds_plan(m, s.qkv_width, s.hidden, group_size=layer.qkv.group, bits=bits) is not None
+                   if ops.lds_plan(m, s.qkv_width, s.hidden, group_size=layer.qkv.group, bits=bits, rope=True)
+                   is not None
                    else f"wide-tile fused-dequant W{bits} GEMM on 32x32x16 bf16 MFMA"
                    if ops.wide_plan(m, s.qkv_width, s.hidden) is not None
                    else f"fused-dequant W{bits} GEMM on bf16 MFMA") + (" with q/k/v bias" if s.qkv_bias else "")

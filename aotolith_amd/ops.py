@@ -392,26 +392,34 @@ LDS_TILE, LDS_WIDE_TILE, LDS_PAIRED_TILE = 822, 823, 821
 #: the paired dequant-once forms for short prompts (128-row blocks of 4 waves):
 #: 64 + 64 and 32 + 32 columns per block
 LDS_SHORT_PAIRED_TILE, LDS_SHORT_NARROW_TILE = 812, 811
+#: the single form's split-K partials for short prompts: 128 x 64 and 128 x 32 blocks
+LDS_SPLIT_TILE, LDS_SPLIT_NARROW_TILE = 814, 813
 
 
 def lds_plan(m: int, n: int, k: int, *, group_size: int = 64, paired: bool = False, bits: int = 4,
-             gate: bool = False) -> int | None:
+             gate: bool = False, rope: bool = False) -> int | None:
     """The tile code the automatic plan runs on the dequant-once kernel for this shape, else
     None: the Python mirror of the C ABI's ``lds_auto`` (4-bit codes, no gate epilogue,
     K % 64 == 0, a power-of-two group with an even count per row; from 1024 rows a grid
     of at least 256 blocks whose last round of 256 is at least 90% full: 128 columns per
     block where that fills the rounds, else 192; for a paired gate/up of 32-256 rows the
     128-row forms: 64 + 64 columns where that gives at least 128 blocks from 65 rows,
-    else 32 + 32 where that fits 256 blocks)."""
+    else 32 + 32 where that fits 256 blocks; for a single projection of 32-256 rows with
+    K >= 2048 and no RoPE epilogue (``rope``) the split-K form, 128 x 64 blocks where
+    those give at least 64 column blocks, else 128 x 32)."""
 
     if bits != 4 or gate or k % 64 or group_size < 32 or group_size & (group_size - 1):
         return None
     if (k // group_size) % 2 or m * k * 2 >= 2 ** 31 or n * k // 2 >= 2 ** 31:
         return None
     if m < 1024:
-        if not paired or m < 32 or m > 256:
+        if m < 32 or m > 256:
             return None
         mb = -(-m // 128)
+        if not paired:
+            if rope or k < 2048:
+                return None
+            return LDS_SPLIT_TILE if -(-n // 64) * mb >= 64 else LDS_SPLIT_NARROW_TILE
         if m > 64 and -(-n // 64) * mb >= 128:
             return LDS_SHORT_PAIRED_TILE
         return LDS_SHORT_NARROW_TILE if -(-n // 32) * mb <= 256 else None

@@ -385,7 +385,7 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
     bits = eng.state.bits
     plan = ops.wide_plan(m, spec.qkv_width, h)
     gemm = f"aoto_w{bits}_gemm_w* (wide tiles, 32x32x16 MFMA)" if ops.wide_plan(m, h, h) else f"aoto_w{bits}_gemm_n*"
-    if ops.lds_plan(m, spec.qkv_width, h, bits=bits) is not None:
+    if ops.lds_plan(m, spec.qkv_width, h, bits=bits, rope=True) is not None:
         qkv_label = ("aoto_w4_gemm_d8w* (packed tiles expanded once per 256-row block into LDS) + bias, then "
                      "aoto_rope_qkv_rows (RoPE and cache fill)")
     elif plan is not None:
@@ -400,6 +400,10 @@ def prefill_kernel_table(runtime, torch, ops) -> list[dict]:
                                    "block into LDS, 32x32x16 MFMA)",
         ops.LDS_SHORT_PAIRED_TILE: "aoto_w4_gemm_d4w2x1_paired (packed tiles expanded once per 128 x (64 + 64) "
                                    "block into LDS, 32x32x16 MFMA)",
+        ops.LDS_SPLIT_NARROW_TILE: "aoto_w4_gemm_d4c1w1x1_split (packed tiles expanded once per 128 x 32 block "
+                                   "into LDS, 32x32x16 MFMA, split-K partials) + reduce",
+        ops.LDS_SPLIT_TILE: "aoto_w4_gemm_d4c2w2x1_split (packed tiles expanded once per 128 x 64 block into "
+                            "LDS, 32x32x16 MFMA, split-K partials) + reduce",
     }
 
     def label(n_, k_, paired=False):

@@ -130,10 +130,14 @@ int aoto_hip_w4_gemv(const void* x, const int32_t* words, const void* scales,
  * short prompts 812 / 811) the dequant-once kernel (each packed tile expanded once per block into
  * LDS; 256 x 128 / 256 x 192 / 256 x (64 + 64) blocks of 8 waves, 128 x (64 + 64) / 128 x (32 +
  * 32) blocks of 4 waves; 4-bit codes, unsplit, no gate epilogue, K % 64 == 0, an even number of
- * power-of-two groups per row, x and the packed words under 2 GiB). Automatic codes take the
- * dequant-once kernel for 4-bit codes from M >= 1024 when its grid's last round of 256 blocks is
- * at least 90% full, for a paired gate/up of 32-256 rows on 128-row blocks (812 where that gives
- * >= 128 blocks from 65 rows, else 811 within 256 blocks), else the wide kernel from M >= 512 when
+ * power-of-two groups per row, x and the packed words under 2 GiB); 814 / 813 its split-K form
+ * for single projections (128 x 64 / 128 x 32 blocks of 4 waves storing f32 partials that the
+ * reduce launch sums with the epilogue, at every split count, so they always take a workspace).
+ * Automatic codes take the dequant-once kernel for 4-bit codes from M >= 1024 when its grid's
+ * last round of 256 blocks is at least 90% full, for a paired gate/up of 32-256 rows on 128-row
+ * blocks (812 where that gives >= 128 blocks from 65 rows, else 811 within 256 blocks), for a
+ * single projection of 32-256 rows with K >= 2048 and no RoPE epilogue the split form (814
+ * where that gives >= 64 column blocks, else 813), else the wide kernel from M >= 512 when
  * K % 256 == 0 (group <= 128), else the 16x16 kernel. splits: 0 chooses (small
  * grids split the reduction), else the split-K count; a split launch stores f32
  * partial tiles in `workspace` (aoto_hip_w4_gemm_workspace() bytes, 16-byte

@@ -101,7 +101,9 @@ def test_lds_plan_takes_the_full_rounds_at_long_prompts():
     columns would be 1.5 rounds, 256 of 192 are one); 1024-row o / down grids (128 blocks),
     8-bit codes, gate epilogues and odd group counts do not; at 32-256 rows the paired
     gate/up takes the 128-row forms (64 + 64 columns where that gives 128 blocks, else 32 +
-    32 within one round); its tiles need no split-K workspace - host logic only."""
+    32 within one round), and single projections with K >= 2048 its split-K form, whose
+    partials the automatic workspace query covers; its unsplit tiles need no split-K
+    workspace - host logic only."""
 
     from aotolith_amd import ops
 
@@ -123,7 +125,15 @@ def test_lds_plan_takes_the_full_rounds_at_long_prompts():
     assert ops.lds_plan(128, 14336, 4096, paired=True) == ops.LDS_SHORT_PAIRED_TILE  # 224 blocks
     assert ops.lds_plan(64, 14336, 4096, paired=True) is None  # 448 blocks of 32 + 32: more than a round
     assert ops.lds_plan(16, 4864, 896, paired=True) is None and ops.lds_plan(300, 4864, 896, paired=True) is None
-    assert ops.lds_plan(128, 4864, 896) is None and ops.lds_plan(128, 4864, 896, paired=True, bits=8) is None
+    assert ops.lds_plan(128, 4864, 896, paired=True, bits=8) is None
+    # short prompts, single projections with K >= 2048 and no RoPE: the split-K form
+    assert ops.lds_plan(128, 896, 4864) == ops.LDS_SPLIT_NARROW_TILE  # 28 column blocks of 32
+    assert ops.lds_plan(128, 4096, 4096) == ops.LDS_SPLIT_TILE  # 64 column blocks of 64
+    assert ops.lds_plan(128, 896, 896) is None and ops.lds_plan(128, 4864, 896) is None  # K < 2048
+    assert ops.lds_plan(128, 6144, 4096, rope=True) is None and ops.lds_plan(16, 896, 4864) is None
+    # the automatic workspace covers the split plan: 232 / 28 -> 8 slices of 10 steps (76 in all)
+    assert ops.gemm_workspace_bytes(128, 896, 4864) == 8 * 128 * 896 * 4
+    assert ops.gemm_workspace_bytes(128, 896, 4864, ops.LDS_SPLIT_NARROW_TILE, 1) == 128 * 896 * 4
     for tile in (ops.LDS_TILE, ops.LDS_WIDE_TILE, ops.LDS_PAIRED_TILE):
         assert ops.gemm_workspace_bytes(2048, 4096, 4096, tile, 0) == 0
         assert ops.gate_up_workspace_bytes(2048, 4096, 4096, tile, 0) == 0

@@ -1,8 +1,8 @@
 """GPU parity of the dequant-once prefill GEMM (csrc/w4_gemm_lds.h, tile codes 811 / 812 /
-821 / 822 / 823).
+813 / 814 / 821 / 822 / 823).
 
 Each 64-k step of a block's packed words is expanded once into an LDS bf16 tile that the
-block's waves (8 on 256-row blocks, 4 on the short prompts' 128-row paired blocks) read as
+block's waves (8 on 256-row blocks, 4 on the short prompts' 128-row blocks) read as
 MFMA operands. Every form is compared with the CPU oracle within one bf16 ulp (two for the
 silu_mul products) and with the wide-tile kernel under an explicit plan: ragged M and N
 tails, step counts that leave every remainder of the six-step unrolled loop, groups of 32 /
@@ -53,6 +53,7 @@ def _lds(names):
 
 
 SHORT_PAIRED = {811: "aoto_w4_gemm_d4c1w1x1_paired", 812: "aoto_w4_gemm_d4w2x1_paired"}
+SHORT_SPLIT = {813: "aoto_w4_gemm_d4c1w1x1_split", 814: "aoto_w4_gemm_d4c2w2x1_split"}
 
 
 @pytest.mark.parametrize("group,k", [(32, 448), (32, 896), (32, 576), (64, 640), (32, 704), (128, 768),
@@ -180,6 +181,74 @@ def test_lds_gate_up_is_the_automatic_plan_at_short_prompts():
     assert not _lds(names), names
 
 
+@pytest.mark.parametrize("tile", [813, 814])
+@pytest.mark.parametrize("m,group,k,splits,epilogue", [
+    (1, 64, 640, 3, "bias"),         # 10 steps in slices of 4, 4, 2
+    (50, 32, 2240, 0, "residual"),   # automatic split count, 35 steps
+    (128, 64, 4864, 0, "norm"),      # the 0.5B down shape's K, residual + next RMSNorm
+    (200, 128, 1536, 1, "none"),     # one slice: partials + reduce all the same
+    (128, 64, 1152, 7, "residual"),  # 18 steps in slices of 3
+])
+def test_lds_split_short_prompt_tiles(tile, m, group, k, splits, epilogue):
+    """Tiles 813 / 814 (the single form's split-K partials on 128 x 32 / 128 x 64 blocks
+    of 4 waves) summed and finished by the reduce launches: ragged rows (1-200), N = 608
+    (19 / 9.5 column blocks), slices that leave every kind of last slice, groups 32-128,
+    the bias, residual and residual + RMSNorm epilogues, within one bf16 ulp of the
+    oracle."""
+
+    ops = _ops()
+    n = 608
+    rng = np.random.default_rng(770 + m + k + splits + len(epilogue))
+    packed, scales, gp, gs = _weights(rng, n, k, group)
+    x = bf16_normal(rng, (m, k))
+    gx = to_gpu_bf16(x)
+    ws = torch.empty(max(ops.gemm_workspace_bytes(m, n, k, tile, splits), 16), dtype=torch.uint8, device="cuda")
+    if epilogue == "norm":
+        residual = bf16_normal(rng, (m, n), 2.0)
+        weight = bf16_normal(rng, (n,), 0.1) + 1.0
+        (y, normed), names = _traced(lambda: ops.matmul_residual_norm(
+            gx, gp, gs, group, to_gpu_bf16(residual), to_gpu_bf16(weight), 1e-6, tile=tile, splits=splits,
+            workspace=ws))
+        assert names == [SHORT_SPLIT[tile], "aoto_w4_gemm_reduce_norm"], names
+        expected = oracle.w4_matmul(x, packed, scales, group, residual=residual)
+        assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0, atol=_atol(expected))
+        want_norm = oracle.rms_norm(from_gpu_bf16(y), round_bf16(weight), 1e-6)
+        assert_bf16_parity(from_gpu_bf16(normed), want_norm, max_ulp=1.0)
+        return
+    kwargs = {}
+    if epilogue == "bias":
+        kwargs["bias"] = bf16_normal(rng, (n,), 0.5)
+    elif epilogue == "residual":
+        kwargs["residual"] = bf16_normal(rng, (m, n), 2.0)
+    gkw = {key: to_gpu_bf16(value) for key, value in kwargs.items()}
+    y, names = _traced(lambda: ops.w4_matmul(gx, gp, gs, group, tile=tile, splits=splits, workspace=ws, **gkw))
+    assert names == [SHORT_SPLIT[tile], "aoto_w4_gemm_reduce"], names
+    expected = oracle.w4_matmul(x, packed, scales, group, **kwargs)
+    assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0, atol=_atol(expected))
+
+
+def test_lds_split_is_the_automatic_plan_for_short_long_k_projections():
+    """At 128 rows a 0.5B down projection (4864 -> 896) takes tile 813 split eight ways by
+    itself and an 8B o projection (4096 -> 4096) tile 814; K = 896 stays on the 16x16
+    kernel; each within one ulp of the oracle."""
+
+    ops = _ops()
+    rng = np.random.default_rng(780)
+    for n, k, want in [(896, 4864, 813), (4096, 4096, 814), (896, 896, None)]:
+        m = 128
+        assert ops.lds_plan(m, n, k) == want
+        packed, scales, gp, gs = _weights(rng, n, k)
+        x = bf16_normal(rng, (m, k))
+        residual = bf16_normal(rng, (m, n), 2.0)
+        y, names = _traced(lambda: ops.w4_matmul(to_gpu_bf16(x), gp, gs, 64, residual=to_gpu_bf16(residual)))
+        if want is None:
+            assert not _lds(names) and not any(name.endswith("_split") for name in names), names
+        else:
+            assert names == [SHORT_SPLIT[want], "aoto_w4_gemm_reduce"], names
+        expected = oracle.w4_matmul(x, packed, scales, 64, residual=residual)
+        assert_bf16_parity(from_gpu_bf16(y), expected, max_ulp=1.0, atol=_atol(expected))
+
+
 def test_lds_gemm_in_place_residual():
     ops = _ops()
     m, n, k = 512, 512, 1024
@@ -229,9 +298,9 @@ def test_lds_gemm_is_the_automatic_plan_at_2048_rows():
 
 
 def test_lds_gemms_replay_in_a_graph_like_eager():
-    """A captured bias, residual (in place) and paired sequence on tiles 822 / 821 / 811
-    replays three times, with eager work and synchronizations between, bit-identical to its
-    eager pass each time."""
+    """A captured bias, residual (in place), paired and split sequence on tiles 822 / 821 /
+    811 / 813 replays three times, with eager work and synchronizations between,
+    bit-identical to its eager pass each time."""
 
     ops = _ops()
     m, n, k = 512, 640, 768
@@ -244,15 +313,18 @@ def test_lds_gemms_replay_in_a_graph_like_eager():
     residual = residual0.clone()
 
     outs["short"] = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    outs["split"] = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(ops.gemm_workspace_bytes(m, n, k, 813, 3), dtype=torch.uint8, device="cuda")
 
     def body():
         ops.w4_matmul(x, *weights[0], 64, bias=bias, out=outs["bias"], tile=822)
         ops.w4_matmul_gate_up(x, *weights[1], *weights[2], 64, out=outs["paired"], tile=821)
         ops.w4_matmul_gate_up(x, *weights[1], *weights[2], 64, out=outs["short"], tile=811)
+        ops.w4_matmul(x, *weights[2], 64, bias=bias, out=outs["split"], tile=813, splits=3, workspace=ws)
         ops.w4_matmul(x, *weights[0], 64, residual=residual, out=residual, tile=822)
 
     _, names = _traced(body)
-    assert len(_lds(names)) == 4, names
+    assert len(_lds(names)) == 5, names
     torch.cuda.synchronize()
     eager = {name: t.clone() for name, t in outs.items()}
     eager["residual"] = residual.clone()
@@ -296,6 +368,8 @@ def test_lds_tiles_refuse_what_they_cannot_run():
         ops.w4_matmul_gate_up(x, gp, gs, gp, gs, 64, tile=812, splits=2)
     with pytest.raises(HipKernelError, match="tile 822"):
         ops.w4_matmul_gate_up(x, gp, gs, gp, gs, 64, tile=822)
+    with pytest.raises(HipKernelError, match="tile 813"):
+        ops.w4_matmul_gate_up(x, gp, gs, gp, gs, 64, tile=813)
     with pytest.raises(HipKernelError, match="tile 822"):
         ops.w4_matmul(x, gp, gs, 64, tile=822, splits=2)
     packed8, scales8 = pack_weight_bits_bf16(bf16_normal(rng, (256, 512), 0.02), 64, 8)

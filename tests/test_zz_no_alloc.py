@@ -96,6 +96,37 @@ def test_noalloc_gemm_takes_the_dequant_once_plan_where_the_workspace_entry_poin
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+def test_noalloc_gemm_takes_the_short_prompt_split_plan_where_the_workspace_entry_point_does():
+    """At 128 rows a down-shaped GEMM (K = 4864 -> 896) runs as the dequant-once split-K
+    partials (tile 813) plus the reduce under automatic codes in both entry points, its
+    3.7 MB of partials in the static scratch, bit-identical to the workspace entry point;
+    then a smaller call (64 rows) on the same scratch."""
+
+    from aotolith_amd import ops
+
+    for m in (128, 64):
+        n, k = 896, 4864
+        assert ops.lds_plan(m, n, k) == ops.LDS_SPLIT_NARROW_TILE
+        assert 0 < ops.gemm_workspace_bytes(m, n, k) <= SCRATCH_BYTES
+        rng = np.random.default_rng(96 + m)
+        packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
+        gp, gs = torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
+        x = to_gpu_bf16(bf16_normal(rng, (m, k)))
+        residual = to_gpu_bf16(bf16_normal(rng, (m, n)))
+        with ops.recording_launches() as take:
+            take()
+            want = ops.w4_matmul(x, gp, gs, 64, residual=residual)
+            got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+            torch.cuda.synchronize()
+            take()
+            status = _noalloc(x, gp, gs, 64, got, residual=residual)
+            names = take()
+        torch.cuda.synchronize()
+        assert status == 0, _last_error()
+        assert names == ["aoto_w4_gemm_d4c1w1x1_split", "aoto_w4_gemm_reduce"], names
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), m
+
+
 def test_noalloc_gemm_refuses_explicit_plans_beyond_its_scratch():
     from aotolith_amd import ops
 
@@ -114,13 +145,15 @@ def test_noalloc_gemm_refuses_explicit_plans_beyond_its_scratch():
 
 def test_noalloc_gemm_fits_automatic_plans_to_its_scratch():
     """Automatic codes whose split would need more than the scratch run with fewer splits:
-    the 16x16 plan at 256 rows (K = 4864 splits 16 ways on its own) and a wide plan at
-    512 rows both match the workspace entry point under the plan the scratch allows, bit
-    for bit; nothing is allocated (the device's free memory is unchanged)."""
+    the 16x16 plan at 256 rows (N = 4096, K = 1536: 4 splits, 16.8 MB of partials on its
+    own) and a wide plan at 1024 rows both match the workspace entry point under the plan
+    the scratch allows, bit for bit; nothing is allocated (the device's free memory is
+    unchanged)."""
 
     from aotolith_amd import ops
 
-    for m, n, k, tile, splits in [(256, 896, 4864, 0, 0), (1024, 1536, 4096, 241, 0)]:
+    for m, n, k, tile, splits in [(256, 4096, 1536, 0, 0), (1024, 1536, 4096, 241, 0)]:
+        assert ops.lds_plan(m, n, k) is None
         rng = np.random.default_rng(90 + m)
         packed, scales = pack_weight_bf16(bf16_normal(rng, (n, k), 0.02), 64)
         gp, gs = torch.from_numpy(packed).cuda(), to_gpu_bits(scales)
