@@ -1,4 +1,6 @@
-// Long-prefill W4 GEMM with each packed tile dequantized once per block into LDS.
+// Prefill W4 GEMM with each packed tile dequantized once per block into LDS (long
+// prompts on 256-row blocks of 8 waves; short prompts on 128-row blocks of 4 waves:
+// the paired gate/up, and single projections as split-K partials).
 //
 //   Y[m][n] = epilogue( sum_k X[m][k] * bf16(code[n][k] * s[n][k/group]) )
 //
@@ -34,7 +36,8 @@
 // rows, one unit) and of the expansion's stores covers the 64 banks once.
 // LDS at 128 weight rows: 3 x 32 + 2 x 16 + 3 x 4.5 KB = 141.5 KB; at 192 (the
 // q/k/v width of an 8B-class model: 6144 columns in 32 blocks) 2 x 32 + 2 x 24 +
-// 3 x 6.75 KB = 132.25 KB; one block per CU.
+// 3 x 6.75 KB = 132.25 KB; one block per CU. The 128-row forms stage [128][64] X
+// tiles (16 KB) and 128, 64 or 32 weight rows (70.75 KB at 64).
 #pragma once
 
 #include "common.h"
